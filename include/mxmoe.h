@@ -1,0 +1,231 @@
+/* mxmoe: MI355X (gfx950) quantized MoE expert arithmetic behind a C ABI.
+ *
+ * Plain pointers and sizes only. Device pointers are HIP device addresses;
+ * `stream` is a hipStream_t (NULL = the device's default stream). Every entry
+ * point returns MX_OK (0) or a negative status; mx_last_error() describes the
+ * most recent failure on the calling thread. Shapes are validated on the host
+ * before any device work, mirroring the reference's ValueError-before-device
+ * rule (tests/test_expert_boundaries.py:31-40 of shell-term/vesper).
+ *
+ * The reference binds CUDA probe kernels through ctypes (src/vesper/cuda.py);
+ * each declaration below names the reference interface it replaces.
+ */
+#ifndef MXMOE_H
+#define MXMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes; the Python adapter maps them to the reference's exception
+ * classes (src/vesper/cuda.py:18-19,62-67 and the ValueError/MemoryError/
+ * RuntimeError conventions of src/vesper/expert.py and src/vesper/moe.py). */
+#define MX_OK 0
+#define MX_ERR_INVALID (-1) /* ValueError: bad shape, range or argument      */
+#define MX_ERR_MEMORY (-2)  /* MemoryError: allocation cap or device memory */
+#define MX_ERR_STATE (-3)   /* RuntimeError: lifecycle misuse               */
+#define MX_ERR_HIP (-4)     /* CudaError analogue: HIP runtime failure      */
+
+typedef struct mx_ctx mx_ctx;
+typedef struct mx_layer mx_layer;
+
+/* ---- context, memory, streams (replaces Driver/Device, src/vesper/cuda.py:28-191) ---- */
+
+/* Description of the most recent failure on this thread (never NULL). */
+const char* mx_last_error(void);
+/* Number of visible HIP devices (0 when none; never fails). */
+int mx_device_count(void);
+/* Open device `device` with an explicit-allocation cap in bytes (0 = no cap);
+ * replaces Device(driver, ordinal, cap) (src/vesper/cuda.py:93-138). */
+int mx_create(int device, uint64_t cap_bytes, mx_ctx** out);
+/* Frees every allocation the context still owns (src/vesper/cuda.py:180-191). */
+int mx_destroy(mx_ctx* ctx);
+/* Name and gfx architecture of the context's device, e.g. "gfx950". */
+int mx_device_name(mx_ctx* ctx, char* name, size_t name_bytes, char* arch, size_t arch_bytes);
+int mx_malloc(mx_ctx* ctx, uint64_t bytes, void** dptr);       /* Device.allocate (cuda.py:121-138) */
+int mx_free(mx_ctx* ctx, void* dptr);                           /* Device.free                        */
+int mx_owned_bytes(mx_ctx* ctx, uint64_t* live, uint64_t* peak);/* Device.peak / allocations          */
+int mx_host_alloc_pinned(mx_ctx* ctx, uint64_t bytes, void** hptr); /* Pinned (cuda.py:200-222)       */
+int mx_host_free_pinned(mx_ctx* ctx, void* hptr);
+int mx_memcpy_h2d(mx_ctx* ctx, void* dst, const void* src, uint64_t bytes, void* stream); /* Device.upload   */
+int mx_memcpy_d2h(mx_ctx* ctx, void* dst, const void* src, uint64_t bytes, void* stream); /* Device.download */
+int mx_memcpy_d2d(mx_ctx* ctx, void* dst, const void* src, uint64_t bytes, void* stream);
+int mx_stream_create(mx_ctx* ctx, void** stream);
+int mx_stream_destroy(mx_ctx* ctx, void* stream);
+int mx_stream_sync(mx_ctx* ctx, void* stream);
+int mx_device_sync(mx_ctx* ctx);
+int mx_event_create(mx_ctx* ctx, void** event);
+int mx_event_destroy(mx_ctx* ctx, void* event);
+int mx_event_record(mx_ctx* ctx, void* event, void* stream);
+int mx_event_sync(mx_ctx* ctx, void* event);
+int mx_event_elapsed_ms(mx_ctx* ctx, void* start, void* stop, float* ms);
+/* Make `stream` wait for `event` (cross-stream ordering for slot reuse). */
+int mx_stream_wait_event(mx_ctx* ctx, void* stream, void* event);
+/* Deterministic synthetic bytes on the device: dst[i] = lo + hash(seed, i) % (hi - lo + 1). */
+int mx_fill_uniform_u8(mx_ctx* ctx, void* dst, uint64_t bytes, uint64_t seed, uint32_t lo, uint32_t hi, void* stream);
+
+/* ---- format hooks (replaces format_probe.cu decode_fp4/encode_fp8/activation32, lines 23-52) ---- */
+
+/* out[r][k] = E2M1(packed[r][k/2] nibble, low first) * E8M0(scales[r][k/32]); bit-exact. */
+int mx_dequant_mxfp4(mx_ctx* ctx, const uint8_t* packed, const uint8_t* scales, float* out,
+                     int64_t rows, int64_t k, void* stream);
+/* out[i] = E4M3(in[i]) (RNE, saturating, NaN -> 0x7F); bit-exact with formats.py:55-66. */
+int mx_encode_e4m3(mx_ctx* ctx, const float* in, uint8_t* out, int64_t n, void* stream);
+/* Per-32 activation quantizer over BF16 input [rows][width] (formats.py:80-94). */
+int mx_act_quant32(mx_ctx* ctx, const uint16_t* x_bf16, uint8_t* q, uint8_t* scales,
+                   int64_t rows, int64_t width, void* stream);
+/* Same quantizer over FP32 input (BF16-rounded first), the activation32 signature. */
+int mx_act_quant32_f32(mx_ctx* ctx, const float* x, uint8_t* q, uint8_t* scales,
+                       int64_t rows, int64_t width, void* stream);
+
+/* ---- expert arithmetic ---- */
+
+/* E4M3 x MXFP4 block GEMV (gemv_fp4 / gemv_fp4_mma, format_probe.cu:54-129; formats.py:97-118):
+ * y[t][n] = BF16(sum_g dot(q[t][g], W[n][g]) * sa[t][g] * sw[n][g]) for T <= 16 tokens;
+ * q [T][K] E4M3, sa [T][K/32] E8M0, W [N][K/2] packed E2M1, sw [N][K/32] E8M0. N % 64 == 0, K % 128 == 0. */
+int mx_gemv_mxfp4(mx_ctx* ctx, const uint8_t* q, const uint8_t* sa, const uint8_t* w, const uint8_t* sw,
+                  uint16_t* y_bf16, int32_t tokens, int32_t n, int32_t k, void* stream);
+
+/* One expert's six tensors in the reference layout (src/vesper/checkpoint.py:139-149):
+ * MXFP4: w*_weight [rows][width/2] bytes, w*_scale [rows][width/32] E8M0.
+ * FP8 block-32 (shared expert, src/vesper/shared.py:20-24): w*_weight [rows][width] E4M3,
+ * w*_scale [rows/32][width/32] E8M0. */
+typedef struct mx_expert_ptrs {
+  const void* w1_weight;
+  const void* w1_scale;
+  const void* w3_weight;
+  const void* w3_scale;
+  const void* w2_weight;
+  const void* w2_scale;
+} mx_expert_ptrs;
+
+#define MX_FMT_MXFP4 0
+#define MX_FMT_FP8_BLOCK32 1
+
+/* Per-stage device buffers of one expert call (all optional; NULL skips the stage copy).
+ * Row r of every buffer is token r. Mirrors the stage dict of ExpertExecutor.execute
+ * (src/vesper/expert.py:71-79): q, s, w1, w3, down_input (BF16 bits here), trace, down_q,
+ * down_s, w2. */
+typedef struct mx_expert_stages {
+  uint8_t* q;            /* [T][H]     */
+  uint8_t* s;            /* [T][H/32]  */
+  uint16_t* w1;          /* [T][I]     */
+  uint16_t* w3;          /* [T][I]     */
+  uint16_t* down_input;  /* [T][I]     */
+  float* trace;          /* [T][I][5]: clamped gate, clamped up, silu, product, routed */
+  uint8_t* down_q;       /* [T][I]     */
+  uint8_t* down_s;       /* [T][I/32]  */
+} mx_expert_stages;
+
+/* y[T][H] (BF16 bits) = expert(x[T][H] BF16) for 1 <= T <= 16 tokens; route_w[T] (device FP32)
+ * multiplies the SwiGLU product before W2, NULL = unweighted (shared expert).
+ * Replaces ExpertExecutor.execute (src/vesper/expert.py:51-79) and ResidentSharedExpert.forward
+ * (src/vesper/shared.py:169-170). */
+int mx_expert_forward(mx_ctx* ctx, const mx_expert_ptrs* w, int32_t format, int32_t hidden, int32_t intermediate,
+                      const uint16_t* x_bf16, int32_t tokens, float swiglu_limit, const float* route_w,
+                      uint16_t* y_bf16, const mx_expert_stages* stages, void* stream);
+
+/* ---- router (replaces GateProjection.project + RouterProbe, src/vesper/gate.py:133-147,
+ *      src/vesper/router.py:227-264, routing_probe.cu:5-86) ---- */
+
+#define MX_SCORE_SIGMOID 0
+#define MX_SCORE_SQRTSOFTPLUS 1
+
+typedef struct mx_router_out {
+  float* logits;       /* [T][E]  (required)   */
+  float* scores;       /* [T][E]  (optional)   */
+  float* selection;    /* [T][E]  (optional)   */
+  int32_t* indices;    /* [T][k]  (required)   */
+  float* weights;      /* [T][k]  (required)   */
+  float* raw;          /* [T][k]  (optional)   */
+  float* denominator;  /* [T]     (optional)   */
+  int32_t* tied;       /* [T]     (optional)   */
+} mx_router_out;
+
+/* logits[T][E] = W_r[E][H] (FP32) . x[T][H] (BF16 -> FP32) only: GateProjection.project
+ * (src/vesper/gate.py:133-147) with cublasSgemm(T, N, E, T, H) (src/vesper/blas.py:70-73). */
+int mx_gate_project(mx_ctx* ctx, const float* router_weight, const uint16_t* x_bf16, int32_t tokens,
+                    int32_t hidden, int32_t experts, float* logits, void* stream);
+
+/* logits = W_r[E][H] (FP32) . x[T][H] (BF16 -> FP32), then scores, selection = score + bias,
+ * top-k (reference tie order), route weights. E <= 1024, k <= 32. */
+int mx_router(mx_ctx* ctx, const float* router_weight, const float* bias, const uint16_t* x_bf16,
+              int32_t tokens, int32_t hidden, int32_t experts, int32_t top_k, int32_t score_func,
+              float route_scale, const mx_router_out* out, void* stream);
+/* Selection postprocessing on supplied logits (RouterProbe.inspect, router.py:227-241):
+ * scores/selection/indices/weights from logits[T][E]. */
+int mx_router_postprocess(mx_ctx* ctx, const float* logits, const float* bias, int32_t tokens, int32_t experts,
+                          int32_t top_k, int32_t score_func, float route_scale, const mx_router_out* out,
+                          void* stream);
+/* Selection on supplied scores and selection values (RouterProbe.inspect_selection, router.py:243-258). */
+int mx_router_select(mx_ctx* ctx, const float* scores, const float* selection, int32_t tokens, int32_t experts,
+                     int32_t top_k, float route_scale, const mx_router_out* out, void* stream);
+
+/* ---- ordered combine (replaces MoEAccumulator, src/vesper/moe.py:42-148, aggregation_probe.cu:4-25) ---- */
+
+int mx_acc_zero(mx_ctx* ctx, float* sum, int64_t count, void* stream);                     /* moe_zero       */
+int mx_acc_add_rows(mx_ctx* ctx, float* sum, const uint16_t* rows_bf16, const int32_t* token_rows,
+                    int32_t nrows, int32_t width, void* stream);                           /* moe_add_expert */
+int mx_acc_add(mx_ctx* ctx, float* sum, const uint16_t* values_bf16, int64_t count, void* stream); /* moe_add_shared */
+int mx_acc_finish(mx_ctx* ctx, const float* sum, uint16_t* out_bf16, int64_t count, void* stream); /* moe_finish     */
+
+/* ---- routed MoE layer (replaces ConnectedMoE.forward, src/vesper/connected.py:125-186) ---- */
+
+typedef struct mx_moe_config {
+  int32_t hidden;         /* H, multiple of 128          */
+  int32_t intermediate;   /* I, multiple of 128          */
+  int32_t experts;        /* E <= 1024                   */
+  int32_t top_k;          /* k <= 32                     */
+  int32_t score_func;     /* MX_SCORE_*                  */
+  float route_scale;      /* 2.5 (BASELINE), 1.5 (ref)   */
+  float swiglu_limit;     /* 0 disables the clamp        */
+  int32_t shared_format;  /* -1 none, MX_FMT_*           */
+  int32_t max_tokens;     /* decode batch capacity, <= 16 */
+} mx_moe_config;
+
+/* Register a layer: FP32 router weight [E][H], optional FP32 selection bias [E], E expert
+ * pointer sets (host array, copied to a device table) and the optional shared expert. */
+int mx_layer_create(mx_ctx* ctx, const mx_moe_config* cfg, const float* router_weight, const float* bias,
+                    const mx_expert_ptrs* experts, const mx_expert_ptrs* shared, mx_layer** out);
+int mx_layer_destroy(mx_layer* layer);
+/* Re-point expert `expert` (e.g. after a cache slot fill); ordered on `stream`. */
+int mx_layer_set_expert(mx_layer* layer, int32_t expert, const mx_expert_ptrs* w, void* stream);
+
+/* y[T][H] = MoE(x[T][H]) for 1 <= T <= max_tokens, inputs resident in HBM: router -> top-k plan ->
+ * fused gate/up + SwiGLU + down-input quantization -> down -> ordered combine (shared last).
+ * `diagnostics` != 0 also writes the per-stage buffers that mx_layer_buffer exposes. */
+int mx_moe_decode(mx_layer* layer, const uint16_t* x_bf16, int32_t tokens, uint16_t* y_bf16,
+                  int32_t diagnostics, void* stream);
+
+/* Internal per-call buffers of a layer (device pointers, valid after mx_moe_decode on the same stream). */
+#define MX_BUF_LOGITS 0      /* float [T][E]          */
+#define MX_BUF_SCORES 1      /* float [T][E]          */
+#define MX_BUF_SELECTION 2   /* float [T][E]          */
+#define MX_BUF_INDICES 3     /* int32 [T][k]          */
+#define MX_BUF_WEIGHTS 4     /* float [T][k]          */
+#define MX_BUF_XQ 5          /* uint8 [T][H]          */
+#define MX_BUF_XS 6          /* uint8 [T][H/32]       */
+#define MX_BUF_PLAN 7        /* int32 plan (see DESIGN) */
+#define MX_BUF_W1 8          /* uint16 [rows][I]      */
+#define MX_BUF_W3 9          /* uint16 [rows][I]      */
+#define MX_BUF_DOWN_INPUT 10 /* uint16 [rows][I]      */
+#define MX_BUF_DOWN_Q 11     /* uint8 [rows][I]       */
+#define MX_BUF_DOWN_S 12     /* uint8 [rows][I/32]    */
+#define MX_BUF_EXPERT_OUT 13 /* uint16 [rows][H]      */
+#define MX_BUF_TRACE 14      /* float [rows][I][5]    */
+#define MX_BUF_RAW 15        /* float [T][k]          */
+#define MX_BUF_DENOMINATOR 16 /* float [T]            */
+#define MX_BUF_TIED 17       /* int32 [T]             */
+int mx_layer_buffer(mx_layer* layer, int32_t which, void** dptr, uint64_t* bytes);
+
+/* Per-kernel HIP event timing of the next mx_moe_decode calls on `stream`: stage_ms[0..3] =
+ * router, gate/up, down, combine averaged over the calls made while enabled. */
+int mx_layer_profile(mx_layer* layer, int32_t enable, float* stage_ms, int32_t* calls);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MXMOE_H */

@@ -1,0 +1,50 @@
+"""Shared test utilities: tolerance metrics and designed inputs."""
+
+import numpy as np
+
+from oracle.formats import bf16_values
+
+# The north-star tolerance for FFN/MoE outputs against the FP32 oracle (BF16 out):
+# normwise max relative error <= 1e-2 and cosine similarity >= 0.9999.
+MAX_REL_ERR = 1e-2
+MIN_COSINE = 0.9999
+
+
+def as_f64(bits_or_values):
+    a = np.asarray(bits_or_values)
+    return (bf16_values(a) if a.dtype == np.uint16 else a).astype(np.float64)
+
+
+def max_rel_err(got, ref) -> float:
+    g, r = as_f64(got), as_f64(ref)
+    return float(np.max(np.abs(g - r)) / max(np.max(np.abs(r)), 1e-30))
+
+
+def cosine(got, ref) -> float:
+    g, r = as_f64(got).ravel(), as_f64(ref).ravel()
+    return float(g @ r / max(np.linalg.norm(g) * np.linalg.norm(r), 1e-300))
+
+
+def assert_close(got, ref, what=""):
+    err, cos = max_rel_err(got, ref), cosine(got, ref)
+    assert err <= MAX_REL_ERR and cos >= MIN_COSINE, f"{what}: max_rel_err={err:.3e} cosine={cos:.8f}"
+
+
+def bf16_ulp_diff(a, b) -> np.ndarray:
+    """Distance in BF16 units in the last place between two BF16 bit arrays (same-sign ordering)."""
+    def key(x):
+        x = np.asarray(x, np.uint16).astype(np.int32)
+        return np.where(x & 0x8000, -(x & 0x7FFF), x)
+    return np.abs(key(a) - key(b))
+
+
+def exact_activation(rng, tokens, hidden):
+    """Inputs whose per-32 quantization is exact: integers in [-16, 16] with one element per block
+    set to +-448 (scale 2^0) or +-224 (scale 2^-1), so every E4M3 code times its scale is the input."""
+    x = rng.integers(-16, 17, (tokens, hidden)).astype(np.float32)
+    blocks = hidden // 32
+    pick = rng.integers(0, 32, (tokens, blocks))
+    big = rng.choice(np.array([448.0, -448.0, 224.0, -224.0], np.float32), (tokens, blocks))
+    for t in range(tokens):
+        x[t, np.arange(blocks) * 32 + pick[t]] = big[t]
+    return x

@@ -1,0 +1,94 @@
+"""GPU parity of one expert, stage by stage (ExpertExecutor.execute, src/vesper/expert.py:51-79).
+
+Bit-exact where the arithmetic is order-free: the activation quantization, the
+SwiGLU epilogue applied to the kernel's own W1/W3 outputs, and the down-input
+quantization of the kernel's own down input; W1/W3 are exact on designed
+exactly-representable inputs; on random inputs the GEMV outputs are within one
+BF16 ulp and the expert output meets the tolerance (max rel err 1e-2, cosine 0.9999).
+"""
+
+import numpy as np
+import pytest
+
+from oracle.expert import expert_forward, swiglu
+from oracle.formats import bf16_bits, mxfp4_gemv_spec, quantize_activation
+from oracle.inputs import activations, mxfp4_expert
+from tests.helpers import assert_close, bf16_ulp_diff, exact_activation
+from vesper_amd.expert import ExpertExecutor, ResidentExpert
+from vesper_amd.shared import ResidentSharedExpert
+
+pytestmark = pytest.mark.gpu
+
+
+def check_stages(got, x, arrays, route, limit):
+    ref = expert_forward(x, arrays, route, limit)
+    np.testing.assert_array_equal(got["q"], ref["q"])
+    np.testing.assert_array_equal(got["s"], ref["s"])
+    for name in ("w1", "w3"):
+        ulps = bf16_ulp_diff(got[name], ref[name])
+        assert ulps.max() <= 1 and np.mean(ulps == 0) > 0.99, (name, ulps.max(), np.mean(ulps == 0))
+    # epilogue on the kernel's own W1/W3: bit-exact
+    down_input, trace = swiglu(got["w1"], got["w3"], limit, route)
+    np.testing.assert_array_equal(got["down_input"].view(np.uint32), down_input.view(np.uint32))
+    np.testing.assert_array_equal(got["trace"].view(np.uint32), trace.view(np.uint32))
+    dq, ds = quantize_activation(got["down_input"])
+    np.testing.assert_array_equal(got["down_q"], dq)
+    np.testing.assert_array_equal(got["down_s"], ds)
+    w2_own = mxfp4_gemv_spec(got["down_q"], got["down_s"], arrays["w2_weight"], arrays["w2_scale"])
+    ulps = bf16_ulp_diff(got["w2"], w2_own)
+    assert ulps.max() <= 1 and np.mean(ulps == 0) > 0.99
+    assert_close(got["w2"], ref["w2"], "expert output")
+    return ref
+
+
+@pytest.mark.parametrize("hidden,intermediate,tokens,limit", [(256, 128, 1, 10.0), (512, 256, 3, 0.0),
+                                                               (1024, 512, 16, 10.0)])
+def test_expert_stages_random(hidden, intermediate, tokens, limit):
+    rng = np.random.default_rng(hidden + tokens)
+    arrays = mxfp4_expert(rng, hidden, intermediate)
+    x = activations(rng, tokens, hidden)
+    route = rng.uniform(0.05, 1.5, tokens).astype(np.float32)
+    with ResidentExpert(arrays, swiglu_limit=limit, hidden=hidden, intermediate=intermediate) as expert:
+        got = expert.forward(x, route)
+    check_stages(got, x, arrays, route, limit)
+
+
+def test_expert_gate_up_exact_on_representable_inputs():
+    rng = np.random.default_rng(77)
+    hidden, intermediate = 1024, 256
+    arrays = mxfp4_expert(rng, hidden, intermediate, scale_lo=126, scale_hi=128)
+    x = exact_activation(rng, 5, hidden)
+    with ResidentExpert(arrays, swiglu_limit=0.0, hidden=hidden, intermediate=intermediate) as expert:
+        got = expert.forward(x, np.ones(5, np.float32))
+    q, s = quantize_activation(x)
+    np.testing.assert_array_equal(got["w1"], mxfp4_gemv_spec(q, s, arrays["w1_weight"], arrays["w1_scale"]))
+    np.testing.assert_array_equal(got["w3"], mxfp4_gemv_spec(q, s, arrays["w3_weight"], arrays["w3_scale"]))
+
+
+def test_reference_model_shapes_and_clamp():
+    """The reference's own expert shapes (5120 x 2304, clamp 10) on one token."""
+    rng = np.random.default_rng(20261018)
+    arrays = mxfp4_expert(rng, 5120, 2304)
+    x = activations(rng, 1, 5120)
+    with ResidentExpert(arrays, swiglu_limit=10.0, hidden=5120, intermediate=2304) as expert:
+        got = expert.forward(x[0], 0.75)
+    assert got["q"].shape == (1, 5120) and got["down_s"].shape == (1, 72)
+    check_stages(got, x, arrays, np.array([0.75], np.float32), 10.0)
+
+
+def test_shared_expert_is_unweighted_and_executor_validates_before_device():
+    rng = np.random.default_rng(3)
+    arrays = mxfp4_expert(rng, 256, 128)
+    x = activations(rng, 2, 256)
+    with ResidentSharedExpert(arrays, swiglu_limit=0.0, hidden=256, intermediate=128) as shared:
+        got = shared.forward(x)
+        with pytest.raises(ValueError):
+            shared.forward(x, 0.5)
+        with pytest.raises(ValueError):
+            shared.forward(np.full((2, 256), np.inf, np.float32))
+        with pytest.raises(ValueError):
+            shared.forward(np.zeros((17, 256), np.float32))
+    check_stages(got, x, arrays, None, 0.0)
+    with ExpertExecutor(hidden=256, intermediate=128) as ex:
+        with pytest.raises(ValueError):
+            ex.execute(x, {"w1_weight": 0})

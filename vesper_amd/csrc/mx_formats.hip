@@ -1,0 +1,116 @@
+// Format hooks: MXFP4 dequantization, E4M3 encoding and the per-32 activation quantizer.
+//
+// Bit-exact counterparts of the reference's conformance kernels decode_fp4,
+// encode_fp8 and activation32 (src/vesper/kernels/format_probe.cu:23-52). The
+// production path never materialises dequantized weights; these exist so the
+// formats can be checked on the device against the oracle.
+#include "mx_internal.h"
+#include "mx_numerics.h"
+
+namespace {
+
+// One thread per packed byte (two outputs); 8 bytes per thread would not help: this is a test hook.
+__global__ void dequant_mxfp4_kernel(const uint8_t* __restrict__ packed, const uint8_t* __restrict__ scales,
+                                     float* __restrict__ out, int64_t rows, int64_t k) {
+  const int64_t half = k / 2;
+  const int64_t total = rows * half;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / half, c = i % half;
+    const uint32_t byte = packed[i];
+    const float s = mx::e8m0_value(scales[r * (k / 32) + (2 * c) / 32]);
+    float2 v;
+    v.x = mx::fp4_value(byte & 15u) * s;
+    v.y = mx::fp4_value(byte >> 4) * s;
+    reinterpret_cast<float2*>(out + r * k)[c] = v;
+  }
+}
+
+__global__ void encode_e4m3_kernel(const float* __restrict__ in, uint8_t* __restrict__ out, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = (uint8_t)mx::e4m3_encode(in[i]);
+}
+
+// One 32-lane half-wave per 32-element block: lane j holds element j, the amax is a
+// butterfly max over the 32 lanes, and each lane encodes its own element.
+template <typename In>
+__global__ void act_quant32_kernel(const In* __restrict__ x, uint8_t* __restrict__ q, uint8_t* __restrict__ s,
+                                   int64_t blocks) {
+  const int lane = threadIdx.x & 31;
+  const int64_t block = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 5;
+  const bool live = block < blocks;
+  float v = 0.f;
+  if (live) {
+    if constexpr (sizeof(In) == 2) v = mx::bf16_value(x[block * 32 + lane]);
+    else v = mx::bf16_round(x[block * 32 + lane]);
+  }
+  float amax = fabsf(v);
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
+  amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
+  const uint32_t code = mx::act_scale_code(amax);
+  if (live) {
+    q[block * 32 + lane] = (uint8_t)mx::act_quant_value(v, mx::e8m0_value(code));
+    if (lane == 0) s[block] = (uint8_t)code;
+  }
+}
+
+unsigned grid_for(int64_t items, int threads) {
+  const int64_t g = (items + threads - 1) / threads;
+  return (unsigned)(g < 1 ? 1 : g > 1048576 ? 1048576 : g);
+}
+
+}  // namespace
+
+using namespace mxi;
+
+extern "C" {
+
+int mx_dequant_mxfp4(mx_ctx* ctx, const uint8_t* packed, const uint8_t* scales, float* out, int64_t rows,
+                     int64_t k, void* stream) {
+  if (int st = use(ctx)) return st;
+  MX_REQUIRE(rows >= 0 && k >= 0 && k % 32 == 0, "mx_dequant_mxfp4: k must be a multiple of 32");
+  if (!rows || !k) return MX_OK;
+  MX_REQUIRE(packed && scales && out, "mx_dequant_mxfp4: null pointer");
+  hipLaunchKernelGGL(dequant_mxfp4_kernel, dim3(grid_for(rows * k / 2, 256)), dim3(256), 0, as_stream(stream),
+                     packed, scales, out, rows, k);
+  MX_LAUNCH_CHECK("dequant_mxfp4_kernel");
+  return MX_OK;
+}
+
+int mx_encode_e4m3(mx_ctx* ctx, const float* in, uint8_t* out, int64_t n, void* stream) {
+  if (int st = use(ctx)) return st;
+  MX_REQUIRE(n >= 0, "mx_encode_e4m3: negative count");
+  if (!n) return MX_OK;
+  MX_REQUIRE(in && out, "mx_encode_e4m3: null pointer");
+  hipLaunchKernelGGL(encode_e4m3_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), in, out, n);
+  MX_LAUNCH_CHECK("encode_e4m3_kernel");
+  return MX_OK;
+}
+
+int mx_act_quant32(mx_ctx* ctx, const uint16_t* x, uint8_t* q, uint8_t* scales, int64_t rows, int64_t width,
+                   void* stream) {
+  if (int st = use(ctx)) return st;
+  MX_REQUIRE(rows >= 0 && width > 0 && width % 32 == 0, "mx_act_quant32: width must be a positive multiple of 32");
+  if (!rows) return MX_OK;
+  MX_REQUIRE(x && q && scales, "mx_act_quant32: null pointer");
+  const int64_t blocks = rows * (width / 32);
+  hipLaunchKernelGGL(act_quant32_kernel<uint16_t>, dim3(grid_for(blocks * 32, 256)), dim3(256), 0,
+                     as_stream(stream), x, q, scales, blocks);
+  MX_LAUNCH_CHECK("act_quant32_kernel");
+  return MX_OK;
+}
+
+int mx_act_quant32_f32(mx_ctx* ctx, const float* x, uint8_t* q, uint8_t* scales, int64_t rows, int64_t width,
+                       void* stream) {
+  if (int st = use(ctx)) return st;
+  MX_REQUIRE(rows >= 0 && width > 0 && width % 32 == 0, "mx_act_quant32_f32: width must be a positive multiple of 32");
+  if (!rows) return MX_OK;
+  MX_REQUIRE(x && q && scales, "mx_act_quant32_f32: null pointer");
+  const int64_t blocks = rows * (width / 32);
+  hipLaunchKernelGGL(act_quant32_kernel<float>, dim3(grid_for(blocks * 32, 256)), dim3(256), 0, as_stream(stream),
+                     x, q, scales, blocks);
+  MX_LAUNCH_CHECK("act_quant32_kernel");
+  return MX_OK;
+}
+
+}  // extern "C"

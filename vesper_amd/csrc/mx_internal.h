@@ -1,0 +1,57 @@
+// Internal declarations shared by the library's translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "../../include/mxmoe.h"
+
+struct mx_ctx {
+  int device = 0;
+  uint64_t cap = 0;      // 0 = unlimited explicit allocations
+  uint64_t live = 0;
+  uint64_t peak = 0;
+  std::mutex lock;
+  std::unordered_map<void*, uint64_t> owned;        // device allocations
+  std::unordered_map<void*, uint64_t> pinned;       // host pinned allocations
+  void* scratch = nullptr;                          // small reusable device scratch
+  uint64_t scratch_bytes = 0;
+};
+
+namespace mxi {
+
+// Thread-local error text; every failing entry point sets it.
+int fail(int status, const char* fmt, ...);
+int hip_fail(hipError_t err, const char* what);
+void clear_error();
+
+// Make the context's device current for this thread.
+int use(mx_ctx* ctx);
+
+// Context-owned scratch of at least `bytes` (grows; never shrinks until destroy).
+int scratch(mx_ctx* ctx, uint64_t bytes, void** out);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace mxi
+
+#define MX_HIP(call)                                           \
+  do {                                                         \
+    hipError_t _e = (call);                                    \
+    if (_e != hipSuccess) return mxi::hip_fail(_e, #call);     \
+  } while (0)
+
+#define MX_REQUIRE(cond, ...)                                  \
+  do {                                                         \
+    if (!(cond)) return mxi::fail(MX_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+#define MX_LAUNCH_CHECK(what)                                  \
+  do {                                                         \
+    hipError_t _e = hipGetLastError();                         \
+    if (_e != hipSuccess) return mxi::hip_fail(_e, what);      \
+  } while (0)

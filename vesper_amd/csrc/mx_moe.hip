@@ -1,0 +1,1210 @@
+// Routed MoE decode on gfx950: router, top-k plan, fused MXFP4 expert GEMVs, ordered combine.
+//
+// Reference behaviour (shell-term/vesper) and where each piece lives here:
+//   GateProjection.project (gate.py:133-147)        router_kernel: FP32 W_r . x, FMA per thread + fixed tree
+//   router_scores / router_top6 (routing_probe.cu)  score_of + topk_token_wave (generalised E, k)
+//   participation (moe.py:18-30)                    build_plan: ascending expert IDs, ascending tokens
+//   ExpertExecutor.execute (expert.py:51-79)        gateup_kernel (W1/W3 + SwiGLU + down-input quant)
+//                                                   + down_kernel (W2)
+//   MoEAccumulator (moe.py:42-148)                  combine_kernel / acc_* kernels
+//
+// Expert GEMVs run on V_MFMA_SCALE_F32_16X16X128_F8F6F4: A = 16 weight rows of packed E2M1 (one
+// 16-byte MX block per lane), B = up to 16 tokens of E4M3 activations, with the E8M0 block scales
+// fed to the instruction. Decode streams each selected expert's weights from HBM exactly once and
+// never materialises dequantized weights.
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+#include "mx_internal.h"
+#include "mx_numerics.h"
+
+namespace {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kMaxTokens = 16;   // MFMA N: tokens per expert per decode call
+constexpr int kMaxTopK = 32;
+constexpr int kMaxExperts = 1024;
+constexpr int kMaxSlots = kMaxTokens * kMaxTopK + 1;
+
+// Device-side execution plan of one decode call (written by the router's last workgroup).
+struct Plan {
+  int32_t n_slots;      // routed + shared
+  int32_t n_routed;
+  int32_t total_rows;   // rows of the compact per-(token, expert) buffers
+  int32_t tokens;
+  int32_t top_k;
+  int32_t pad[3];
+  int32_t slot_expert[kMaxSlots];   // expert ID per slot, ascending; E marks the shared expert
+  int32_t slot_ntok[kMaxSlots];
+  int32_t slot_row0[kMaxSlots];
+  int32_t slot_weighted[kMaxSlots];
+  int32_t slot_tok[kMaxSlots][kMaxTokens];
+  float slot_w[kMaxSlots][kMaxTokens];
+  int32_t tok_rows[kMaxTokens][kMaxTopK + 1];   // a token's rows in ascending expert order, shared last
+};
+
+// ----------------------------------------------------------------------------------------------
+// small helpers
+
+__device__ __forceinline__ uint32_t ordered_key(float v) {
+  const uint32_t b = mx::f2u(v);
+  return b ^ ((b & 0x80000000u) ? 0xFFFFFFFFu : 0x80000000u);
+}
+
+// FP32 score of one logit: exp/log1p in float64 rounded once to FP32 (the oracle does the same).
+__device__ __forceinline__ float score_of(float z, int score_func) {
+  if (score_func == MX_SCORE_SIGMOID) {
+    const float e = (float)exp(-(double)z);
+    return 1.0f / (1.0f + e);
+  }
+  const float sp = z > 20.0f ? z : (float)log1p(exp((double)z));
+  return sqrtf(sp);
+}
+
+__device__ __forceinline__ float silu_of(float g) {
+  const float e = (float)exp(-(double)g);
+  return g / (1.0f + e);
+}
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const uint32_t o = __shfl_xor(v, m, 64);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// inclusive prefix sum over the 64 lanes
+__device__ __forceinline__ int wave_scan_i(int v, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(v, d, 64);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+// ----------------------------------------------------------------------------------------------
+// Top-k of one token by one wavefront (routing_probe.cu:17-86, router.py:23-61, generalised).
+//
+// 1. threshold = k-th largest order-preserving key, found by distinct-value rounds; a round whose
+//    value occurs twice sets the tie flag (the reference's serial arg-max passes).
+// 2. gather keys above the threshold by ascending ID, then keys equal to it by ascending ID, k total.
+// 3. the 32-slot bitonic network (slot i pairs with i ^ stride; the pair's direction is bit `size`
+//    of the lower slot for sizes 2..16, ascending-false for the final merge).
+// 4. raw = score[id], denominator = halving-tree sum + 1e-20, weight = raw / den * route_scale.
+struct TopkOut {
+  int32_t* indices;
+  float* weights;
+  float* raw;
+  float* den;
+  int32_t* tied;
+};
+
+__device__ void topk_token_wave(const float* __restrict__ selection, const float* __restrict__ scores, int E, int k,
+                                float route_scale, int t, const TopkOut& o) {
+  const int lane = threadIdx.x & 63;
+  constexpr int kPer = kMaxExperts / 64;
+  const int per = (E + 63) / 64;
+  uint32_t key[kPer];
+  float sel[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int e = lane * per + j;
+    const bool ok = j < per && e < E;
+    sel[j] = ok ? selection[e] : 0.f;
+    key[j] = ok ? ordered_key(sel[j]) : 0u;
+  }
+  // 1. threshold search
+  uint64_t bound = 1ull << 32;   // exclusive upper bound on keys still to rank
+  int taken = 0, tied = 0;
+  uint32_t thr = 0;
+  for (int round = 0; round < k; ++round) {
+    uint32_t m = 0;
+    bool any = false;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int e = lane * per + j;
+      if (j < per && e < E && (uint64_t)key[j] < bound && (!any || key[j] > m)) { m = key[j]; any = true; }
+    }
+    // lanes without a candidate contribute key 0; a real key 0 (-NaN pattern) is excluded upstream
+    const uint32_t best = wave_max_u(any ? m : 0u);
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int e = lane * per + j;
+      c += (j < per && e < E && key[j] == best) ? 1 : 0;
+    }
+    c = wave_sum_i(c);
+    tied |= c >= 2;
+    taken += c;
+    thr = best;
+    if (taken >= k) break;
+    bound = best;
+  }
+  // 2. gather by ascending ID: lane-major then j (experts are laid out contiguously per lane)
+  int n_gt = 0, n_eq = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int e = lane * per + j;
+    if (j < per && e < E) {
+      n_gt += key[j] > thr;
+      n_eq += key[j] == thr;
+    }
+  }
+  const int inc_gt = wave_scan_i(n_gt, lane);
+  const int inc_eq = wave_scan_i(n_eq, lane);
+  const int total_gt = __shfl(inc_gt, 63, 64);
+  int pos_gt = inc_gt - n_gt, pos_eq = total_gt + inc_eq - n_eq;
+  __shared__ float s_key[4][32];
+  __shared__ int32_t s_id[4][32];
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int e = lane * per + j;
+    if (j < per && e < E) {
+      if (key[j] > thr) {
+        if (pos_gt < k) { s_key[wave][pos_gt] = sel[j]; s_id[wave][pos_gt] = e; }
+        ++pos_gt;
+      } else if (key[j] == thr) {
+        if (pos_eq < k) { s_key[wave][pos_eq] = sel[j]; s_id[wave][pos_eq] = e; }
+        ++pos_eq;
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  // 3. bitonic network on lanes 0..31 (lanes 32..63 mirror them and are ignored)
+  const int slot = lane & 31;
+  float kv = slot < k ? s_key[wave][slot] : 0.f;
+  int32_t iv = slot < k ? s_id[wave][slot] : 0;
+  int vv = slot < k;
+#pragma unroll
+  for (int size = 2; size <= 32; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride >= 1; stride >>= 1) {
+      const float pk = __shfl_xor(kv, stride, 32);
+      const int32_t pi = __shfl_xor(iv, stride, 32);
+      const int pv = __shfl_xor(vv, stride, 32);
+      const bool lower = (slot & stride) == 0;
+      const int lo = lower ? slot : (slot ^ stride);
+      const float klo = lower ? kv : pk, khi = lower ? pk : kv;
+      const int vlo = lower ? vv : pv, vhi = lower ? pv : vv;
+      const bool promote = (klo > khi && vlo) || !vhi;
+      const bool dir = size < 32 ? (lo & size) != 0 : false;
+      if (promote == dir) { kv = pk; iv = pi; vv = pv; }
+    }
+  }
+  // 4. raw scores, tree denominator, weights
+  float raw = slot < k ? scores[iv] : 0.f;
+  float acc = raw;
+  int width = 1;
+  while (width < k) width <<= 1;
+  int present = k;
+  for (int stride = width >> 1; stride >= 1; stride >>= 1) {
+    const float other = __shfl_down(acc, stride, 32);
+    if (slot < stride && slot + stride < present) acc = acc + other;
+    present = present < stride ? present : stride;
+  }
+  const float den = __shfl(acc, 0, 32) + 1e-20f;
+  if (lane < k) {
+    const float w = (raw / den) * route_scale;
+    o.indices[t * k + lane] = iv;
+    o.weights[t * k + lane] = w;
+    if (o.raw) o.raw[t * k + lane] = raw;
+  }
+  if (lane == 0) {
+    if (o.den) o.den[t] = den;
+    if (o.tied) o.tied[t] = tied;
+  }
+}
+
+// ----------------------------------------------------------------------------------------------
+// Plan from the routed IDs (participation, moe.py:18-30): slots are the distinct experts in ascending
+// ID order, each with its tokens ascending; rows are numbered expert-major; the shared expert is the
+// last slot with every token. Executed by one 256-thread workgroup.
+__device__ void build_plan(Plan* __restrict__ plan, const int32_t* __restrict__ ids, const float* __restrict__ w,
+                           int T, int k, int E, int has_shared) {
+  __shared__ int32_t cnt[kMaxExperts];
+  __shared__ int32_t slot_of[kMaxExperts];
+  __shared__ int32_t row_of[kMaxExperts];
+  __shared__ int32_t part[256][2];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += 256) cnt[e] = 0;
+  __syncthreads();
+  for (int i = tid; i < T * k; i += 256) atomicAdd(&cnt[ids[i]], 1);
+  __syncthreads();
+  // block-exclusive scans of (cnt > 0) and cnt over experts; thread tid owns experts [tid*per, ...)
+  const int per = (E + 255) / 256;
+  int ns = 0, nr = 0;
+  for (int j = 0; j < per; ++j) {
+    const int e = tid * per + j;
+    if (e < E) { ns += cnt[e] > 0; nr += cnt[e]; }
+  }
+  part[tid][0] = ns;
+  part[tid][1] = nr;
+  __syncthreads();
+  if (tid == 0) {
+    int a = 0, b = 0;
+    for (int i = 0; i < 256; ++i) {
+      const int x = part[i][0], y = part[i][1];
+      part[i][0] = a;
+      part[i][1] = b;
+      a += x;
+      b += y;
+    }
+    plan->n_routed = a;
+    plan->n_slots = a + has_shared;
+    plan->total_rows = b + (has_shared ? T : 0);
+    plan->tokens = T;
+    plan->top_k = k;
+  }
+  __syncthreads();
+  {
+    int s = part[tid][0], r = part[tid][1];
+    for (int j = 0; j < per; ++j) {
+      const int e = tid * per + j;
+      if (e < E) {
+        slot_of[e] = s;
+        row_of[e] = r;
+        if (cnt[e] > 0) {
+          plan->slot_expert[s] = e;
+          plan->slot_ntok[s] = cnt[e];
+          plan->slot_row0[s] = r;
+          plan->slot_weighted[s] = 1;
+          ++s;
+          r += cnt[e];
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // token lists (ascending) and each token's rows in ascending expert order
+  for (int t = tid; t < T; t += 256) {
+    int32_t es[kMaxTopK], rs[kMaxTopK];
+    for (int i = 0; i < k; ++i) {
+      const int e = ids[t * k + i];
+      int before = 0;   // tokens t' < t routed to e
+      for (int u = 0; u < t; ++u)
+        for (int j = 0; j < k; ++j) before += ids[u * k + j] == e;
+      const int s = slot_of[e];
+      plan->slot_tok[s][before] = t;
+      plan->slot_w[s][before] = w[t * k + i];
+      es[i] = e;
+      rs[i] = row_of[e] + before;
+    }
+    for (int i = 1; i < k; ++i) {   // insertion sort by expert ID
+      const int e = es[i], r = rs[i];
+      int j = i - 1;
+      while (j >= 0 && es[j] > e) { es[j + 1] = es[j]; rs[j + 1] = rs[j]; --j; }
+      es[j + 1] = e;
+      rs[j + 1] = r;
+    }
+    for (int i = 0; i < k; ++i) plan->tok_rows[t][i] = rs[i];
+  }
+  __syncthreads();
+  if (has_shared) {
+    const int s = plan->n_routed;
+    for (int t = tid; t < T; t += 256) {
+      plan->slot_tok[s][t] = t;
+      plan->slot_w[s][t] = 1.0f;
+      plan->tok_rows[t][k] = T * k + t;
+    }
+    if (tid == 0) {
+      plan->slot_expert[s] = E;
+      plan->slot_ntok[s] = T;
+      plan->slot_row0[s] = T * k;
+      plan->slot_weighted[s] = 0;
+    }
+  }
+}
+
+// One slot holding all tokens of a single expert call (mx_expert_forward).
+__global__ void single_plan_kernel(Plan* plan, int T, const float* __restrict__ route_w) {
+  const int t = threadIdx.x;
+  if (t < T) {
+    plan->slot_tok[0][t] = t;
+    plan->slot_w[0][t] = route_w ? route_w[t] : 1.0f;
+    plan->tok_rows[t][0] = t;
+  }
+  if (t == 0) {
+    plan->n_slots = 1;
+    plan->n_routed = route_w ? 1 : 0;
+    plan->total_rows = T;
+    plan->tokens = T;
+    plan->top_k = 1;
+    plan->slot_expert[0] = 0;
+    plan->slot_ntok[0] = T;
+    plan->slot_row0[0] = 0;
+    plan->slot_weighted[0] = route_w ? 1 : 0;
+  }
+}
+
+// ----------------------------------------------------------------------------------------------
+// Router: grid (E, ceil(T / kMaxTokens)); workgroup e computes logits/scores/selection of expert e
+// for up to 16 tokens; workgroups also share the per-32 quantization of x. With `fuse_plan`, the
+// last workgroup to finish (device-scope counter) runs top-k for every token and builds the plan,
+// then resets the counter for the next launch (no memset: safe inside a captured graph).
+struct RouterArgs {
+  const float* W;
+  const float* bias;
+  const uint16_t* x;
+  int T, H, E, k, score_func;
+  float route_scale;
+  float* logits;
+  float* scores;
+  float* selection;
+  uint8_t* xq;
+  uint8_t* xs;
+  TopkOut topk;
+  Plan* plan;
+  uint32_t* counter;
+  int has_shared;
+};
+
+__global__ __launch_bounds__(256) void router_kernel(RouterArgs a) {
+  const int e = blockIdx.x;
+  const int t0 = blockIdx.y * kMaxTokens;
+  const int nt = min(kMaxTokens, a.T - t0);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float acc[kMaxTokens];
+#pragma unroll
+  for (int t = 0; t < kMaxTokens; ++t) acc[t] = 0.f;
+  const float* wrow = a.W + (size_t)e * a.H;
+  for (int k0 = tid * 4; k0 < a.H; k0 += 1024) {
+    const float4 w = *reinterpret_cast<const float4*>(wrow + k0);
+#pragma unroll
+    for (int t = 0; t < kMaxTokens; ++t) {
+      if (t < nt) {
+        const uint2 xb = *reinterpret_cast<const uint2*>(a.x + (size_t)(t0 + t) * a.H + k0);
+        acc[t] = fmaf(w.x, mx::bf16_value(xb.x & 0xFFFFu), acc[t]);
+        acc[t] = fmaf(w.y, mx::bf16_value(xb.x >> 16), acc[t]);
+        acc[t] = fmaf(w.z, mx::bf16_value(xb.y & 0xFFFFu), acc[t]);
+        acc[t] = fmaf(w.w, mx::bf16_value(xb.y >> 16), acc[t]);
+      }
+    }
+  }
+  __shared__ float part[4][kMaxTokens];
+#pragma unroll
+  for (int t = 0; t < kMaxTokens; ++t) {
+    float v = acc[t];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    if (lane == 0) part[wave][t] = v;
+  }
+  // share the per-32 quantization of x (blocks of 32 handled by 32-lane halves)
+  if (a.xq && blockIdx.y == 0) {
+    const int nblocks = a.T * (a.H / 32);
+    const int half = tid >> 5, l32 = tid & 31;
+    for (int b = blockIdx.x * 8 + half; b < nblocks; b += gridDim.x * 8) {
+      const float v = mx::bf16_value(a.x[(size_t)b * 32 + l32]);
+      float amax = fabsf(v);
+#pragma unroll
+      for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
+      amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
+      const uint32_t code = mx::act_scale_code(amax);
+      a.xq[(size_t)b * 32 + l32] = (uint8_t)mx::act_quant_value(v, mx::e8m0_value(code));
+      if (l32 == 0) a.xs[b] = (uint8_t)code;
+    }
+  }
+  __syncthreads();
+  if (tid < nt) {
+    const float z = ((part[0][tid] + part[1][tid]) + part[2][tid]) + part[3][tid];
+    const size_t o = (size_t)(t0 + tid) * a.E + e;
+    a.logits[o] = z;
+    const float s = score_of(z, a.score_func);
+    if (a.scores) a.scores[o] = s;
+    if (a.selection) a.selection[o] = a.bias ? s + a.bias[e] : s;
+  }
+  if (!a.plan) return;
+  // ---- last workgroup: top-k for all tokens, then the plan ----
+  __shared__ int last;
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t done = atomicAdd(a.counter, 1u);
+    last = done == gridDim.x * gridDim.y - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  for (int t = wave; t < a.T; t += 4)
+    topk_token_wave(a.selection + (size_t)t * a.E, a.scores + (size_t)t * a.E, a.E, a.k, a.route_scale, t, a.topk);
+  __threadfence();
+  __syncthreads();
+  __threadfence();
+  build_plan(a.plan, a.topk.indices, a.topk.weights, a.T, a.k, a.E, a.has_shared);
+  if (tid == 0) atomicExch(a.counter, 0u);
+}
+
+// Stand-alone top-k over supplied selection/scores: one wave per token.
+__global__ __launch_bounds__(256) void topk_kernel(const float* selection, const float* scores, int T, int E, int k,
+                                                   float route_scale, TopkOut o) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t < T) topk_token_wave(selection + (size_t)t * E, scores + (size_t)t * E, E, k, route_scale, t, o);
+}
+
+__global__ void scores_kernel(const float* logits, const float* bias, int T, int E, int score_func, float* scores,
+                              float* selection) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= T * E) return;
+  const float s = score_of(logits[i], score_func);
+  scores[i] = s;
+  selection[i] = bias ? s + bias[i % E] : s;
+}
+
+// ----------------------------------------------------------------------------------------------
+// Expert GEMVs on scaled MFMA.
+
+struct ExpertArgs {
+  const mx_expert_ptrs* table;   // device table [E+1] or nullptr
+  mx_expert_ptrs single;         // used when table == nullptr
+  const Plan* plan;
+  int H, I;
+  float limit;
+  const uint8_t* xq;             // [T][H]
+  const uint8_t* xs;             // [T][H/32]
+  uint8_t* dq;                   // [rows][I]
+  uint8_t* ds;                   // [rows][I/32]
+  uint16_t* out;                 // [rows][H]
+  // diagnostics (nullable)
+  uint16_t* w1;
+  uint16_t* w3;
+  uint16_t* din;
+  float* trace;
+};
+
+__device__ __forceinline__ v4f mfma_fp4xfp8(uint4 a, uint4 b0, uint4 b1, v4f c, int sa, int sb) {
+  v8i av = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
+  v8i bv = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+  // cbsz = 4: A is FP4 E2M1; blgp = 0: B is FP8 E4M3; op_sel 0 selects scale byte 0.
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 4, 0, 0, sa, 0, sb);
+}
+
+// grid (I/32, slots), 256 threads. Wave w computes intermediate rows [32g+8w, +8) of W1 (MFMA rows
+// 0-7) and W3 (MFMA rows 8-15) for the slot's tokens, then the workgroup applies the SwiGLU epilogue
+// and quantizes its 32-row block of the down input per token (the per-32 E4M3/E8M0 boundary).
+__global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
+  const Plan* __restrict__ plan = a.plan;
+  const int s = blockIdx.y;
+  if (s >= plan->n_slots) return;
+  const int g = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int m = lane & 15, q = lane >> 4;
+  const int ntok = plan->slot_ntok[s];
+  const int expert = plan->slot_expert[s];
+  const mx_expert_ptrs p = a.table ? a.table[expert] : a.single;
+  const int H = a.H, I = a.I;
+  const int row = g * 32 + wave * 8 + (m & 7);
+  const bool up = m >= 8;
+  const uint8_t* __restrict__ wrow = (const uint8_t*)(up ? p.w3_weight : p.w1_weight) + (size_t)row * (H / 2);
+  const uint8_t* __restrict__ srow = (const uint8_t*)(up ? p.w3_scale : p.w1_scale) + (size_t)row * (H / 32);
+  const int n = lane & 15;
+  const int tok = n < ntok ? plan->slot_tok[s][n] : -1;
+  const uint8_t* __restrict__ xrow = a.xq + (size_t)(tok < 0 ? 0 : tok) * H;
+  const uint8_t* __restrict__ xsrow = a.xs + (size_t)(tok < 0 ? 0 : tok) * (H / 32);
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+  const int chunks = H / 128;
+  const uint4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll 4
+  for (int c = 0; c < chunks; ++c) {
+    const int kb = 4 * c + q;
+    const uint4 wa = *reinterpret_cast<const uint4*>(wrow + (size_t)kb * 16);
+    const uint32_t sw = *reinterpret_cast<const uint32_t*>(srow + 4 * c);
+    uint4 b0 = zero, b1 = zero;
+    uint32_t sx = 0x7F7F7F7Fu;
+    if (tok >= 0) {
+      b0 = *reinterpret_cast<const uint4*>(xrow + (size_t)kb * 32);
+      b1 = *reinterpret_cast<const uint4*>(xrow + (size_t)kb * 32 + 16);
+      sx = *reinterpret_cast<const uint32_t*>(xsrow + 4 * c);
+    }
+    acc = mfma_fp4xfp8(wa, b0, b1, acc, (int)((sw >> (8 * q)) & 0xFF), (int)((sx >> (8 * q)) & 0xFF));
+  }
+  // D[4q + i][n]: lanes q < 2 hold W1 rows 4q+i; lane + 32 holds the W3 rows with the same index.
+  __shared__ float s_din[kMaxTokens][32];
+  float upv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) upv[i] = __shfl_xor(acc[i], 32, 64);
+  if (q < 2 && n < ntok) {
+    const int row0 = plan->slot_row0[s];
+    const bool weighted = plan->slot_weighted[s] != 0;
+    const float rw = plan->slot_w[s][n];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int li = wave * 8 + 4 * q + i;        // row within the 32-row block
+      const int gi = g * 32 + li;                 // intermediate index
+      const uint32_t b1 = mx::bf16_bits(acc[i]);
+      const uint32_t b3 = mx::bf16_bits(upv[i]);
+      float gate = mx::bf16_value(b1), upf = mx::bf16_value(b3);
+      if (a.limit > 0.f) {
+        if (gate > a.limit) gate = a.limit;
+        if (upf > a.limit) upf = a.limit;
+        if (upf < -a.limit) upf = -a.limit;
+      }
+      const float silu = silu_of(gate);
+      const float product = silu * upf;
+      const float routed = weighted ? rw * product : product;
+      const float din = mx::bf16_round(routed);
+      s_din[n][li] = din;
+      const size_t o = (size_t)(row0 + n) * I + gi;
+      if (a.w1) a.w1[o] = (uint16_t)b1;
+      if (a.w3) a.w3[o] = (uint16_t)b3;
+      if (a.din) a.din[o] = (uint16_t)mx::bf16_bits(din);
+      if (a.trace) {
+        float* tr = a.trace + o * 5;
+        tr[0] = gate; tr[1] = upf; tr[2] = silu; tr[3] = product; tr[4] = routed;
+      }
+    }
+  }
+  __syncthreads();
+  // per-token quantization of the 32-row block: 16 threads per token, 2 values each
+  const int tn = tid >> 4, j2 = tid & 15;
+  if (tn < ntok) {
+    const float v0 = s_din[tn][2 * j2], v1 = s_din[tn][2 * j2 + 1];
+    float amax = fmaxf(fabsf(v0), fabsf(v1));
+#pragma unroll
+    for (int mm = 8; mm >= 1; mm >>= 1) amax = fmaxf(amax, __shfl_xor(amax, mm, 16));
+    amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
+    const uint32_t code = mx::act_scale_code(amax);
+    const float sc = mx::e8m0_value(code);
+    const uint32_t q0 = mx::act_quant_value(v0, sc), q1 = mx::act_quant_value(v1, sc);
+    const size_t r = (size_t)(plan->slot_row0[s] + tn);
+    *reinterpret_cast<uint16_t*>(a.dq + r * I + g * 32 + 2 * j2) = (uint16_t)(q0 | (q1 << 8));
+    if (j2 == 0) a.ds[r * (I / 32) + g] = (uint8_t)code;
+  }
+}
+
+// grid (H/64, slots), 256 threads; wave w computes 16 output rows [64b + 16w, +16) of W2 for the slot's
+// tokens and writes them as BF16 (the reference's w2 stage).
+__global__ __launch_bounds__(256) void down_kernel(ExpertArgs a) {
+  const Plan* __restrict__ plan = a.plan;
+  const int s = blockIdx.y;
+  if (s >= plan->n_slots) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int m = lane & 15, q = lane >> 4, n = lane & 15;
+  const int ntok = plan->slot_ntok[s];
+  const int row0 = plan->slot_row0[s];
+  const mx_expert_ptrs p = a.table ? a.table[plan->slot_expert[s]] : a.single;
+  const int H = a.H, I = a.I;
+  const int h0 = blockIdx.x * 64 + wave * 16;
+  const uint8_t* __restrict__ wrow = (const uint8_t*)p.w2_weight + (size_t)(h0 + m) * (I / 2);
+  const uint8_t* __restrict__ srow = (const uint8_t*)p.w2_scale + (size_t)(h0 + m) * (I / 32);
+  const bool live = n < ntok;
+  const uint8_t* __restrict__ xrow = a.dq + (size_t)(row0 + (live ? n : 0)) * I;
+  const uint8_t* __restrict__ xsrow = a.ds + (size_t)(row0 + (live ? n : 0)) * (I / 32);
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+  const uint4 zero = {0u, 0u, 0u, 0u};
+  const int chunks = I / 128;
+#pragma unroll 4
+  for (int c = 0; c < chunks; ++c) {
+    const int kb = 4 * c + q;
+    const uint4 wa = *reinterpret_cast<const uint4*>(wrow + (size_t)kb * 16);
+    const uint32_t sw = *reinterpret_cast<const uint32_t*>(srow + 4 * c);
+    uint4 b0 = zero, b1 = zero;
+    uint32_t sx = 0x7F7F7F7Fu;
+    if (live) {
+      b0 = *reinterpret_cast<const uint4*>(xrow + (size_t)kb * 32);
+      b1 = *reinterpret_cast<const uint4*>(xrow + (size_t)kb * 32 + 16);
+      sx = *reinterpret_cast<const uint32_t*>(xsrow + 4 * c);
+    }
+    acc = mfma_fp4xfp8(wa, b0, b1, acc, (int)((sw >> (8 * q)) & 0xFF), (int)((sx >> (8 * q)) & 0xFF));
+  }
+  if (live) {
+    uint2 packed;
+    packed.x = mx::bf16_bits(acc[0]) | (mx::bf16_bits(acc[1]) << 16);
+    packed.y = mx::bf16_bits(acc[2]) | (mx::bf16_bits(acc[3]) << 16);
+    *reinterpret_cast<uint2*>(a.out + (size_t)(row0 + n) * H + h0 + 4 * q) = packed;
+  }
+}
+
+// Ordered combine (aggregation_probe.cu:4-25): per token, FP32 sum from +0 of its expert rows in
+// ascending expert ID, the shared row last, one BF16 rounding. 8 hidden positions per thread.
+__global__ void combine_kernel(const Plan* __restrict__ plan, const uint16_t* __restrict__ rows, int H, int k,
+                               int has_shared, uint16_t* __restrict__ y) {
+  const int t = blockIdx.y;
+  const int h = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (t >= plan->tokens || h >= H) return;
+  float acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+  const int n = k + has_shared;
+  for (int i = 0; i < n; ++i) {
+    const uint4 v = *reinterpret_cast<const uint4*>(rows + (size_t)plan->tok_rows[t][i] * H + h);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[2 * j] = acc[2 * j] + mx::bf16_value(w[j] & 0xFFFFu);
+      acc[2 * j + 1] = acc[2 * j + 1] + mx::bf16_value(w[j] >> 16);
+    }
+  }
+  uint4 o;
+  o.x = mx::bf16_bits(acc[0]) | (mx::bf16_bits(acc[1]) << 16);
+  o.y = mx::bf16_bits(acc[2]) | (mx::bf16_bits(acc[3]) << 16);
+  o.z = mx::bf16_bits(acc[4]) | (mx::bf16_bits(acc[5]) << 16);
+  o.w = mx::bf16_bits(acc[6]) | (mx::bf16_bits(acc[7]) << 16);
+  *reinterpret_cast<uint4*>(y + (size_t)t * H + h) = o;
+}
+
+// MoEAccumulator kernels (aggregation_probe.cu:4-25), one element per thread.
+__global__ void acc_zero_kernel(float* sum, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) sum[i] = 0.f;
+}
+__global__ void acc_add_rows_kernel(float* sum, const uint16_t* vals, const int32_t* rows, int nrows, int width) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)nrows * width) return;
+  const int64_t target = (int64_t)rows[i / width] * width + i % width;
+  sum[target] = sum[target] + mx::bf16_value(vals[i]);
+}
+__global__ void acc_add_kernel(float* sum, const uint16_t* vals, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) sum[i] = sum[i] + mx::bf16_value(vals[i]);
+}
+__global__ void acc_finish_kernel(const float* sum, uint16_t* out, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = (uint16_t)mx::bf16_bits(sum[i]);
+}
+
+__global__ void set_expert_kernel(mx_expert_ptrs* slot, mx_expert_ptrs value) { *slot = value; }
+
+unsigned blocks_for(int64_t n, int threads) { return (unsigned)((n + threads - 1) / threads); }
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+int check_expert_ptrs(const mx_expert_ptrs& w, const char* who) {
+  const void* ws[3] = {w.w1_weight, w.w3_weight, w.w2_weight};
+  const void* ss[3] = {w.w1_scale, w.w3_scale, w.w2_scale};
+  for (int i = 0; i < 3; ++i) {
+    MX_REQUIRE(ws[i] && ss[i], "%s: expert tensor pointer is null", who);
+    MX_REQUIRE(aligned(ws[i], 16), "%s: packed weights must be 16-byte aligned", who);
+    MX_REQUIRE(aligned(ss[i], 4), "%s: scales must be 4-byte aligned", who);
+  }
+  return MX_OK;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------------------------
+// Layer object
+
+struct mx_layer {
+  mx_ctx* ctx = nullptr;
+  mx_moe_config cfg{};
+  const float* router_weight = nullptr;
+  const float* bias = nullptr;
+  int has_shared = 0;
+  mx_expert_ptrs* table = nullptr;  // device [E + 1]
+  // per-call buffers
+  float *logits = nullptr, *scores = nullptr, *selection = nullptr, *weights = nullptr, *raw = nullptr,
+        *den = nullptr, *trace = nullptr;
+  int32_t *indices = nullptr, *tied = nullptr;
+  uint8_t *xq = nullptr, *xs = nullptr, *dq = nullptr, *ds = nullptr;
+  uint16_t *w1 = nullptr, *w3 = nullptr, *din = nullptr, *eout = nullptr;
+  Plan* plan = nullptr;
+  uint32_t* counter = nullptr;
+  int max_rows = 0;
+  std::vector<std::pair<void*, uint64_t>> allocs;
+  // profiling
+  bool profile = false;
+  hipEvent_t ev[5] = {};
+  double stage_ms[4] = {0, 0, 0, 0};
+  int profiled_calls = 0;
+};
+
+namespace {
+
+int layer_alloc(mx_layer* L, uint64_t bytes, void** out) {
+  void* p = nullptr;
+  MX_HIP(hipMalloc(&p, bytes));
+  L->allocs.emplace_back(p, bytes);
+  *out = p;
+  return MX_OK;
+}
+
+template <typename T>
+int layer_alloc_t(mx_layer* L, uint64_t count, T** out) {
+  void* p = nullptr;
+  if (int s = layer_alloc(L, count * sizeof(T), &p)) return s;
+  *out = (T*)p;
+  return MX_OK;
+}
+
+void layer_release(mx_layer* L) {
+  for (auto& a : L->allocs) (void)hipFree(a.first);
+  L->allocs.clear();
+  for (auto& e : L->ev)
+    if (e) (void)hipEventDestroy(e);
+}
+
+int validate_config(const mx_moe_config* c) {
+  MX_REQUIRE(c != nullptr, "mx_layer_create: null config");
+  MX_REQUIRE(c->hidden > 0 && c->hidden % 128 == 0, "hidden size must be a positive multiple of 128");
+  MX_REQUIRE(c->intermediate > 0 && c->intermediate % 128 == 0,
+             "intermediate size must be a positive multiple of 128");
+  MX_REQUIRE(c->experts >= 1 && c->experts <= kMaxExperts, "experts must be in [1, %d]", kMaxExperts);
+  MX_REQUIRE(c->top_k >= 1 && c->top_k <= kMaxTopK && c->top_k <= c->experts, "top_k must be in [1, min(32, E)]");
+  MX_REQUIRE(c->score_func == MX_SCORE_SIGMOID || c->score_func == MX_SCORE_SQRTSOFTPLUS, "unknown score function");
+  MX_REQUIRE(std::isfinite(c->route_scale), "route scale must be finite");
+  MX_REQUIRE(std::isfinite(c->swiglu_limit) && c->swiglu_limit >= 0.f, "Invalid SwiGLU limit");
+  MX_REQUIRE(c->shared_format == -1 || c->shared_format == MX_FMT_MXFP4,
+             "shared expert format must be none or MXFP4 in the decode layer");
+  MX_REQUIRE(c->max_tokens >= 1 && c->max_tokens <= kMaxTokens, "max_tokens must be in [1, %d]", kMaxTokens);
+  return MX_OK;
+}
+
+}  // namespace
+
+using namespace mxi;
+
+extern "C" {
+
+int mx_layer_create(mx_ctx* ctx, const mx_moe_config* cfg, const float* router_weight, const float* bias,
+                    const mx_expert_ptrs* experts, const mx_expert_ptrs* shared, mx_layer** out) {
+  if (int s = use(ctx)) return s;
+  if (int s = validate_config(cfg)) return s;
+  MX_REQUIRE(out != nullptr, "mx_layer_create: null output");
+  MX_REQUIRE(router_weight != nullptr && aligned(router_weight, 16), "router weight must be a 16-byte aligned pointer");
+  MX_REQUIRE(experts != nullptr, "expert pointer table is null");
+  for (int e = 0; e < cfg->experts; ++e)
+    if (int s = check_expert_ptrs(experts[e], "mx_layer_create")) return s;
+  MX_REQUIRE((cfg->shared_format == -1) == (shared == nullptr), "shared expert pointers and format disagree");
+  if (shared)
+    if (int s = check_expert_ptrs(*shared, "mx_layer_create(shared)")) return s;
+  mx_layer* L = new mx_layer();
+  L->ctx = ctx;
+  L->cfg = *cfg;
+  L->router_weight = router_weight;
+  L->bias = bias;
+  L->has_shared = shared != nullptr;
+  const int T = cfg->max_tokens, E = cfg->experts, k = cfg->top_k, H = cfg->hidden, I = cfg->intermediate;
+  L->max_rows = T * k + T;
+  int s = MX_OK;
+  auto fail_out = [&](int st) {
+    layer_release(L);
+    delete L;
+    return st;
+  };
+  if ((s = layer_alloc_t(L, (uint64_t)E + 1, &L->table))) return fail_out(s);
+  if ((s = layer_alloc_t(L, (uint64_t)T * E, &L->logits))) return fail_out(s);
+  if ((s = layer_alloc_t(L, (uint64_t)T * E, &L->scores))) return fail_out(s);
+  if ((s = layer_alloc_t(L, (uint64_t)T * E, &L->selection))) return fail_out(s);
+  if ((s = layer_alloc_t(L, (uint64_t)T * k, &L->indices))) return fail_out(s);
+  if ((s = layer_alloc_t(L, (uint64_t)T * k, &L->weights))) return fail_out(s);
+  if ((s = layer_alloc_t(L, (uint64_t)T * k, &L->raw))) return fail_out(s);
+  if ((s = layer_alloc_t(L, (uint64_t)T, &L->den))) return fail_out(s);
+  if ((s = layer_alloc_t(L, (uint64_t)T, &L->tied))) return fail_out(s);
+  if ((s = layer_alloc_t(L, (uint64_t)T * H, &L->xq))) return fail_out(s);
+  if ((s = layer_alloc_t(L, (uint64_t)T * H / 32 + 16, &L->xs))) return fail_out(s);
+  if ((s = layer_alloc_t(L, 1, &L->plan))) return fail_out(s);
+  if ((s = layer_alloc_t(L, 4, &L->counter))) return fail_out(s);
+  const uint64_t R = (uint64_t)L->max_rows;
+  if ((s = layer_alloc_t(L, R * I, &L->w1))) return fail_out(s);
+  if ((s = layer_alloc_t(L, R * I, &L->w3))) return fail_out(s);
+  if ((s = layer_alloc_t(L, R * I, &L->din))) return fail_out(s);
+  if ((s = layer_alloc_t(L, R * I * 5, &L->trace))) return fail_out(s);
+  if ((s = layer_alloc_t(L, R * I, &L->dq))) return fail_out(s);
+  if ((s = layer_alloc_t(L, R * I / 32 + 16, &L->ds))) return fail_out(s);
+  if ((s = layer_alloc_t(L, R * H, &L->eout))) return fail_out(s);
+  std::vector<mx_expert_ptrs> host(E + 1);
+  for (int e = 0; e < E; ++e) host[e] = experts[e];
+  host[E] = shared ? *shared : experts[0];
+  hipError_t err = hipMemcpy(L->table, host.data(), sizeof(mx_expert_ptrs) * (E + 1), hipMemcpyHostToDevice);
+  if (err == hipSuccess) err = hipMemset(L->counter, 0, 16);
+  if (err == hipSuccess) err = hipMemset(L->plan, 0, sizeof(Plan));
+  if (err == hipSuccess) err = hipDeviceSynchronize();
+  if (err != hipSuccess) return fail_out(hip_fail(err, "mx_layer_create: table upload"));
+  *out = L;
+  return MX_OK;
+}
+
+int mx_layer_destroy(mx_layer* L) {
+  if (!L) return MX_OK;
+  if (int s = use(L->ctx)) return s;
+  (void)hipDeviceSynchronize();
+  layer_release(L);
+  delete L;
+  return MX_OK;
+}
+
+int mx_layer_set_expert(mx_layer* L, int32_t expert, const mx_expert_ptrs* w, void* stream) {
+  MX_REQUIRE(L != nullptr, "layer is closed");
+  if (int s = use(L->ctx)) return s;
+  MX_REQUIRE(expert >= 0 && expert < L->cfg.experts, "expert %d outside the layer", expert);
+  MX_REQUIRE(w != nullptr, "null expert pointers");
+  if (int s = check_expert_ptrs(*w, "mx_layer_set_expert")) return s;
+  // A by-value kernel argument carries the six pointers, so the host copy may go out of scope.
+  hipLaunchKernelGGL(set_expert_kernel, dim3(1), dim3(1), 0, as_stream(stream), L->table + expert, *w);
+  MX_LAUNCH_CHECK("set_expert");
+  return MX_OK;
+}
+
+int mx_layer_buffer(mx_layer* L, int32_t which, void** dptr, uint64_t* bytes) {
+  MX_REQUIRE(L != nullptr && dptr != nullptr, "mx_layer_buffer: bad arguments");
+  const uint64_t T = L->cfg.max_tokens, E = L->cfg.experts, k = L->cfg.top_k, H = L->cfg.hidden,
+                 I = L->cfg.intermediate, R = L->max_rows;
+  void* p = nullptr;
+  uint64_t b = 0;
+  switch (which) {
+    case MX_BUF_LOGITS: p = L->logits; b = T * E * 4; break;
+    case MX_BUF_SCORES: p = L->scores; b = T * E * 4; break;
+    case MX_BUF_SELECTION: p = L->selection; b = T * E * 4; break;
+    case MX_BUF_INDICES: p = L->indices; b = T * k * 4; break;
+    case MX_BUF_WEIGHTS: p = L->weights; b = T * k * 4; break;
+    case MX_BUF_XQ: p = L->xq; b = T * H; break;
+    case MX_BUF_XS: p = L->xs; b = T * H / 32; break;
+    case MX_BUF_PLAN: p = L->plan; b = sizeof(Plan); break;
+    case MX_BUF_W1: p = L->w1; b = R * I * 2; break;
+    case MX_BUF_W3: p = L->w3; b = R * I * 2; break;
+    case MX_BUF_DOWN_INPUT: p = L->din; b = R * I * 2; break;
+    case MX_BUF_DOWN_Q: p = L->dq; b = R * I; break;
+    case MX_BUF_DOWN_S: p = L->ds; b = R * I / 32; break;
+    case MX_BUF_EXPERT_OUT: p = L->eout; b = R * H * 2; break;
+    case MX_BUF_TRACE: p = L->trace; b = R * I * 5 * 4; break;
+    case MX_BUF_RAW: p = L->raw; b = T * k * 4; break;
+    case MX_BUF_DENOMINATOR: p = L->den; b = T * 4; break;
+    case MX_BUF_TIED: p = L->tied; b = T * 4; break;
+    default: return fail(MX_ERR_INVALID, "mx_layer_buffer: unknown buffer %d", which);
+  }
+  *dptr = p;
+  if (bytes) *bytes = b;
+  return MX_OK;
+}
+
+int mx_layer_profile(mx_layer* L, int32_t enable, float* stage_ms, int32_t* calls) {
+  MX_REQUIRE(L != nullptr, "layer is closed");
+  if (int s = use(L->ctx)) return s;
+  if (stage_ms)
+    for (int i = 0; i < 4; ++i) stage_ms[i] = L->profiled_calls ? (float)(L->stage_ms[i] / L->profiled_calls) : 0.f;
+  if (calls) *calls = L->profiled_calls;
+  if (enable && !L->ev[0])
+    for (auto& e : L->ev) MX_HIP(hipEventCreate(&e));
+  if (enable) {
+    for (auto& v : L->stage_ms) v = 0;
+    L->profiled_calls = 0;
+  }
+  L->profile = enable != 0;
+  return MX_OK;
+}
+
+int mx_moe_decode(mx_layer* L, const uint16_t* x, int32_t T, uint16_t* y, int32_t diagnostics, void* stream) {
+  MX_REQUIRE(L != nullptr, "layer is closed");
+  if (int s = use(L->ctx)) return s;
+  const mx_moe_config& c = L->cfg;
+  MX_REQUIRE(T >= 0 && T <= c.max_tokens, "token count %d outside [0, %d]", T, c.max_tokens);
+  if (T == 0) return MX_OK;
+  MX_REQUIRE(x && y && aligned(x, 16) && aligned(y, 16), "x and y must be 16-byte aligned device pointers");
+  hipStream_t st = as_stream(stream);
+  const bool prof = L->profile;
+  if (prof) MX_HIP(hipEventRecord(L->ev[0], st));
+  RouterArgs r{};
+  r.W = L->router_weight;
+  r.bias = L->bias;
+  r.x = x;
+  r.T = T;
+  r.H = c.hidden;
+  r.E = c.experts;
+  r.k = c.top_k;
+  r.score_func = c.score_func;
+  r.route_scale = c.route_scale;
+  r.logits = L->logits;
+  r.scores = L->scores;
+  r.selection = L->selection;
+  r.xq = L->xq;
+  r.xs = L->xs;
+  r.topk = TopkOut{L->indices, L->weights, L->raw, L->den, L->tied};
+  r.plan = L->plan;
+  r.counter = L->counter;
+  r.has_shared = L->has_shared;
+  hipLaunchKernelGGL(router_kernel, dim3(c.experts, 1), dim3(256), 0, st, r);
+  MX_LAUNCH_CHECK("router_kernel");
+  if (prof) MX_HIP(hipEventRecord(L->ev[1], st));
+  ExpertArgs a{};
+  a.table = L->table;
+  a.plan = L->plan;
+  a.H = c.hidden;
+  a.I = c.intermediate;
+  a.limit = c.swiglu_limit;
+  a.xq = L->xq;
+  a.xs = L->xs;
+  a.dq = L->dq;
+  a.ds = L->ds;
+  a.out = L->eout;
+  if (diagnostics) {
+    a.w1 = L->w1;
+    a.w3 = L->w3;
+    a.din = L->din;
+    a.trace = L->trace;
+  }
+  const int slots = std::min(c.experts, T * c.top_k) + L->has_shared;
+  hipLaunchKernelGGL(gateup_kernel, dim3(c.intermediate / 32, slots), dim3(256), 0, st, a);
+  MX_LAUNCH_CHECK("gateup_kernel");
+  if (prof) MX_HIP(hipEventRecord(L->ev[2], st));
+  hipLaunchKernelGGL(down_kernel, dim3(c.hidden / 64, slots), dim3(256), 0, st, a);
+  MX_LAUNCH_CHECK("down_kernel");
+  if (prof) MX_HIP(hipEventRecord(L->ev[3], st));
+  hipLaunchKernelGGL(combine_kernel, dim3((c.hidden / 8 + 255) / 256, T), dim3(256), 0, st, (const Plan*)L->plan,
+                     (const uint16_t*)L->eout, c.hidden, c.top_k, L->has_shared, y);
+  MX_LAUNCH_CHECK("combine_kernel");
+  if (prof) {
+    MX_HIP(hipEventRecord(L->ev[4], st));
+    MX_HIP(hipEventSynchronize(L->ev[4]));
+    for (int i = 0; i < 4; ++i) {
+      float ms = 0.f;
+      MX_HIP(hipEventElapsedTime(&ms, L->ev[i], L->ev[i + 1]));
+      L->stage_ms[i] += ms;
+    }
+    ++L->profiled_calls;
+  }
+  return MX_OK;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Single expert, T tokens (ExpertExecutor.execute / ResidentSharedExpert.forward)
+
+int mx_expert_forward(mx_ctx* ctx, const mx_expert_ptrs* w, int32_t format, int32_t H, int32_t I,
+                      const uint16_t* x, int32_t T, float limit, const float* route_w, uint16_t* y,
+                      const mx_expert_stages* stages, void* stream) {
+  if (int s = use(ctx)) return s;
+  MX_REQUIRE(w != nullptr, "mx_expert_forward: null expert pointers");
+  MX_REQUIRE(format == MX_FMT_MXFP4, "mx_expert_forward: only the MXFP4 format runs on this path");
+  MX_REQUIRE(H > 0 && H % 128 == 0 && I > 0 && I % 128 == 0, "expert shapes must be positive multiples of 128");
+  MX_REQUIRE(T >= 0 && T <= kMaxTokens, "token count %d outside [0, %d]", T, kMaxTokens);
+  MX_REQUIRE(std::isfinite(limit) && limit >= 0.f, "Invalid SwiGLU limit");
+  if (int s = check_expert_ptrs(*w, "mx_expert_forward")) return s;
+  if (T == 0) return MX_OK;
+  MX_REQUIRE(x && y && aligned(x, 16) && aligned(y, 16), "x and y must be 16-byte aligned device pointers");
+  hipStream_t st = as_stream(stream);
+  // scratch: plan | xq | xs | dq | ds (stage buffers replace them when supplied)
+  const uint64_t plan_b = (sizeof(Plan) + 255) & ~255ull;
+  const uint64_t xq_b = ((uint64_t)T * H + 255) & ~255ull, xs_b = ((uint64_t)T * H / 32 + 255) & ~255ull;
+  const uint64_t dq_b = ((uint64_t)T * I + 255) & ~255ull, ds_b = ((uint64_t)T * I / 32 + 255) & ~255ull;
+  void* base = nullptr;
+  if (int s = scratch(ctx, plan_b + xq_b + xs_b + dq_b + ds_b, &base)) return s;
+  uint8_t* b8 = (uint8_t*)base;
+  Plan* plan = (Plan*)b8;
+  uint8_t* xq = (stages && stages->q) ? stages->q : b8 + plan_b;
+  uint8_t* xs = (stages && stages->s) ? stages->s : b8 + plan_b + xq_b;
+  uint8_t* dq = (stages && stages->down_q) ? stages->down_q : b8 + plan_b + xq_b + xs_b;
+  uint8_t* ds = (stages && stages->down_s) ? stages->down_s : b8 + plan_b + xq_b + xs_b + dq_b;
+  MX_REQUIRE(aligned(xq, 16) && aligned(dq, 16) && aligned(xs, 4) && aligned(ds, 4),
+             "stage buffers q/down_q must be 16-byte and s/down_s 4-byte aligned");
+  hipLaunchKernelGGL(single_plan_kernel, dim3(1), dim3(64), 0, st, plan, T, route_w);
+  MX_LAUNCH_CHECK("single_plan_kernel");
+  if (int s = mx_act_quant32(ctx, x, xq, xs, T, H, stream)) return s;
+  ExpertArgs a{};
+  a.table = nullptr;
+  a.single = *w;
+  a.plan = plan;
+  a.H = H;
+  a.I = I;
+  a.limit = limit;
+  a.xq = xq;
+  a.xs = xs;
+  a.dq = dq;
+  a.ds = ds;
+  a.out = y;
+  if (stages) {
+    a.w1 = stages->w1;
+    a.w3 = stages->w3;
+    a.din = stages->down_input;
+    a.trace = stages->trace;
+  }
+  hipLaunchKernelGGL(gateup_kernel, dim3(I / 32, 1), dim3(256), 0, st, a);
+  MX_LAUNCH_CHECK("gateup_kernel");
+  hipLaunchKernelGGL(down_kernel, dim3(H / 64, 1), dim3(256), 0, st, a);
+  MX_LAUNCH_CHECK("down_kernel");
+  return MX_OK;
+}
+
+int mx_gemv_mxfp4(mx_ctx* ctx, const uint8_t* q, const uint8_t* sa, const uint8_t* w, const uint8_t* sw,
+                  uint16_t* y, int32_t T, int32_t N, int32_t K, void* stream) {
+  if (int s = use(ctx)) return s;
+  MX_REQUIRE(T >= 0 && T <= kMaxTokens, "token count %d outside [0, %d]", T, kMaxTokens);
+  MX_REQUIRE(N > 0 && N % 64 == 0 && K > 0 && K % 128 == 0, "mx_gemv_mxfp4 needs N %% 64 == 0 and K %% 128 == 0");
+  if (!T) return MX_OK;
+  MX_REQUIRE(q && sa && w && sw && y, "mx_gemv_mxfp4: null pointer");
+  MX_REQUIRE(aligned(q, 16) && aligned(w, 16) && aligned(sa, 4) && aligned(sw, 4) && aligned(y, 8),
+             "mx_gemv_mxfp4: q/w 16-byte, scales 4-byte and y 8-byte alignment required");
+  hipStream_t st = as_stream(stream);
+  void* base = nullptr;
+  if (int s = scratch(ctx, sizeof(Plan), &base)) return s;
+  Plan* plan = (Plan*)base;
+  hipLaunchKernelGGL(single_plan_kernel, dim3(1), dim3(64), 0, st, plan, T, (const float*)nullptr);
+  MX_LAUNCH_CHECK("single_plan_kernel");
+  ExpertArgs a{};
+  a.single.w2_weight = w;
+  a.single.w2_scale = sw;
+  a.plan = plan;
+  a.H = N;
+  a.I = K;
+  a.dq = const_cast<uint8_t*>(q);
+  a.ds = const_cast<uint8_t*>(sa);
+  a.out = y;
+  hipLaunchKernelGGL(down_kernel, dim3(N / 64, 1), dim3(256), 0, st, a);
+  MX_LAUNCH_CHECK("down_kernel");
+  return MX_OK;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Router entry points
+
+static int router_common(mx_ctx* ctx, int T, int E, int k, int score_func, float route_scale,
+                         const mx_router_out* out) {
+  if (int s = use(ctx)) return s;
+  MX_REQUIRE(out && out->indices && out->weights, "router outputs indices and weights are required");
+  MX_REQUIRE(T >= 0, "negative token count");
+  MX_REQUIRE(E >= 1 && E <= kMaxExperts, "experts must be in [1, %d]", kMaxExperts);
+  MX_REQUIRE(k >= 1 && k <= kMaxTopK && k <= E, "top_k must be in [1, min(32, E)]");
+  MX_REQUIRE(score_func == MX_SCORE_SIGMOID || score_func == MX_SCORE_SQRTSOFTPLUS, "unknown score function");
+  MX_REQUIRE(std::isfinite(route_scale), "route scale must be finite");
+  return MX_OK;
+}
+
+int mx_router(mx_ctx* ctx, const float* W, const float* bias, const uint16_t* x, int32_t T, int32_t H, int32_t E,
+              int32_t k, int32_t score_func, float route_scale, const mx_router_out* out, void* stream) {
+  if (int s = router_common(ctx, T, E, k, score_func, route_scale, out)) return s;
+  MX_REQUIRE(H > 0 && H % 4 == 0, "hidden size must be a positive multiple of 4");
+  MX_REQUIRE(out->logits != nullptr, "router logits output is required");
+  MX_REQUIRE(W && x && aligned(W, 16) && aligned(x, 8), "W must be 16-byte and x 8-byte aligned");
+  if (!T) return MX_OK;
+  hipStream_t st = as_stream(stream);
+  // scores/selection scratch when the caller does not keep them
+  float *scores = out->scores, *selection = out->selection;
+  if (!scores || !selection) {
+    void* base = nullptr;
+    if (int s = scratch(ctx, (uint64_t)T * E * 8, &base)) return s;
+    if (!scores) scores = (float*)base;
+    if (!selection) selection = (float*)base + (uint64_t)T * E;
+  }
+  RouterArgs r{};
+  r.W = W;
+  r.bias = bias;
+  r.x = x;
+  r.T = T;
+  r.H = H;
+  r.E = E;
+  r.k = k;
+  r.score_func = score_func;
+  r.route_scale = route_scale;
+  r.logits = out->logits;
+  r.scores = scores;
+  r.selection = selection;
+  hipLaunchKernelGGL(router_kernel, dim3(E, (T + kMaxTokens - 1) / kMaxTokens), dim3(256), 0, st, r);
+  MX_LAUNCH_CHECK("router_kernel");
+  TopkOut o{out->indices, out->weights, out->raw, out->denominator, out->tied};
+  hipLaunchKernelGGL(topk_kernel, dim3((T + 3) / 4), dim3(256), 0, st, (const float*)selection, (const float*)scores,
+                     T, E, k, route_scale, o);
+  MX_LAUNCH_CHECK("topk_kernel");
+  return MX_OK;
+}
+
+int mx_gate_project(mx_ctx* ctx, const float* W, const uint16_t* x, int32_t T, int32_t H, int32_t E, float* logits,
+                    void* stream) {
+  if (int s = use(ctx)) return s;
+  MX_REQUIRE(T >= 0 && H > 0 && H % 4 == 0, "hidden size must be a positive multiple of 4");
+  MX_REQUIRE(E >= 1, "experts must be positive");
+  if (!T) return MX_OK;
+  MX_REQUIRE(W && x && logits && aligned(W, 16) && aligned(x, 8), "W must be 16-byte and x 8-byte aligned");
+  RouterArgs r{};
+  r.W = W;
+  r.x = x;
+  r.T = T;
+  r.H = H;
+  r.E = E;
+  r.logits = logits;
+  hipLaunchKernelGGL(router_kernel, dim3(E, (T + kMaxTokens - 1) / kMaxTokens), dim3(256), 0, as_stream(stream), r);
+  MX_LAUNCH_CHECK("router_kernel");
+  return MX_OK;
+}
+
+int mx_router_postprocess(mx_ctx* ctx, const float* logits, const float* bias, int32_t T, int32_t E, int32_t k,
+                          int32_t score_func, float route_scale, const mx_router_out* out, void* stream) {
+  if (int s = router_common(ctx, T, E, k, score_func, route_scale, out)) return s;
+  MX_REQUIRE(logits != nullptr, "logits are required");
+  if (!T) return MX_OK;
+  hipStream_t st = as_stream(stream);
+  float *scores = out->scores, *selection = out->selection;
+  if (!scores || !selection) {
+    void* base = nullptr;
+    if (int s = scratch(ctx, (uint64_t)T * E * 8, &base)) return s;
+    if (!scores) scores = (float*)base;
+    if (!selection) selection = (float*)base + (uint64_t)T * E;
+  }
+  hipLaunchKernelGGL(scores_kernel, dim3(blocks_for((int64_t)T * E, 256)), dim3(256), 0, st, logits, bias, T, E,
+                     score_func, scores, selection);
+  MX_LAUNCH_CHECK("scores_kernel");
+  TopkOut o{out->indices, out->weights, out->raw, out->denominator, out->tied};
+  hipLaunchKernelGGL(topk_kernel, dim3((T + 3) / 4), dim3(256), 0, st, (const float*)selection, (const float*)scores,
+                     T, E, k, route_scale, o);
+  MX_LAUNCH_CHECK("topk_kernel");
+  return MX_OK;
+}
+
+int mx_router_select(mx_ctx* ctx, const float* scores, const float* selection, int32_t T, int32_t E, int32_t k,
+                     float route_scale, const mx_router_out* out, void* stream) {
+  if (int s = router_common(ctx, T, E, k, MX_SCORE_SIGMOID, route_scale, out)) return s;
+  MX_REQUIRE(scores && selection, "scores and selection are required");
+  if (!T) return MX_OK;
+  TopkOut o{out->indices, out->weights, out->raw, out->denominator, out->tied};
+  hipLaunchKernelGGL(topk_kernel, dim3((T + 3) / 4), dim3(256), 0, as_stream(stream), scores, selection, T, E, k,
+                     route_scale, o);
+  MX_LAUNCH_CHECK("topk_kernel");
+  return MX_OK;
+}
+
+// ------------------------------------------------------------------------------------------------
+// MoEAccumulator kernels
+
+int mx_acc_zero(mx_ctx* ctx, float* sum, int64_t n, void* stream) {
+  if (int s = use(ctx)) return s;
+  MX_REQUIRE(n >= 0 && (n == 0 || sum), "mx_acc_zero: bad arguments");
+  if (!n) return MX_OK;
+  hipLaunchKernelGGL(acc_zero_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, as_stream(stream), sum, n);
+  MX_LAUNCH_CHECK("acc_zero_kernel");
+  return MX_OK;
+}
+
+int mx_acc_add_rows(mx_ctx* ctx, float* sum, const uint16_t* vals, const int32_t* rows, int32_t nrows, int32_t width,
+                    void* stream) {
+  if (int s = use(ctx)) return s;
+  MX_REQUIRE(nrows >= 0 && width > 0, "mx_acc_add_rows: bad shape");
+  if (!nrows) return MX_OK;
+  MX_REQUIRE(sum && vals && rows, "mx_acc_add_rows: null pointer");
+  hipLaunchKernelGGL(acc_add_rows_kernel, dim3(blocks_for((int64_t)nrows * width, 256)), dim3(256), 0,
+                     as_stream(stream), sum, vals, rows, nrows, width);
+  MX_LAUNCH_CHECK("acc_add_rows_kernel");
+  return MX_OK;
+}
+
+int mx_acc_add(mx_ctx* ctx, float* sum, const uint16_t* vals, int64_t n, void* stream) {
+  if (int s = use(ctx)) return s;
+  MX_REQUIRE(n >= 0, "mx_acc_add: bad count");
+  if (!n) return MX_OK;
+  MX_REQUIRE(sum && vals, "mx_acc_add: null pointer");
+  hipLaunchKernelGGL(acc_add_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, as_stream(stream), sum, vals, n);
+  MX_LAUNCH_CHECK("acc_add_kernel");
+  return MX_OK;
+}
+
+int mx_acc_finish(mx_ctx* ctx, const float* sum, uint16_t* out, int64_t n, void* stream) {
+  if (int s = use(ctx)) return s;
+  MX_REQUIRE(n >= 0, "mx_acc_finish: bad count");
+  if (!n) return MX_OK;
+  MX_REQUIRE(sum && out, "mx_acc_finish: null pointer");
+  hipLaunchKernelGGL(acc_finish_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, as_stream(stream), sum, out, n);
+  MX_LAUNCH_CHECK("acc_finish_kernel");
+  return MX_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,207 @@
+"""Resident expert bank and the batched MoE decode layer (the fast path).
+
+ExpertBank keeps every expert of a layer in one HBM allocation using the
+reference's per-expert contiguous byte layout (w1_weight, w1_scale, w3_weight,
+w3_scale, w2_weight, w2_scale; src/vesper/storage.py:33-41), so a cache slot
+and a store entry have the same shape. MoELayer drives mx_moe_decode: router,
+top-k plan, fused expert GEMVs and ordered combine in four kernel launches on
+one stream, with inputs resident in HBM.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+from .config import MoEConfig
+
+TENSORS = ("w1_weight", "w1_scale", "w3_weight", "w3_scale", "w2_weight", "w2_scale")
+
+# Plan struct layout (mx_moe.hip `Plan`): 8 header ints, then per-slot arrays.
+_MAX_TOKENS, _MAX_TOPK = 16, 32
+_MAX_SLOTS = _MAX_TOKENS * _MAX_TOPK + 1
+
+
+def _plan_views(raw: np.ndarray) -> dict:
+    words = raw.view(np.int32)
+    o = 8
+    out = {"n_slots": int(words[0]), "n_routed": int(words[1]), "total_rows": int(words[2]),
+           "tokens": int(words[3]), "top_k": int(words[4])}
+    for name in ("slot_expert", "slot_ntok", "slot_row0", "slot_weighted"):
+        out[name] = words[o:o + _MAX_SLOTS]
+        o += _MAX_SLOTS
+    out["slot_tok"] = words[o:o + _MAX_SLOTS * _MAX_TOKENS].reshape(_MAX_SLOTS, _MAX_TOKENS)
+    o += _MAX_SLOTS * _MAX_TOKENS
+    out["slot_w"] = words[o:o + _MAX_SLOTS * _MAX_TOKENS].view(np.float32).reshape(_MAX_SLOTS, _MAX_TOKENS)
+    o += _MAX_SLOTS * _MAX_TOKENS
+    out["tok_rows"] = words[o:o + _MAX_TOKENS * (_MAX_TOPK + 1)].reshape(_MAX_TOKENS, _MAX_TOPK + 1)
+    return out
+
+
+class ExpertBank:
+    """`count` experts of one layer resident in a single device allocation."""
+
+    def __init__(self, ctx: _lib.Context, config: MoEConfig, count: int):
+        self.ctx, self.config, self.count = ctx, config, int(count)
+        layout = config.expert_layout()
+        self.offsets, offset = {}, 0
+        for name in TENSORS:
+            rows, cols = layout[name]
+            self.offsets[name] = (offset, (rows, cols))
+            offset += rows * cols
+        self.expert_bytes = offset
+        if offset % 256:
+            raise ValueError("expert byte size must keep every expert 256-byte aligned")
+        self.base = ctx.malloc(self.expert_bytes * self.count)
+
+    def tensor_ptr(self, expert: int, name: str) -> int:
+        return self.base + expert * self.expert_bytes + self.offsets[name][0]
+
+    def ptrs(self, expert: int) -> _lib.MxExpertPtrs:
+        if not 0 <= expert < self.count:
+            raise ValueError("expert index outside the bank")
+        return _lib.MxExpertPtrs(*[self.tensor_ptr(expert, n) for n in TENSORS])
+
+    def upload(self, expert: int, arrays: dict, stream=None):
+        validate_expert_arrays(arrays, self.config)
+        for name in TENSORS:
+            self.ctx.copy_h2d(self.tensor_ptr(expert, name), np.ascontiguousarray(arrays[name], np.uint8), stream)
+
+    def download(self, expert: int) -> dict:
+        return {name: self.ctx.download(self.tensor_ptr(expert, name), shape, np.uint8)
+                for name, (_, shape) in self.offsets.items()}
+
+    def fill_synthetic(self, seed: int, scale_lo: int = 118, scale_hi: int = 126, stream=None):
+        """BASELINE inputs generated in HBM: uniform packed bytes, E8M0 codes uniform in [lo, hi]."""
+        for e in range(self.count):
+            for t, name in enumerate(TENSORS):
+                offset, (rows, cols) = self.offsets[name]
+                lo, hi = (0, 255) if name.endswith("weight") else (scale_lo, scale_hi)
+                self.ctx.fill_uniform_u8(self.base + e * self.expert_bytes + offset, rows * cols,
+                                         (seed * 1_000_003 + e * 8 + t), lo, hi, stream)
+
+    def free(self):
+        if self.base:
+            self.ctx.free(self.base)
+            self.base = 0
+
+
+def validate_expert_arrays(arrays: dict, config: MoEConfig):
+    """Layout check before any device work (checkpoint.py:143-149, test_expert_boundaries.py)."""
+    layout = config.expert_layout()
+    if set(arrays) != set(layout):
+        raise ValueError("A complete expert requires exactly six native tensors")
+    for name, shape in layout.items():
+        a = arrays[name]
+        if not isinstance(a, np.ndarray) or a.dtype != np.uint8 or a.shape != shape:
+            raise ValueError("Expert tensor layout differs from the pinned shape")
+
+
+class MoELayer:
+    """One routed MoE layer resident on the device; `decode` runs T <= 16 tokens."""
+
+    def __init__(self, ctx: _lib.Context, config: MoEConfig, router_weight, bank: ExpertBank, bias=None):
+        if bank.count != config.experts + (1 if config.shared else 0):
+            raise ValueError("expert bank size must be experts (+1 for the shared expert)")
+        self.ctx, self.config, self.bank = ctx, config, bank
+        self.lib = ctx.lib
+        self._owned = []
+        self.router_weight = self._device_f32(router_weight, (config.experts, config.hidden))
+        self.bias = None if bias is None else self._device_f32(bias, (config.experts,))
+        cfg = _lib.MxMoeConfig(config.hidden, config.intermediate, config.experts, config.top_k,
+                               _lib.MX_SCORE[config.score_func], config.route_scale, config.swiglu_limit,
+                               _lib.MX_FMT_MXFP4 if config.shared else -1, config.max_tokens)
+        table = (_lib.MxExpertPtrs * config.experts)(*[bank.ptrs(e) for e in range(config.experts)])
+        shared = C.byref(bank.ptrs(config.experts)) if config.shared else None
+        handle = C.c_void_p()
+        self.lib.layer_create(ctx._h(), C.byref(cfg), _lib.vp(self.router_weight), _lib.vp(self.bias),
+                              table, shared, C.byref(handle))
+        self.handle = handle
+
+    def _device_f32(self, value, shape):
+        if isinstance(value, _lib.DeviceArray):
+            if value.dtype != np.float32 or value.shape != shape:
+                raise ValueError(f"expected an FP32 device array of shape {shape}")
+            return value
+        array = np.ascontiguousarray(value, dtype=np.float32)
+        if array.shape != shape or not np.isfinite(array).all():
+            raise ValueError(f"expected finite FP32 values of shape {shape}")
+        dev = self.ctx.upload(array)
+        self._owned.append(dev)
+        return dev
+
+    def close(self):
+        if self.handle:
+            handle, self.handle = self.handle, C.c_void_p()
+            self.lib.layer_destroy(handle)
+        for dev in self._owned:
+            dev.free()
+        self._owned.clear()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *_):
+        self.close()
+
+    # -- fast path --------------------------------------------------------------------------
+    def decode_device(self, x_ptr: int, tokens: int, y_ptr: int, stream=None, diagnostics: bool = False):
+        """y = MoE(x) with x, y device BF16 [tokens, hidden]; no host synchronisation."""
+        self.lib.moe_decode(self.handle, C.c_void_p(int(x_ptr)), int(tokens), C.c_void_p(int(y_ptr)),
+                            int(bool(diagnostics)), _lib._stream(stream))
+
+    def decode(self, x, diagnostics: bool = False) -> np.ndarray:
+        """Host convenience: BF16 bits or FP32 [T, H] in, BF16 bits [T, H] out."""
+        bits = bf16_input(x, self.config.hidden)
+        t = bits.shape[0]
+        xd = self.ctx.upload(bits)
+        yd = self.ctx.empty((t, self.config.hidden), np.uint16)
+        try:
+            self.decode_device(xd.ptr, t, yd.ptr, diagnostics=diagnostics)
+            return yd.download()
+        finally:
+            xd.free()
+            yd.free()
+
+    # -- diagnostics ------------------------------------------------------------------------
+    def buffer(self, name: str):
+        p, n = C.c_void_p(), C.c_uint64()
+        self.lib.layer_buffer(self.handle, _lib.BUFFERS[name], C.byref(p), C.byref(n))
+        return int(p.value), int(n.value)
+
+    def read(self, name: str, shape, dtype) -> np.ndarray:
+        p, n = self.buffer(name)
+        want = int(np.prod(shape)) * np.dtype(dtype).itemsize
+        if want > n:
+            raise ValueError(f"buffer {name} holds {n} bytes, {want} requested")
+        return self.ctx.download(p, shape, dtype)
+
+    def plan(self) -> dict:
+        p, n = self.buffer("plan")
+        return _plan_views(self.ctx.download(p, (n,), np.uint8))
+
+    def profile(self, enable: bool):
+        ms = (C.c_float * 4)()
+        calls = C.c_int32()
+        self.lib.layer_profile(self.handle, int(bool(enable)), ms, C.byref(calls))
+        return {"router": ms[0], "gateup": ms[1], "down": ms[2], "combine": ms[3], "calls": calls.value}
+
+
+def bf16_input(x, hidden: int) -> np.ndarray:
+    """[T, H] BF16 storage bits from BF16 bits or FP32 values (connected.py:45-53, batched)."""
+    x = np.asarray(x)
+    if x.ndim == 1:
+        x = x.reshape(1, -1)
+    if x.ndim != 2 or x.shape[1] != hidden or x.dtype not in (np.dtype(np.uint16), np.dtype(np.float32)):
+        raise ValueError(f"MoE input must be BF16 storage bits or FP32 values of shape (T, {hidden})")
+    if x.dtype == np.uint16:
+        bits = np.ascontiguousarray(x)
+    else:
+        b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+        nan = ((b & 0x7F800000) == 0x7F800000) & ((b & 0x7FFFFF) != 0)
+        bits = np.where(nan, (b >> 16) | 0x40, (b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+    if np.any((bits & 0x7F80) == 0x7F80):
+        raise ValueError("MoE activation leaves the finite BF16 scope")
+    return bits
