@@ -5,7 +5,7 @@ import pytest
 
 from oracle.formats import (bf16_bits, bf16_values, e4m3_values, encode_e4m3, mxfp4_gemv_spec, quantize_activation,
                             unpack_fp4)
-from tests.helpers import bf16_ulp_diff, exact_activation
+from tests.helpers import assert_gemv_close, exact_activation
 from tests.test_oracle_formats import conversion_space
 from vesper_amd import _lib, conformance
 
@@ -83,7 +83,7 @@ def test_block_gemv_is_exact_on_exactly_representable_inputs(gpu_ctx, tokens, n,
     np.testing.assert_array_equal(got, mxfp4_gemv_spec(q, sa, w, sw))
 
 
-def test_block_gemv_random_inputs_within_one_bf16_ulp(gpu_ctx):
+def test_block_gemv_random_inputs_close_to_in_order_sum(gpu_ctx):
     rng = np.random.default_rng(42)
     x = bf16_values(bf16_bits(rng.standard_normal((4, 2048)).astype(np.float32)))
     q, sa = quantize_activation(x)
@@ -91,6 +91,4 @@ def test_block_gemv_random_inputs_within_one_bf16_ulp(gpu_ctx):
     sw = rng.integers(118, 127, (1024, 64), dtype=np.uint8)
     got = run_gemv(gpu_ctx, q, sa, w, sw)
     ref = mxfp4_gemv_spec(q, sa, w, sw)
-    ulps = bf16_ulp_diff(got, ref)
-    assert ulps.max() <= 1, ulps.max()
-    assert np.mean(ulps == 0) > 0.99
+    assert_gemv_close(got, ref, "random GEMV")

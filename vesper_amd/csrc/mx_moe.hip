@@ -485,6 +485,19 @@ struct ExpertArgs {
   float* trace;
 };
 
+// Operand layout of V_MFMA_SCALE_F32_16X16X128_F8F6F4 (measured on gfx950):
+//   A (FP4, 4 VGPRs): lane l holds row l%16, K = 32*(l/16) + j for nibble j (low nibble first),
+//                     i.e. one whole 16-byte MX block of the reference layout.
+//   B (FP8, 8 VGPRs): lane l holds column l%16; bytes 0-15 are K = 16*(l/16) + j and bytes 16-31
+//                     are K = 64 + 16*(l/16) + j.
+//   scale_a / scale_b: lane l scales row / column l%16 over the 32-wide K block l/16.
+//   D: lane l, register i holds row 4*(l/16) + i, column l%16.
+// So the FP8 side of a 128-wide K chunk is read as two 16-byte pieces at 16q and 64 + 16q.
+__device__ __forceinline__ void load_b_operand(const uint8_t* chunk, int q, uint4& b0, uint4& b1) {
+  b0 = *reinterpret_cast<const uint4*>(chunk + 16 * q);
+  b1 = *reinterpret_cast<const uint4*>(chunk + 64 + 16 * q);
+}
+
 __device__ __forceinline__ v4f mfma_fp4xfp8(uint4 a, uint4 b0, uint4 b1, v4f c, int sa, int sb) {
   v8i av = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
   v8i bv = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
@@ -525,8 +538,7 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
     uint4 b0 = zero, b1 = zero;
     uint32_t sx = 0x7F7F7F7Fu;
     if (tok >= 0) {
-      b0 = *reinterpret_cast<const uint4*>(xrow + (size_t)kb * 32);
-      b1 = *reinterpret_cast<const uint4*>(xrow + (size_t)kb * 32 + 16);
+      load_b_operand(xrow + (size_t)c * 128, q, b0, b1);
       sx = *reinterpret_cast<const uint32_t*>(xsrow + 4 * c);
     }
     acc = mfma_fp4xfp8(wa, b0, b1, acc, (int)((sw >> (8 * q)) & 0xFF), (int)((sx >> (8 * q)) & 0xFF));
@@ -614,8 +626,7 @@ __global__ __launch_bounds__(256) void down_kernel(ExpertArgs a) {
     uint4 b0 = zero, b1 = zero;
     uint32_t sx = 0x7F7F7F7Fu;
     if (live) {
-      b0 = *reinterpret_cast<const uint4*>(xrow + (size_t)kb * 32);
-      b1 = *reinterpret_cast<const uint4*>(xrow + (size_t)kb * 32 + 16);
+      load_b_operand(xrow + (size_t)c * 128, q, b0, b1);
       sx = *reinterpret_cast<const uint32_t*>(xsrow + 4 * c);
     }
     acc = mfma_fp4xfp8(wa, b0, b1, acc, (int)((sw >> (8 * q)) & 0xFF), (int)((sx >> (8 * q)) & 0xFF));
@@ -1157,7 +1168,7 @@ int mx_router_select(mx_ctx* ctx, const float* scores, const float* selection, i
   MX_REQUIRE(scores && selection, "scores and selection are required");
   if (!T) return MX_OK;
   TopkOut o{out->indices, out->weights, out->raw, out->denominator, out->tied};
-  hipLaunchKernelGGL(topk_kernel, dim3((T + 3) / 4), dim3(256), 0, as_stream(stream), scores, selection, T, E, k,
+  hipLaunchKernelGGL(topk_kernel, dim3((T + 3) / 4), dim3(256), 0, as_stream(stream), selection, scores, T, E, k,
                      route_scale, o);
   MX_LAUNCH_CHECK("topk_kernel");
   return MX_OK;
