@@ -221,8 +221,10 @@ int mx_moe_decode(mx_layer* layer, const uint16_t* x_bf16, int32_t tokens, uint1
 #define MX_BUF_TIED 17       /* int32 [T]             */
 int mx_layer_buffer(mx_layer* layer, int32_t which, void** dptr, uint64_t* bytes);
 
-/* Per-kernel HIP event timing of the next mx_moe_decode calls on `stream`: stage_ms[0..3] =
- * router, gate/up, down, combine averaged over the calls made while enabled. */
+/* Per-kernel HIP event timing of mx_moe_decode: while enabled, each call records events around its
+ * four kernels on its stream (no host synchronisation; a ring of 64 calls is folded into the totals
+ * when full). Reading (any call) reports stage_ms[0..3] = router, gate/up, down, combine averaged
+ * over the calls recorded since profiling was last enabled. */
 int mx_layer_profile(mx_layer* layer, int32_t enable, float* stage_ms, int32_t* calls);
 
 #ifdef __cplusplus

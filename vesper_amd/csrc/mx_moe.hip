@@ -28,6 +28,7 @@ constexpr int kMaxTokens = 16;   // MFMA N: tokens per expert per decode call
 constexpr int kMaxTopK = 32;
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxSlots = kMaxTokens * kMaxTopK + 1;
+constexpr int kRouterKIter = 8;   // router GEMV: hidden size <= 8 * 1024 per thread-strided pass
 
 // Device-side execution plan of one decode call (written by the router's last workgroup).
 struct Plan {
@@ -69,29 +70,58 @@ __device__ __forceinline__ float silu_of(float g) {
   return g / (1.0f + e);
 }
 
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  return v;
-}
-
-__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    const uint32_t o = __shfl_xor(v, m, 64);
-    v = o > v ? o : v;
-  }
-  return v;
+// Wavefront reductions and scans on DPP (row_shr 1/2/4/8 inside 16-lane rows, then row_bcast 15/31
+// across rows): VALU-latency steps instead of LDS-routed shuffles. `ident` fills lanes whose DPP
+// source is out of range or whose row is masked off.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ int dpp_i(int v, int ident) {
+  return __builtin_amdgcn_update_dpp(ident, v, kCtrl, kRowMask, 0xF, false);
 }
 
 // inclusive prefix sum over the 64 lanes
-__device__ __forceinline__ int wave_scan_i(int v, int lane) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int o = __shfl_up(v, d, 64);
-    if (lane >= d) v += o;
-  }
+__device__ __forceinline__ int wave_scan_i(int v, int /*lane*/) {
+  v += dpp_i<0x111, 0xF>(v, 0);   // row_shr:1
+  v += dpp_i<0x112, 0xF>(v, 0);   // row_shr:2
+  v += dpp_i<0x114, 0xF>(v, 0);   // row_shr:4
+  v += dpp_i<0x118, 0xF>(v, 0);   // row_shr:8
+  v += dpp_i<0x142, 0xA>(v, 0);   // row_bcast:15 into rows 1 and 3
+  v += dpp_i<0x143, 0xC>(v, 0);   // row_bcast:31 into rows 2 and 3
   return v;
+}
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+  return __builtin_amdgcn_readlane(wave_scan_i(v, 0), 63);
+}
+
+// FP32 wavefront sum in the fixed DPP order (row scans, then across rows), result in every lane.
+__device__ __forceinline__ float wave_sum_f(float v) {
+  auto step = [](float x, int y) { return x + __int_as_float(y); };
+  v = step(v, dpp_i<0x111, 0xF>(__float_as_int(v), 0));
+  v = step(v, dpp_i<0x112, 0xF>(__float_as_int(v), 0));
+  v = step(v, dpp_i<0x114, 0xF>(__float_as_int(v), 0));
+  v = step(v, dpp_i<0x118, 0xF>(__float_as_int(v), 0));
+  v = step(v, dpp_i<0x142, 0xA>(__float_as_int(v), 0));
+  v = step(v, dpp_i<0x143, 0xC>(__float_as_int(v), 0));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+__device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
+  int x = (int)v;
+  x = (int)umax32((uint32_t)x, (uint32_t)dpp_i<0x111, 0xF>(x, 0));
+  x = (int)umax32((uint32_t)x, (uint32_t)dpp_i<0x112, 0xF>(x, 0));
+  x = (int)umax32((uint32_t)x, (uint32_t)dpp_i<0x114, 0xF>(x, 0));
+  x = (int)umax32((uint32_t)x, (uint32_t)dpp_i<0x118, 0xF>(x, 0));
+  x = (int)umax32((uint32_t)x, (uint32_t)dpp_i<0x142, 0xA>(x, 0));
+  x = (int)umax32((uint32_t)x, (uint32_t)dpp_i<0x143, 0xC>(x, 0));
+  return (uint32_t)__builtin_amdgcn_readlane(x, 63);
+}
+
+// value of lane (lane ^ kXor) within each 32-lane half (ds_swizzle bit-mask mode: and 0x1F, xor kXor)
+template <int kXor>
+__device__ __forceinline__ int swizzle_xor(int v) {
+  return __builtin_amdgcn_ds_swizzle(v, (kXor << 10) | 0x1F);
 }
 
 // ----------------------------------------------------------------------------------------------
@@ -103,6 +133,21 @@ __device__ __forceinline__ int wave_scan_i(int v, int lane) {
 // 3. the 32-slot bitonic network (slot i pairs with i ^ stride; the pair's direction is bit `size`
 //    of the lower slot for sizes 2..16, ascending-false for the final merge).
 // 4. raw = score[id], denominator = halving-tree sum + 1e-20, weight = raw / den * route_scale.
+// One compare-exchange stage of the 32-slot network on lanes (slot, slot ^ kStride).
+template <int kSize, int kStride>
+__device__ __forceinline__ void bitonic_stage(float& kv, int32_t& iv, int& vv, int slot) {
+  const float pk = __int_as_float(swizzle_xor<kStride>(__float_as_int(kv)));
+  const int32_t pi = swizzle_xor<kStride>(iv);
+  const int pv = swizzle_xor<kStride>(vv);
+  const bool lower = (slot & kStride) == 0;
+  const int lo = lower ? slot : (slot ^ kStride);
+  const float klo = lower ? kv : pk, khi = lower ? pk : kv;
+  const int vlo = lower ? vv : pv, vhi = lower ? pv : vv;
+  const bool promote = (klo > khi && vlo) || !vhi;
+  const bool dir = kSize < 32 ? (lo & kSize) != 0 : false;
+  if (promote == dir) { kv = pk; iv = pi; vv = pv; }
+}
+
 struct TopkOut {
   int32_t* indices;
   float* weights;
@@ -111,17 +156,17 @@ struct TopkOut {
   int32_t* tied;
 };
 
-__device__ void topk_token_wave(const float* __restrict__ selection, const float* __restrict__ scores, int E, int k,
-                                float route_scale, int t, const TopkOut& o) {
+template <int kPer>
+__device__ void topk_token_wave_t(const float* __restrict__ selection, const float* __restrict__ scores, int E, int k,
+                                  float route_scale, int t, const TopkOut& o) {
   const int lane = threadIdx.x & 63;
-  constexpr int kPer = kMaxExperts / 64;
-  const int per = (E + 63) / 64;
+  const int per = kPer;
   uint32_t key[kPer];
   float sel[kPer];
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
     const int e = lane * per + j;
-    const bool ok = j < per && e < E;
+    const bool ok = e < E;
     sel[j] = ok ? selection[e] : 0.f;
     key[j] = ok ? ordered_key(sel[j]) : 0u;
   }
@@ -135,7 +180,7 @@ __device__ void topk_token_wave(const float* __restrict__ selection, const float
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
       const int e = lane * per + j;
-      if (j < per && e < E && (uint64_t)key[j] < bound && (!any || key[j] > m)) { m = key[j]; any = true; }
+      if (e < E && (uint64_t)key[j] < bound && (!any || key[j] > m)) { m = key[j]; any = true; }
     }
     // lanes without a candidate contribute key 0; a real key 0 (-NaN pattern) is excluded upstream
     const uint32_t best = wave_max_u(any ? m : 0u);
@@ -143,7 +188,7 @@ __device__ void topk_token_wave(const float* __restrict__ selection, const float
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
       const int e = lane * per + j;
-      c += (j < per && e < E && key[j] == best) ? 1 : 0;
+      c += (e < E && key[j] == best) ? 1 : 0;
     }
     c = wave_sum_i(c);
     tied |= c >= 2;
@@ -157,14 +202,14 @@ __device__ void topk_token_wave(const float* __restrict__ selection, const float
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
     const int e = lane * per + j;
-    if (j < per && e < E) {
+    if (e < E) {
       n_gt += key[j] > thr;
       n_eq += key[j] == thr;
     }
   }
   const int inc_gt = wave_scan_i(n_gt, lane);
   const int inc_eq = wave_scan_i(n_eq, lane);
-  const int total_gt = __shfl(inc_gt, 63, 64);
+  const int total_gt = __builtin_amdgcn_readlane(inc_gt, 63);
   int pos_gt = inc_gt - n_gt, pos_eq = total_gt + inc_eq - n_eq;
   __shared__ float s_key[4][32];
   __shared__ int32_t s_id[4][32];
@@ -172,7 +217,7 @@ __device__ void topk_token_wave(const float* __restrict__ selection, const float
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
     const int e = lane * per + j;
-    if (j < per && e < E) {
+    if (e < E) {
       if (key[j] > thr) {
         if (pos_gt < k) { s_key[wave][pos_gt] = sel[j]; s_id[wave][pos_gt] = e; }
         ++pos_gt;
@@ -190,22 +235,21 @@ __device__ void topk_token_wave(const float* __restrict__ selection, const float
   float kv = slot < k ? s_key[wave][slot] : 0.f;
   int32_t iv = slot < k ? s_id[wave][slot] : 0;
   int vv = slot < k;
-#pragma unroll
-  for (int size = 2; size <= 32; size <<= 1) {
-#pragma unroll
-    for (int stride = size >> 1; stride >= 1; stride >>= 1) {
-      const float pk = __shfl_xor(kv, stride, 32);
-      const int32_t pi = __shfl_xor(iv, stride, 32);
-      const int pv = __shfl_xor(vv, stride, 32);
-      const bool lower = (slot & stride) == 0;
-      const int lo = lower ? slot : (slot ^ stride);
-      const float klo = lower ? kv : pk, khi = lower ? pk : kv;
-      const int vlo = lower ? vv : pv, vhi = lower ? pv : vv;
-      const bool promote = (klo > khi && vlo) || !vhi;
-      const bool dir = size < 32 ? (lo & size) != 0 : false;
-      if (promote == dir) { kv = pk; iv = pi; vv = pv; }
-    }
-  }
+  bitonic_stage<2, 1>(kv, iv, vv, slot);
+  bitonic_stage<4, 2>(kv, iv, vv, slot);
+  bitonic_stage<4, 1>(kv, iv, vv, slot);
+  bitonic_stage<8, 4>(kv, iv, vv, slot);
+  bitonic_stage<8, 2>(kv, iv, vv, slot);
+  bitonic_stage<8, 1>(kv, iv, vv, slot);
+  bitonic_stage<16, 8>(kv, iv, vv, slot);
+  bitonic_stage<16, 4>(kv, iv, vv, slot);
+  bitonic_stage<16, 2>(kv, iv, vv, slot);
+  bitonic_stage<16, 1>(kv, iv, vv, slot);
+  bitonic_stage<32, 16>(kv, iv, vv, slot);
+  bitonic_stage<32, 8>(kv, iv, vv, slot);
+  bitonic_stage<32, 4>(kv, iv, vv, slot);
+  bitonic_stage<32, 2>(kv, iv, vv, slot);
+  bitonic_stage<32, 1>(kv, iv, vv, slot);
   // 4. raw scores, tree denominator, weights
   float raw = slot < k ? scores[iv] : 0.f;
   float acc = raw;
@@ -213,11 +257,15 @@ __device__ void topk_token_wave(const float* __restrict__ selection, const float
   while (width < k) width <<= 1;
   int present = k;
   for (int stride = width >> 1; stride >= 1; stride >>= 1) {
-    const float other = __shfl_down(acc, stride, 32);
+    // lanes below `stride` read lane + stride, which is lane ^ stride for them
+    const int bits = __float_as_int(acc);
+    const int ob = stride == 16 ? swizzle_xor<16>(bits) : stride == 8 ? swizzle_xor<8>(bits)
+                 : stride == 4 ? swizzle_xor<4>(bits) : stride == 2 ? swizzle_xor<2>(bits) : swizzle_xor<1>(bits);
+    const float other = __int_as_float(ob);
     if (slot < stride && slot + stride < present) acc = acc + other;
     present = present < stride ? present : stride;
   }
-  const float den = __shfl(acc, 0, 32) + 1e-20f;
+  const float den = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 0)) + 1e-20f;
   if (lane < k) {
     const float w = (raw / den) * route_scale;
     o.indices[t * k + lane] = iv;
@@ -230,103 +278,116 @@ __device__ void topk_token_wave(const float* __restrict__ selection, const float
   }
 }
 
+// Experts are spread kPer per lane (E <= 64 * kPer); the smallest power-of-two kPer keeps the
+// per-lane loops short for E = 256 (4 per lane).
+__device__ __forceinline__ void topk_token_wave(const float* __restrict__ selection, const float* __restrict__ scores,
+                                                int E, int k, float route_scale, int t, const TopkOut& o) {
+  if (E <= 64) topk_token_wave_t<1>(selection, scores, E, k, route_scale, t, o);
+  else if (E <= 128) topk_token_wave_t<2>(selection, scores, E, k, route_scale, t, o);
+  else if (E <= 256) topk_token_wave_t<4>(selection, scores, E, k, route_scale, t, o);
+  else if (E <= 512) topk_token_wave_t<8>(selection, scores, E, k, route_scale, t, o);
+  else topk_token_wave_t<16>(selection, scores, E, k, route_scale, t, o);
+}
+
 // ----------------------------------------------------------------------------------------------
 // Plan from the routed IDs (participation, moe.py:18-30): slots are the distinct experts in ascending
 // ID order, each with its tokens ascending; rows are numbered expert-major; the shared expert is the
-// last slot with every token. Executed by one 256-thread workgroup.
+// last slot with every token. One 256-thread workgroup, all steps parallel (LDS atomics for counts,
+// wavefront scans for slot and row offsets).
+__device__ __forceinline__ int block_exclusive_scan(int v, int tid, int* wave_tot, int* total) {
+  const int lane = tid & 63, wave = tid >> 6;
+  const int inc = wave_scan_i(v, lane);
+  if (lane == 63) wave_tot[wave] = inc;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += wave_tot[w];
+  *total = wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3];
+  __syncthreads();
+  return base + inc - v;
+}
+
 __device__ void build_plan(Plan* __restrict__ plan, const int32_t* __restrict__ ids, const float* __restrict__ w,
                            int T, int k, int E, int has_shared) {
+  __shared__ int32_t s_ids[kMaxTokens * kMaxTopK];
+  __shared__ int32_t s_row[kMaxTokens * kMaxTopK];
   __shared__ int32_t cnt[kMaxExperts];
   __shared__ int32_t slot_of[kMaxExperts];
   __shared__ int32_t row_of[kMaxExperts];
-  __shared__ int32_t part[256][2];
+  __shared__ int32_t wave_tot[2][4];
   const int tid = threadIdx.x;
+  const int n = T * k;
+  for (int i = tid; i < n; i += 256) s_ids[i] = ids[i];
   for (int e = tid; e < E; e += 256) cnt[e] = 0;
   __syncthreads();
-  for (int i = tid; i < T * k; i += 256) atomicAdd(&cnt[ids[i]], 1);
+  for (int i = tid; i < n; i += 256) atomicAdd(&cnt[s_ids[i]], 1);
   __syncthreads();
-  // block-exclusive scans of (cnt > 0) and cnt over experts; thread tid owns experts [tid*per, ...)
+  // slot and row offsets: thread tid owns experts [tid*per, tid*per + per)
   const int per = (E + 255) / 256;
   int ns = 0, nr = 0;
   for (int j = 0; j < per; ++j) {
     const int e = tid * per + j;
     if (e < E) { ns += cnt[e] > 0; nr += cnt[e]; }
   }
-  part[tid][0] = ns;
-  part[tid][1] = nr;
-  __syncthreads();
-  if (tid == 0) {
-    int a = 0, b = 0;
-    for (int i = 0; i < 256; ++i) {
-      const int x = part[i][0], y = part[i][1];
-      part[i][0] = a;
-      part[i][1] = b;
-      a += x;
-      b += y;
+  int n_routed = 0, routed_rows = 0;
+  int slot = block_exclusive_scan(ns, tid, wave_tot[0], &n_routed);
+  int row = block_exclusive_scan(nr, tid, wave_tot[1], &routed_rows);
+  for (int j = 0; j < per; ++j) {
+    const int e = tid * per + j;
+    if (e < E) {
+      slot_of[e] = slot;
+      row_of[e] = row;
+      if (cnt[e] > 0) {
+        plan->slot_expert[slot] = e;
+        plan->slot_ntok[slot] = cnt[e];
+        plan->slot_row0[slot] = row;
+        plan->slot_weighted[slot] = 1;
+        ++slot;
+        row += cnt[e];
+      }
     }
-    plan->n_routed = a;
-    plan->n_slots = a + has_shared;
-    plan->total_rows = b + (has_shared ? T : 0);
+  }
+  if (tid == 0) {
+    plan->n_routed = n_routed;
+    plan->n_slots = n_routed + has_shared;
+    plan->total_rows = routed_rows + (has_shared ? T : 0);
     plan->tokens = T;
     plan->top_k = k;
   }
   __syncthreads();
-  {
-    int s = part[tid][0], r = part[tid][1];
-    for (int j = 0; j < per; ++j) {
-      const int e = tid * per + j;
-      if (e < E) {
-        slot_of[e] = s;
-        row_of[e] = r;
-        if (cnt[e] > 0) {
-          plan->slot_expert[s] = e;
-          plan->slot_ntok[s] = cnt[e];
-          plan->slot_row0[s] = r;
-          plan->slot_weighted[s] = 1;
-          ++s;
-          r += cnt[e];
-        }
-      }
-    }
+  // each routed pair (t, i): its position among expert e's tokens = tokens t' < t routed to e
+  for (int idx = tid; idx < n; idx += 256) {
+    const int t = idx / k, e = s_ids[idx];
+    int before = 0;
+    for (int u = 0; u < t * k; ++u) before += s_ids[u] == e;
+    const int sl = slot_of[e];
+    plan->slot_tok[sl][before] = t;
+    plan->slot_w[sl][before] = w[idx];
+    s_row[idx] = row_of[e] + before;
   }
   __syncthreads();
-  // token lists (ascending) and each token's rows in ascending expert order
-  for (int t = tid; t < T; t += 256) {
+  // each token's rows in ascending expert order (insertion sort of k entries), shared row last
+  if (tid < T) {
+    const int t = tid;
     int32_t es[kMaxTopK], rs[kMaxTopK];
     for (int i = 0; i < k; ++i) {
-      const int e = ids[t * k + i];
-      int before = 0;   // tokens t' < t routed to e
-      for (int u = 0; u < t; ++u)
-        for (int j = 0; j < k; ++j) before += ids[u * k + j] == e;
-      const int s = slot_of[e];
-      plan->slot_tok[s][before] = t;
-      plan->slot_w[s][before] = w[t * k + i];
-      es[i] = e;
-      rs[i] = row_of[e] + before;
-    }
-    for (int i = 1; i < k; ++i) {   // insertion sort by expert ID
-      const int e = es[i], r = rs[i];
+      const int e = s_ids[t * k + i], r = s_row[t * k + i];
       int j = i - 1;
       while (j >= 0 && es[j] > e) { es[j + 1] = es[j]; rs[j + 1] = rs[j]; --j; }
       es[j + 1] = e;
       rs[j + 1] = r;
     }
     for (int i = 0; i < k; ++i) plan->tok_rows[t][i] = rs[i];
-  }
-  __syncthreads();
-  if (has_shared) {
-    const int s = plan->n_routed;
-    for (int t = tid; t < T; t += 256) {
-      plan->slot_tok[s][t] = t;
-      plan->slot_w[s][t] = 1.0f;
+    if (has_shared) {
+      plan->slot_tok[n_routed][t] = t;
+      plan->slot_w[n_routed][t] = 1.0f;
       plan->tok_rows[t][k] = T * k + t;
     }
-    if (tid == 0) {
-      plan->slot_expert[s] = E;
-      plan->slot_ntok[s] = T;
-      plan->slot_row0[s] = T * k;
-      plan->slot_weighted[s] = 0;
-    }
+  }
+  if (has_shared && tid == 0) {
+    plan->slot_expert[n_routed] = E;
+    plan->slot_ntok[n_routed] = T;
+    plan->slot_row0[n_routed] = T * k;
+    plan->slot_weighted[n_routed] = 0;
   }
 }
 
@@ -382,26 +443,46 @@ __global__ __launch_bounds__(256) void router_kernel(RouterArgs a) {
 #pragma unroll
   for (int t = 0; t < kMaxTokens; ++t) acc[t] = 0.f;
   const float* wrow = a.W + (size_t)e * a.H;
-  for (int k0 = tid * 4; k0 < a.H; k0 += 1024) {
-    const float4 w = *reinterpret_cast<const float4*>(wrow + k0);
+  // All of this thread's W_r loads are issued before any FMA (kRouterKIter * 1024 >= H, checked on
+  // the host); x rows are then read four tokens at a time with their loads hoisted likewise.
+  float4 w[kRouterKIter];
 #pragma unroll
-    for (int t = 0; t < kMaxTokens; ++t) {
-      if (t < nt) {
-        const uint2 xb = *reinterpret_cast<const uint2*>(a.x + (size_t)(t0 + t) * a.H + k0);
-        acc[t] = fmaf(w.x, mx::bf16_value(xb.x & 0xFFFFu), acc[t]);
-        acc[t] = fmaf(w.y, mx::bf16_value(xb.x >> 16), acc[t]);
-        acc[t] = fmaf(w.z, mx::bf16_value(xb.y & 0xFFFFu), acc[t]);
-        acc[t] = fmaf(w.w, mx::bf16_value(xb.y >> 16), acc[t]);
-      }
+  for (int i = 0; i < kRouterKIter; ++i) {
+    const int k0 = tid * 4 + i * 1024;
+    w[i] = k0 < a.H ? *reinterpret_cast<const float4*>(wrow + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int t4 = 0; t4 < kMaxTokens; t4 += 4) {
+    if (t4 < nt) {
+      uint2 xb[4][kRouterKIter];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int i = 0; i < kRouterKIter; ++i) {
+          const int k0 = tid * 4 + i * 1024;
+          xb[u][i] = (t4 + u < nt && k0 < a.H) ? *reinterpret_cast<const uint2*>(a.x + (size_t)(t0 + t4 + u) * a.H + k0)
+                                               : make_uint2(0u, 0u);
+        }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int i = 0; i < kRouterKIter; ++i) {
+          float v = acc[t4 + u];
+          v = fmaf(w[i].x, mx::bf16_value(xb[u][i].x & 0xFFFFu), v);
+          v = fmaf(w[i].y, mx::bf16_value(xb[u][i].x >> 16), v);
+          v = fmaf(w[i].z, mx::bf16_value(xb[u][i].y & 0xFFFFu), v);
+          v = fmaf(w[i].w, mx::bf16_value(xb[u][i].y >> 16), v);
+          acc[t4 + u] = v;
+        }
     }
   }
   __shared__ float part[4][kMaxTokens];
 #pragma unroll
   for (int t = 0; t < kMaxTokens; ++t) {
-    float v = acc[t];
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-    if (lane == 0) part[wave][t] = v;
+    if (t < nt) {
+      const float v = wave_sum_f(acc[t]);
+      if (lane == 0) part[wave][t] = v;
+    }
   }
   // share the per-32 quantization of x (blocks of 32 handled by 32-lane halves)
   if (a.xq && blockIdx.y == 0) {
@@ -505,49 +586,147 @@ __device__ __forceinline__ v4f mfma_fp4xfp8(uint4 a, uint4 b0, uint4 b1, v4f c, 
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 4, 0, 0, sa, 0, sb);
 }
 
-// grid (I/32, slots), 256 threads. Wave w computes intermediate rows [32g+8w, +8) of W1 (MFMA rows
-// 0-7) and W3 (MFMA rows 8-15) for the slot's tokens, then the workgroup applies the SwiGLU epilogue
-// and quantizes its 32-row block of the down input per token (the per-32 E4M3/E8M0 boundary).
+// ---- K-split streaming core shared by the gate/up and down kernels -------------------------------
+//
+// A workgroup of 4 waves owns 4 MFMA tiles of 16 weight rows. Wave w walks its own contiguous quarter
+// of the 128-wide K chunks and multiplies every chunk into all 4 tiles, so one load of the activation
+// operand serves 4 MFMAs.
+// Loads run P chunks ahead of the MFMAs (a register ring unrolled so every index is static), which
+// keeps P * 4 KB of weights in flight per wave. The 4 partial accumulators per tile are then summed
+// in a fixed wave order through LDS, so results do not depend on scheduling.
+constexpr int kTiles = 4;
+
+struct ChunkRegs {
+  uint4 wa[kTiles];
+  uint32_t sw[kTiles];
+  uint4 b0, b1;
+  uint32_t sx;
+};
+
+struct StreamOperands {
+  const uint8_t* wrow[kTiles];   // this lane's weight row of each tile (packed E2M1)
+  const uint8_t* srow[kTiles];   // and its E8M0 scale row
+  const uint8_t* xrow;           // this lane's token row of E4M3 activations
+  const uint8_t* xsrow;          // and its E8M0 scales
+  bool live;                     // lane's token column is in use
+};
+
+// Loads through the global address space (the pointers come from a device table, so the compiler
+// cannot infer it and would otherwise emit flat loads).
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t ldg32(const uint8_t* p) {
+  return *(const __attribute__((address_space(1))) uint32_t*)(p);
+}
+
+__device__ __forceinline__ uint4 ldg128(const uint8_t* p) {
+  const u32x4_t v = *(const __attribute__((address_space(1))) u32x4_t*)(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ void load_chunk(ChunkRegs& r, const StreamOperands& o, int c, int q) {
+  const int kb = 4 * c + q;
+#pragma unroll
+  for (int t = 0; t < kTiles; ++t) {
+    r.wa[t] = ldg128(o.wrow[t] + (size_t)kb * 16);
+    r.sw[t] = ldg32(o.srow[t] + 4 * c);
+  }
+  // Idle token columns read a valid row too (no divergent branch around the loads, which would
+  // force the operands through scratch); mma_chunk zeroes them, and their outputs are dropped.
+  const uint8_t* chunk = o.xrow + (size_t)c * 128;
+  r.b0 = ldg128(chunk + 16 * q);
+  r.b1 = ldg128(chunk + 64 + 16 * q);
+  r.sx = ldg32(o.xsrow + 4 * c);
+}
+
+__device__ __forceinline__ void mma_chunk(const ChunkRegs& r, v4f (&acc)[kTiles], int q, uint32_t keep) {
+  const int sx = (int)((r.sx >> (8 * q)) & 0xFF);
+  const uint4 b0 = make_uint4(r.b0.x & keep, r.b0.y & keep, r.b0.z & keep, r.b0.w & keep);
+  const uint4 b1 = make_uint4(r.b1.x & keep, r.b1.y & keep, r.b1.z & keep, r.b1.w & keep);
+#pragma unroll
+  for (int t = 0; t < kTiles; ++t) acc[t] = mfma_fp4xfp8(r.wa[t], b0, b1, acc[t], (int)((r.sw[t] >> (8 * q)) & 0xFF), sx);
+}
+
+template <int P>
+__device__ __forceinline__ void stream_ksplit(const StreamOperands& o, int chunks, int wave, int q, v4f (&acc)[kTiles]) {
+#pragma unroll
+  for (int t = 0; t < kTiles; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+  // wave w reads the contiguous chunk range [c0, c0 + n): every 128-byte line of a row is fetched by
+  // one wave in consecutive loads
+  const int c0 = (chunks * wave) / 4;
+  const int n = (chunks * (wave + 1)) / 4 - c0;
+  if (n == 0) return;
+  const uint32_t live = o.live ? 0xFFFFFFFFu : 0u;
+  ChunkRegs buf[P];
+#pragma unroll
+  for (int j = 0; j < P; ++j) load_chunk(buf[j], o, c0 + min(j, n - 1), q);
+  // Steady state: consume P chunks and refill them P ahead, with no per-chunk branches so the
+  // waitcnt pass can keep the refills in flight. Slots past the end repeat the last chunk (an L2
+  // hit) and are masked to zero.
+  int i = 0;
+  for (; i + P < n; i += P) {
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+      mma_chunk(buf[j], acc, q, live);
+      load_chunk(buf[j], o, c0 + min(i + j + P, n - 1), q);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < P; ++j) mma_chunk(buf[j], acc, q, i + j < n ? live : 0u);
+}
+
+// Sum the 4 waves' partial tiles in wave order; wave w returns tile w's accumulator.
+__device__ __forceinline__ v4f reduce_tiles(const v4f (&acc)[kTiles], int wave, int lane, float (*red)[kTiles][64][4]) {
+#pragma unroll
+  for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][t][lane][i] = acc[t][i];
+  __syncthreads();
+  v4f out;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    out[i] = ((red[0][wave][lane][i] + red[1][wave][lane][i]) + red[2][wave][lane][i]) + red[3][wave][lane][i];
+  return out;
+}
+
+// grid (I/32, slots), 256 threads. The workgroup computes intermediate rows [32g, 32g + 32) of W1 and
+// W3 for the slot's tokens: tile t holds W1 rows 32g + 8t + (0..7) as MFMA rows 0-7 and the same W3
+// rows as MFMA rows 8-15. After the cross-wave sum, wave t owns tile t, applies the SwiGLU epilogue,
+// and the workgroup quantizes its 32-row block of the down input per token (one E8M0 block).
 __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
   const Plan* __restrict__ plan = a.plan;
   const int s = blockIdx.y;
   if (s >= plan->n_slots) return;
   const int g = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int m = lane & 15, q = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int m = lane & 15, q = lane >> 4, n = lane & 15;
   const int ntok = plan->slot_ntok[s];
-  const int expert = plan->slot_expert[s];
-  const mx_expert_ptrs p = a.table ? a.table[expert] : a.single;
+  const mx_expert_ptrs p = a.table ? a.table[plan->slot_expert[s]] : a.single;
   const int H = a.H, I = a.I;
-  const int row = g * 32 + wave * 8 + (m & 7);
+  StreamOperands o;
   const bool up = m >= 8;
-  const uint8_t* __restrict__ wrow = (const uint8_t*)(up ? p.w3_weight : p.w1_weight) + (size_t)row * (H / 2);
-  const uint8_t* __restrict__ srow = (const uint8_t*)(up ? p.w3_scale : p.w1_scale) + (size_t)row * (H / 32);
-  const int n = lane & 15;
-  const int tok = n < ntok ? plan->slot_tok[s][n] : -1;
-  const uint8_t* __restrict__ xrow = a.xq + (size_t)(tok < 0 ? 0 : tok) * H;
-  const uint8_t* __restrict__ xsrow = a.xs + (size_t)(tok < 0 ? 0 : tok) * (H / 32);
-  v4f acc = {0.f, 0.f, 0.f, 0.f};
-  const int chunks = H / 128;
-  const uint4 zero = {0u, 0u, 0u, 0u};
-#pragma unroll 4
-  for (int c = 0; c < chunks; ++c) {
-    const int kb = 4 * c + q;
-    const uint4 wa = *reinterpret_cast<const uint4*>(wrow + (size_t)kb * 16);
-    const uint32_t sw = *reinterpret_cast<const uint32_t*>(srow + 4 * c);
-    uint4 b0 = zero, b1 = zero;
-    uint32_t sx = 0x7F7F7F7Fu;
-    if (tok >= 0) {
-      load_b_operand(xrow + (size_t)c * 128, q, b0, b1);
-      sx = *reinterpret_cast<const uint32_t*>(xsrow + 4 * c);
-    }
-    acc = mfma_fp4xfp8(wa, b0, b1, acc, (int)((sw >> (8 * q)) & 0xFF), (int)((sx >> (8 * q)) & 0xFF));
+  const uint8_t* wbase = (const uint8_t*)(up ? p.w3_weight : p.w1_weight);
+  const uint8_t* sbase = (const uint8_t*)(up ? p.w3_scale : p.w1_scale);
+#pragma unroll
+  for (int t = 0; t < kTiles; ++t) {
+    const int row = g * 32 + t * 8 + (m & 7);
+    o.wrow[t] = wbase + (size_t)row * (H / 2);
+    o.srow[t] = sbase + (size_t)row * (H / 32);
   }
-  // D[4q + i][n]: lanes q < 2 hold W1 rows 4q+i; lane + 32 holds the W3 rows with the same index.
+  o.live = n < ntok;
+  const int tok = o.live ? plan->slot_tok[s][n] : 0;
+  o.xrow = a.xq + (size_t)tok * H;
+  o.xsrow = a.xs + (size_t)tok * (H / 32);
+  v4f acc[kTiles];
+  stream_ksplit<3>(o, H / 128, wave, q, acc);
+  __shared__ float red[4][kTiles][64][4];
   __shared__ float s_din[kMaxTokens][32];
+  const v4f mine = reduce_tiles(acc, wave, lane, red);
+  // D[4q + i][n] of tile `wave`: lanes q < 2 hold W1 rows 4q+i; lane + 32 holds the matching W3 rows.
   float upv[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) upv[i] = __shfl_xor(acc[i], 32, 64);
+  for (int i = 0; i < 4; ++i) upv[i] = __shfl_xor(mine[i], 32, 64);
   if (q < 2 && n < ntok) {
     const int row0 = plan->slot_row0[s];
     const bool weighted = plan->slot_weighted[s] != 0;
@@ -556,7 +735,7 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
     for (int i = 0; i < 4; ++i) {
       const int li = wave * 8 + 4 * q + i;        // row within the 32-row block
       const int gi = g * 32 + li;                 // intermediate index
-      const uint32_t b1 = mx::bf16_bits(acc[i]);
+      const uint32_t b1 = mx::bf16_bits(mine[i]);
       const uint32_t b3 = mx::bf16_bits(upv[i]);
       float gate = mx::bf16_value(b1), upf = mx::bf16_value(b3);
       if (a.limit > 0.f) {
@@ -569,12 +748,12 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
       const float routed = weighted ? rw * product : product;
       const float din = mx::bf16_round(routed);
       s_din[n][li] = din;
-      const size_t o = (size_t)(row0 + n) * I + gi;
-      if (a.w1) a.w1[o] = (uint16_t)b1;
-      if (a.w3) a.w3[o] = (uint16_t)b3;
-      if (a.din) a.din[o] = (uint16_t)mx::bf16_bits(din);
+      const size_t o2 = (size_t)(row0 + n) * I + gi;
+      if (a.w1) a.w1[o2] = (uint16_t)b1;
+      if (a.w3) a.w3[o2] = (uint16_t)b3;
+      if (a.din) a.din[o2] = (uint16_t)mx::bf16_bits(din);
       if (a.trace) {
-        float* tr = a.trace + o * 5;
+        float* tr = a.trace + o2 * 5;
         tr[0] = gate; tr[1] = upf; tr[2] = silu; tr[3] = product; tr[4] = routed;
       }
     }
@@ -597,45 +776,38 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
   }
 }
 
-// grid (H/64, slots), 256 threads; wave w computes 16 output rows [64b + 16w, +16) of W2 for the slot's
-// tokens and writes them as BF16 (the reference's w2 stage).
+// grid (H/64, slots), 256 threads: output rows [64b, 64b + 64) of W2 as 4 tiles of 16 rows; after
+// the cross-wave sum wave t writes tile t as BF16 (the reference's w2 stage).
 __global__ __launch_bounds__(256) void down_kernel(ExpertArgs a) {
   const Plan* __restrict__ plan = a.plan;
   const int s = blockIdx.y;
   if (s >= plan->n_slots) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int m = lane & 15, q = lane >> 4, n = lane & 15;
   const int ntok = plan->slot_ntok[s];
   const int row0 = plan->slot_row0[s];
   const mx_expert_ptrs p = a.table ? a.table[plan->slot_expert[s]] : a.single;
   const int H = a.H, I = a.I;
-  const int h0 = blockIdx.x * 64 + wave * 16;
-  const uint8_t* __restrict__ wrow = (const uint8_t*)p.w2_weight + (size_t)(h0 + m) * (I / 2);
-  const uint8_t* __restrict__ srow = (const uint8_t*)p.w2_scale + (size_t)(h0 + m) * (I / 32);
-  const bool live = n < ntok;
-  const uint8_t* __restrict__ xrow = a.dq + (size_t)(row0 + (live ? n : 0)) * I;
-  const uint8_t* __restrict__ xsrow = a.ds + (size_t)(row0 + (live ? n : 0)) * (I / 32);
-  v4f acc = {0.f, 0.f, 0.f, 0.f};
-  const uint4 zero = {0u, 0u, 0u, 0u};
-  const int chunks = I / 128;
-#pragma unroll 4
-  for (int c = 0; c < chunks; ++c) {
-    const int kb = 4 * c + q;
-    const uint4 wa = *reinterpret_cast<const uint4*>(wrow + (size_t)kb * 16);
-    const uint32_t sw = *reinterpret_cast<const uint32_t*>(srow + 4 * c);
-    uint4 b0 = zero, b1 = zero;
-    uint32_t sx = 0x7F7F7F7Fu;
-    if (live) {
-      load_b_operand(xrow + (size_t)c * 128, q, b0, b1);
-      sx = *reinterpret_cast<const uint32_t*>(xsrow + 4 * c);
-    }
-    acc = mfma_fp4xfp8(wa, b0, b1, acc, (int)((sw >> (8 * q)) & 0xFF), (int)((sx >> (8 * q)) & 0xFF));
+  const int hb = blockIdx.x * 64;
+  StreamOperands o;
+#pragma unroll
+  for (int t = 0; t < kTiles; ++t) {
+    o.wrow[t] = (const uint8_t*)p.w2_weight + (size_t)(hb + 16 * t + m) * (I / 2);
+    o.srow[t] = (const uint8_t*)p.w2_scale + (size_t)(hb + 16 * t + m) * (I / 32);
   }
-  if (live) {
+  o.live = n < ntok;
+  o.xrow = a.dq + (size_t)(row0 + (o.live ? n : 0)) * I;
+  o.xsrow = a.ds + (size_t)(row0 + (o.live ? n : 0)) * (I / 32);
+  v4f acc[kTiles];
+  stream_ksplit<4>(o, I / 128, wave, q, acc);
+  __shared__ float red[4][kTiles][64][4];
+  const v4f mine = reduce_tiles(acc, wave, lane, red);
+  if (n < ntok) {
     uint2 packed;
-    packed.x = mx::bf16_bits(acc[0]) | (mx::bf16_bits(acc[1]) << 16);
-    packed.y = mx::bf16_bits(acc[2]) | (mx::bf16_bits(acc[3]) << 16);
-    *reinterpret_cast<uint2*>(a.out + (size_t)(row0 + n) * H + h0 + 4 * q) = packed;
+    packed.x = mx::bf16_bits(mine[0]) | (mx::bf16_bits(mine[1]) << 16);
+    packed.y = mx::bf16_bits(mine[2]) | (mx::bf16_bits(mine[3]) << 16);
+    *reinterpret_cast<uint2*>(a.out + (size_t)(row0 + n) * H + hb + 16 * wave + 4 * q) = packed;
   }
 }
 
@@ -726,9 +898,12 @@ struct mx_layer {
   uint32_t* counter = nullptr;
   int max_rows = 0;
   std::vector<std::pair<void*, uint64_t>> allocs;
-  // profiling
+  // profiling: events bracket each kernel of a call; a ring of kProfRing calls is recorded without
+  // host synchronisation and folded into the totals when full or when the profile is read.
+  static constexpr int kProfRing = 64;
   bool profile = false;
-  hipEvent_t ev[5] = {};
+  std::vector<hipEvent_t> ev;   // kProfRing * 5
+  int pending = 0;
   double stage_ms[4] = {0, 0, 0, 0};
   int profiled_calls = 0;
 };
@@ -756,11 +931,27 @@ void layer_release(mx_layer* L) {
   L->allocs.clear();
   for (auto& e : L->ev)
     if (e) (void)hipEventDestroy(e);
+  L->ev.clear();
+}
+
+int profile_flush(mx_layer* L) {
+  if (!L->pending) return MX_OK;
+  MX_HIP(hipEventSynchronize(L->ev[(L->pending - 1) * 5 + 4]));
+  for (int c = 0; c < L->pending; ++c)
+    for (int i = 0; i < 4; ++i) {
+      float ms = 0.f;
+      MX_HIP(hipEventElapsedTime(&ms, L->ev[c * 5 + i], L->ev[c * 5 + i + 1]));
+      L->stage_ms[i] += ms;
+    }
+  L->profiled_calls += L->pending;
+  L->pending = 0;
+  return MX_OK;
 }
 
 int validate_config(const mx_moe_config* c) {
   MX_REQUIRE(c != nullptr, "mx_layer_create: null config");
-  MX_REQUIRE(c->hidden > 0 && c->hidden % 128 == 0, "hidden size must be a positive multiple of 128");
+  MX_REQUIRE(c->hidden > 0 && c->hidden % 128 == 0 && c->hidden <= kRouterKIter * 1024,
+             "hidden size must be a positive multiple of 128, at most %d", kRouterKIter * 1024);
   MX_REQUIRE(c->intermediate > 0 && c->intermediate % 128 == 0,
              "intermediate size must be a positive multiple of 128");
   MX_REQUIRE(c->experts >= 1 && c->experts <= kMaxExperts, "experts must be in [1, %d]", kMaxExperts);
@@ -895,11 +1086,14 @@ int mx_layer_buffer(mx_layer* L, int32_t which, void** dptr, uint64_t* bytes) {
 int mx_layer_profile(mx_layer* L, int32_t enable, float* stage_ms, int32_t* calls) {
   MX_REQUIRE(L != nullptr, "layer is closed");
   if (int s = use(L->ctx)) return s;
+  if (int s = profile_flush(L)) return s;
   if (stage_ms)
     for (int i = 0; i < 4; ++i) stage_ms[i] = L->profiled_calls ? (float)(L->stage_ms[i] / L->profiled_calls) : 0.f;
   if (calls) *calls = L->profiled_calls;
-  if (enable && !L->ev[0])
+  if (enable && L->ev.empty()) {
+    L->ev.assign(mx_layer::kProfRing * 5, nullptr);
     for (auto& e : L->ev) MX_HIP(hipEventCreate(&e));
+  }
   if (enable) {
     for (auto& v : L->stage_ms) v = 0;
     L->profiled_calls = 0;
@@ -917,7 +1111,13 @@ int mx_moe_decode(mx_layer* L, const uint16_t* x, int32_t T, uint16_t* y, int32_
   MX_REQUIRE(x && y && aligned(x, 16) && aligned(y, 16), "x and y must be 16-byte aligned device pointers");
   hipStream_t st = as_stream(stream);
   const bool prof = L->profile;
-  if (prof) MX_HIP(hipEventRecord(L->ev[0], st));
+  hipEvent_t* ev = nullptr;
+  if (prof) {
+    if (L->pending == mx_layer::kProfRing)
+      if (int s2 = profile_flush(L)) return s2;
+    ev = &L->ev[L->pending * 5];
+    MX_HIP(hipEventRecord(ev[0], st));
+  }
   RouterArgs r{};
   r.W = L->router_weight;
   r.bias = L->bias;
@@ -939,7 +1139,7 @@ int mx_moe_decode(mx_layer* L, const uint16_t* x, int32_t T, uint16_t* y, int32_
   r.has_shared = L->has_shared;
   hipLaunchKernelGGL(router_kernel, dim3(c.experts, 1), dim3(256), 0, st, r);
   MX_LAUNCH_CHECK("router_kernel");
-  if (prof) MX_HIP(hipEventRecord(L->ev[1], st));
+  if (prof) MX_HIP(hipEventRecord(ev[1], st));
   ExpertArgs a{};
   a.table = L->table;
   a.plan = L->plan;
@@ -960,22 +1160,16 @@ int mx_moe_decode(mx_layer* L, const uint16_t* x, int32_t T, uint16_t* y, int32_
   const int slots = std::min(c.experts, T * c.top_k) + L->has_shared;
   hipLaunchKernelGGL(gateup_kernel, dim3(c.intermediate / 32, slots), dim3(256), 0, st, a);
   MX_LAUNCH_CHECK("gateup_kernel");
-  if (prof) MX_HIP(hipEventRecord(L->ev[2], st));
+  if (prof) MX_HIP(hipEventRecord(ev[2], st));
   hipLaunchKernelGGL(down_kernel, dim3(c.hidden / 64, slots), dim3(256), 0, st, a);
   MX_LAUNCH_CHECK("down_kernel");
-  if (prof) MX_HIP(hipEventRecord(L->ev[3], st));
+  if (prof) MX_HIP(hipEventRecord(ev[3], st));
   hipLaunchKernelGGL(combine_kernel, dim3((c.hidden / 8 + 255) / 256, T), dim3(256), 0, st, (const Plan*)L->plan,
                      (const uint16_t*)L->eout, c.hidden, c.top_k, L->has_shared, y);
   MX_LAUNCH_CHECK("combine_kernel");
   if (prof) {
-    MX_HIP(hipEventRecord(L->ev[4], st));
-    MX_HIP(hipEventSynchronize(L->ev[4]));
-    for (int i = 0; i < 4; ++i) {
-      float ms = 0.f;
-      MX_HIP(hipEventElapsedTime(&ms, L->ev[i], L->ev[i + 1]));
-      L->stage_ms[i] += ms;
-    }
-    ++L->profiled_calls;
+    MX_HIP(hipEventRecord(ev[4], st));
+    ++L->pending;
   }
   return MX_OK;
 }
@@ -1085,7 +1279,8 @@ static int router_common(mx_ctx* ctx, int T, int E, int k, int score_func, float
 int mx_router(mx_ctx* ctx, const float* W, const float* bias, const uint16_t* x, int32_t T, int32_t H, int32_t E,
               int32_t k, int32_t score_func, float route_scale, const mx_router_out* out, void* stream) {
   if (int s = router_common(ctx, T, E, k, score_func, route_scale, out)) return s;
-  MX_REQUIRE(H > 0 && H % 4 == 0, "hidden size must be a positive multiple of 4");
+  MX_REQUIRE(H > 0 && H % 4 == 0 && H <= kRouterKIter * 1024, "hidden size must be a positive multiple of 4, at most %d",
+             kRouterKIter * 1024);
   MX_REQUIRE(out->logits != nullptr, "router logits output is required");
   MX_REQUIRE(W && x && aligned(W, 16) && aligned(x, 8), "W must be 16-byte and x 8-byte aligned");
   if (!T) return MX_OK;
@@ -1123,7 +1318,8 @@ int mx_router(mx_ctx* ctx, const float* W, const float* bias, const uint16_t* x,
 int mx_gate_project(mx_ctx* ctx, const float* W, const uint16_t* x, int32_t T, int32_t H, int32_t E, float* logits,
                     void* stream) {
   if (int s = use(ctx)) return s;
-  MX_REQUIRE(T >= 0 && H > 0 && H % 4 == 0, "hidden size must be a positive multiple of 4");
+  MX_REQUIRE(T >= 0 && H > 0 && H % 4 == 0 && H <= kRouterKIter * 1024,
+             "hidden size must be a positive multiple of 4, at most %d", kRouterKIter * 1024);
   MX_REQUIRE(E >= 1, "experts must be positive");
   if (!T) return MX_OK;
   MX_REQUIRE(W && x && logits && aligned(W, 16) && aligned(x, 8), "W must be 16-byte and x 8-byte aligned");
