@@ -128,6 +128,26 @@ int mx_expert_forward(mx_ctx* ctx, const mx_expert_ptrs* w, int32_t format, int3
                       const uint16_t* x_bf16, int32_t tokens, float swiglu_limit, const float* route_w,
                       uint16_t* y_bf16, const mx_expert_stages* stages, void* stream);
 
+/* ---- device-native expert layout ----
+ *
+ * The decode layer reads experts in a tiled layout chosen for the gfx950 scaled MFMA: per 128-wide
+ * K chunk, a group of 64 MFMA rows stores its four 16-row A operands as 4 consecutive KB (lane l's
+ * 16-byte MX block at 16*l), so every wave load is 1 KB of contiguous HBM, and one 4-byte word per
+ * lane carries that lane's E8M0 code for all four tiles. Gate/up groups interleave 32 W1 rows and
+ * the same 32 W3 rows (8 + 8 per tile) so the SwiGLU pair lands in one accumulator. Same byte count
+ * as the reference layout (1.59375 * H * I); conversion is bit-for-bit in both directions.
+ * The reference stores experts row-major (src/vesper/checkpoint.py:139-149, storage.py:33-41);
+ * these calls are the boundary between that store layout and the resident one. */
+
+/* Bytes of one tiled expert (0 if H or I is not a positive multiple of 128). */
+uint64_t mx_tiled_expert_bytes(int32_t hidden, int32_t intermediate);
+/* Reference layout (six device tensors) -> tiled blob (256-byte aligned device memory). */
+int mx_tile_expert(mx_ctx* ctx, const mx_expert_ptrs* ref, int32_t hidden, int32_t intermediate, void* tiled,
+                   void* stream);
+/* Tiled blob -> reference layout; writes through the six pointers of `ref`. */
+int mx_untile_expert(mx_ctx* ctx, const void* tiled, int32_t hidden, int32_t intermediate, const mx_expert_ptrs* ref,
+                     void* stream);
+
 /* ---- router (replaces GateProjection.project + RouterProbe, src/vesper/gate.py:133-147,
  *      src/vesper/router.py:227-264, routing_probe.cu:5-86) ---- */
 
@@ -186,15 +206,15 @@ typedef struct mx_moe_config {
   int32_t max_tokens;     /* decode batch capacity, <= 16 */
 } mx_moe_config;
 
-/* Register a layer: FP32 router weight [E][H], optional FP32 selection bias [E], E expert
- * pointer sets (host array, copied to a device table) and the optional shared expert. */
+/* Register a layer: FP32 router weight [E][H], optional FP32 selection bias [E], E tiled expert
+ * blobs (host array of device pointers, copied to a device table) and the optional shared expert. */
 int mx_layer_create(mx_ctx* ctx, const mx_moe_config* cfg, const float* router_weight, const float* bias,
-                    const mx_expert_ptrs* experts, const mx_expert_ptrs* shared, mx_layer** out);
+                    const void* const* experts_tiled, const void* shared_tiled, mx_layer** out);
 int mx_layer_destroy(mx_layer* layer);
-/* Re-point expert `expert` (e.g. after a cache slot fill); ordered on `stream`. */
-int mx_layer_set_expert(mx_layer* layer, int32_t expert, const mx_expert_ptrs* w, void* stream);
+/* Re-point expert `expert` to another tiled blob (e.g. after a cache slot fill); ordered on `stream`. */
+int mx_layer_set_expert(mx_layer* layer, int32_t expert, const void* tiled, void* stream);
 
-/* y[T][H] = MoE(x[T][H]) for 1 <= T <= max_tokens, inputs resident in HBM: router -> top-k plan ->
+/* y[T][H] = MoE(x[T][H]) for 1 <= T <= max_tokens, inputs resident in HBM: router -> top-k + plan ->
  * fused gate/up + SwiGLU + down-input quantization -> down -> ordered combine (shared last).
  * `diagnostics` != 0 also writes the per-stage buffers that mx_layer_buffer exposes. */
 int mx_moe_decode(mx_layer* layer, const uint16_t* x_bf16, int32_t tokens, uint16_t* y_bf16,

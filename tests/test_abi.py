@@ -44,3 +44,15 @@ def test_loader_reports_devices_without_failing_and_errors_map_to_python():
         with pytest.raises(ValueError):
             _lib.Context(0)
         assert "not present" in lib.last_error()
+
+
+def test_tiled_expert_size_is_the_reference_byte_count():
+    """mx_tiled_expert_bytes is host arithmetic (no device): same bytes as the six reference tensors."""
+    from vesper_amd import _lib
+    from vesper_amd.config import BASELINE, REFERENCE
+    lib = _lib.load()
+    for cfg in (BASELINE, REFERENCE):
+        assert lib.cdll.mx_tiled_expert_bytes(cfg.hidden, cfg.intermediate) == cfg.expert_bytes
+    assert lib.cdll.mx_tiled_expert_bytes(7168, 2048) == 23_396_352
+    for bad in ((100, 128), (128, 0), (-128, 128)):
+        assert lib.cdll.mx_tiled_expert_bytes(*bad) == 0

@@ -94,10 +94,12 @@ SIGNATURES = {
     "mx_acc_add_rows": ([_P, _P, _P, _P, _I32, _I32, _P], C.c_int),
     "mx_acc_add": ([_P, _P, _P, _I64, _P], C.c_int),
     "mx_acc_finish": ([_P, _P, _P, _I64, _P], C.c_int),
-    "mx_layer_create": ([_P, C.POINTER(MxMoeConfig), _P, _P, C.POINTER(MxExpertPtrs), C.POINTER(MxExpertPtrs),
-                         C.POINTER(_P)], C.c_int),
+    "mx_tiled_expert_bytes": ([_I32, _I32], _U64),
+    "mx_tile_expert": ([_P, C.POINTER(MxExpertPtrs), _I32, _I32, _P, _P], C.c_int),
+    "mx_untile_expert": ([_P, _P, _I32, _I32, C.POINTER(MxExpertPtrs), _P], C.c_int),
+    "mx_layer_create": ([_P, C.POINTER(MxMoeConfig), _P, _P, C.POINTER(_P), _P, C.POINTER(_P)], C.c_int),
     "mx_layer_destroy": ([_P], C.c_int),
-    "mx_layer_set_expert": ([_P, _I32, C.POINTER(MxExpertPtrs), _P], C.c_int),
+    "mx_layer_set_expert": ([_P, _I32, _P, _P], C.c_int),
     "mx_moe_decode": ([_P, _P, _I32, _P, _I32, _P], C.c_int),
     "mx_layer_buffer": ([_P, _I32, C.POINTER(_P), C.POINTER(_U64)], C.c_int),
     "mx_layer_profile": ([_P, _I32, C.POINTER(_F), C.POINTER(_I32)], C.c_int),

@@ -29,6 +29,8 @@ constexpr int kMaxTopK = 32;
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxSlots = kMaxTokens * kMaxTopK + 1;
 constexpr int kRouterKIter = 8;   // router GEMV: hidden size <= 8 * 1024 per thread-strided pass
+constexpr int kRouteThreads = 1024;             // top-k + plan workgroup: one wave per token
+constexpr int kRouteWaves = kRouteThreads / 64;
 
 // Device-side execution plan of one decode call (written by the router's last workgroup).
 struct Plan {
@@ -211,8 +213,8 @@ __device__ void topk_token_wave_t(const float* __restrict__ selection, const flo
   const int inc_eq = wave_scan_i(n_eq, lane);
   const int total_gt = __builtin_amdgcn_readlane(inc_gt, 63);
   int pos_gt = inc_gt - n_gt, pos_eq = total_gt + inc_eq - n_eq;
-  __shared__ float s_key[4][32];
-  __shared__ int32_t s_id[4][32];
+  __shared__ float s_key[kRouteWaves][32];
+  __shared__ int32_t s_id[kRouteWaves][32];
   const int wave = threadIdx.x >> 6;
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
@@ -292,37 +294,41 @@ __device__ __forceinline__ void topk_token_wave(const float* __restrict__ select
 // ----------------------------------------------------------------------------------------------
 // Plan from the routed IDs (participation, moe.py:18-30): slots are the distinct experts in ascending
 // ID order, each with its tokens ascending; rows are numbered expert-major; the shared expert is the
-// last slot with every token. One 256-thread workgroup, all steps parallel (LDS atomics for counts,
-// wavefront scans for slot and row offsets).
+// last slot with every token. Run by one workgroup of any multiple of 64 threads up to 1024, all
+// steps parallel (LDS atomics for counts, wavefront scans for slot and row offsets). `ids` and `w`
+// may live in LDS.
 __device__ __forceinline__ int block_exclusive_scan(int v, int tid, int* wave_tot, int* total) {
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
   const int inc = wave_scan_i(v, lane);
   if (lane == 63) wave_tot[wave] = inc;
   __syncthreads();
-  int base = 0;
-  for (int w = 0; w < wave; ++w) base += wave_tot[w];
-  *total = wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3];
+  int base = 0, all = 0;
+  for (int w = 0; w < nwaves; ++w) {
+    base += w < wave ? wave_tot[w] : 0;
+    all += wave_tot[w];
+  }
+  *total = all;
   __syncthreads();
   return base + inc - v;
 }
 
-__device__ void build_plan(Plan* __restrict__ plan, const int32_t* __restrict__ ids, const float* __restrict__ w,
-                           int T, int k, int E, int has_shared) {
+__device__ void build_plan(Plan* __restrict__ plan, const int32_t* ids, const float* w, int T, int k, int E,
+                           int has_shared) {
   __shared__ int32_t s_ids[kMaxTokens * kMaxTopK];
   __shared__ int32_t s_row[kMaxTokens * kMaxTopK];
   __shared__ int32_t cnt[kMaxExperts];
   __shared__ int32_t slot_of[kMaxExperts];
   __shared__ int32_t row_of[kMaxExperts];
-  __shared__ int32_t wave_tot[2][4];
-  const int tid = threadIdx.x;
+  __shared__ int32_t wave_tot[2][kRouteWaves];
+  const int tid = threadIdx.x, nth = blockDim.x;
   const int n = T * k;
-  for (int i = tid; i < n; i += 256) s_ids[i] = ids[i];
-  for (int e = tid; e < E; e += 256) cnt[e] = 0;
+  for (int i = tid; i < n; i += nth) s_ids[i] = ids[i];
+  for (int e = tid; e < E; e += nth) cnt[e] = 0;
   __syncthreads();
-  for (int i = tid; i < n; i += 256) atomicAdd(&cnt[s_ids[i]], 1);
+  for (int i = tid; i < n; i += nth) atomicAdd(&cnt[s_ids[i]], 1);
   __syncthreads();
   // slot and row offsets: thread tid owns experts [tid*per, tid*per + per)
-  const int per = (E + 255) / 256;
+  const int per = (E + nth - 1) / nth;
   int ns = 0, nr = 0;
   for (int j = 0; j < per; ++j) {
     const int e = tid * per + j;
@@ -355,7 +361,7 @@ __device__ void build_plan(Plan* __restrict__ plan, const int32_t* __restrict__ 
   }
   __syncthreads();
   // each routed pair (t, i): its position among expert e's tokens = tokens t' < t routed to e
-  for (int idx = tid; idx < n; idx += 256) {
+  for (int idx = tid; idx < n; idx += nth) {
     const int t = idx / k, e = s_ids[idx];
     int before = 0;
     for (int u = 0; u < t * k; ++u) before += s_ids[u] == e;
@@ -414,9 +420,8 @@ __global__ void single_plan_kernel(Plan* plan, int T, const float* __restrict__ 
 
 // ----------------------------------------------------------------------------------------------
 // Router: grid (E, ceil(T / kMaxTokens)); workgroup e computes logits/scores/selection of expert e
-// for up to 16 tokens; workgroups also share the per-32 quantization of x. With `fuse_plan`, the
-// last workgroup to finish (device-scope counter) runs top-k for every token and builds the plan,
-// then resets the counter for the next launch (no memset: safe inside a captured graph).
+// for up to 16 tokens; workgroups also share the per-32 quantization of x. Top-k and the plan run in
+// route_plan_kernel, the next launch on the same stream, so no workgroup waits on another.
 struct RouterArgs {
   const float* W;
   const float* bias;
@@ -428,10 +433,6 @@ struct RouterArgs {
   float* selection;
   uint8_t* xq;
   uint8_t* xs;
-  TopkOut topk;
-  Plan* plan;
-  uint32_t* counter;
-  int has_shared;
 };
 
 __global__ __launch_bounds__(256) void router_kernel(RouterArgs a) {
@@ -508,25 +509,24 @@ __global__ __launch_bounds__(256) void router_kernel(RouterArgs a) {
     if (a.scores) a.scores[o] = s;
     if (a.selection) a.selection[o] = a.bias ? s + a.bias[e] : s;
   }
-  if (!a.plan) return;
-  // ---- last workgroup: top-k for all tokens, then the plan ----
-  __shared__ int last;
-  __threadfence();
+}
+
+// One workgroup: wave t ranks token t (tokens beyond 16 loop), the results are staged in LDS and
+// written out, then the same workgroup builds the plan from the staged IDs.
+__global__ __launch_bounds__(kRouteThreads) void route_plan_kernel(const float* selection, const float* scores, int T,
+                                                                   int E, int k, float route_scale, TopkOut o,
+                                                                   Plan* plan, int has_shared) {
+  __shared__ int32_t s_idx[kMaxTokens * kMaxTopK];
+  __shared__ float s_w[kMaxTokens * kMaxTopK];
+  const TopkOut staged{s_idx, s_w, o.raw, o.den, o.tied};
+  for (int t = threadIdx.x >> 6; t < T; t += kRouteWaves)
+    topk_token_wave(selection + (size_t)t * E, scores + (size_t)t * E, E, k, route_scale, t, staged);
   __syncthreads();
-  if (tid == 0) {
-    const uint32_t done = atomicAdd(a.counter, 1u);
-    last = done == gridDim.x * gridDim.y - 1;
+  for (int i = threadIdx.x; i < T * k; i += kRouteThreads) {
+    o.indices[i] = s_idx[i];
+    o.weights[i] = s_w[i];
   }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  for (int t = wave; t < a.T; t += 4)
-    topk_token_wave(a.selection + (size_t)t * a.E, a.scores + (size_t)t * a.E, a.E, a.k, a.route_scale, t, a.topk);
-  __threadfence();
-  __syncthreads();
-  __threadfence();
-  build_plan(a.plan, a.topk.indices, a.topk.weights, a.T, a.k, a.E, a.has_shared);
-  if (tid == 0) atomicExch(a.counter, 0u);
+  build_plan(plan, s_idx, s_w, T, k, E, has_shared);
 }
 
 // Stand-alone top-k over supplied selection/scores: one wave per token.
@@ -549,8 +549,8 @@ __global__ void scores_kernel(const float* logits, const float* bias, int T, int
 // Expert GEMVs on scaled MFMA.
 
 struct ExpertArgs {
-  const mx_expert_ptrs* table;   // device table [E+1] or nullptr
-  mx_expert_ptrs single;         // used when table == nullptr
+  const uint8_t* const* tiles;   // tiled layout: device table [E+1] of expert blobs
+  mx_expert_ptrs single;         // reference layout: the one expert of mx_expert_forward / mx_gemv_mxfp4
   const Plan* plan;
   int H, I;
   float limit;
@@ -588,28 +588,12 @@ __device__ __forceinline__ v4f mfma_fp4xfp8(uint4 a, uint4 b0, uint4 b1, v4f c, 
 
 // ---- K-split streaming core shared by the gate/up and down kernels -------------------------------
 //
-// A workgroup of 4 waves owns 4 MFMA tiles of 16 weight rows. Wave w walks its own contiguous quarter
-// of the 128-wide K chunks and multiplies every chunk into all 4 tiles, so one load of the activation
-// operand serves 4 MFMAs.
-// Loads run P chunks ahead of the MFMAs (a register ring unrolled so every index is static), which
-// keeps P * 4 KB of weights in flight per wave. The 4 partial accumulators per tile are then summed
-// in a fixed wave order through LDS, so results do not depend on scheduling.
+// A workgroup of 4 waves owns a row group of 4 MFMA tiles x 16 weight rows. Wave w walks its own
+// contiguous quarter of the 128-wide K chunks and multiplies every chunk into all 4 tiles, so one
+// load of the activation operand serves 4 MFMAs. Loads run P chunks ahead of the MFMAs (a register
+// ring unrolled so every index is static). The 4 partial accumulators per tile are then summed in a
+// fixed wave order through LDS, so results do not depend on scheduling.
 constexpr int kTiles = 4;
-
-struct ChunkRegs {
-  uint4 wa[kTiles];
-  uint32_t sw[kTiles];
-  uint4 b0, b1;
-  uint32_t sx;
-};
-
-struct StreamOperands {
-  const uint8_t* wrow[kTiles];   // this lane's weight row of each tile (packed E2M1)
-  const uint8_t* srow[kTiles];   // and its E8M0 scale row
-  const uint8_t* xrow;           // this lane's token row of E4M3 activations
-  const uint8_t* xsrow;          // and its E8M0 scales
-  bool live;                     // lane's token column is in use
-};
 
 // Loads through the global address space (the pointers come from a device table, so the compiler
 // cannot infer it and would otherwise emit flat loads).
@@ -624,51 +608,99 @@ __device__ __forceinline__ uint4 ldg128(const uint8_t* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-__device__ __forceinline__ void load_chunk(ChunkRegs& r, const StreamOperands& o, int c, int q) {
-  const int kb = 4 * c + q;
+// Weight operand in the device-native tiled layout: for every (row group, K chunk) the 4 tiles'
+// A operands are 4 consecutive KB (lane l's 16 bytes at 16 * l), so each load instruction of a
+// wave reads 1 KB of contiguous memory, and one 4-byte word per lane (256 contiguous bytes per
+// chunk) carries that lane's E8M0 code for each of the 4 tiles (byte t = tile t).
+struct TiledW {
+  const uint8_t* w;   // row group's weights + 16 * lane
+  const uint8_t* s;   // row group's scale words + 4 * lane
+  struct Regs {
+    uint4 wa[kTiles];
+    uint32_t sw;
+  };
+  __device__ __forceinline__ void load(Regs& r, int c, int /*q*/) const {
 #pragma unroll
-  for (int t = 0; t < kTiles; ++t) {
-    r.wa[t] = ldg128(o.wrow[t] + (size_t)kb * 16);
-    r.sw[t] = ldg32(o.srow[t] + 4 * c);
+    for (int t = 0; t < kTiles; ++t) r.wa[t] = ldg128(w + (size_t)c * 4096 + t * 1024);
+    r.sw = ldg32(s + (size_t)c * 256);
   }
+  __device__ __forceinline__ static int scale(const Regs& r, int t, int /*q*/) { return (int)((r.sw >> (8 * t)) & 0xFF); }
+};
+
+// Weight operand in the reference row-major layout (w[row][K/2], s[row][K/32]): each load covers
+// 16 rows x 64 bytes, and every tile needs its own scale load.
+struct RowMajorW {
+  const uint8_t* wrow[kTiles];   // this lane's weight row of each tile
+  const uint8_t* srow[kTiles];   // and its E8M0 scale row
+  struct Regs {
+    uint4 wa[kTiles];
+    uint32_t sw[kTiles];
+  };
+  __device__ __forceinline__ void load(Regs& r, int c, int q) const {
+    const int kb = 4 * c + q;
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+      r.wa[t] = ldg128(wrow[t] + (size_t)kb * 16);
+      r.sw[t] = ldg32(srow[t] + 4 * c);
+    }
+  }
+  __device__ __forceinline__ static int scale(const Regs& r, int t, int q) { return (int)((r.sw[t] >> (8 * q)) & 0xFF); }
+};
+
+struct ActOperand {
+  const uint8_t* xrow;    // this lane's token row of E4M3 activations
+  const uint8_t* xsrow;   // and its E8M0 scales
+  bool live;              // lane's token column is in use
+};
+
+template <class W>
+struct ChunkRegs {
+  typename W::Regs w;
+  uint4 b0, b1;
+  uint32_t sx;
+};
+
+template <class W>
+__device__ __forceinline__ void load_chunk(ChunkRegs<W>& r, const W& ws, const ActOperand& x, int c, int q) {
+  ws.load(r.w, c, q);
   // Idle token columns read a valid row too (no divergent branch around the loads, which would
   // force the operands through scratch); mma_chunk zeroes them, and their outputs are dropped.
-  const uint8_t* chunk = o.xrow + (size_t)c * 128;
+  const uint8_t* chunk = x.xrow + (size_t)c * 128;
   r.b0 = ldg128(chunk + 16 * q);
   r.b1 = ldg128(chunk + 64 + 16 * q);
-  r.sx = ldg32(o.xsrow + 4 * c);
+  r.sx = ldg32(x.xsrow + 4 * c);
 }
 
-__device__ __forceinline__ void mma_chunk(const ChunkRegs& r, v4f (&acc)[kTiles], int q, uint32_t keep) {
+template <class W>
+__device__ __forceinline__ void mma_chunk(const ChunkRegs<W>& r, v4f (&acc)[kTiles], int q, uint32_t keep) {
   const int sx = (int)((r.sx >> (8 * q)) & 0xFF);
   const uint4 b0 = make_uint4(r.b0.x & keep, r.b0.y & keep, r.b0.z & keep, r.b0.w & keep);
   const uint4 b1 = make_uint4(r.b1.x & keep, r.b1.y & keep, r.b1.z & keep, r.b1.w & keep);
 #pragma unroll
-  for (int t = 0; t < kTiles; ++t) acc[t] = mfma_fp4xfp8(r.wa[t], b0, b1, acc[t], (int)((r.sw[t] >> (8 * q)) & 0xFF), sx);
+  for (int t = 0; t < kTiles; ++t) acc[t] = mfma_fp4xfp8(r.w.wa[t], b0, b1, acc[t], W::scale(r.w, t, q), sx);
 }
 
-template <int P>
-__device__ __forceinline__ void stream_ksplit(const StreamOperands& o, int chunks, int wave, int q, v4f (&acc)[kTiles]) {
+template <int P, class W>
+__device__ __forceinline__ void stream_ksplit(const W& ws, const ActOperand& x, int chunks, int wave, int q,
+                                              v4f (&acc)[kTiles]) {
 #pragma unroll
   for (int t = 0; t < kTiles; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
-  // wave w reads the contiguous chunk range [c0, c0 + n): every 128-byte line of a row is fetched by
-  // one wave in consecutive loads
   const int c0 = (chunks * wave) / 4;
   const int n = (chunks * (wave + 1)) / 4 - c0;
   if (n == 0) return;
-  const uint32_t live = o.live ? 0xFFFFFFFFu : 0u;
-  ChunkRegs buf[P];
+  const uint32_t live = x.live ? 0xFFFFFFFFu : 0u;
+  ChunkRegs<W> buf[P];
 #pragma unroll
-  for (int j = 0; j < P; ++j) load_chunk(buf[j], o, c0 + min(j, n - 1), q);
+  for (int j = 0; j < P; ++j) load_chunk(buf[j], ws, x, c0 + min(j, n - 1), q);
   // Steady state: consume P chunks and refill them P ahead, with no per-chunk branches so the
-  // waitcnt pass can keep the refills in flight. Slots past the end repeat the last chunk (an L2
+  // waitcnt pass can keep the refills in flight. Slots past the end repeat the last chunk (a cache
   // hit) and are masked to zero.
   int i = 0;
   for (; i + P < n; i += P) {
 #pragma unroll
     for (int j = 0; j < P; ++j) {
       mma_chunk(buf[j], acc, q, live);
-      load_chunk(buf[j], o, c0 + min(i + j + P, n - 1), q);
+      load_chunk(buf[j], ws, x, c0 + min(i + j + P, n - 1), q);
     }
   }
 #pragma unroll
@@ -689,10 +721,33 @@ __device__ __forceinline__ v4f reduce_tiles(const v4f (&acc)[kTiles], int wave, 
   return out;
 }
 
+// Byte offsets of the tiled expert blob for hidden H and intermediate I:
+//   [0, I*H)            gate/up A operands: row group g (I/32 groups) x chunk c (H/128) x tile t x lane
+//                       (16 B), tile t = W1 rows 32g + 8t + (0..7) as MFMA rows 0-7 and the same W3
+//                       rows as MFMA rows 8-15; lane l = MFMA row l % 16, K block 4c + l / 16
+//   [gu_s, +I*H/16)     gate/up scale words: g x c x lane (4 B, byte t = tile t)
+//   [dn_w, +H*I/2)      down A operands: row group b (H/64) x chunk c (I/128) x tile t x lane, tile t =
+//                       W2 rows 64b + 16t + (0..15)
+//   [dn_s, +H*I/32)     down scale words: b x c x lane
+struct TiledOffsets {
+  size_t gu_s, dn_w, dn_s, total;
+};
+
+__host__ __device__ __forceinline__ TiledOffsets tiled_offsets(int H, int I) {
+  const size_t ih = (size_t)I * H;
+  TiledOffsets o;
+  o.gu_s = ih;
+  o.dn_w = ih + ih / 16;
+  o.dn_s = o.dn_w + ih / 2;
+  o.total = o.dn_s + ih / 32;
+  return o;
+}
+
 // grid (I/32, slots), 256 threads. The workgroup computes intermediate rows [32g, 32g + 32) of W1 and
 // W3 for the slot's tokens: tile t holds W1 rows 32g + 8t + (0..7) as MFMA rows 0-7 and the same W3
 // rows as MFMA rows 8-15. After the cross-wave sum, wave t owns tile t, applies the SwiGLU epilogue,
 // and the workgroup quantizes its 32-row block of the down input per token (one E8M0 block).
+template <bool kTiled>
 __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
   const Plan* __restrict__ plan = a.plan;
   const int s = blockIdx.y;
@@ -702,24 +757,34 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int m = lane & 15, q = lane >> 4, n = lane & 15;
   const int ntok = plan->slot_ntok[s];
-  const mx_expert_ptrs p = a.table ? a.table[plan->slot_expert[s]] : a.single;
   const int H = a.H, I = a.I;
-  StreamOperands o;
-  const bool up = m >= 8;
-  const uint8_t* wbase = (const uint8_t*)(up ? p.w3_weight : p.w1_weight);
-  const uint8_t* sbase = (const uint8_t*)(up ? p.w3_scale : p.w1_scale);
-#pragma unroll
-  for (int t = 0; t < kTiles; ++t) {
-    const int row = g * 32 + t * 8 + (m & 7);
-    o.wrow[t] = wbase + (size_t)row * (H / 2);
-    o.srow[t] = sbase + (size_t)row * (H / 32);
-  }
-  o.live = n < ntok;
-  const int tok = o.live ? plan->slot_tok[s][n] : 0;
-  o.xrow = a.xq + (size_t)tok * H;
-  o.xsrow = a.xs + (size_t)tok * (H / 32);
+  ActOperand x;
+  x.live = n < ntok;
+  const int tok = x.live ? plan->slot_tok[s][n] : 0;
+  x.xrow = a.xq + (size_t)tok * H;
+  x.xsrow = a.xs + (size_t)tok * (H / 32);
   v4f acc[kTiles];
-  stream_ksplit<3>(o, H / 128, wave, q, acc);
+  if constexpr (kTiled) {
+    const uint8_t* blob = a.tiles[plan->slot_expert[s]];
+    const size_t chunks = H / 128;
+    TiledW ws;
+    ws.w = blob + (size_t)g * chunks * 4096 + 16 * lane;
+    ws.s = blob + tiled_offsets(H, I).gu_s + (size_t)g * chunks * 256 + 4 * lane;
+    stream_ksplit<3>(ws, x, H / 128, wave, q, acc);
+  } else {
+    const mx_expert_ptrs& p = a.single;
+    const bool up = m >= 8;
+    const uint8_t* wbase = (const uint8_t*)(up ? p.w3_weight : p.w1_weight);
+    const uint8_t* sbase = (const uint8_t*)(up ? p.w3_scale : p.w1_scale);
+    RowMajorW ws;
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+      const int row = g * 32 + t * 8 + (m & 7);
+      ws.wrow[t] = wbase + (size_t)row * (H / 2);
+      ws.srow[t] = sbase + (size_t)row * (H / 32);
+    }
+    stream_ksplit<3>(ws, x, H / 128, wave, q, acc);
+  }
   __shared__ float red[4][kTiles][64][4];
   __shared__ float s_din[kMaxTokens][32];
   const v4f mine = reduce_tiles(acc, wave, lane, red);
@@ -778,6 +843,7 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
 
 // grid (H/64, slots), 256 threads: output rows [64b, 64b + 64) of W2 as 4 tiles of 16 rows; after
 // the cross-wave sum wave t writes tile t as BF16 (the reference's w2 stage).
+template <bool kTiled>
 __global__ __launch_bounds__(256) void down_kernel(ExpertArgs a) {
   const Plan* __restrict__ plan = a.plan;
   const int s = blockIdx.y;
@@ -787,20 +853,30 @@ __global__ __launch_bounds__(256) void down_kernel(ExpertArgs a) {
   const int m = lane & 15, q = lane >> 4, n = lane & 15;
   const int ntok = plan->slot_ntok[s];
   const int row0 = plan->slot_row0[s];
-  const mx_expert_ptrs p = a.table ? a.table[plan->slot_expert[s]] : a.single;
   const int H = a.H, I = a.I;
-  const int hb = blockIdx.x * 64;
-  StreamOperands o;
-#pragma unroll
-  for (int t = 0; t < kTiles; ++t) {
-    o.wrow[t] = (const uint8_t*)p.w2_weight + (size_t)(hb + 16 * t + m) * (I / 2);
-    o.srow[t] = (const uint8_t*)p.w2_scale + (size_t)(hb + 16 * t + m) * (I / 32);
-  }
-  o.live = n < ntok;
-  o.xrow = a.dq + (size_t)(row0 + (o.live ? n : 0)) * I;
-  o.xsrow = a.ds + (size_t)(row0 + (o.live ? n : 0)) * (I / 32);
+  const int b = blockIdx.x, hb = b * 64;
+  ActOperand x;
+  x.live = n < ntok;
+  x.xrow = a.dq + (size_t)(row0 + (x.live ? n : 0)) * I;
+  x.xsrow = a.ds + (size_t)(row0 + (x.live ? n : 0)) * (I / 32);
   v4f acc[kTiles];
-  stream_ksplit<4>(o, I / 128, wave, q, acc);
+  if constexpr (kTiled) {
+    const uint8_t* blob = a.tiles[plan->slot_expert[s]];
+    const TiledOffsets off = tiled_offsets(H, I);
+    const size_t chunks = I / 128;
+    TiledW ws;
+    ws.w = blob + off.dn_w + (size_t)b * chunks * 4096 + 16 * lane;
+    ws.s = blob + off.dn_s + (size_t)b * chunks * 256 + 4 * lane;
+    stream_ksplit<4>(ws, x, I / 128, wave, q, acc);
+  } else {
+    RowMajorW ws;
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+      ws.wrow[t] = (const uint8_t*)a.single.w2_weight + (size_t)(hb + 16 * t + m) * (I / 2);
+      ws.srow[t] = (const uint8_t*)a.single.w2_scale + (size_t)(hb + 16 * t + m) * (I / 32);
+    }
+    stream_ksplit<4>(ws, x, I / 128, wave, q, acc);
+  }
   __shared__ float red[4][kTiles][64][4];
   const v4f mine = reduce_tiles(acc, wave, lane, red);
   if (n < ntok) {
@@ -808,6 +884,71 @@ __global__ __launch_bounds__(256) void down_kernel(ExpertArgs a) {
     packed.x = mx::bf16_bits(mine[0]) | (mx::bf16_bits(mine[1]) << 16);
     packed.y = mx::bf16_bits(mine[2]) | (mx::bf16_bits(mine[3]) << 16);
     *reinterpret_cast<uint2*>(a.out + (size_t)(row0 + n) * H + hb + 16 * wave + 4 * q) = packed;
+  }
+}
+
+// Reference layout <-> tiled layout of one expert (both directions bit-for-bit; every byte of
+// either layout has exactly one counterpart). One thread per 16-byte A operand piece, then one per
+// 4-byte scale word; gate/up and down sections in one grid-stride pass.
+__global__ void tile_expert_kernel(mx_expert_ptrs ref, uint8_t* blob, int H, int I, int to_tiled) {
+  const TiledOffsets off = tiled_offsets(H, I);
+  const int64_t cg = H / 128, cd = I / 128;
+  const int64_t gu_pieces = (int64_t)I * H / 16, gu_words = (int64_t)I * H / 64;
+  const int64_t dn_pieces = (int64_t)H * I / 32, dn_words = (int64_t)H * I / 128;
+  const int64_t total = gu_pieces + gu_words + dn_pieces + dn_words;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    int64_t i = idx;
+    if (i < gu_pieces) {
+      const int l = (int)(i & 63), t = (int)((i >> 6) & 3), m = l & 15, q = l >> 4;
+      const int64_t rest = i >> 8, c = rest % cg, g = rest / cg;
+      const int64_t row = 32 * g + 8 * t + (m & 7);
+      uint8_t* r = (uint8_t*)(m < 8 ? ref.w1_weight : ref.w3_weight) + row * (H / 2) + (4 * c + q) * 16;
+      uint4* d = reinterpret_cast<uint4*>(blob + i * 16);
+      if (to_tiled) *d = *reinterpret_cast<const uint4*>(r);
+      else *reinterpret_cast<uint4*>(r) = *d;
+      continue;
+    }
+    i -= gu_pieces;
+    if (i < gu_words) {
+      const int l = (int)(i & 63), m = l & 15, q = l >> 4;
+      const int64_t rest = i >> 6, c = rest % cg, g = rest / cg;
+      uint8_t* sref = (uint8_t*)(m < 8 ? ref.w1_scale : ref.w3_scale);
+      uint32_t* d = reinterpret_cast<uint32_t*>(blob + off.gu_s + i * 4);
+      uint32_t word = to_tiled ? 0u : *d;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        uint8_t* r = sref + (32 * g + 8 * t + (m & 7)) * (H / 32) + 4 * c + q;
+        if (to_tiled) word |= (uint32_t)*r << (8 * t);
+        else *r = (uint8_t)(word >> (8 * t));
+      }
+      if (to_tiled) *d = word;
+      continue;
+    }
+    i -= gu_words;
+    if (i < dn_pieces) {
+      const int l = (int)(i & 63), t = (int)((i >> 6) & 3), m = l & 15, q = l >> 4;
+      const int64_t rest = i >> 8, c = rest % cd, b = rest / cd;
+      uint8_t* r = (uint8_t*)ref.w2_weight + (64 * b + 16 * t + m) * (I / 2) + (4 * c + q) * 16;
+      uint4* d = reinterpret_cast<uint4*>(blob + off.dn_w + i * 16);
+      if (to_tiled) *d = *reinterpret_cast<const uint4*>(r);
+      else *reinterpret_cast<uint4*>(r) = *d;
+      continue;
+    }
+    i -= dn_pieces;
+    {
+      const int l = (int)(i & 63), m = l & 15, q = l >> 4;
+      const int64_t rest = i >> 6, c = rest % cd, b = rest / cd;
+      uint32_t* d = reinterpret_cast<uint32_t*>(blob + off.dn_s + i * 4);
+      uint32_t word = to_tiled ? 0u : *d;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        uint8_t* r = (uint8_t*)ref.w2_scale + (64 * b + 16 * t + m) * (I / 32) + 4 * c + q;
+        if (to_tiled) word |= (uint32_t)*r << (8 * t);
+        else *r = (uint8_t)(word >> (8 * t));
+      }
+      if (to_tiled) *d = word;
+    }
   }
 }
 
@@ -859,7 +1000,7 @@ __global__ void acc_finish_kernel(const float* sum, uint16_t* out, int64_t n) {
   if (i < n) out[i] = (uint16_t)mx::bf16_bits(sum[i]);
 }
 
-__global__ void set_expert_kernel(mx_expert_ptrs* slot, mx_expert_ptrs value) { *slot = value; }
+__global__ void set_expert_kernel(const uint8_t** slot, const uint8_t* value) { *slot = value; }
 
 unsigned blocks_for(int64_t n, int threads) { return (unsigned)((n + threads - 1) / threads); }
 
@@ -887,7 +1028,7 @@ struct mx_layer {
   const float* router_weight = nullptr;
   const float* bias = nullptr;
   int has_shared = 0;
-  mx_expert_ptrs* table = nullptr;  // device [E + 1]
+  const uint8_t** tiles = nullptr;  // device [E + 1]: tiled expert blobs, shared last
   // per-call buffers
   float *logits = nullptr, *scores = nullptr, *selection = nullptr, *weights = nullptr, *raw = nullptr,
         *den = nullptr, *trace = nullptr;
@@ -895,7 +1036,6 @@ struct mx_layer {
   uint8_t *xq = nullptr, *xs = nullptr, *dq = nullptr, *ds = nullptr;
   uint16_t *w1 = nullptr, *w3 = nullptr, *din = nullptr, *eout = nullptr;
   Plan* plan = nullptr;
-  uint32_t* counter = nullptr;
   int max_rows = 0;
   std::vector<std::pair<void*, uint64_t>> allocs;
   // profiling: events bracket each kernel of a call; a ring of kProfRing calls is recorded without
@@ -972,17 +1112,16 @@ using namespace mxi;
 extern "C" {
 
 int mx_layer_create(mx_ctx* ctx, const mx_moe_config* cfg, const float* router_weight, const float* bias,
-                    const mx_expert_ptrs* experts, const mx_expert_ptrs* shared, mx_layer** out) {
+                    const void* const* experts, const void* shared, mx_layer** out) {
   if (int s = use(ctx)) return s;
   if (int s = validate_config(cfg)) return s;
   MX_REQUIRE(out != nullptr, "mx_layer_create: null output");
   MX_REQUIRE(router_weight != nullptr && aligned(router_weight, 16), "router weight must be a 16-byte aligned pointer");
   MX_REQUIRE(experts != nullptr, "expert pointer table is null");
   for (int e = 0; e < cfg->experts; ++e)
-    if (int s = check_expert_ptrs(experts[e], "mx_layer_create")) return s;
-  MX_REQUIRE((cfg->shared_format == -1) == (shared == nullptr), "shared expert pointers and format disagree");
-  if (shared)
-    if (int s = check_expert_ptrs(*shared, "mx_layer_create(shared)")) return s;
+    MX_REQUIRE(experts[e] && aligned(experts[e], 256), "expert %d: tiled expert must be a 256-byte aligned pointer", e);
+  MX_REQUIRE((cfg->shared_format == -1) == (shared == nullptr), "shared expert pointer and format disagree");
+  MX_REQUIRE(!shared || aligned(shared, 256), "shared expert: tiled expert must be 256-byte aligned");
   mx_layer* L = new mx_layer();
   L->ctx = ctx;
   L->cfg = *cfg;
@@ -997,7 +1136,7 @@ int mx_layer_create(mx_ctx* ctx, const mx_moe_config* cfg, const float* router_w
     delete L;
     return st;
   };
-  if ((s = layer_alloc_t(L, (uint64_t)E + 1, &L->table))) return fail_out(s);
+  if ((s = layer_alloc_t(L, (uint64_t)E + 1, &L->tiles))) return fail_out(s);
   if ((s = layer_alloc_t(L, (uint64_t)T * E, &L->logits))) return fail_out(s);
   if ((s = layer_alloc_t(L, (uint64_t)T * E, &L->scores))) return fail_out(s);
   if ((s = layer_alloc_t(L, (uint64_t)T * E, &L->selection))) return fail_out(s);
@@ -1009,7 +1148,6 @@ int mx_layer_create(mx_ctx* ctx, const mx_moe_config* cfg, const float* router_w
   if ((s = layer_alloc_t(L, (uint64_t)T * H, &L->xq))) return fail_out(s);
   if ((s = layer_alloc_t(L, (uint64_t)T * H / 32 + 16, &L->xs))) return fail_out(s);
   if ((s = layer_alloc_t(L, 1, &L->plan))) return fail_out(s);
-  if ((s = layer_alloc_t(L, 4, &L->counter))) return fail_out(s);
   const uint64_t R = (uint64_t)L->max_rows;
   if ((s = layer_alloc_t(L, R * I, &L->w1))) return fail_out(s);
   if ((s = layer_alloc_t(L, R * I, &L->w3))) return fail_out(s);
@@ -1018,11 +1156,10 @@ int mx_layer_create(mx_ctx* ctx, const mx_moe_config* cfg, const float* router_w
   if ((s = layer_alloc_t(L, R * I, &L->dq))) return fail_out(s);
   if ((s = layer_alloc_t(L, R * I / 32 + 16, &L->ds))) return fail_out(s);
   if ((s = layer_alloc_t(L, R * H, &L->eout))) return fail_out(s);
-  std::vector<mx_expert_ptrs> host(E + 1);
+  std::vector<const void*> host(E + 1);
   for (int e = 0; e < E; ++e) host[e] = experts[e];
-  host[E] = shared ? *shared : experts[0];
-  hipError_t err = hipMemcpy(L->table, host.data(), sizeof(mx_expert_ptrs) * (E + 1), hipMemcpyHostToDevice);
-  if (err == hipSuccess) err = hipMemset(L->counter, 0, 16);
+  host[E] = shared ? shared : experts[0];
+  hipError_t err = hipMemcpy(L->tiles, host.data(), sizeof(void*) * (E + 1), hipMemcpyHostToDevice);
   if (err == hipSuccess) err = hipMemset(L->plan, 0, sizeof(Plan));
   if (err == hipSuccess) err = hipDeviceSynchronize();
   if (err != hipSuccess) return fail_out(hip_fail(err, "mx_layer_create: table upload"));
@@ -1039,14 +1176,14 @@ int mx_layer_destroy(mx_layer* L) {
   return MX_OK;
 }
 
-int mx_layer_set_expert(mx_layer* L, int32_t expert, const mx_expert_ptrs* w, void* stream) {
+int mx_layer_set_expert(mx_layer* L, int32_t expert, const void* tiled, void* stream) {
   MX_REQUIRE(L != nullptr, "layer is closed");
   if (int s = use(L->ctx)) return s;
   MX_REQUIRE(expert >= 0 && expert < L->cfg.experts, "expert %d outside the layer", expert);
-  MX_REQUIRE(w != nullptr, "null expert pointers");
-  if (int s = check_expert_ptrs(*w, "mx_layer_set_expert")) return s;
-  // A by-value kernel argument carries the six pointers, so the host copy may go out of scope.
-  hipLaunchKernelGGL(set_expert_kernel, dim3(1), dim3(1), 0, as_stream(stream), L->table + expert, *w);
+  MX_REQUIRE(tiled != nullptr && aligned(tiled, 256), "tiled expert must be a 256-byte aligned pointer");
+  // A kernel on the caller's stream writes the table entry, ordered after a slot fill on that stream.
+  hipLaunchKernelGGL(set_expert_kernel, dim3(1), dim3(1), 0, as_stream(stream), L->tiles + expert,
+                     (const uint8_t*)tiled);
   MX_LAUNCH_CHECK("set_expert");
   return MX_OK;
 }
@@ -1133,15 +1270,15 @@ int mx_moe_decode(mx_layer* L, const uint16_t* x, int32_t T, uint16_t* y, int32_
   r.selection = L->selection;
   r.xq = L->xq;
   r.xs = L->xs;
-  r.topk = TopkOut{L->indices, L->weights, L->raw, L->den, L->tied};
-  r.plan = L->plan;
-  r.counter = L->counter;
-  r.has_shared = L->has_shared;
   hipLaunchKernelGGL(router_kernel, dim3(c.experts, 1), dim3(256), 0, st, r);
   MX_LAUNCH_CHECK("router_kernel");
+  hipLaunchKernelGGL(route_plan_kernel, dim3(1), dim3(kRouteThreads), 0, st, (const float*)L->selection,
+                     (const float*)L->scores, T, c.experts, c.top_k, c.route_scale,
+                     TopkOut{L->indices, L->weights, L->raw, L->den, L->tied}, L->plan, L->has_shared);
+  MX_LAUNCH_CHECK("route_plan_kernel");
   if (prof) MX_HIP(hipEventRecord(ev[1], st));
   ExpertArgs a{};
-  a.table = L->table;
+  a.tiles = L->tiles;
   a.plan = L->plan;
   a.H = c.hidden;
   a.I = c.intermediate;
@@ -1158,10 +1295,10 @@ int mx_moe_decode(mx_layer* L, const uint16_t* x, int32_t T, uint16_t* y, int32_
     a.trace = L->trace;
   }
   const int slots = std::min(c.experts, T * c.top_k) + L->has_shared;
-  hipLaunchKernelGGL(gateup_kernel, dim3(c.intermediate / 32, slots), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(gateup_kernel<true>, dim3(c.intermediate / 32, slots), dim3(256), 0, st, a);
   MX_LAUNCH_CHECK("gateup_kernel");
   if (prof) MX_HIP(hipEventRecord(ev[2], st));
-  hipLaunchKernelGGL(down_kernel, dim3(c.hidden / 64, slots), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(down_kernel<true>, dim3(c.hidden / 64, slots), dim3(256), 0, st, a);
   MX_LAUNCH_CHECK("down_kernel");
   if (prof) MX_HIP(hipEventRecord(ev[3], st));
   hipLaunchKernelGGL(combine_kernel, dim3((c.hidden / 8 + 255) / 256, T), dim3(256), 0, st, (const Plan*)L->plan,
@@ -1208,7 +1345,6 @@ int mx_expert_forward(mx_ctx* ctx, const mx_expert_ptrs* w, int32_t format, int3
   MX_LAUNCH_CHECK("single_plan_kernel");
   if (int s = mx_act_quant32(ctx, x, xq, xs, T, H, stream)) return s;
   ExpertArgs a{};
-  a.table = nullptr;
   a.single = *w;
   a.plan = plan;
   a.H = H;
@@ -1225,9 +1361,9 @@ int mx_expert_forward(mx_ctx* ctx, const mx_expert_ptrs* w, int32_t format, int3
     a.din = stages->down_input;
     a.trace = stages->trace;
   }
-  hipLaunchKernelGGL(gateup_kernel, dim3(I / 32, 1), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(gateup_kernel<false>, dim3(I / 32, 1), dim3(256), 0, st, a);
   MX_LAUNCH_CHECK("gateup_kernel");
-  hipLaunchKernelGGL(down_kernel, dim3(H / 64, 1), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(down_kernel<false>, dim3(H / 64, 1), dim3(256), 0, st, a);
   MX_LAUNCH_CHECK("down_kernel");
   return MX_OK;
 }
@@ -1256,8 +1392,40 @@ int mx_gemv_mxfp4(mx_ctx* ctx, const uint8_t* q, const uint8_t* sa, const uint8_
   a.dq = const_cast<uint8_t*>(q);
   a.ds = const_cast<uint8_t*>(sa);
   a.out = y;
-  hipLaunchKernelGGL(down_kernel, dim3(N / 64, 1), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(down_kernel<false>, dim3(N / 64, 1), dim3(256), 0, st, a);
   MX_LAUNCH_CHECK("down_kernel");
+  return MX_OK;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Tiled expert layout
+
+uint64_t mx_tiled_expert_bytes(int32_t H, int32_t I) {
+  if (H <= 0 || I <= 0 || H % 128 || I % 128) return 0;
+  return tiled_offsets(H, I).total;
+}
+
+static int tile_common(mx_ctx* ctx, const mx_expert_ptrs* ref, const void* blob, int32_t H, int32_t I,
+                       const char* who) {
+  if (int s = use(ctx)) return s;
+  MX_REQUIRE(ref != nullptr && blob != nullptr, "%s: null pointer", who);
+  MX_REQUIRE(H > 0 && H % 128 == 0 && I > 0 && I % 128 == 0, "%s: shapes must be positive multiples of 128", who);
+  MX_REQUIRE(aligned(blob, 256), "%s: the tiled expert must be 256-byte aligned", who);
+  return check_expert_ptrs(*ref, who);
+}
+
+int mx_tile_expert(mx_ctx* ctx, const mx_expert_ptrs* ref, int32_t H, int32_t I, void* tiled, void* stream) {
+  if (int s = tile_common(ctx, ref, tiled, H, I, "mx_tile_expert")) return s;
+  hipLaunchKernelGGL(tile_expert_kernel, dim3(2048), dim3(256), 0, as_stream(stream), *ref, (uint8_t*)tiled, H, I, 1);
+  MX_LAUNCH_CHECK("tile_expert_kernel");
+  return MX_OK;
+}
+
+int mx_untile_expert(mx_ctx* ctx, const void* tiled, int32_t H, int32_t I, const mx_expert_ptrs* ref, void* stream) {
+  if (int s = tile_common(ctx, ref, tiled, H, I, "mx_untile_expert")) return s;
+  hipLaunchKernelGGL(tile_expert_kernel, dim3(2048), dim3(256), 0, as_stream(stream), *ref,
+                     (uint8_t*)const_cast<void*>(tiled), H, I, 0);
+  MX_LAUNCH_CHECK("tile_expert_kernel");
   return MX_OK;
 }
 

@@ -1,10 +1,13 @@
 """Resident expert bank and the batched MoE decode layer (the fast path).
 
-ExpertBank keeps every expert of a layer in one HBM allocation using the
-reference's per-expert contiguous byte layout (w1_weight, w1_scale, w3_weight,
-w3_scale, w2_weight, w2_scale; src/vesper/storage.py:33-41), so a cache slot
-and a store entry have the same shape. MoELayer drives mx_moe_decode: router,
-top-k plan, fused expert GEMVs and ordered combine in four kernel launches on
+ExpertBank keeps every expert of a layer in one HBM allocation in the
+device-native tiled layout (mx_tile_expert): the expert kernels then read each
+wave's operands as 1 KB of contiguous memory with one coalesced scale word per
+chunk. Experts enter and leave the bank in the reference's per-expert layout
+(w1_weight, w1_scale, w3_weight, w3_scale, w2_weight, w2_scale;
+src/vesper/storage.py:33-41) through a one-expert staging area and the
+bit-exact tile/untile conversion. MoELayer drives mx_moe_decode: router,
+top-k + plan, fused expert GEMVs and ordered combine in five kernel launches on
 one stream, with inputs resident in HBM.
 """
 
@@ -41,7 +44,7 @@ def _plan_views(raw: np.ndarray) -> dict:
 
 
 class ExpertBank:
-    """`count` experts of one layer resident in a single device allocation."""
+    """`count` experts of one layer resident in a single device allocation (tiled layout)."""
 
     def __init__(self, ctx: _lib.Context, config: MoEConfig, count: int):
         self.ctx, self.config, self.count = ctx, config, int(count)
@@ -51,41 +54,64 @@ class ExpertBank:
             rows, cols = layout[name]
             self.offsets[name] = (offset, (rows, cols))
             offset += rows * cols
-        self.expert_bytes = offset
-        if offset % 256:
-            raise ValueError("expert byte size must keep every expert 256-byte aligned")
+        self.expert_bytes = int(ctx.lib.cdll.mx_tiled_expert_bytes(config.hidden, config.intermediate))
+        if self.expert_bytes != offset or offset % 256:
+            raise ValueError("expert shapes must be multiples of 128 (tiled and reference sizes agree)")
         self.base = ctx.malloc(self.expert_bytes * self.count)
+        self._staging = 0
 
-    def tensor_ptr(self, expert: int, name: str) -> int:
-        return self.base + expert * self.expert_bytes + self.offsets[name][0]
-
-    def ptrs(self, expert: int) -> _lib.MxExpertPtrs:
+    def tiled_ptr(self, expert: int) -> int:
         if not 0 <= expert < self.count:
             raise ValueError("expert index outside the bank")
-        return _lib.MxExpertPtrs(*[self.tensor_ptr(expert, n) for n in TENSORS])
+        return self.base + expert * self.expert_bytes
+
+    def _stage(self) -> int:
+        if not self._staging:
+            self._staging = self.ctx.malloc(self.expert_bytes)
+        return self._staging
+
+    def _staging_ptrs(self) -> _lib.MxExpertPtrs:
+        base = self._stage()
+        return _lib.MxExpertPtrs(*[base + self.offsets[n][0] for n in TENSORS])
 
     def upload(self, expert: int, arrays: dict, stream=None):
+        """Reference-layout arrays -> staging -> tiled slot `expert`."""
         validate_expert_arrays(arrays, self.config)
+        dst = self.tiled_ptr(expert)
+        ptrs = self._staging_ptrs()
         for name in TENSORS:
-            self.ctx.copy_h2d(self.tensor_ptr(expert, name), np.ascontiguousarray(arrays[name], np.uint8), stream)
+            self.ctx.copy_h2d(getattr(ptrs, name), np.ascontiguousarray(arrays[name], np.uint8), stream)
+        self.ctx.lib.tile_expert(self.ctx._h(), C.byref(ptrs), self.config.hidden, self.config.intermediate,
+                                 C.c_void_p(dst), _lib._stream(stream))
 
     def download(self, expert: int) -> dict:
-        return {name: self.ctx.download(self.tensor_ptr(expert, name), shape, np.uint8)
+        """Tiled slot `expert` -> reference-layout arrays (bit-exact inverse of upload)."""
+        src = self.tiled_ptr(expert)
+        ptrs = self._staging_ptrs()
+        self.ctx.lib.untile_expert(self.ctx._h(), C.c_void_p(src), self.config.hidden, self.config.intermediate,
+                                   C.byref(ptrs), None)
+        return {name: self.ctx.download(getattr(ptrs, name), shape, np.uint8)
                 for name, (_, shape) in self.offsets.items()}
 
     def fill_synthetic(self, seed: int, scale_lo: int = 118, scale_hi: int = 126, stream=None):
-        """BASELINE inputs generated in HBM: uniform packed bytes, E8M0 codes uniform in [lo, hi]."""
+        """BASELINE inputs generated in HBM: uniform packed bytes, E8M0 codes uniform in [lo, hi], drawn in
+        the reference layout (one seed per expert tensor) and tiled into place."""
+        ptrs = self._staging_ptrs()
         for e in range(self.count):
             for t, name in enumerate(TENSORS):
-                offset, (rows, cols) = self.offsets[name]
+                _, (rows, cols) = self.offsets[name]
                 lo, hi = (0, 255) if name.endswith("weight") else (scale_lo, scale_hi)
-                self.ctx.fill_uniform_u8(self.base + e * self.expert_bytes + offset, rows * cols,
-                                         (seed * 1_000_003 + e * 8 + t), lo, hi, stream)
+                self.ctx.fill_uniform_u8(getattr(ptrs, name), rows * cols, (seed * 1_000_003 + e * 8 + t), lo, hi,
+                                         stream)
+            self.ctx.lib.tile_expert(self.ctx._h(), C.byref(ptrs), self.config.hidden, self.config.intermediate,
+                                     C.c_void_p(self.tiled_ptr(e)), _lib._stream(stream))
 
     def free(self):
-        if self.base:
-            self.ctx.free(self.base)
-            self.base = 0
+        for attr in ("base", "_staging"):
+            ptr = getattr(self, attr)
+            if ptr:
+                self.ctx.free(ptr)
+                setattr(self, attr, 0)
 
 
 def validate_expert_arrays(arrays: dict, config: MoEConfig):
@@ -113,8 +139,8 @@ class MoELayer:
         cfg = _lib.MxMoeConfig(config.hidden, config.intermediate, config.experts, config.top_k,
                                _lib.MX_SCORE[config.score_func], config.route_scale, config.swiglu_limit,
                                _lib.MX_FMT_MXFP4 if config.shared else -1, config.max_tokens)
-        table = (_lib.MxExpertPtrs * config.experts)(*[bank.ptrs(e) for e in range(config.experts)])
-        shared = C.byref(bank.ptrs(config.experts)) if config.shared else None
+        table = (C.c_void_p * config.experts)(*[bank.tiled_ptr(e) for e in range(config.experts)])
+        shared = C.c_void_p(bank.tiled_ptr(config.experts)) if config.shared else None
         handle = C.c_void_p()
         self.lib.layer_create(ctx._h(), C.byref(cfg), _lib.vp(self.router_weight), _lib.vp(self.bias),
                               table, shared, C.byref(handle))
