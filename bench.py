@@ -22,6 +22,8 @@ import numpy as np
 
 HBM_PEAK_GBS = 8000.0
 TOKENS = (1, 4, 16)
+ROOT = os.path.dirname(os.path.abspath(__file__))
+TRAFFIC = os.path.join(ROOT, "profiles", "gateup_T16_traffic.json")
 
 
 def parse():
@@ -55,6 +57,20 @@ def gateup_bytes(cfg, plan, tokens):
     rows = plan["total_rows"]
     return (plan["n_slots"] * per_slot + tokens * (cfg.hidden + cfg.hidden // 32)
             + rows * (cfg.intermediate + cfg.intermediate // 32))
+
+
+def measured_traffic(algorithmic):
+    """HBM bytes per gate/up launch at T=16 from the committed counter runs (FETCH_SIZE + WRITE_SIZE per
+    dispatch, each divided by the copy-kernel calibration factor), or None when they do not describe this
+    workload (different algorithmic byte count)."""
+    try:
+        with open(TRAFFIC) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if rec.get("algorithmic_bytes") != algorithmic:
+        return None
+    return rec.get("traffic_bytes")
 
 
 def cpu_baseline(layer, bank, w, x_rows, cfg):
@@ -147,14 +163,12 @@ def main():
         us = ctx.elapsed_ms(start, stop) / args.steps * 1000
         b = algorithmic_bytes(cfg, plans[t], t)
         step_bytes += b
-        layer.profile(True)
-        for _ in range(args.profile_iters):
-            layer.decode_device(xs[t].ptr, t, ys[t].ptr, stream)
-        prof = layer.profile(False)
+        # each stage re-launched back to back on the launch stream, HIP events around the loop
+        layer.decode_device(xs[t].ptr, t, ys[t].ptr, stream)
+        kernel_us = {stage: layer.time_stage(stage, args.profile_iters, stream) for stage in layer.STAGES}
         per_t[t] = {"us_per_layer": us, "distinct_experts": plans[t]["n_routed"], "bytes": b,
                     "GB_per_s": b / (us * 1e-6) / 1e9, "hbm_frac": b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-                    "kernel_us": {k: v * 1000 for k, v in prof.items() if k != "calls"},
-                    "gateup_bytes": gateup_bytes(cfg, plans[t], t)}
+                    "kernel_us": kernel_us, "gateup_bytes": gateup_bytes(cfg, plans[t], t)}
         log(f"T={t}: {us:.1f} us/layer, {per_t[t]['GB_per_s']:.0f} GB/s, kernels {per_t[t]['kernel_us']}")
 
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
@@ -175,7 +189,8 @@ def main():
                       for t, d in per_t.items()},
         "roofline": {"kernel": "gateup_kernel (T=16)", "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "launch_us": round(gu_us, 2), "algorithmic_bytes": head["gateup_bytes"]},
+                     "traffic": measured_traffic(head["gateup_bytes"]), "launch_us": round(gu_us, 2),
+                     "algorithmic_bytes": head["gateup_bytes"]},
         "device": {"name": name, "arch": arch},
     }
     if not args.no_cpu_baseline:

@@ -67,6 +67,10 @@ int mx_stream_wait_event(mx_ctx* ctx, void* stream, void* event);
 /* Deterministic synthetic bytes on the device: dst[i] = lo + hash(seed, i) % (hi - lo + 1). */
 int mx_fill_uniform_u8(mx_ctx* ctx, void* dst, uint64_t bytes, uint64_t seed, uint32_t lo, uint32_t hi, void* stream);
 
+/* Device-side copy by a plain streaming kernel (16 B per thread): the known-size workload used to
+ * calibrate the profiler's HBM byte counters. Pointers 16-byte aligned, bytes a multiple of 16. */
+int mx_copy_kernel(mx_ctx* ctx, void* dst, const void* src, uint64_t bytes, void* stream);
+
 /* ---- format hooks (replaces format_probe.cu decode_fp4/encode_fp8/activation32, lines 23-52) ---- */
 
 /* out[r][k] = E2M1(packed[r][k/2] nibble, low first) * E8M0(scales[r][k/32]); bit-exact. */
@@ -246,6 +250,17 @@ int mx_layer_buffer(mx_layer* layer, int32_t which, void** dptr, uint64_t* bytes
  * when full). Reading (any call) reports stage_ms[0..3] = router, gate/up, down, combine averaged
  * over the calls recorded since profiling was last enabled. */
 int mx_layer_profile(mx_layer* layer, int32_t enable, float* stage_ms, int32_t* calls);
+
+/* Measurement hook: re-launch one stage of the layer's most recent mx_moe_decode call `iters` times
+ * back to back on `stream` (each stage is idempotent given its inputs) and report the average
+ * duration per launch from HIP events around the loop. Stages: MX_STAGE_*. No reference counterpart
+ * (the reference times whole Python calls); used by the benchmark's roofline figure. */
+#define MX_STAGE_ROUTER 0
+#define MX_STAGE_ROUTE_PLAN 1
+#define MX_STAGE_GATEUP 2
+#define MX_STAGE_DOWN 3
+#define MX_STAGE_COMBINE 4
+int mx_layer_time_stage(mx_layer* layer, int32_t stage, int32_t iters, float* us_per_launch, void* stream);
 
 #ifdef __cplusplus
 }

@@ -164,12 +164,14 @@ __device__ void topk_token_wave_t(const float* __restrict__ selection, const flo
   const int lane = threadIdx.x & 63;
   const int per = kPer;
   uint32_t key[kPer];
-  float sel[kPer];
+  float sel[kPer], scr[kPer];
+  // the raw scores are loaded with the selection values (no dependent load after the sort)
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
     const int e = lane * per + j;
     const bool ok = e < E;
     sel[j] = ok ? selection[e] : 0.f;
+    scr[j] = ok ? scores[e] : 0.f;
     key[j] = ok ? ordered_key(sel[j]) : 0u;
   }
   // 1. threshold search
@@ -253,7 +255,14 @@ __device__ void topk_token_wave_t(const float* __restrict__ selection, const flo
   bitonic_stage<32, 2>(kv, iv, vv, slot);
   bitonic_stage<32, 1>(kv, iv, vv, slot);
   // 4. raw scores, tree denominator, weights
-  float raw = slot < k ? scores[iv] : 0.f;
+  // expert iv's raw score lives in lane iv / kPer, register iv % kPer
+  float raw = 0.f;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const float v = __shfl(scr[j], iv / kPer, 64);
+    raw = (iv % kPer == j) ? v : raw;
+  }
+  raw = slot < k ? raw : 0.f;
   float acc = raw;
   int width = 1;
   while (width < k) width <<= 1;
@@ -294,106 +303,82 @@ __device__ __forceinline__ void topk_token_wave(const float* __restrict__ select
 // ----------------------------------------------------------------------------------------------
 // Plan from the routed IDs (participation, moe.py:18-30): slots are the distinct experts in ascending
 // ID order, each with its tokens ascending; rows are numbered expert-major; the shared expert is the
-// last slot with every token. Run by one workgroup of any multiple of 64 threads up to 1024, all
-// steps parallel (LDS atomics for counts, wavefront scans for slot and row offsets). `ids` and `w`
-// may live in LDS.
-__device__ __forceinline__ int block_exclusive_scan(int v, int tid, int* wave_tot, int* total) {
-  const int lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
-  const int inc = wave_scan_i(v, lane);
-  if (lane == 63) wave_tot[wave] = inc;
-  __syncthreads();
-  int base = 0, all = 0;
-  for (int w = 0; w < nwaves; ++w) {
-    base += w < wave ? wave_tot[w] : 0;
-    all += wave_tot[w];
-  }
-  *total = all;
-  __syncthreads();
-  return base + inc - v;
-}
-
+// last slot with every token.
+//
+// Every routed pair (t, e) has the unique key e * 16 + t, and its row is the key's rank among all
+// T * k keys: sorted by key, the pairs run expert-major with ascending tokens, which is exactly the
+// row order. Ranks, slot numbers and positions are all counts over the staged keys, so the plan is
+// two counting passes with one barrier between them. A group of S = 2^j lanes shares each pair's
+// count and combines it with xor-shuffles. `ids` and `w` are in LDS.
 __device__ void build_plan(Plan* __restrict__ plan, const int32_t* ids, const float* w, int T, int k, int E,
                            int has_shared) {
-  __shared__ int32_t s_ids[kMaxTokens * kMaxTopK];
-  __shared__ int32_t s_row[kMaxTokens * kMaxTopK];
-  __shared__ int32_t cnt[kMaxExperts];
-  __shared__ int32_t slot_of[kMaxExperts];
-  __shared__ int32_t row_of[kMaxExperts];
-  __shared__ int32_t wave_tot[2][kRouteWaves];
+  __shared__ int32_t s_start[kMaxTokens * kMaxTopK];   // 1 where the pair opens its expert's run
   const int tid = threadIdx.x, nth = blockDim.x;
-  const int n = T * k;
-  for (int i = tid; i < n; i += nth) s_ids[i] = ids[i];
-  for (int e = tid; e < E; e += nth) cnt[e] = 0;
-  __syncthreads();
-  for (int i = tid; i < n; i += nth) atomicAdd(&cnt[s_ids[i]], 1);
-  __syncthreads();
-  // slot and row offsets: thread tid owns experts [tid*per, tid*per + per)
-  const int per = (E + nth - 1) / nth;
-  int ns = 0, nr = 0;
-  for (int j = 0; j < per; ++j) {
-    const int e = tid * per + j;
-    if (e < E) { ns += cnt[e] > 0; nr += cnt[e]; }
+  const int n = T * k;   // <= 32 * T <= nth / 2 (the launch has one wave per token)
+  int S = 1;
+  while (S < 64 && 2 * S * n <= nth) S <<= 1;
+  const int p = tid / S, part = tid % S;
+  const bool active = p < n;
+  const int ep = active ? ids[p] : 0, tp = active ? p / k : 0;
+  const int kp = ep * kMaxTokens + tp;
+  int less = 0, same_before = 0, same = 0, tok_before = 0;
+  if (active) {
+    for (int u = part; u < n; u += S) {
+      const int eu = ids[u], tu = u / k, ku = eu * kMaxTokens + tu;
+      less += ku < kp;
+      same_before += (eu == ep) & (tu < tp);
+      same += eu == ep;
+      tok_before += (tu == tp) & (eu < ep);
+    }
   }
-  int n_routed = 0, routed_rows = 0;
-  int slot = block_exclusive_scan(ns, tid, wave_tot[0], &n_routed);
-  int row = block_exclusive_scan(nr, tid, wave_tot[1], &routed_rows);
-  for (int j = 0; j < per; ++j) {
-    const int e = tid * per + j;
-    if (e < E) {
-      slot_of[e] = slot;
-      row_of[e] = row;
-      if (cnt[e] > 0) {
-        plan->slot_expert[slot] = e;
-        plan->slot_ntok[slot] = cnt[e];
-        plan->slot_row0[slot] = row;
-        plan->slot_weighted[slot] = 1;
-        ++slot;
-        row += cnt[e];
+  for (int m = 1; m < S; m <<= 1) {
+    less += __shfl_xor(less, m, 64);
+    same_before += __shfl_xor(same_before, m, 64);
+    same += __shfl_xor(same, m, 64);
+    tok_before += __shfl_xor(tok_before, m, 64);
+  }
+  if (active && part == 0) s_start[p] = same_before == 0;
+  __syncthreads();
+  int slot = 0, routed = 0;
+  if (active) {
+    for (int u = part; u < n; u += S) {
+      const int st = s_start[u];
+      routed += st;
+      slot += st & (ids[u] < ep);
+    }
+  }
+  for (int m = 1; m < S; m <<= 1) {
+    slot += __shfl_xor(slot, m, 64);
+    routed += __shfl_xor(routed, m, 64);
+  }
+  if (active && part == 0) {
+    if (same_before == 0) {
+      plan->slot_expert[slot] = ep;
+      plan->slot_ntok[slot] = same;
+      plan->slot_row0[slot] = less;
+      plan->slot_weighted[slot] = 1;
+    }
+    plan->slot_tok[slot][same_before] = tp;
+    plan->slot_w[slot][same_before] = w[p];
+    plan->tok_rows[tp][tok_before] = less;
+    if (p == 0) {
+      plan->n_routed = routed;
+      plan->n_slots = routed + has_shared;
+      plan->total_rows = n + (has_shared ? T : 0);
+      plan->tokens = T;
+      plan->top_k = k;
+      if (has_shared) {
+        plan->slot_expert[routed] = E;
+        plan->slot_ntok[routed] = T;
+        plan->slot_row0[routed] = n;
+        plan->slot_weighted[routed] = 0;
+        for (int t = 0; t < T; ++t) {
+          plan->slot_tok[routed][t] = t;
+          plan->slot_w[routed][t] = 1.0f;
+          plan->tok_rows[t][k] = n + t;
+        }
       }
     }
-  }
-  if (tid == 0) {
-    plan->n_routed = n_routed;
-    plan->n_slots = n_routed + has_shared;
-    plan->total_rows = routed_rows + (has_shared ? T : 0);
-    plan->tokens = T;
-    plan->top_k = k;
-  }
-  __syncthreads();
-  // each routed pair (t, i): its position among expert e's tokens = tokens t' < t routed to e
-  for (int idx = tid; idx < n; idx += nth) {
-    const int t = idx / k, e = s_ids[idx];
-    int before = 0;
-    for (int u = 0; u < t * k; ++u) before += s_ids[u] == e;
-    const int sl = slot_of[e];
-    plan->slot_tok[sl][before] = t;
-    plan->slot_w[sl][before] = w[idx];
-    s_row[idx] = row_of[e] + before;
-  }
-  __syncthreads();
-  // each token's rows in ascending expert order (insertion sort of k entries), shared row last
-  if (tid < T) {
-    const int t = tid;
-    int32_t es[kMaxTopK], rs[kMaxTopK];
-    for (int i = 0; i < k; ++i) {
-      const int e = s_ids[t * k + i], r = s_row[t * k + i];
-      int j = i - 1;
-      while (j >= 0 && es[j] > e) { es[j + 1] = es[j]; rs[j + 1] = rs[j]; --j; }
-      es[j + 1] = e;
-      rs[j + 1] = r;
-    }
-    for (int i = 0; i < k; ++i) plan->tok_rows[t][i] = rs[i];
-    if (has_shared) {
-      plan->slot_tok[n_routed][t] = t;
-      plan->slot_w[n_routed][t] = 1.0f;
-      plan->tok_rows[t][k] = T * k + t;
-    }
-  }
-  if (has_shared && tid == 0) {
-    plan->slot_expert[n_routed] = E;
-    plan->slot_ntok[n_routed] = T;
-    plan->slot_row0[n_routed] = T * k;
-    plan->slot_weighted[n_routed] = 0;
   }
 }
 
@@ -511,18 +496,18 @@ __global__ __launch_bounds__(256) void router_kernel(RouterArgs a) {
   }
 }
 
-// One workgroup: wave t ranks token t (tokens beyond 16 loop), the results are staged in LDS and
-// written out, then the same workgroup builds the plan from the staged IDs.
+// One workgroup of one wave per token: wave t ranks token t, the results are staged in LDS and written
+// out, then the same workgroup builds the plan from the staged IDs.
 __global__ __launch_bounds__(kRouteThreads) void route_plan_kernel(const float* selection, const float* scores, int T,
                                                                    int E, int k, float route_scale, TopkOut o,
                                                                    Plan* plan, int has_shared) {
   __shared__ int32_t s_idx[kMaxTokens * kMaxTopK];
   __shared__ float s_w[kMaxTokens * kMaxTopK];
   const TopkOut staged{s_idx, s_w, o.raw, o.den, o.tied};
-  for (int t = threadIdx.x >> 6; t < T; t += kRouteWaves)
-    topk_token_wave(selection + (size_t)t * E, scores + (size_t)t * E, E, k, route_scale, t, staged);
+  const int t = threadIdx.x >> 6;
+  topk_token_wave(selection + (size_t)t * E, scores + (size_t)t * E, E, k, route_scale, t, staged);
   __syncthreads();
-  for (int i = threadIdx.x; i < T * k; i += kRouteThreads) {
+  for (int i = threadIdx.x; i < T * k; i += blockDim.x) {
     o.indices[i] = s_idx[i];
     o.weights[i] = s_w[i];
   }
@@ -953,23 +938,33 @@ __global__ void tile_expert_kernel(mx_expert_ptrs ref, uint8_t* blob, int H, int
 }
 
 // Ordered combine (aggregation_probe.cu:4-25): per token, FP32 sum from +0 of its expert rows in
-// ascending expert ID, the shared row last, one BF16 rounding. 8 hidden positions per thread.
-__global__ void combine_kernel(const Plan* __restrict__ plan, const uint16_t* __restrict__ rows, int H, int k,
-                               int has_shared, uint16_t* __restrict__ y) {
+// ascending expert ID, the shared row last, one BF16 rounding. grid (H / 512, T) of 64 threads, 8
+// hidden positions per thread; every row's load is issued before the first add (one memory round trip).
+constexpr int kCombineThreads = 64;
+
+__global__ __launch_bounds__(kCombineThreads) void combine_kernel(const Plan* __restrict__ plan,
+                                                                  const uint16_t* __restrict__ rows, int H, int k,
+                                                                  int has_shared, uint16_t* __restrict__ y) {
   const int t = blockIdx.y;
-  const int h = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  const int h = (blockIdx.x * kCombineThreads + threadIdx.x) * 8;
   if (t >= plan->tokens || h >= H) return;
+  const int n = k + has_shared;
+  uint4 v[kMaxTopK + 1];
+#pragma unroll
+  for (int i = 0; i < kMaxTopK + 1; ++i)
+    if (i < n) v[i] = *reinterpret_cast<const uint4*>(rows + (size_t)plan->tok_rows[t][i] * H + h);
   float acc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0.f;
-  const int n = k + has_shared;
-  for (int i = 0; i < n; ++i) {
-    const uint4 v = *reinterpret_cast<const uint4*>(rows + (size_t)plan->tok_rows[t][i] * H + h);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      acc[2 * j] = acc[2 * j] + mx::bf16_value(w[j] & 0xFFFFu);
-      acc[2 * j + 1] = acc[2 * j + 1] + mx::bf16_value(w[j] >> 16);
+  for (int i = 0; i < kMaxTopK + 1; ++i) {
+    if (i < n) {
+      const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[2 * j] = acc[2 * j] + mx::bf16_value(w[j] & 0xFFFFu);
+        acc[2 * j + 1] = acc[2 * j + 1] + mx::bf16_value(w[j] >> 16);
+      }
     }
   }
   uint4 o;
@@ -1037,6 +1032,11 @@ struct mx_layer {
   uint16_t *w1 = nullptr, *w3 = nullptr, *din = nullptr, *eout = nullptr;
   Plan* plan = nullptr;
   int max_rows = 0;
+  // the most recent decode call (mx_layer_time_stage repeats its stages)
+  const uint16_t* last_x = nullptr;
+  uint16_t* last_y = nullptr;
+  int last_T = 0;
+  bool last_diag = false;
   std::vector<std::pair<void*, uint64_t>> allocs;
   // profiling: events bracket each kernel of a call; a ring of kProfRing calls is recorded without
   // host synchronisation and folded into the totals when full or when the profile is read.
@@ -1102,6 +1102,73 @@ int validate_config(const mx_moe_config* c) {
   MX_REQUIRE(c->shared_format == -1 || c->shared_format == MX_FMT_MXFP4,
              "shared expert format must be none or MXFP4 in the decode layer");
   MX_REQUIRE(c->max_tokens >= 1 && c->max_tokens <= kMaxTokens, "max_tokens must be in [1, %d]", kMaxTokens);
+  return MX_OK;
+}
+
+// One stage of a decode call on the arguments recorded in L->last_*.
+int launch_stage(mx_layer* L, int stage, hipStream_t st) {
+  const mx_moe_config& c = L->cfg;
+  const int T = L->last_T;
+  if (stage == MX_STAGE_ROUTER) {
+    RouterArgs r{};
+    r.W = L->router_weight;
+    r.bias = L->bias;
+    r.x = L->last_x;
+    r.T = T;
+    r.H = c.hidden;
+    r.E = c.experts;
+    r.k = c.top_k;
+    r.score_func = c.score_func;
+    r.route_scale = c.route_scale;
+    r.logits = L->logits;
+    r.scores = L->scores;
+    r.selection = L->selection;
+    r.xq = L->xq;
+    r.xs = L->xs;
+    hipLaunchKernelGGL(router_kernel, dim3(c.experts, 1), dim3(256), 0, st, r);
+    MX_LAUNCH_CHECK("router_kernel");
+    return MX_OK;
+  }
+  if (stage == MX_STAGE_ROUTE_PLAN) {
+    hipLaunchKernelGGL(route_plan_kernel, dim3(1), dim3(64 * T), 0, st, (const float*)L->selection,
+                       (const float*)L->scores, T, c.experts, c.top_k, c.route_scale,
+                       TopkOut{L->indices, L->weights, L->raw, L->den, L->tied}, L->plan, L->has_shared);
+    MX_LAUNCH_CHECK("route_plan_kernel");
+    return MX_OK;
+  }
+  if (stage == MX_STAGE_COMBINE) {
+    hipLaunchKernelGGL(combine_kernel, dim3((c.hidden / 8 + kCombineThreads - 1) / kCombineThreads, T),
+                       dim3(kCombineThreads), 0, st, (const Plan*)L->plan, (const uint16_t*)L->eout, c.hidden,
+                       c.top_k, L->has_shared, L->last_y);
+    MX_LAUNCH_CHECK("combine_kernel");
+    return MX_OK;
+  }
+  ExpertArgs a{};
+  a.tiles = L->tiles;
+  a.plan = L->plan;
+  a.H = c.hidden;
+  a.I = c.intermediate;
+  a.limit = c.swiglu_limit;
+  a.xq = L->xq;
+  a.xs = L->xs;
+  a.dq = L->dq;
+  a.ds = L->ds;
+  a.out = L->eout;
+  if (L->last_diag) {
+    a.w1 = L->w1;
+    a.w3 = L->w3;
+    a.din = L->din;
+    a.trace = L->trace;
+  }
+  // grid rows beyond the plan's slot count exit at once
+  const int slots = std::min(c.experts, T * c.top_k) + L->has_shared;
+  if (stage == MX_STAGE_GATEUP) {
+    hipLaunchKernelGGL(gateup_kernel<true>, dim3(c.intermediate / 32, slots), dim3(256), 0, st, a);
+    MX_LAUNCH_CHECK("gateup_kernel");
+  } else {
+    hipLaunchKernelGGL(down_kernel<true>, dim3(c.hidden / 64, slots), dim3(256), 0, st, a);
+    MX_LAUNCH_CHECK("down_kernel");
+  }
   return MX_OK;
 }
 
@@ -1255,59 +1322,42 @@ int mx_moe_decode(mx_layer* L, const uint16_t* x, int32_t T, uint16_t* y, int32_
     ev = &L->ev[L->pending * 5];
     MX_HIP(hipEventRecord(ev[0], st));
   }
-  RouterArgs r{};
-  r.W = L->router_weight;
-  r.bias = L->bias;
-  r.x = x;
-  r.T = T;
-  r.H = c.hidden;
-  r.E = c.experts;
-  r.k = c.top_k;
-  r.score_func = c.score_func;
-  r.route_scale = c.route_scale;
-  r.logits = L->logits;
-  r.scores = L->scores;
-  r.selection = L->selection;
-  r.xq = L->xq;
-  r.xs = L->xs;
-  hipLaunchKernelGGL(router_kernel, dim3(c.experts, 1), dim3(256), 0, st, r);
-  MX_LAUNCH_CHECK("router_kernel");
-  hipLaunchKernelGGL(route_plan_kernel, dim3(1), dim3(kRouteThreads), 0, st, (const float*)L->selection,
-                     (const float*)L->scores, T, c.experts, c.top_k, c.route_scale,
-                     TopkOut{L->indices, L->weights, L->raw, L->den, L->tied}, L->plan, L->has_shared);
-  MX_LAUNCH_CHECK("route_plan_kernel");
-  if (prof) MX_HIP(hipEventRecord(ev[1], st));
-  ExpertArgs a{};
-  a.tiles = L->tiles;
-  a.plan = L->plan;
-  a.H = c.hidden;
-  a.I = c.intermediate;
-  a.limit = c.swiglu_limit;
-  a.xq = L->xq;
-  a.xs = L->xs;
-  a.dq = L->dq;
-  a.ds = L->ds;
-  a.out = L->eout;
-  if (diagnostics) {
-    a.w1 = L->w1;
-    a.w3 = L->w3;
-    a.din = L->din;
-    a.trace = L->trace;
+  L->last_x = x;
+  L->last_y = y;
+  L->last_T = T;
+  L->last_diag = diagnostics != 0;
+  // event i + 1 closes profiled stage i: router (GEMV + top-k/plan), gate/up, down, combine
+  static const int kEventAfter[5] = {-1, 1, 2, 3, 4};
+  for (int stage = 0; stage < 5; ++stage) {
+    if (int s2 = launch_stage(L, stage, st)) return s2;
+    if (prof && kEventAfter[stage] > 0) MX_HIP(hipEventRecord(ev[kEventAfter[stage]], st));
   }
-  const int slots = std::min(c.experts, T * c.top_k) + L->has_shared;
-  hipLaunchKernelGGL(gateup_kernel<true>, dim3(c.intermediate / 32, slots), dim3(256), 0, st, a);
-  MX_LAUNCH_CHECK("gateup_kernel");
-  if (prof) MX_HIP(hipEventRecord(ev[2], st));
-  hipLaunchKernelGGL(down_kernel<true>, dim3(c.hidden / 64, slots), dim3(256), 0, st, a);
-  MX_LAUNCH_CHECK("down_kernel");
-  if (prof) MX_HIP(hipEventRecord(ev[3], st));
-  hipLaunchKernelGGL(combine_kernel, dim3((c.hidden / 8 + 255) / 256, T), dim3(256), 0, st, (const Plan*)L->plan,
-                     (const uint16_t*)L->eout, c.hidden, c.top_k, L->has_shared, y);
-  MX_LAUNCH_CHECK("combine_kernel");
-  if (prof) {
-    MX_HIP(hipEventRecord(ev[4], st));
-    ++L->pending;
-  }
+  if (prof) ++L->pending;
+  return MX_OK;
+}
+
+int mx_layer_time_stage(mx_layer* L, int32_t stage, int32_t iters, float* us_per_launch, void* stream) {
+  MX_REQUIRE(L != nullptr, "layer is closed");
+  if (int s = use(L->ctx)) return s;
+  MX_REQUIRE(L->last_T > 0, "mx_layer_time_stage: no decode call to repeat yet");
+  MX_REQUIRE(stage >= MX_STAGE_ROUTER && stage <= MX_STAGE_COMBINE, "unknown stage %d", stage);
+  MX_REQUIRE(iters >= 1 && us_per_launch != nullptr, "mx_layer_time_stage: need iters >= 1 and an output");
+  hipStream_t st = as_stream(stream);
+  hipEvent_t a = nullptr, b = nullptr;
+  MX_HIP(hipEventCreate(&a));
+  hipError_t err = hipEventCreate(&b);
+  int status = MX_OK;
+  if (err == hipSuccess) err = hipEventRecord(a, st);
+  for (int i = 0; err == hipSuccess && status == MX_OK && i < iters; ++i) status = launch_stage(L, stage, st);
+  if (err == hipSuccess && status == MX_OK) err = hipEventRecord(b, st);
+  if (err == hipSuccess && status == MX_OK) err = hipEventSynchronize(b);
+  float ms = 0.f;
+  if (err == hipSuccess && status == MX_OK) err = hipEventElapsedTime(&ms, a, b);
+  (void)hipEventDestroy(a);
+  if (b) (void)hipEventDestroy(b);
+  if (status != MX_OK) return status;
+  if (err != hipSuccess) return hip_fail(err, "mx_layer_time_stage");
+  *us_per_launch = ms * 1000.f / (float)iters;
   return MX_OK;
 }
 

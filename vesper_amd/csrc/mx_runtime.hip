@@ -281,3 +281,25 @@ extern "C" int mx_fill_uniform_u8(mx_ctx* ctx, void* dst, uint64_t bytes, uint64
   MX_LAUNCH_CHECK("fill_uniform_u8_kernel");
   return MX_OK;
 }
+
+// Plain streaming copy, 16 bytes per thread per step: the known-size workload against which the
+// profiler's HBM byte counters (FETCH_SIZE, WRITE_SIZE) are calibrated.
+__global__ void copy_u8x16_kernel(uint4* __restrict__ dst, const uint4* __restrict__ src, uint64_t n16) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
+}
+
+extern "C" int mx_copy_kernel(mx_ctx* ctx, void* dst, const void* src, uint64_t bytes, void* stream) {
+  if (int s = use(ctx)) return s;
+  MX_REQUIRE(dst != nullptr && src != nullptr, "mx_copy_kernel: null pointer");
+  MX_REQUIRE(((uintptr_t)dst & 15) == 0 && ((uintptr_t)src & 15) == 0 && bytes % 16 == 0,
+             "mx_copy_kernel: 16-byte aligned pointers and a multiple of 16 bytes required");
+  if (!bytes) return MX_OK;
+  const uint64_t n16 = bytes / 16;
+  const uint64_t want = (n16 + 255) / 256;
+  const unsigned blocks = (unsigned)(want < 8192 ? want : 8192);
+  hipLaunchKernelGGL(copy_u8x16_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), (uint4*)dst,
+                     (const uint4*)src, n16);
+  MX_LAUNCH_CHECK("copy_u8x16_kernel");
+  return MX_OK;
+}

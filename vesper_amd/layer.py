@@ -208,6 +208,15 @@ class MoELayer:
         p, n = self.buffer("plan")
         return _plan_views(self.ctx.download(p, (n,), np.uint8))
 
+    STAGES = {"router": 0, "route_plan": 1, "gateup": 2, "down": 3, "combine": 4}
+
+    def time_stage(self, stage: str, iters: int = 20, stream=None) -> float:
+        """Average us per launch of one stage of the most recent decode call, re-launched `iters` times
+        back to back with HIP events around the loop (mx_layer_time_stage)."""
+        us = C.c_float()
+        self.lib.layer_time_stage(self.handle, self.STAGES[stage], int(iters), C.byref(us), _lib._stream(stream))
+        return float(us.value)
+
     def profile(self, enable: bool):
         ms = (C.c_float * 4)()
         calls = C.c_int32()
