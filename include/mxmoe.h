@@ -188,6 +188,32 @@ int mx_router_postprocess(mx_ctx* ctx, const float* logits, const float* bias, i
 int mx_router_select(mx_ctx* ctx, const float* scores, const float* selection, int32_t tokens, int32_t experts,
                      int32_t top_k, float route_scale, const mx_router_out* out, void* stream);
 
+/* ---- FP8 E4M3 block-scaled projections (replaces NativeProjections.fp8, src/vesper/projections.py:135-154,
+ *      and projection_fp8, src/vesper/kernels/projection_probe.cu:9-51) ----
+ *
+ * block 32:  weight E8M0 scales [N/32][K/32] (the reference's layout), activations per-32 E8M0
+ *            (mx_act_quant32); the scales are applied inside the scaled MFMA (exact powers of two).
+ * block 128: weight FP32 scales [ceil(N/128)][K/128], activations per-token per-128 FP32
+ *            (mx_act_quant128); per 128-wide chunk acc += (dot * sa) * sw in FP32.
+ * Weights are tiled once (mx_fp8_tile) into 64-row groups of MFMA-ordered 1 KB pieces plus scales.
+ * N % 64 == 0, K % 128 == 0. */
+
+#define MX_FP8_BLOCK32 32
+#define MX_FP8_BLOCK128 128
+/* Bytes of a tiled FP8 weight (0 for unsupported shapes or block). */
+uint64_t mx_fp8_tiled_bytes(int32_t n, int32_t k, int32_t block);
+/* Reference layout (E4M3 codes [N][K] + scales) -> tiled blob (256-byte aligned device memory). */
+int mx_fp8_tile(mx_ctx* ctx, const uint8_t* weight, const void* scales, int32_t n, int32_t k, int32_t block,
+                void* tiled, void* stream);
+/* Per-token per-128 quantizer of BF16 x [rows][width]: q E4M3 codes, s FP32 = max(amax, 1e-4) / 448. */
+int mx_act_quant128(mx_ctx* ctx, const uint16_t* x_bf16, uint8_t* q, float* s, int64_t rows, int64_t width,
+                    void* stream);
+/* y[T][N] (BF16) = projection of x[T][H=K] (BF16): quantize with the block's activation quantizer, then the
+ * block-scaled product. Optional outputs: trace [T][N] FP32 sums, q_out [T][K] codes, s_out scales
+ * ([T][K/32] E8M0 or [T][K/128] FP32) -- the stage dict of projections.py:146-154. */
+int mx_fp8_projection(mx_ctx* ctx, const void* tiled, int32_t n, int32_t k, int32_t block, const uint16_t* x_bf16,
+                      int32_t tokens, uint16_t* y_bf16, float* trace, uint8_t* q_out, void* s_out, void* stream);
+
 /* ---- ordered combine (replaces MoEAccumulator, src/vesper/moe.py:42-148, aggregation_probe.cu:4-25) ---- */
 
 int mx_acc_zero(mx_ctx* ctx, float* sum, int64_t count, void* stream);                     /* moe_zero       */

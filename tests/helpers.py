@@ -38,16 +38,19 @@ def bf16_ulp_diff(a, b) -> np.ndarray:
     return np.abs(key(a) - key(b))
 
 
-def assert_gemv_close(got, ref, what=""):
+def assert_gemv_close(got, ref, what="", min_equal=0.97):
     """GEMV outputs from a different FP32 summation order than the in-order oracle: almost all BF16
     results identical, and every difference within 2^-7 of the row's largest magnitude (an ulp bound
-    is meaningless where a sum cancels to near zero)."""
+    is meaningless where a sum cancels to near zero). `min_equal` is 0.97 for E2M1 x E4M3 products
+    (5 significant bits); FP8 x FP8 products carry 8, so a reordered FP32 sum rounds differently more
+    often and those callers pass 0.95."""
     ulps = bf16_ulp_diff(got, ref)
     equal = float(np.mean(ulps == 0))
     g, r = as_f64(got), as_f64(ref)
     scale = np.max(np.abs(r), axis=-1, keepdims=True)
     worst = float(np.max(np.abs(g - r) / np.maximum(scale, 1e-30)))
-    assert equal >= 0.97 and worst <= 2 ** -7, f"{what}: equal fraction {equal:.4f}, worst normwise diff {worst:.3e}"
+    assert equal >= min_equal and worst <= 2 ** -7, \
+        f"{what}: equal fraction {equal:.4f}, worst normwise diff {worst:.3e}"
 
 
 def exact_activation(rng, tokens, hidden):

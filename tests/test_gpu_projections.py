@@ -1,0 +1,172 @@
+"""GPU parity of the FP8 block-scaled projections (NativeProjections.fp8, projections.py:135-154).
+
+* The per-128 activation quantizer: bit-exact against the oracle (codes and FP32 scales).
+* The tiled weight layout: against an independent NumPy construction from its definition.
+* The product: exact on designed inputs whose every partial sum is representable (both profiles), so
+  the operand layouts, scale placement and the (d * sa) * sw order are pinned bit for bit; random
+  inputs within the GEMV bar; configuration-3 and reference shapes within the north-star tolerance.
+"""
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle.formats import bf16_bits, bf16_values, encode_e4m3, quantize_activation
+from oracle.projections import (CONFIG3_LAYOUT, fp8_block128_gemm_fp32, fp8_projection, fp8_weights,
+                                quantize_activation_128)
+from tests.helpers import assert_close, assert_gemv_close
+from vesper_amd import _lib
+from vesper_amd.projections import FP8_LAYOUT, NativeProjections
+
+pytestmark = pytest.mark.gpu
+
+
+def tile_numpy(w, sw, block):
+    n, k = w.shape
+    g, c, t, h, l = np.meshgrid(np.arange(n // 64), np.arange(k // 128), np.arange(4), np.arange(2), np.arange(64),
+                                indexing="ij")
+    rows = 64 * g + 16 * t + (l % 16)
+    k0 = 128 * c + 64 * h + 16 * (l // 16)
+    pieces = w[rows[..., None], k0[..., None] + np.arange(16)]
+    out = [pieces.reshape(-1)]
+    if block == 32:
+        g, c, l = np.meshgrid(np.arange(n // 64), np.arange(k // 128), np.arange(64), indexing="ij")
+        word = np.zeros(g.shape, np.uint32)
+        for t in range(4):
+            word |= sw[(64 * g + 16 * t) // 32, 4 * c + l // 16].astype(np.uint32) << (8 * t)
+        out.append(word.reshape(-1).view(np.uint8))
+    else:
+        out.append(np.ascontiguousarray(sw, np.float32).reshape(-1).view(np.uint8))
+    return np.concatenate(out)                               # the blob's tail padding is not defined
+
+
+def arrays_for(layout, block, rng, layer=0):
+    arrays = {}
+    for name, (rows, width) in layout.items():
+        w, s = fp8_weights(rng, rows, width, block)
+        arrays[f"layers.{layer}.attn.{name}.weight"] = w
+        arrays[f"layers.{layer}.attn.{name}.scale"] = s
+    return arrays
+
+
+def test_act_quant128_bit_exact(gpu_ctx):
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((9, 1024)).astype(np.float32)
+    x *= np.ldexp(np.ones((9, 1), np.float32), rng.integers(-30, 10, (9, 1)))
+    x[0] = 0
+    x[1, :128] = 448.0
+    x[2, 256:384] = -1e-7
+    bits = bf16_bits(x)
+    xd = gpu_ctx.upload(bits)
+    q = gpu_ctx.empty((9, 1024), np.uint8)
+    s = gpu_ctx.empty((9, 8), np.float32)
+    gpu_ctx.lib.act_quant128(gpu_ctx._h(), _lib.vp(xd), _lib.vp(q), _lib.vp(s), 9, 1024, None)
+    q_ref, s_ref = quantize_activation_128(bf16_values(bits))
+    np.testing.assert_array_equal(s.download().view(np.uint32), s_ref.view(np.uint32))
+    np.testing.assert_array_equal(q.download(), q_ref)
+    for d in (xd, q, s):
+        d.free()
+
+
+@pytest.mark.parametrize("block", [32, 128])
+def test_tiled_layout_matches_definition(gpu_ctx, block):
+    rng = np.random.default_rng(block)
+    w, sw = fp8_weights(rng, 192, 384, block)
+    wd, sd = gpu_ctx.upload(w), gpu_ctx.upload(sw)
+    n = int(gpu_ctx.lib.cdll.mx_fp8_tiled_bytes(192, 384, block))
+    blob = gpu_ctx.malloc(n)
+    try:
+        gpu_ctx.lib.fp8_tile(gpu_ctx._h(), _lib.vp(wd), _lib.vp(sd), 192, 384, block, C.c_void_p(blob), None)
+        got = gpu_ctx.download(blob, (n,), np.uint8)
+        want = tile_numpy(w, sw, block)
+        assert n == (len(want) + 255) // 256 * 256
+        np.testing.assert_array_equal(got[:len(want)], want)
+    finally:
+        gpu_ctx.free(blob)
+        wd.free()
+        sd.free()
+
+
+def run_projection(block, w, sw, x_bits):
+    rows, width = w.shape
+    layout = {"p": (rows, width)}
+    arrays = {"layers.0.attn.p.weight": w, "layers.0.attn.p.scale": sw}
+    with NativeProjections(arrays, block=block, layout=layout) as proj:
+        return proj.fp8("p", x_bits)
+
+
+@pytest.mark.parametrize("block", [32, 128])
+@pytest.mark.parametrize("tokens", [1, 5, 16, 21])
+def test_exact_on_representable_inputs(block, tokens):
+    """Small-integer codes, power-of-two scales: every partial sum is exact, so any order gives the
+    same FP32 result and the trace must equal the oracle bit for bit."""
+    rng = np.random.default_rng(block * 100 + tokens)
+    rows, width = 128, 512
+    w = encode_e4m3(rng.integers(-8, 9, (rows, width)).astype(np.float32))
+    if block == 32:
+        sw = rng.integers(125, 130, (rows // 32, width // 32), dtype=np.uint8)
+        x = rng.integers(-16, 17, (tokens, width)).astype(np.float32)
+        x[:, ::32] = 448.0                                   # per-32 scale 2^0: codes are the integers
+    else:
+        sw = np.exp2(rng.integers(-8, -2, ((rows + 127) // 128, width // 128))).astype(np.float32)
+        x = rng.integers(-16, 17, (tokens, width)).astype(np.float32)
+        x[:, ::128] = 448.0                                  # per-128 scale exactly 1
+    bits = bf16_bits(x)
+    got = run_projection(block, w, sw, bits)
+    ref = fp8_projection(bf16_values(bits), w, sw, block)
+    np.testing.assert_array_equal(got["input_fp8"], ref["input_fp8"])
+    scale_key = "scale_e8m0" if block == 32 else "scale_f32"
+    np.testing.assert_array_equal(got[scale_key].view(np.uint8), np.asarray(ref["scale"]).view(np.uint8))
+    np.testing.assert_array_equal(got["output_fp32"].view(np.uint32), ref["output_fp32"].view(np.uint32))
+    np.testing.assert_array_equal(got["output_bf16"], ref["output_bf16"])
+
+
+@pytest.mark.parametrize("block", [32, 128])
+def test_random_inputs_close_to_ordered_sum(block):
+    rng = np.random.default_rng(11 + block)
+    w, sw = fp8_weights(rng, 320, 2048, block)
+    bits = bf16_bits(rng.standard_normal((7, 2048)).astype(np.float32))
+    got = run_projection(block, w, sw, bits)
+    ref = fp8_projection(bf16_values(bits), w, sw, block)
+    np.testing.assert_array_equal(got["input_fp8"], ref["input_fp8"])
+    assert_gemv_close(got["output_bf16"], ref["output_bf16"], f"block {block}", min_equal=0.95)
+    assert_close(got["output_bf16"], ref["output_bf16"], f"block {block}")
+
+
+@pytest.mark.parametrize("tokens", [1, 16])
+def test_config3_projections_within_tolerance(tokens):
+    rng = np.random.default_rng(20261018 + tokens)
+    arrays = arrays_for(CONFIG3_LAYOUT, 128, rng)
+    x = {name: bf16_bits(rng.standard_normal((tokens, width)).astype(np.float32))
+         for name, (_, width) in CONFIG3_LAYOUT.items()}
+    with NativeProjections(arrays, block=128) as proj:
+        for name, (rows, width) in CONFIG3_LAYOUT.items():
+            got = proj.fp8(name, x[name])
+            ref = fp8_projection(bf16_values(x[name]), arrays[f"layers.0.attn.{name}.weight"],
+                                 arrays[f"layers.0.attn.{name}.scale"], 128)
+            assert got["output_bf16"].shape == (tokens, rows)
+            np.testing.assert_array_equal(got["input_fp8"], ref["input_fp8"])
+            assert_close(got["output_bf16"], ref["output_bf16"], name)
+
+
+def test_reference_shapes_block32_and_refusals():
+    rng = np.random.default_rng(5)
+    arrays = arrays_for(FP8_LAYOUT, 32, rng)
+    with NativeProjections(arrays, block=32) as proj:
+        x = bf16_bits(rng.standard_normal((2, 4, 5120)).astype(np.float32))
+        got = proj.fp8("wq_a", x)
+        assert got["output_bf16"].shape == (2, 4, 1280) and got["scale_e8m0"].shape == (2, 4, 160)
+        ref = fp8_projection(bf16_values(x.reshape(8, 5120)), arrays["layers.0.attn.wq_a.weight"],
+                             arrays["layers.0.attn.wq_a.scale"], 32)
+        assert_close(got["output_bf16"].reshape(8, 1280), ref["output_bf16"], "wq_a")
+        with pytest.raises(ValueError):
+            proj.fp8("wq_a", x.astype(np.float32))
+        with pytest.raises(ValueError):
+            proj.fp8("wq_a", np.full((1, 5120), 0x7F80, np.uint16))
+        with pytest.raises(ValueError):
+            proj.fp8("wo_a", x)
+    bad = dict(arrays)
+    bad["layers.0.attn.wkv.scale"] = np.full((16, 160), 255, np.uint8)
+    with pytest.raises(ValueError):
+        NativeProjections(bad, block=32)

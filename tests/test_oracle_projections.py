@@ -1,0 +1,106 @@
+"""The FP8 projection oracle (oracle/projections.py), pinned independently of its own formulas."""
+
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+from oracle.formats import e4m3_values, encode_e4m3, fp8_block32_gemv_fp32
+from oracle.projections import (CONFIG3_LAYOUT, fp8_block128_gemm_fp32, fp8_projection, fp8_reference_fp32,
+                                fp8_weights, quantize_activation_128)
+
+
+def small_int_codes(rng, shape, lo=-8, hi=8):
+    """E4M3 codes of small integers (exactly representable)."""
+    return encode_e4m3(rng.integers(lo, hi + 1, shape).astype(np.float32))
+
+
+def test_quantizer_closed_form_cases():
+    x = np.zeros((3, 256), np.float32)
+    x[1, :128] = np.linspace(-448, 448, 128, dtype=np.float32)       # amax 448 -> scale exactly 1
+    x[2, 128:] = 1e-6                                                # below the floor
+    q, s = quantize_activation_128(x)
+    assert s.dtype == np.float32 and s.shape == (3, 2)
+    floor_scale = np.float32(np.float32(1e-4) / np.float32(448))
+    assert s[0, 0] == floor_scale and np.all(q[0] == 0)
+    assert s[1, 0] == np.float32(1.0)
+    np.testing.assert_array_equal(q[1, :128], encode_e4m3(x[1, :128]))
+    assert s[2, 1] == floor_scale
+    # every code times its scale is within half an E4M3 step of the input (relative 2^-4)
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((4, 512)).astype(np.float32) * 3
+    q, s = quantize_activation_128(x)
+    back = e4m3_values(q).reshape(4, 4, 128) * s[..., None]
+    err = np.abs(back.reshape(4, 512) - x)
+    assert np.all(err <= np.maximum(np.abs(x) * 2.0 ** -4, np.repeat(s, 128, 1) * 2.0 ** -10))
+
+
+def test_block128_gemm_equals_integer_matmul_on_unit_scales():
+    rng = np.random.default_rng(2)
+    q = small_int_codes(rng, (5, 384))
+    w = small_int_codes(rng, (200, 384))
+    got = fp8_block128_gemm_fp32(q, np.ones((5, 3), np.float32), w, np.ones((2, 3), np.float32))
+    ints = e4m3_values(q).astype(np.int64) @ e4m3_values(w).astype(np.int64).T
+    np.testing.assert_array_equal(got, ints.astype(np.float32))
+
+
+def test_block128_scaling_is_per_block_and_in_order():
+    """One nonzero K block per weight row: the result is the exact rational ((d * sa) * sw) rounded
+    at each step, computed here with Fractions."""
+    rng = np.random.default_rng(3)
+    t, n, k = 2, 130, 256
+    q = encode_e4m3(rng.standard_normal((t, k)).astype(np.float32))
+    w = np.zeros((n, k), np.uint8)
+    blocks = rng.integers(0, 2, n)
+    for r in range(n):
+        w[r, 128 * blocks[r]:128 * blocks[r] + 128] = encode_e4m3(rng.standard_normal(128).astype(np.float32))
+    sa = np.exp2(rng.integers(-6, 6, (t, 2))).astype(np.float32) * np.float32(1.5)
+    sw = np.exp2(rng.uniform(-8, -2, (2, 2))).astype(np.float32)
+    got = fp8_block128_gemm_fp32(q, sa, w, sw)
+    for i in range(t):
+        for r in range(n):
+            g = blocks[r]
+            d = sum(Fraction(float(a)) * Fraction(float(b)) for a, b in
+                    zip(e4m3_values(q[i, 128 * g:128 * g + 128]), e4m3_values(w[r, 128 * g:128 * g + 128])))
+            d32 = np.float32(float(d))
+            want = np.float32(np.float32(d32 * sa[i, g]) * sw[r // 128, g])
+            assert got[i, r] == want
+
+
+def test_profiles_agree_on_unit_scales_and_exact_inputs():
+    """Block 32 (E8M0 127 = 1.0) and block 128 (FP32 1.0) give identical sums on integer inputs."""
+    rng = np.random.default_rng(4)
+    q = small_int_codes(rng, (3, 512))
+    w = small_int_codes(rng, (128, 512))
+    b32 = fp8_block32_gemv_fp32(q, np.full((3, 16), 127, np.uint8), w, np.full((4, 16), 127, np.uint8))
+    b128 = fp8_block128_gemm_fp32(q, np.ones((3, 4), np.float32), w, np.ones((1, 4), np.float32))
+    np.testing.assert_array_equal(b32, b128)
+
+
+def test_linearity_in_power_of_two_weight_scales():
+    rng = np.random.default_rng(5)
+    w, sw = fp8_weights(rng, 256, 256, 128)
+    x = rng.standard_normal((2, 256)).astype(np.float32)
+    a = fp8_projection(x, w, sw, 128)["output_fp32"]
+    b = fp8_projection(x, w, sw * np.float32(4), 128)["output_fp32"]
+    np.testing.assert_array_equal(b, a * np.float32(4))
+
+
+@pytest.mark.parametrize("block", [32, 128])
+def test_projection_tracks_the_unquantized_product(block):
+    rng = np.random.default_rng(6 + block)
+    w, sw = fp8_weights(rng, 256, 1024, block)
+    x = rng.standard_normal((4, 1024)).astype(np.float32)
+    got = fp8_projection(x, w, sw, block)["output_fp32"].astype(np.float64)
+    ref = fp8_reference_fp32(x, w, sw, block).astype(np.float64)
+    cos = float((got * ref).sum() / np.sqrt((got * got).sum() * (ref * ref).sum()))
+    assert cos > 0.999
+
+
+def test_config3_layout_and_weights():
+    assert CONFIG3_LAYOUT == {"q_a": (1536, 7168), "q_b": (24576, 1536), "kv_a": (576, 7168), "o": (7168, 16384)}
+    total = sum(r * c for r, c in CONFIG3_LAYOUT.values())
+    assert total == 170_328_064
+    w, s = fp8_weights(np.random.default_rng(0), 576, 256, 128)
+    assert s.shape == (5, 2) and np.all((w & 0x7F) != 0x7F)
+    assert np.all((s >= 2.0 ** -8) & (s <= 2.0 ** -2))

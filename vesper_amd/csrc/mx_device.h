@@ -1,0 +1,45 @@
+// Device-side helpers shared by the kernel translation units (gfx950 only).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mxd {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// Loads through the global address space. Pointers that come from device tables or structs are
+// otherwise treated as generic (flat) addresses.
+__device__ __forceinline__ uint32_t ldg32(const uint8_t* p) {
+  return *(const __attribute__((address_space(1))) uint32_t*)(p);
+}
+
+__device__ __forceinline__ uint4 ldg128(const uint8_t* p) {
+  const u32x4_t v = *(const __attribute__((address_space(1))) u32x4_t*)(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ float ldgf(const float* p) {
+  return *(const __attribute__((address_space(1))) float*)(p);
+}
+
+// V_MFMA_SCALE_F32_16X16X128_F8F6F4 operand layouts (measured on gfx950 with one-hot probes):
+//   FP4 A (cbsz 4, 4 VGPRs): lane l = row l % 16, K = 32 (l / 16) + nibble j, low nibble first.
+//   FP8 A (cbsz 0) and FP8 B (blgp 0), 8 VGPRs: lane l = row / column l % 16; bytes 0-15 hold
+//     K = 16 (l / 16) + j and bytes 16-31 hold K = 64 + 16 (l / 16) + j.
+//   scale_a / scale_b: lane l scales row / column l % 16 over the 32-wide K block l / 16.
+//   D: lane l, register i = row 4 (l / 16) + i, column l % 16.
+__device__ __forceinline__ v4f mfma_fp4_fp8(uint4 a, uint4 b0, uint4 b1, v4f c, int sa, int sb) {
+  const v8i av = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
+  const v8i bv = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 4, 0, 0, sa, 0, sb);
+}
+
+__device__ __forceinline__ v4f mfma_fp8_fp8(uint4 a0, uint4 a1, uint4 b0, uint4 b1, v4f c, int sa, int sb) {
+  const v8i av = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+  const v8i bv = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 0, 0, 0, sa, 0, sb);
+}
+
+}  // namespace mxd

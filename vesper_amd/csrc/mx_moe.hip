@@ -16,13 +16,16 @@
 #include <cmath>
 #include <vector>
 
+#include "mx_device.h"
 #include "mx_internal.h"
 #include "mx_numerics.h"
 
 namespace {
 
-typedef int v8i __attribute__((ext_vector_type(8)));
-typedef float v4f __attribute__((ext_vector_type(4)));
+using mxd::ldg128;
+using mxd::ldg32;
+using mxd::v4f;
+using mxd::v8i;
 
 constexpr int kMaxTokens = 16;   // MFMA N: tokens per expert per decode call
 constexpr int kMaxTopK = 32;
@@ -579,19 +582,6 @@ __device__ __forceinline__ v4f mfma_fp4xfp8(uint4 a, uint4 b0, uint4 b1, v4f c, 
 // ring unrolled so every index is static). The 4 partial accumulators per tile are then summed in a
 // fixed wave order through LDS, so results do not depend on scheduling.
 constexpr int kTiles = 4;
-
-// Loads through the global address space (the pointers come from a device table, so the compiler
-// cannot infer it and would otherwise emit flat loads).
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ uint32_t ldg32(const uint8_t* p) {
-  return *(const __attribute__((address_space(1))) uint32_t*)(p);
-}
-
-__device__ __forceinline__ uint4 ldg128(const uint8_t* p) {
-  const u32x4_t v = *(const __attribute__((address_space(1))) u32x4_t*)(p);
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
 
 // Weight operand in the device-native tiled layout: for every (row group, K chunk) the 4 tiles'
 // A operands are 4 consecutive KB (lane l's 16 bytes at 16 * l), so each load instruction of a

@@ -114,4 +114,11 @@ MX_HD uint32_t act_quant_value(float x, float s) {
   return e4m3_encode(y);
 }
 
+// FP32 scale of one per-token 128-wide activation block (the FP32-scale FP8 profile):
+// s = f32(max(amax, 1e-4)) / 448 with one IEEE division; the codes are then act_quant_value(x, s).
+MX_HD float act128_scale(float amax) {
+  const float floor = u2f(kAmaxFloorBits);
+  return (amax > floor ? amax : floor) / 448.0f;
+}
+
 }  // namespace mx

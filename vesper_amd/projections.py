@@ -1,0 +1,141 @@
+"""FP8 E4M3 block-scaled attention projections (mirrors NativeProjections, src/vesper/projections.py:67-154).
+
+NativeProjections(arrays, ordinal, *, layer, block) uploads each projection's E4M3 weight and scales once,
+tiled for the gfx950 MFMA (mx_fp8_tile), and `fp8(name, values)` returns the reference's stage dict:
+input_fp8, scale_e8m0 (block 32) or scale_f32 (block 128), output_fp32, output_bf16.
+
+block 32 is the reference's own projection arithmetic (E8M0 scales per 32 x 32 weight block, per-32
+activation quantization, `layers.{layer}.attn.{name}.{weight,scale}` arrays of FP8_LAYOUT shapes).
+block 128 is BASELINE configuration 3 (FP32 scales per 128 x 128 block, per-token per-128 FP32
+activation scales, CONFIG3_LAYOUT shapes). Inputs are validated before any device work. The
+reference bounds a call to 8 rows; here any number of rows runs in one launch (16 tokens per MFMA
+column group), and `project_device` is the pointer-level fast path.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import math
+import threading
+
+import numpy as np
+
+from . import _lib
+
+FP8_LAYOUT = {"wq_a": (1280, 5120), "wq_b": (32768, 1280), "wkv": (512, 5120), "wo_b": (5120, 8192)}
+CONFIG3_LAYOUT = {"q_a": (1536, 7168), "q_b": (24576, 1536), "kv_a": (576, 7168), "o": (7168, 16384)}
+MAX_ROWS = 1 << 16
+
+
+def validate_values(values, width):
+    """Finite contiguous BF16 rows of the projection's width (projections.py:20-26, without the 8-row cap)."""
+    if (not isinstance(values, np.ndarray) or values.dtype != np.uint16 or values.ndim not in (1, 2, 3)
+            or values.shape[-1] != width or not values.flags.c_contiguous
+            or not 1 <= math.prod(values.shape[:-1]) <= MAX_ROWS
+            or np.any((values & 0x7F80) == 0x7F80)):
+        raise ValueError("Expected bounded contiguous finite BF16 projection input")
+    return math.prod(values.shape[:-1])
+
+
+def scale_shape(rows, width, block):
+    return (rows // 32, width // 32) if block == 32 else ((rows + 127) // 128, width // 128)
+
+
+def validate_projection_weights(arrays, layer, layout, block):
+    for name, (rows, width) in layout.items():
+        for suffix, dtype, shape in (("weight", np.uint8, (rows, width)),
+                                     ("scale", np.uint8 if block == 32 else np.float32, scale_shape(rows, width, block))):
+            a = arrays.get(f"layers.{layer}.attn.{name}.{suffix}")
+            if (not isinstance(a, np.ndarray) or a.dtype != dtype or a.shape != shape or not a.flags.c_contiguous):
+                raise ValueError("Expected block-scaled FP8 Attention weights/scales")
+            bad = np.any((a & 127) == 127) if suffix == "weight" else (
+                np.any(a == 255) if block == 32 else not (np.isfinite(a).all() and np.all(a > 0)))
+            if bad:
+                raise ValueError("FP8 Attention weights/scales must be finite")
+
+
+class NativeProjections:
+    """Resident tiled FP8 matrices, serialized calls."""
+
+    def __init__(self, arrays, ordinal=0, *, layer=0, block=32, layout=None):
+        if block not in (32, 128):
+            raise ValueError("block must be 32 or 128")
+        self.layout = dict(layout or (FP8_LAYOUT if block == 32 else CONFIG3_LAYOUT))
+        for rows, width in self.layout.values():
+            if rows % 64 or width % 128:
+                raise ValueError("projection rows must be a multiple of 64 and width of 128")
+        validate_projection_weights(arrays, layer, self.layout, block)
+        self.arrays, self.ordinal, self.layer, self.block = arrays, ordinal, layer, block
+        self.lock, self.opened, self.ctx = threading.Lock(), False, None
+        self.tiled = {}
+
+    def __enter__(self):
+        with self.lock:
+            if self.opened:
+                raise RuntimeError("Projection runtime is already open")
+            self.ctx = _lib.Context(self.ordinal, 0)
+            try:
+                lib = self.ctx.lib
+                for name, (rows, width) in self.layout.items():
+                    w = self.ctx.upload(self.arrays[f"layers.{self.layer}.attn.{name}.weight"])
+                    s = self.ctx.upload(self.arrays[f"layers.{self.layer}.attn.{name}.scale"])
+                    nbytes = int(lib.cdll.mx_fp8_tiled_bytes(rows, width, self.block))
+                    blob = self.ctx.malloc(nbytes)
+                    self.tiled[name] = blob
+                    lib.fp8_tile(self.ctx._h(), _lib.vp(w), _lib.vp(s), rows, width, self.block, C.c_void_p(blob), None)
+                    self.ctx.sync()
+                    w.free()
+                    s.free()
+                self.resident_bytes = sum(int(lib.cdll.mx_fp8_tiled_bytes(r, c, self.block))
+                                          for r, c in self.layout.values())
+                self.opened = True
+                return self
+            except BaseException:
+                self.ctx.close()
+                self.ctx = None
+                raise
+
+    def _ready(self):
+        if not self.opened:
+            raise RuntimeError("Projection runtime is not open")
+
+    def project_device(self, name, x_ptr, tokens, y_ptr, stream=None, trace_ptr=None, q_ptr=None, s_ptr=None):
+        """y[T][rows] BF16 = projection of device BF16 x[T][width]; no host synchronisation."""
+        self._ready()
+        rows, width = self.layout[name]
+        self.ctx.lib.fp8_projection(self.ctx._h(), C.c_void_p(self.tiled[name]), rows, width, self.block,
+                                    C.c_void_p(int(x_ptr)), int(tokens), C.c_void_p(int(y_ptr)),
+                                    _lib.vp(trace_ptr), _lib.vp(q_ptr), _lib.vp(s_ptr), _lib._stream(stream))
+
+    def fp8(self, name, values):
+        with self.lock:
+            self._ready()
+            if name not in self.layout:
+                raise ValueError("Unknown FP8 Attention projection")
+            rows, width = self.layout[name]
+            tokens = validate_values(values, width)
+            lead = values.shape[:-1]
+            sdt, sw = (np.uint8, width // 32) if self.block == 32 else (np.float32, width // 128)
+            x = self.ctx.upload(np.ascontiguousarray(values).reshape(tokens, width))
+            q = self.ctx.empty((tokens, width), np.uint8)
+            s = self.ctx.empty((tokens, sw), sdt)
+            trace = self.ctx.empty((tokens, rows), np.float32)
+            out = self.ctx.empty((tokens, rows), np.uint16)
+            try:
+                self.project_device(name, x.ptr, tokens, out.ptr, trace_ptr=trace, q_ptr=q, s_ptr=s)
+                scale_key = "scale_e8m0" if self.block == 32 else "scale_f32"
+                return {"input_fp8": q.download().reshape(*lead, width),
+                        scale_key: s.download().reshape(*lead, sw),
+                        "output_fp32": trace.download().reshape(*lead, rows),
+                        "output_bf16": out.download().reshape(*lead, rows)}
+            finally:
+                for d in (x, q, s, trace, out):
+                    d.free()
+
+    def __exit__(self, *_):
+        with self.lock:
+            self.opened = False
+            if self.ctx is not None:
+                self.ctx.close()
+                self.ctx = None
+            self.tiled.clear()
