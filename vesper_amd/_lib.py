@@ -108,6 +108,8 @@ SIGNATURES = {
     "mx_fp8_tile": ([_P, _P, _P, _I32, _I32, _I32, _P, _P], C.c_int),
     "mx_act_quant128": ([_P, _P, _P, _P, _I64, _I64, _P], C.c_int),
     "mx_fp8_projection": ([_P, _P, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _P, _P], C.c_int),
+    "mx_fp8_expert_forward": ([_P, _P, _P, _P, _I32, _I32, _P, _I32, _F, _P, _P, C.POINTER(MxExpertStages), _P],
+                              C.c_int),
     "mx_copy_kernel": ([_P, _P, _P, _U64, _P], C.c_int),
 }
 

@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "mx_numerics.h"
+
 namespace mxd {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
@@ -40,6 +42,37 @@ __device__ __forceinline__ v4f mfma_fp8_fp8(uint4 a0, uint4 a1, uint4 b0, uint4 
   const v8i av = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
   const v8i bv = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 0, 0, 0, sa, 0, sb);
+}
+
+// silu(g) = g / (1 + exp(-g)); exp is evaluated in float64 and rounded once to FP32.
+__device__ __forceinline__ float silu_f32(float g) {
+  const float e = (float)exp(-(double)g);
+  return g / (1.0f + e);
+}
+
+// SwiGLU epilogue of one intermediate element (expert_probe.cu:10-25): W1/W3 outputs as BF16 bits ->
+// clamp (limit > 0: gate <= limit, -limit <= up <= limit) -> silu(gate) * up -> times the route weight
+// when weighted -> BF16. Returns the BF16-valued down input; `tr` (nullable) receives the FP32 trace
+// {clamped gate, clamped up, silu, product, routed}.
+__device__ __forceinline__ float swiglu_element(uint32_t b1, uint32_t b3, float limit, bool weighted, float rw,
+                                                float* tr) {
+  float gate = mx::bf16_value(b1), upf = mx::bf16_value(b3);
+  if (limit > 0.f) {
+    if (gate > limit) gate = limit;
+    if (upf > limit) upf = limit;
+    if (upf < -limit) upf = -limit;
+  }
+  const float silu = silu_f32(gate);
+  const float product = silu * upf;
+  const float routed = weighted ? rw * product : product;
+  if (tr) {
+    tr[0] = gate;
+    tr[1] = upf;
+    tr[2] = silu;
+    tr[3] = product;
+    tr[4] = routed;
+  }
+  return mx::bf16_round(routed);
 }
 
 }  // namespace mxd

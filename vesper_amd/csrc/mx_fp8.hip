@@ -30,6 +30,7 @@ using mxd::v4f;
 
 constexpr int kTiles = 4;   // 16-row MFMA tiles per workgroup: 64 weight rows
 constexpr int kTok = 16;    // token columns per MFMA
+constexpr int kGemvMaxTokens = 32;   // above this the tiled GEMM reuses each weight tile for 128 tokens
 
 struct Fp8Blob {
   size_t scales;   // byte offset of the scale section
@@ -103,6 +104,7 @@ struct Fp8Args {
   const void* xs;      // block 32: uint8 [T][K/32]; block 128: float [T][K/128]
   uint16_t* y;         // [T][N] BF16
   float* trace;        // [T][N] FP32 sums, nullable
+  float* partial;      // split K: [splits][T][N] FP32 partial sums (the GEMV writes these instead of y)
 };
 
 template <int kBlock>
@@ -153,9 +155,10 @@ __device__ __forceinline__ void fp8_mma(const Fp8Chunk<kBlock>& r, v4f (&acc)[kT
   }
 }
 
-// grid (N / 64, ceil(T / 16)), 256 threads: 64 weight rows x 16 tokens per workgroup. Wave w streams its
-// quarter of the K chunks (P = 2 chunks of 8 KB in flight), the quarters are summed through LDS in wave
-// order, then wave t writes tile t.
+// grid (N / 64, ceil(T / 16), splits), 256 threads: 64 weight rows x 16 tokens x one K range per
+// workgroup. Wave w streams its quarter of the workgroup's K chunks (P = 2 chunks of 8 KB in flight), the
+// quarters are summed through LDS in wave order, then wave t writes tile t: BF16 (and the FP32 trace)
+// when K is not split, else its FP32 partial sums for fp8_splitk_reduce_kernel.
 template <int kBlock>
 __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
   constexpr int P = 2;
@@ -175,8 +178,10 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
   v4f acc[kTiles];
 #pragma unroll
   for (int t = 0; t < kTiles; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
-  const int c0 = (C * wave) / 4;
-  const int cn = (C * (wave + 1)) / 4 - c0;
+  const int z = blockIdx.z, S = gridDim.z;
+  const int cb = (C * z) / S, cw = (C * (z + 1)) / S - cb;   // this workgroup's chunk range
+  const int c0 = cb + (cw * wave) / 4;
+  const int cn = cb + (cw * (wave + 1)) / 4 - c0;
   if (cn > 0) {
     const uint32_t keep = live ? 0xFFFFFFFFu : 0u;
     Fp8Chunk<kBlock> buf[P];
@@ -205,6 +210,10 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
     out[i] = ((red[0][wave][lane][i] + red[1][wave][lane][i]) + red[2][wave][lane][i]) + red[3][wave][lane][i];
   if (live) {
     const size_t o = (size_t)tok * a.N + 64 * g + 16 * wave + 4 * q;
+    if (S > 1) {
+      *reinterpret_cast<float4*>(a.partial + (size_t)z * a.T * a.N + o) = make_float4(out[0], out[1], out[2], out[3]);
+      return;
+    }
     uint2 packed;
     packed.x = mx::bf16_bits(out[0]) | (mx::bf16_bits(out[1]) << 16);
     packed.y = mx::bf16_bits(out[2]) | (mx::bf16_bits(out[3]) << 16);
@@ -213,11 +222,228 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
   }
 }
 
+// Split-K epilogue: y = BF16(sum over splits in order), 4 outputs per thread.
+__global__ void fp8_splitk_reduce_kernel(const float* __restrict__ partial, int splits, int64_t count,
+                                         uint16_t* __restrict__ y, float* __restrict__ trace) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i >= count) return;
+  float4 s = *reinterpret_cast<const float4*>(partial + i);
+  for (int z = 1; z < splits; ++z) {
+    const float4 v = *reinterpret_cast<const float4*>(partial + (size_t)z * count + i);
+    s.x = s.x + v.x;
+    s.y = s.y + v.y;
+    s.z = s.z + v.z;
+    s.w = s.w + v.w;
+  }
+  uint2 packed;
+  packed.x = mx::bf16_bits(s.x) | (mx::bf16_bits(s.y) << 16);
+  packed.y = mx::bf16_bits(s.z) | (mx::bf16_bits(s.w) << 16);
+  *reinterpret_cast<uint2*>(y + i) = packed;
+  if (trace) *reinterpret_cast<float4*>(trace + i) = s;
+}
+
+// ---- GEMM for many tokens ------------------------------------------------------------------------
+//
+// grid (ceil(N / 256), ceil(T / 128)), 512 threads = 8 waves. Wave w owns the 64-row group
+// 4 * blockIdx.x + (w % 4) and the token half w / 4 (64 tokens = 4 MFMA column tiles); it reads its A
+// operands straight from the tiled blob (1 KB contiguous per load; the two waves of a row group read the
+// same bytes in step, the second from L2). The workgroup's 128 tokens x 128 K of activation codes (and
+// their scales) are staged in LDS, double-buffered, and shared by the 8 waves. Each wave accumulates
+// 4 row tiles x 4 token tiles of 16 x 16 in registers; A for the next chunk is prefetched into a second
+// register set while the current chunk's 16 MFMAs run.
+constexpr int kGemmTok = 128;                 // tokens per workgroup
+constexpr int kGemmThreads = 512;
+constexpr int kWaveTiles = 4;                 // token tiles per wave
+constexpr int kLdsRow = 144;                  // 128 bytes of a token's K chunk + 16 bytes of bank padding
+
+template <int kBlock>
+__global__ __launch_bounds__(kGemmThreads) void fp8_gemm_kernel(Fp8Args a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds_b[2][kGemmTok * kLdsRow];
+  __shared__ uint32_t lds_s[2][kGemmTok];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q = lane >> 4, n = lane & 15;
+  const int C = a.K / 128;
+  const int groups = a.N / 64;
+  const int g_raw = blockIdx.x * 4 + (wave & 3);
+  const bool has_rows = g_raw < groups;
+  const int g = has_rows ? g_raw : groups - 1;
+  const int u0 = (wave >> 2) * kWaveTiles;
+  const int m0 = blockIdx.y * kGemmTok;
+  const Fp8Blob off = fp8_blob(a.N, a.K, kBlock);
+  const uint8_t* wlane = a.blob + (size_t)g * C * 8192 + 16 * lane;
+  const uint8_t* slane = a.blob + off.scales + (size_t)g * C * 256 + 4 * lane;
+  const float* swrow = reinterpret_cast<const float*>(a.blob + off.scales) + (size_t)((64 * g) / 128) * C;
+
+  // staging: thread tid moves pieces tid and tid + 512 (token = piece / 8, 16-byte part = piece % 8)
+  const uint8_t* xsrc[2];
+  int ldst[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int p = tid + kGemmThreads * j, tok = p >> 3, part = p & 7;
+    const int tc = min(m0 + tok, a.T - 1);
+    xsrc[j] = a.xq + (size_t)tc * a.K + 16 * part;
+    ldst[j] = tok * kLdsRow + 16 * part;
+  }
+  const int stok = min(m0 + (tid & (kGemmTok - 1)), a.T - 1);
+
+  auto load_b = [&](int c, uint4 (&bst)[2], uint32_t& sst) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) bst[j] = ldg128(xsrc[j] + (size_t)c * 128);
+    if constexpr (kBlock == 32) sst = ldg32((const uint8_t*)a.xs + (size_t)stok * (a.K / 32) + 4 * c);
+    else sst = __float_as_uint(ldgf((const float*)a.xs + (size_t)stok * C + c));
+  };
+  auto store_b = [&](int stage, const uint4 (&bst)[2], uint32_t sst) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) *reinterpret_cast<uint4*>(&lds_b[stage][ldst[j]]) = bst[j];
+    if (tid < kGemmTok) lds_s[stage][tid] = sst;
+  };
+  auto load_a = [&](int c, uint4 (&am)[kTiles][2], uint32_t& sw) {
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+      am[t][0] = ldg128(wlane + (size_t)c * 8192 + t * 2048);
+      am[t][1] = ldg128(wlane + (size_t)c * 8192 + t * 2048 + 1024);
+    }
+    if constexpr (kBlock == 32) sw = ldg32(slane + (size_t)c * 256);
+    else sw = __float_as_uint(ldgf(swrow + c));
+  };
+
+  v4f acc[kTiles][kWaveTiles];
+#pragma unroll
+  for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+    for (int u = 0; u < kWaveTiles; ++u) acc[t][u] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int stage, const uint4 (&am)[kTiles][2], uint32_t sw) {
+#pragma unroll
+    for (int u = 0; u < kWaveTiles; ++u) {
+      const uint8_t* row = &lds_b[stage][(16 * (u0 + u) + n) * kLdsRow];
+      const uint4 b0 = *reinterpret_cast<const uint4*>(row + 16 * q);
+      const uint4 b1 = *reinterpret_cast<const uint4*>(row + 64 + 16 * q);
+      const uint32_t sx = lds_s[stage][16 * (u0 + u) + n];
+      if constexpr (kBlock == 32) {
+        const int sxb = (int)((sx >> (8 * q)) & 0xFF);
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t)
+          acc[t][u] = mfma_fp8_fp8(am[t][0], am[t][1], b0, b1, acc[t][u], (int)((sw >> (8 * t)) & 0xFF), sxb);
+      } else {
+        const float sa = __uint_as_float(sx), swf = __uint_as_float(sw);
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) {
+          const v4f d = mfma_fp8_fp8(am[t][0], am[t][1], b0, b1, v4f{0.f, 0.f, 0.f, 0.f}, 127, 127);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[t][u][i] = acc[t][u][i] + (d[i] * sa) * swf;
+        }
+      }
+    }
+  };
+
+  uint4 bst[2];
+  uint32_t sst = 0;
+  uint4 a0[kTiles][2], a1[kTiles][2];
+  uint32_t sw0 = 0, sw1 = 0;
+  load_b(0, bst, sst);
+  load_a(0, a0, sw0);
+  store_b(0, bst, sst);
+  __syncthreads();
+  // two chunks per iteration so the A register sets alternate with static indices
+  for (int c = 0; c < C; c += 2) {
+    const bool more1 = c + 1 < C;
+    if (more1) {
+      load_b(c + 1, bst, sst);
+      load_a(c + 1, a1, sw1);
+    }
+    compute(0, a0, sw0);
+    if (more1) store_b(1, bst, sst);
+    __syncthreads();
+    if (!more1) break;
+    const bool more2 = c + 2 < C;
+    if (more2) {
+      load_b(c + 2, bst, sst);
+      load_a(c + 2, a0, sw0);
+    }
+    compute(1, a1, sw1);
+    if (more2) store_b(0, bst, sst);
+    __syncthreads();
+  }
+  if (!has_rows) return;
+#pragma unroll
+  for (int u = 0; u < kWaveTiles; ++u) {
+    const int tok = m0 + 16 * (u0 + u) + n;
+    if (tok >= a.T) continue;
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+      const size_t o = (size_t)tok * a.N + 64 * g + 16 * t + 4 * q;
+      uint2 packed;
+      packed.x = mx::bf16_bits(acc[t][u][0]) | (mx::bf16_bits(acc[t][u][1]) << 16);
+      packed.y = mx::bf16_bits(acc[t][u][2]) | (mx::bf16_bits(acc[t][u][3]) << 16);
+      *reinterpret_cast<uint2*>(a.y + o) = packed;
+      if (a.trace)
+        *reinterpret_cast<float4*>(a.trace + o) = make_float4(acc[t][u][0], acc[t][u][1], acc[t][u][2], acc[t][u][3]);
+    }
+  }
+}
+
 int check_fp8_shape(int N, int K, int block, const char* who) {
   MX_REQUIRE(block == 32 || block == 128, "%s: block must be 32 or 128", who);
   MX_REQUIRE(N > 0 && N % 64 == 0 && K > 0 && K % 128 == 0, "%s: rows must be a multiple of 64 and width of 128",
              who);
   return MX_OK;
+}
+
+// K splits of the decode GEMV: about 1024 workgroups, every wave keeping at least one chunk.
+int fp8_splits(int N, int K, int T) {
+  if (T > kGemvMaxTokens) return 1;
+  const int base_wgs = (N / 64) * ((T + kTok - 1) / kTok);
+  return std::max(1, std::min({16, (K / 128) / 4, (1024 + base_wgs - 1) / base_wgs}));
+}
+
+// The product on quantized activations: GEMV (T <= 32, split K + ordered reduce into `partial`, which
+// holds fp8_splits(N, K, T) * T * N floats) or the tiled GEMM.
+int launch_fp8_product(const uint8_t* blob, int N, int K, int block, const uint8_t* q, const void* sc, int T,
+                       uint16_t* y, float* trace, float* partial, hipStream_t st) {
+  Fp8Args a{};
+  a.blob = blob;
+  a.N = N;
+  a.K = K;
+  a.T = T;
+  a.xq = q;
+  a.xs = sc;
+  a.y = y;
+  a.trace = trace;
+  a.partial = partial;
+  if (T <= kGemvMaxTokens) {
+    const int splits = fp8_splits(N, K, T);
+    const dim3 grid(N / 64, (T + kTok - 1) / kTok, splits);
+    if (block == 32) hipLaunchKernelGGL(fp8_gemv_kernel<32>, grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(fp8_gemv_kernel<128>, grid, dim3(256), 0, st, a);
+    MX_LAUNCH_CHECK("fp8_gemv_kernel");
+    if (splits > 1) {
+      const int64_t count = (int64_t)T * N;
+      hipLaunchKernelGGL(fp8_splitk_reduce_kernel, dim3((unsigned)((count / 4 + 255) / 256)), dim3(256), 0, st,
+                         (const float*)partial, splits, count, y, trace);
+      MX_LAUNCH_CHECK("fp8_splitk_reduce_kernel");
+    }
+  } else {
+    const dim3 grid((N / 64 + 3) / 4, (T + kGemmTok - 1) / kGemmTok);
+    if (block == 32) hipLaunchKernelGGL(fp8_gemm_kernel<32>, grid, dim3(kGemmThreads), 0, st, a);
+    else hipLaunchKernelGGL(fp8_gemm_kernel<128>, grid, dim3(kGemmThreads), 0, st, a);
+    MX_LAUNCH_CHECK("fp8_gemm_kernel");
+  }
+  return MX_OK;
+}
+
+// SwiGLU of the FP8 expert, one element per thread (the gate/up kernel of the MXFP4 path applies the
+// same mxd::swiglu_element in its epilogue).
+__global__ void swiglu_kernel(const uint16_t* __restrict__ w1, const uint16_t* __restrict__ w3, int T, int I,
+                              float limit, const float* __restrict__ route_w, uint16_t* __restrict__ din,
+                              float* __restrict__ trace) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)T * I) return;
+  const int t = (int)(i / I);
+  const float v = mxd::swiglu_element(w1[i], w3[i], limit, route_w != nullptr, route_w ? route_w[t] : 1.f,
+                                      trace ? trace + i * 5 : nullptr);
+  din[i] = (uint16_t)mx::bf16_bits(v);
 }
 
 }  // namespace
@@ -269,10 +495,10 @@ int mx_fp8_projection(mx_ctx* ctx, const void* tiled, int32_t N, int32_t K, int3
              "mx_fp8_projection: tiled 256-byte, x 16-byte, y 8-byte and trace 16-byte alignment required");
   hipStream_t st = as_stream(stream);
   const uint64_t q_b = ((uint64_t)T * K + 255) & ~255ull;
-  const uint64_t s_b = block == 32 ? (uint64_t)T * (K / 32) : (uint64_t)T * (K / 128) * 4;
+  const uint64_t s_b = ((block == 32 ? (uint64_t)T * (K / 32) : (uint64_t)T * (K / 128) * 4) + 255) & ~255ull;
+  const uint64_t p_b = (uint64_t)fp8_splits(N, K, T) * T * N * 4;
   void* base = nullptr;
-  if (!q_out || !s_out)
-    if (int s = scratch(ctx, q_b + s_b + 256, &base)) return s;
+  if (int s = scratch(ctx, q_b + s_b + p_b + 256, &base)) return s;
   uint8_t* q = q_out ? q_out : (uint8_t*)base;
   void* sc = s_out ? s_out : (void*)((uint8_t*)base + q_b);
   MX_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)sc & 3) == 0, "mx_fp8_projection: q 16-byte, s 4-byte aligned");
@@ -281,20 +507,61 @@ int mx_fp8_projection(mx_ctx* ctx, const void* tiled, int32_t N, int32_t K, int3
   } else {
     if (int s = mx_act_quant128(ctx, x, q, (float*)sc, T, K, stream)) return s;
   }
-  Fp8Args a{};
-  a.blob = (const uint8_t*)tiled;
-  a.N = N;
-  a.K = K;
-  a.T = T;
-  a.xq = q;
-  a.xs = sc;
-  a.y = y;
-  a.trace = trace;
-  const dim3 grid(N / 64, (T + kTok - 1) / kTok);
-  if (block == 32) hipLaunchKernelGGL(fp8_gemv_kernel<32>, grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL(fp8_gemv_kernel<128>, grid, dim3(256), 0, st, a);
-  MX_LAUNCH_CHECK("fp8_gemv_kernel");
-  return MX_OK;
+  return launch_fp8_product((const uint8_t*)tiled, N, K, block, q, sc, T, y, trace,
+                            (float*)((uint8_t*)base + q_b + s_b), st);
+}
+
+int mx_fp8_expert_forward(mx_ctx* ctx, const void* w1, const void* w3, const void* w2, int32_t H, int32_t I,
+                          const uint16_t* x, int32_t T, float limit, const float* route_w, uint16_t* y,
+                          const mx_expert_stages* stages, void* stream) {
+  if (int s = use(ctx)) return s;
+  MX_REQUIRE(w1 && w3 && w2, "mx_fp8_expert_forward: null tiled weight");
+  MX_REQUIRE(((uintptr_t)w1 & 255) == 0 && ((uintptr_t)w3 & 255) == 0 && ((uintptr_t)w2 & 255) == 0,
+             "mx_fp8_expert_forward: tiled weights must be 256-byte aligned");
+  MX_REQUIRE(H > 0 && H % 128 == 0 && I > 0 && I % 128 == 0, "expert shapes must be positive multiples of 128");
+  MX_REQUIRE(T >= 0 && T <= kTok, "token count %d outside [0, %d]", T, kTok);
+  MX_REQUIRE(std::isfinite(limit) && limit >= 0.f, "Invalid SwiGLU limit");
+  if (!T) return MX_OK;
+  MX_REQUIRE(x && y && ((uintptr_t)x & 15) == 0 && ((uintptr_t)y & 15) == 0,
+             "x and y must be 16-byte aligned device pointers");
+  hipStream_t st = as_stream(stream);
+  auto r256 = [](uint64_t b) { return (b + 255) & ~255ull; };
+  const uint64_t sizes[7] = {r256((uint64_t)T * H),     r256((uint64_t)T * H / 32), r256((uint64_t)T * I * 2),
+                             r256((uint64_t)T * I * 2), r256((uint64_t)T * I * 2),  r256((uint64_t)T * I),
+                             r256((uint64_t)T * I / 32)};
+  const uint64_t p_b = (uint64_t)std::max(fp8_splits(I, H, T) * I, fp8_splits(H, I, T) * H) * T * 4;
+  uint64_t total = p_b;
+  for (uint64_t b : sizes) total += b;
+  void* base = nullptr;
+  if (int s = scratch(ctx, total, &base)) return s;
+  uint8_t* cur = (uint8_t*)base;
+  uint8_t* buf[7];
+  for (int i = 0; i < 7; ++i) {
+    buf[i] = cur;
+    cur += sizes[i];
+  }
+  float* partial = (float*)cur;
+  uint8_t* q = (stages && stages->q) ? stages->q : buf[0];
+  uint8_t* s = (stages && stages->s) ? stages->s : buf[1];
+  uint16_t* b1 = (stages && stages->w1) ? stages->w1 : (uint16_t*)buf[2];
+  uint16_t* b3 = (stages && stages->w3) ? stages->w3 : (uint16_t*)buf[3];
+  uint16_t* din = (stages && stages->down_input) ? stages->down_input : (uint16_t*)buf[4];
+  uint8_t* dq = (stages && stages->down_q) ? stages->down_q : buf[5];
+  uint8_t* ds = (stages && stages->down_s) ? stages->down_s : buf[6];
+  float* trace = stages ? stages->trace : nullptr;
+  MX_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)dq & 15) == 0 && ((uintptr_t)b1 & 7) == 0 &&
+                 ((uintptr_t)b3 & 7) == 0 && ((uintptr_t)din & 3) == 0 && ((uintptr_t)s & 3) == 0 &&
+                 ((uintptr_t)ds & 3) == 0,
+             "stage buffers: q/down_q 16-byte, w1/w3 8-byte, scales and down_input 4-byte aligned");
+  if (int e = mx_act_quant32(ctx, x, q, s, T, H, stream)) return e;
+  if (int e = launch_fp8_product((const uint8_t*)w1, I, H, 32, q, s, T, b1, nullptr, partial, st)) return e;
+  if (int e = launch_fp8_product((const uint8_t*)w3, I, H, 32, q, s, T, b3, nullptr, partial, st)) return e;
+  const int64_t n = (int64_t)T * I;
+  hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (const uint16_t*)b1,
+                     (const uint16_t*)b3, T, I, limit, route_w, din, trace);
+  MX_LAUNCH_CHECK("swiglu_kernel");
+  if (int e = mx_act_quant32(ctx, din, dq, ds, T, I, stream)) return e;
+  return launch_fp8_product((const uint8_t*)w2, H, I, 32, dq, ds, T, y, nullptr, partial, st);
 }
 
 }  // extern "C"

@@ -70,11 +70,6 @@ __device__ __forceinline__ float score_of(float z, int score_func) {
   return sqrtf(sp);
 }
 
-__device__ __forceinline__ float silu_of(float g) {
-  const float e = (float)exp(-(double)g);
-  return g / (1.0f + e);
-}
-
 // Wavefront reductions and scans on DPP (row_shr 1/2/4/8 inside 16-lane rows, then row_bcast 15/31
 // across rows): VALU-latency steps instead of LDS-routed shuffles. `ident` fills lanes whose DPP
 // source is out of range or whose row is masked off.
@@ -777,25 +772,12 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
       const int gi = g * 32 + li;                 // intermediate index
       const uint32_t b1 = mx::bf16_bits(mine[i]);
       const uint32_t b3 = mx::bf16_bits(upv[i]);
-      float gate = mx::bf16_value(b1), upf = mx::bf16_value(b3);
-      if (a.limit > 0.f) {
-        if (gate > a.limit) gate = a.limit;
-        if (upf > a.limit) upf = a.limit;
-        if (upf < -a.limit) upf = -a.limit;
-      }
-      const float silu = silu_of(gate);
-      const float product = silu * upf;
-      const float routed = weighted ? rw * product : product;
-      const float din = mx::bf16_round(routed);
-      s_din[n][li] = din;
       const size_t o2 = (size_t)(row0 + n) * I + gi;
+      const float din = mxd::swiglu_element(b1, b3, a.limit, weighted, rw, a.trace ? a.trace + o2 * 5 : nullptr);
+      s_din[n][li] = din;
       if (a.w1) a.w1[o2] = (uint16_t)b1;
       if (a.w3) a.w3[o2] = (uint16_t)b3;
       if (a.din) a.din[o2] = (uint16_t)mx::bf16_bits(din);
-      if (a.trace) {
-        float* tr = a.trace + o2 * 5;
-        tr[0] = gate; tr[1] = upf; tr[2] = silu; tr[3] = product; tr[4] = routed;
-      }
     }
   }
   __syncthreads();

@@ -76,8 +76,7 @@ class ExpertExecutor:
         t = bits.shape[0]
         if not 1 <= t <= 16:
             raise ValueError("One expert call accepts 1 to 16 tokens")
-        if set(weights) != set(TENSORS):
-            raise ValueError("A complete expert requires exactly six native tensors")
+        self._check_weights(weights)
         route = None
         if routing_weight is not None:
             route = np.broadcast_to(np.asarray(routing_weight, dtype=np.float32).reshape(-1), (t,)).copy()
@@ -90,12 +89,8 @@ class ExpertExecutor:
                 self.ctx.copy_h2d(w["route"].ptr, route)
         stages = _lib.MxExpertStages(*[w[n].ptr for n in ("q", "s", "w1", "w3", "down_input", "trace",
                                                           "down_q", "down_s")])
-        ptrs = _lib.MxExpertPtrs(*[int(weights[n]) for n in TENSORS])
         with self.timings.section("compute.kernels"):
-            self.ctx.lib.expert_forward(self.ctx._h(), C.byref(ptrs), _lib.MX_FMT_MXFP4, self.hidden,
-                                        self.intermediate, C.c_void_p(w["x"].ptr), t, self.limit,
-                                        None if route is None else C.c_void_p(w["route"].ptr),
-                                        C.c_void_p(w["w2"].ptr), C.byref(stages), None)
+            self._compute(weights, t, None if route is None else C.c_void_p(w["route"].ptr), stages)
             self.ctx.sync()
         h, i = self.hidden, self.intermediate
         layout = {"q": ((t, h), np.uint8), "s": ((t, h // 32), np.uint8), "w1": ((t, i), np.uint16),
@@ -106,6 +101,18 @@ class ExpertExecutor:
         # the reference reports down_input as FP32 values of the BF16 boundary
         out["down_input"] = (out["down_input"].astype(np.uint32) << 16).view(np.float32)
         return out
+
+    def _check_weights(self, weights):
+        if set(weights) != set(TENSORS):
+            raise ValueError("A complete expert requires exactly six native tensors")
+
+    def _compute(self, weights, t, route_ptr, stages):
+        """The MXFP4 expert on the reference-layout tensors at `weights` (device pointers)."""
+        w = self.work
+        ptrs = _lib.MxExpertPtrs(*[int(weights[n]) for n in TENSORS])
+        self.ctx.lib.expert_forward(self.ctx._h(), C.byref(ptrs), _lib.MX_FMT_MXFP4, self.hidden, self.intermediate,
+                                    C.c_void_p(w["x"].ptr), t, self.limit, route_ptr, C.c_void_p(w["w2"].ptr),
+                                    C.byref(stages), None)
 
     def close(self):
         if self.ctx is not None:

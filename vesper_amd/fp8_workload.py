@@ -1,0 +1,93 @@
+"""Timing workload for the FP8 projections, used by bench.py and for counter runs.
+
+  python -m vesper_amd.fp8_workload --tokens 1 16 2048 --iters 20
+
+Builds the four configuration-3 projections (q_a 7168->1536, q_b 1536->24576, kv_a 7168->576,
+o 16384->7168; E4M3 weights with FP32 128 x 128 block scales, log-uniform in [2^-8, 2^-2]; synthetic,
+generated in HBM) and times each projection call (quantizer + product) with HIP events over `iters`
+back-to-back calls. Algorithmic work per call: weight bytes N*K + scales, x and y; FLOP 2*T*N*K.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import sys
+
+import numpy as np
+
+LAYOUT = {"q_a": (1536, 7168), "q_b": (24576, 1536), "kv_a": (576, 7168), "o": (7168, 16384)}
+
+
+def run(tokens=(1, 16, 2048), iters=20, seed=20261018, ctx=None):
+    from . import _lib
+    own = ctx is None
+    ctx = ctx or _lib.Context(0)
+    lib = ctx.lib
+    rng = np.random.default_rng(seed)
+    blobs, keep = {}, []
+    for i, (name, (n, k)) in enumerate(LAYOUT.items()):
+        w = ctx.malloc(n * k)
+        ctx.fill_uniform_u8(w, n * k, seed * 31 + i, 0, 126)      # finite E4M3 codes (no 0x7F / 0xFF)
+        sw = np.exp2(rng.uniform(-8.0, -2.0, ((n + 127) // 128, k // 128))).astype(np.float32)
+        swd = ctx.upload(sw)
+        blob = ctx.malloc(int(lib.cdll.mx_fp8_tiled_bytes(n, k, 128)))
+        lib.fp8_tile(ctx._h(), C.c_void_p(w), _lib.vp(swd), n, k, 128, C.c_void_p(blob), None)
+        ctx.sync()
+        ctx.free(w)
+        swd.free()
+        blobs[name] = blob
+    tmax = max(tokens)
+    kmax = max(k for _, k in LAYOUT.values())
+    nmax = max(n for n, _ in LAYOUT.values())
+    x = rng.standard_normal((tmax, kmax)).astype(np.float32)
+    b = x.view(np.uint32).astype(np.uint64)
+    xd = ctx.upload(((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16))
+    yd = ctx.empty((tmax, nmax), np.uint16)
+    start, stop = ctx.event(), ctx.event()
+    out = {}
+    for t in tokens:
+        per = {}
+        total_us, total_bytes, total_flop = 0.0, 0, 0
+        for name, (n, k) in LAYOUT.items():
+            # the input is the first T rows of a [T, k] view of the buffer
+            args = (ctx._h(), C.c_void_p(blobs[name]), n, k, 128, _lib.vp(xd), t, _lib.vp(yd), None, None, None, None)
+            for _ in range(3):
+                lib.fp8_projection(*args)
+            ctx.sync()
+            ctx.record(start)
+            for _ in range(iters):
+                lib.fp8_projection(*args)
+            ctx.record(stop)
+            us = ctx.elapsed_ms(start, stop) * 1000 / iters
+            nbytes = n * k + ((n + 127) // 128) * (k // 128) * 4 + t * k * 2 + t * n * 2
+            flop = 2 * t * n * k
+            per[name] = {"us": round(us, 2), "GB_per_s": round(nbytes / us / 1e3, 1),
+                         "TFLOP_per_s": round(flop / us / 1e6, 2)}
+            total_us += us
+            total_bytes += nbytes
+            total_flop += flop
+        out[t] = {"projections": per, "us": round(total_us, 2), "bytes": total_bytes, "flop": total_flop,
+                  "GB_per_s": round(total_bytes / total_us / 1e3, 1),
+                  "TFLOP_per_s": round(total_flop / total_us / 1e6, 2)}
+    for blob in blobs.values():
+        ctx.free(blob)
+    xd.free()
+    yd.free()
+    if own:
+        ctx.close()
+    return out
+
+
+def main():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--tokens", type=int, nargs="+", default=[1, 16, 2048])
+    p.add_argument("--iters", type=int, default=20)
+    args = p.parse_args()
+    print(json.dumps(run(tuple(args.tokens), args.iters)), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
