@@ -259,6 +259,16 @@ int mx_layer_set_expert(mx_layer* layer, int32_t expert, const void* tiled, void
 int mx_moe_decode(mx_layer* layer, const uint16_t* x_bf16, int32_t tokens, uint16_t* y_bf16,
                   int32_t diagnostics, void* stream);
 
+/* Prefill: T tokens through the layer (routed experts + shared) as token-sorted grouped GEMMs on the
+ * scaled MXFP4 MFMA; same per-token arithmetic as mx_moe_decode.
+ * ids [T][k] (device int32, distinct per token) and weights [T][k] (device FP32) give the routing, or both
+ * NULL to run the layer's router on x. The caller provides a device workspace of at least
+ * mx_prefill_workspace_bytes(layer, T) bytes, 256-byte aligned (no allocation inside the call).
+ * H % 256 == 0. Replaces the reference's per-token ConnectedMoE.forward loop (connected.py:125-186). */
+uint64_t mx_prefill_workspace_bytes(mx_layer* layer, int32_t tokens);
+int mx_moe_prefill(mx_layer* layer, const uint16_t* x_bf16, int32_t tokens, const int32_t* ids, const float* weights,
+                   uint16_t* y_bf16, void* workspace, uint64_t workspace_bytes, void* stream);
+
 /* Internal per-call buffers of a layer (device pointers, valid after mx_moe_decode on the same stream). */
 #define MX_BUF_LOGITS 0      /* float [T][E]          */
 #define MX_BUF_SCORES 1      /* float [T][E]          */

@@ -7,6 +7,8 @@
                  then += FP32(BF16 shared); one final BF16 rounding
   moe_layer      src/vesper/connected.py:125-186 order: gate -> router -> participation ->
                  routed experts (weight applied before W2) -> shared expert -> combine
+  moe_layer_routed  the same after the router, on given indices and route weights (prefill workloads
+                 whose routing is drawn, e.g. Zipf-skewed)
 """
 
 from __future__ import annotations
@@ -77,3 +79,26 @@ def moe_layer(x, router_weight, experts: dict, shared: dict | None, *, top_k: in
                           n_experts, top_k)
     return {"input_bf16": bf16_bits(x), "logits": routing["logits"], "routing": routing, "experts": outputs,
             "shared": shared_out, "aggregation": aggregation, "output_bf16": aggregation["output_bf16"]}
+
+
+def moe_layer_routed(x, indices, weights, experts: dict, shared: dict | None, *, num_experts: int,
+                     swiglu_limit: float = 0.0, shared_format: str = "mxfp4", tokens=None) -> dict:
+    """The layer after routing, on given `indices` [T, k] and `weights` [T, k]; `tokens` (optional) limits the
+    work to those tokens' rows (the result then covers only them, in that order). `experts` maps the
+    needed expert IDs to their six tensors."""
+    x = bf16_round(np.atleast_2d(np.asarray(x, dtype=np.float32)))
+    sel = np.arange(x.shape[0]) if tokens is None else np.asarray(tokens)
+    idx = np.asarray(indices)[sel]
+    wts = np.asarray(weights, dtype=np.float32)[sel]
+    xs = x[sel]
+    selected = participation(idx, num_experts, idx.shape[1], max_tokens=max(len(sel), 1))
+    outputs = {}
+    for expert, rows in selected.items():
+        ranks = [int(np.flatnonzero(idx[r] == expert)[0]) for r in rows]
+        outputs[expert] = expert_forward(xs[rows], experts[expert], wts[rows, ranks], swiglu_limit)
+    if shared is not None:
+        shared_bits = expert_forward(xs, shared, None, swiglu_limit, shared_format)["w2"]
+    else:
+        shared_bits = np.zeros(xs.shape, np.uint16)
+    aggregation = combine(idx, {e: o["w2"] for e, o in outputs.items()}, shared_bits, num_experts, idx.shape[1])
+    return {"experts": outputs, "aggregation": aggregation, "output_bf16": aggregation["output_bf16"]}

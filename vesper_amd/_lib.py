@@ -104,6 +104,8 @@ SIGNATURES = {
     "mx_layer_buffer": ([_P, _I32, C.POINTER(_P), C.POINTER(_U64)], C.c_int),
     "mx_layer_profile": ([_P, _I32, C.POINTER(_F), C.POINTER(_I32)], C.c_int),
     "mx_layer_time_stage": ([_P, _I32, _I32, C.POINTER(_F), _P], C.c_int),
+    "mx_prefill_workspace_bytes": ([_P, _I32], _U64),
+    "mx_moe_prefill": ([_P, _P, _I32, _P, _P, _P, _P, _U64, _P], C.c_int),
     "mx_fp8_tiled_bytes": ([_I32, _I32, _I32], _U64),
     "mx_fp8_tile": ([_P, _P, _P, _I32, _I32, _I32, _P, _P], C.c_int),
     "mx_act_quant128": ([_P, _P, _P, _P, _I64, _I64, _P], C.c_int),

@@ -75,4 +75,26 @@ __device__ __forceinline__ float swiglu_element(uint32_t b1, uint32_t b3, float 
   return mx::bf16_round(routed);
 }
 
+// Byte offsets of the tiled expert blob for hidden H and intermediate I:
+//   [0, I*H)            gate/up A operands: row group g (I/32 groups) x chunk c (H/128) x tile t x lane
+//                       (16 B), tile t = W1 rows 32g + 8t + (0..7) as MFMA rows 0-7 and the same W3
+//                       rows as MFMA rows 8-15; lane l = MFMA row l % 16, K block 4c + l / 16
+//   [gu_s, +I*H/16)     gate/up scale words: g x c x lane (4 B, byte t = tile t)
+//   [dn_w, +H*I/2)      down A operands: row group b (H/64) x chunk c (I/128) x tile t x lane, tile t =
+//                       W2 rows 64b + 16t + (0..15)
+//   [dn_s, +H*I/32)     down scale words: b x c x lane
+struct TiledOffsets {
+  size_t gu_s, dn_w, dn_s, total;
+};
+
+__host__ __device__ __forceinline__ TiledOffsets tiled_offsets(int H, int I) {
+  const size_t ih = (size_t)I * H;
+  TiledOffsets o;
+  o.gu_s = ih;
+  o.dn_w = ih + ih / 16;
+  o.dn_s = o.dn_w + ih / 2;
+  o.total = o.dn_s + ih / 32;
+  return o;
+}
+
 }  // namespace mxd

@@ -37,6 +37,17 @@ int scratch(mx_ctx* ctx, uint64_t bytes, void** out);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// What other translation units need of a decode layer (defined with the layer in mx_moe.hip).
+struct LayerView {
+  mx_ctx* ctx;
+  mx_moe_config cfg;
+  const float* router_weight;
+  const float* bias;
+  const uint8_t** tiles;   // device [E + 1] tiled expert blobs, shared last
+  int has_shared;
+};
+LayerView layer_view(mx_layer* layer);
+
 }  // namespace mxi
 
 #define MX_HIP(call)                                           \

@@ -24,6 +24,8 @@ namespace {
 
 using mxd::ldg128;
 using mxd::ldg32;
+using mxd::tiled_offsets;
+using mxd::TiledOffsets;
 using mxd::v4f;
 using mxd::v8i;
 
@@ -691,28 +693,6 @@ __device__ __forceinline__ v4f reduce_tiles(const v4f (&acc)[kTiles], int wave, 
   return out;
 }
 
-// Byte offsets of the tiled expert blob for hidden H and intermediate I:
-//   [0, I*H)            gate/up A operands: row group g (I/32 groups) x chunk c (H/128) x tile t x lane
-//                       (16 B), tile t = W1 rows 32g + 8t + (0..7) as MFMA rows 0-7 and the same W3
-//                       rows as MFMA rows 8-15; lane l = MFMA row l % 16, K block 4c + l / 16
-//   [gu_s, +I*H/16)     gate/up scale words: g x c x lane (4 B, byte t = tile t)
-//   [dn_w, +H*I/2)      down A operands: row group b (H/64) x chunk c (I/128) x tile t x lane, tile t =
-//                       W2 rows 64b + 16t + (0..15)
-//   [dn_s, +H*I/32)     down scale words: b x c x lane
-struct TiledOffsets {
-  size_t gu_s, dn_w, dn_s, total;
-};
-
-__host__ __device__ __forceinline__ TiledOffsets tiled_offsets(int H, int I) {
-  const size_t ih = (size_t)I * H;
-  TiledOffsets o;
-  o.gu_s = ih;
-  o.dn_w = ih + ih / 16;
-  o.dn_s = o.dn_w + ih / 2;
-  o.total = o.dn_s + ih / 32;
-  return o;
-}
-
 // grid (I/32, slots), 256 threads. The workgroup computes intermediate rows [32g, 32g + 32) of W1 and
 // W3 for the slot's tokens: tile t holds W1 rows 32g + 8t + (0..7) as MFMA rows 0-7 and the same W3
 // rows as MFMA rows 8-15. After the cross-wave sum, wave t owns tile t, applies the SwiGLU epilogue,
@@ -1076,6 +1056,26 @@ int validate_config(const mx_moe_config* c) {
   MX_REQUIRE(c->max_tokens >= 1 && c->max_tokens <= kMaxTokens, "max_tokens must be in [1, %d]", kMaxTokens);
   return MX_OK;
 }
+
+}  // namespace
+
+namespace mxi {
+
+LayerView layer_view(mx_layer* L) {
+  LayerView v{};
+  if (!L) return v;
+  v.ctx = L->ctx;
+  v.cfg = L->cfg;
+  v.router_weight = L->router_weight;
+  v.bias = L->bias;
+  v.tiles = L->tiles;
+  v.has_shared = L->has_shared;
+  return v;
+}
+
+}  // namespace mxi
+
+namespace {
 
 // One stage of a decode call on the arguments recorded in L->last_*.
 int launch_stage(mx_layer* L, int stage, hipStream_t st) {

@@ -191,6 +191,48 @@ class MoELayer:
             xd.free()
             yd.free()
 
+    # -- prefill ----------------------------------------------------------------------------
+    def workspace_bytes(self, tokens: int) -> int:
+        return int(self.lib.cdll.mx_prefill_workspace_bytes(self.handle, int(tokens)))
+
+    def prefill_device(self, x_ptr: int, tokens: int, y_ptr: int, workspace: int, workspace_bytes: int,
+                       ids_ptr=None, weights_ptr=None, stream=None):
+        """y = MoE(x) for `tokens` rows as grouped GEMMs (mx_moe_prefill); routing given by device ids/weights
+        [T, k] or, when both are None, by the layer's router. No host synchronisation."""
+        self.lib.moe_prefill(self.handle, C.c_void_p(int(x_ptr)), int(tokens), _lib.vp(ids_ptr), _lib.vp(weights_ptr),
+                             C.c_void_p(int(y_ptr)), C.c_void_p(int(workspace)), int(workspace_bytes),
+                             _lib._stream(stream))
+
+    def prefill(self, x, ids=None, weights=None) -> np.ndarray:
+        """Host convenience: BF16 bits or FP32 [T, H] in (and optional int32 ids / FP32 weights [T, k]),
+        BF16 bits [T, H] out."""
+        bits = bf16_input(x, self.config.hidden)
+        t = bits.shape[0]
+        k = self.config.top_k
+        if (ids is None) != (weights is None):
+            raise ValueError("routing ids and weights are given together or not at all")
+        if ids is not None:
+            ids = np.ascontiguousarray(ids, dtype=np.int32)
+            weights = np.ascontiguousarray(weights, dtype=np.float32)
+            if ids.shape != (t, k) or weights.shape != (t, k):
+                raise ValueError(f"routing must be [{t}, {k}]")
+            if ids.min() < 0 or ids.max() >= self.config.experts or np.any(np.diff(np.sort(ids, 1), axis=1) == 0):
+                raise ValueError("routing ids must be distinct experts of the layer")
+            if not np.isfinite(weights).all():
+                raise ValueError("route weights must be finite")
+        nbytes = self.workspace_bytes(t)
+        xd = self.ctx.upload(bits)
+        yd = self.ctx.empty((t, self.config.hidden), np.uint16)
+        ws = self.ctx.malloc(nbytes)
+        dev = [self.ctx.upload(ids), self.ctx.upload(weights)] if ids is not None else [None, None]
+        try:
+            self.prefill_device(xd.ptr, t, yd.ptr, ws, nbytes, dev[0], dev[1])
+            return yd.download()
+        finally:
+            for d in [xd, yd] + [d for d in dev if d is not None]:
+                d.free()
+            self.ctx.free(ws)
+
     # -- diagnostics ------------------------------------------------------------------------
     def buffer(self, name: str):
         p, n = C.c_void_p(), C.c_uint64()
