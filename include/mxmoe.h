@@ -152,6 +152,13 @@ int mx_tile_expert(mx_ctx* ctx, const mx_expert_ptrs* ref, int32_t hidden, int32
 int mx_untile_expert(mx_ctx* ctx, const void* tiled, int32_t hidden, int32_t intermediate, const mx_expert_ptrs* ref,
                      void* stream);
 
+/* mx_expert_forward on a tiled expert (a cache slot or bank entry): same stages and arithmetic as the
+ * decode layer's expert kernels. Used by the tiered runtime (TieredExpertRuntime.forward,
+ * src/vesper/tiered.py:199-211). */
+int mx_expert_forward_tiled(mx_ctx* ctx, const void* tiled, int32_t hidden, int32_t intermediate,
+                            const uint16_t* x_bf16, int32_t tokens, float swiglu_limit, const float* route_w,
+                            uint16_t* y_bf16, const mx_expert_stages* stages, void* stream);
+
 /* ---- router (replaces GateProjection.project + RouterProbe, src/vesper/gate.py:133-147,
  *      src/vesper/router.py:227-264, routing_probe.cu:5-86) ---- */
 
@@ -258,6 +265,39 @@ int mx_layer_set_expert(mx_layer* layer, int32_t expert, const void* tiled, void
  * `diagnostics` != 0 also writes the per-stage buffers that mx_layer_buffer exposes. */
 int mx_moe_decode(mx_layer* layer, const uint16_t* x_bf16, int32_t tokens, uint16_t* y_bf16,
                   int32_t diagnostics, void* stream);
+
+/* Decode with routing decided elsewhere (a seeded trace, an expert-parallel dispatcher): ids [T][k] and
+ * weights [T][k] on the device replace the router; an id outside [0, E) or repeated within a token is
+ * replaced (smallest expert the token does not name, weight 0) so the call stays in bounds. */
+int mx_moe_decode_routed(mx_layer* layer, const uint16_t* x_bf16, int32_t tokens, const int32_t* ids,
+                         const float* weights, uint16_t* y_bf16, void* stream);
+/* Re-point n experts at once (one launch per 64), ordered on `stream`: experts[i] -> tiled[i]. */
+int mx_layer_set_experts(mx_layer* layer, int32_t n, const int32_t* experts, const void* const* tiled, void* stream);
+
+/* ---- expert streaming: device slot cache over host-pinned experts (replaces TieredCache /
+ *      CudaCacheBackend / TieredExpertRuntime, src/vesper/cache.py:19-287, src/vesper/tiered.py:50-216) ----
+ *
+ * `slots` device slots of `slot_bytes` (an expert's tiled bytes); keys are caller-chosen 64-bit ids
+ * (e.g. layer << 32 | expert), each registered with its host-pinned source. mx_cache_ensure maps a batch
+ * of keys to slot pointers: hits refresh the LRU order, misses evict the least recently used slot that
+ * the batch does not need and copy the source with hipMemcpyAsync on the cache's copy stream, after the
+ * evicted slot's release event. The caller makes its compute stream wait for mx_cache_ready_event (after
+ * each ensure) and records mx_cache_release on the compute stream after the work that reads the slots.
+ * No host synchronisation; copies overlap compute. */
+typedef struct mx_cache mx_cache;
+int mx_cache_create(mx_ctx* ctx, uint64_t slot_bytes, int32_t slots, mx_cache** out);
+int mx_cache_destroy(mx_cache* cache);
+/* host_src must be pinned (mx_host_alloc_pinned) and hold slot_bytes bytes. */
+int mx_cache_register(mx_cache* cache, int64_t key, const void* host_src);
+/* dev_ptrs[i] <- slot of keys[i] (n <= slots, distinct registered keys); hit[i] (nullable) = 1 if resident. */
+int mx_cache_ensure(mx_cache* cache, const int64_t* keys, int32_t n, void** dev_ptrs, int32_t* hit);
+int mx_cache_ready_event(mx_cache* cache, void** event);
+int mx_cache_release(mx_cache* cache, const int64_t* keys, int32_t n, void* stream);
+int mx_cache_copy_stream(mx_cache* cache, void** stream);
+/* Counters since the last mx_cache_set_timing; copy_ms sums per-copy event pairs (timing enabled). */
+int mx_cache_stats(mx_cache* cache, uint64_t* hits, uint64_t* misses, uint64_t* bytes_copied, double* copy_ms,
+                   int32_t* resident);
+int mx_cache_set_timing(mx_cache* cache, int32_t enable);
 
 /* Prefill: T tokens through the layer (routed experts + shared) as token-sorted grouped GEMMs on the
  * scaled MXFP4 MFMA; same per-token arithmetic as mx_moe_decode.

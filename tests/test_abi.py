@@ -56,3 +56,14 @@ def test_tiled_expert_size_is_the_reference_byte_count():
     assert lib.cdll.mx_tiled_expert_bytes(7168, 2048) == 23_396_352
     for bad in ((100, 128), (128, 0), (-128, 128)):
         assert lib.cdll.mx_tiled_expert_bytes(*bad) == 0
+
+
+def test_expert_keys_round_trip_and_refuse_bad_forms():
+    from vesper_amd.tiered import expert_key, parse_key
+    assert expert_key(*parse_key("7:255")) == (7 << 32) | 255
+    assert parse_key("0:0") == (0, 0)
+    for bad in ("7", "a:b", "1:2:3", None):
+        with pytest.raises(ValueError):
+            parse_key(bad)
+    with pytest.raises(ValueError):
+        expert_key(-1, 0)

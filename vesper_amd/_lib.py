@@ -105,6 +105,19 @@ SIGNATURES = {
     "mx_layer_profile": ([_P, _I32, C.POINTER(_F), C.POINTER(_I32)], C.c_int),
     "mx_layer_time_stage": ([_P, _I32, _I32, C.POINTER(_F), _P], C.c_int),
     "mx_prefill_workspace_bytes": ([_P, _I32], _U64),
+    "mx_moe_decode_routed": ([_P, _P, _I32, _P, _P, _P, _P], C.c_int),
+    "mx_expert_forward_tiled": ([_P, _P, _I32, _I32, _P, _I32, _F, _P, _P, C.POINTER(MxExpertStages), _P], C.c_int),
+    "mx_layer_set_experts": ([_P, _I32, _P, _P, _P], C.c_int),
+    "mx_cache_create": ([_P, _U64, _I32, C.POINTER(_P)], C.c_int),
+    "mx_cache_destroy": ([_P], C.c_int),
+    "mx_cache_register": ([_P, C.c_int64, _P], C.c_int),
+    "mx_cache_ensure": ([_P, _P, _I32, _P, _P], C.c_int),
+    "mx_cache_ready_event": ([_P, C.POINTER(_P)], C.c_int),
+    "mx_cache_release": ([_P, _P, _I32, _P], C.c_int),
+    "mx_cache_copy_stream": ([_P, C.POINTER(_P)], C.c_int),
+    "mx_cache_stats": ([_P, C.POINTER(_U64), C.POINTER(_U64), C.POINTER(_U64), C.POINTER(C.c_double),
+                        C.POINTER(_I32)], C.c_int),
+    "mx_cache_set_timing": ([_P, _I32], C.c_int),
     "mx_moe_prefill": ([_P, _P, _I32, _P, _P, _P, _P, _U64, _P], C.c_int),
     "mx_fp8_tiled_bytes": ([_I32, _I32, _I32], _U64),
     "mx_fp8_tile": ([_P, _P, _P, _I32, _I32, _I32, _P, _P], C.c_int),
@@ -284,6 +297,15 @@ class Context:
             self.lib.device_sync(self._h())
         else:
             self.lib.stream_sync(self._h(), _stream(stream))
+
+    def host_alloc_pinned(self, nbytes: int) -> int:
+        """Pinned host memory (hipHostMalloc through the context; Pinned, cuda.py:200-222)."""
+        p = C.c_void_p()
+        self.lib.host_alloc_pinned(self._h(), int(nbytes), C.byref(p))
+        return int(p.value)
+
+    def host_free_pinned(self, p: int):
+        self.lib.host_free_pinned(self._h(), C.c_void_p(int(p)))
 
     def stream(self) -> int:
         s = C.c_void_p()

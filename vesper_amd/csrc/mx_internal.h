@@ -22,6 +22,13 @@ struct mx_ctx {
   uint64_t scratch_bytes = 0;
 };
 
+// By-value kernel argument of mx_layer_set_experts: up to 64 table entries per launch.
+#define MX_EXPERT_BATCH 64
+struct mx_expert_batch {
+  int32_t expert[MX_EXPERT_BATCH];
+  const void* tiled[MX_EXPERT_BATCH];
+};
+
 namespace mxi {
 
 // Thread-local error text; every failing entry point sets it.

@@ -514,6 +514,51 @@ __global__ __launch_bounds__(kRouteThreads) void route_plan_kernel(const float* 
   build_plan(plan, s_idx, s_w, T, k, E, has_shared);
 }
 
+// Plan from given routing (decode with routing decided elsewhere): ids [T][k] and weights [T][k] are
+// staged in LDS, each token's list is made valid first -- an id outside [0, E) or repeated within the
+// token is replaced by the smallest expert the token does not name, with weight 0 -- so any input keeps
+// the plan's invariants (k distinct experts per token) and every access in bounds.
+__global__ __launch_bounds__(kRouteThreads) void routed_plan_kernel(const int32_t* ids, const float* w, int T, int k,
+                                                                    int E, int32_t* out_ids, float* out_w, Plan* plan,
+                                                                    int has_shared) {
+  __shared__ int32_t s_idx[kMaxTokens * kMaxTopK];
+  __shared__ float s_w[kMaxTokens * kMaxTopK];
+  for (int i = threadIdx.x; i < T * k; i += blockDim.x) {
+    s_idx[i] = ids[i];
+    s_w[i] = w[i];
+  }
+  __syncthreads();
+  if (threadIdx.x < T) {
+    int32_t* row = s_idx + threadIdx.x * k;
+    float* wr = s_w + threadIdx.x * k;
+    for (int i = 0; i < k; ++i) {
+      bool bad = row[i] < 0 || row[i] >= E;
+      for (int j = 0; j < i && !bad; ++j) bad = row[j] == row[i];
+      if (!bad) continue;
+      for (int e = 0; e < E; ++e) {
+        bool used = false;
+        for (int j = 0; j < k && !used; ++j) used = (j != i) && row[j] == e;
+        if (!used) {
+          row[i] = e;
+          break;
+        }
+      }
+      wr[i] = 0.f;
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < T * k; i += blockDim.x) {
+    out_ids[i] = s_idx[i];
+    out_w[i] = s_w[i];
+  }
+  build_plan(plan, s_idx, s_w, T, k, E, has_shared);
+}
+
+__global__ void set_experts_kernel(const uint8_t** table, int n, mx_expert_batch b) {
+  const int i = threadIdx.x;
+  if (i < n) table[b.expert[i]] = (const uint8_t*)b.tiled[i];
+}
+
 // Stand-alone top-k over supplied selection/scores: one wave per token.
 __global__ __launch_bounds__(256) void topk_kernel(const float* selection, const float* scores, int T, int E, int k,
                                                    float route_scale, TopkOut o) {
@@ -1308,6 +1353,50 @@ int mx_moe_decode(mx_layer* L, const uint16_t* x, int32_t T, uint16_t* y, int32_
   return MX_OK;
 }
 
+int mx_moe_decode_routed(mx_layer* L, const uint16_t* x, int32_t T, const int32_t* ids, const float* weights,
+                         uint16_t* y, void* stream) {
+  MX_REQUIRE(L != nullptr, "layer is closed");
+  if (int s = use(L->ctx)) return s;
+  const mx_moe_config& c = L->cfg;
+  MX_REQUIRE(T >= 0 && T <= c.max_tokens, "token count %d outside [0, %d]", T, c.max_tokens);
+  if (T == 0) return MX_OK;
+  MX_REQUIRE(x && y && ids && weights && aligned(x, 16) && aligned(y, 16),
+             "x, y (16-byte aligned), ids and weights must be device pointers");
+  hipStream_t st = as_stream(stream);
+  if (int s = mx_act_quant32(L->ctx, x, L->xq, L->xs, T, c.hidden, stream)) return s;
+  hipLaunchKernelGGL(routed_plan_kernel, dim3(1), dim3(64 * T), 0, st, ids, weights, T, c.top_k, c.experts, L->indices,
+                     L->weights, L->plan, L->has_shared);
+  MX_LAUNCH_CHECK("routed_plan_kernel");
+  L->last_x = x;
+  L->last_y = y;
+  L->last_T = T;
+  L->last_diag = false;
+  for (int stage = MX_STAGE_GATEUP; stage <= MX_STAGE_COMBINE; ++stage)
+    if (int s = launch_stage(L, stage, st)) return s;
+  return MX_OK;
+}
+
+int mx_layer_set_experts(mx_layer* L, int32_t n, const int32_t* experts, const void* const* tiled, void* stream) {
+  MX_REQUIRE(L != nullptr, "layer is closed");
+  if (int s = use(L->ctx)) return s;
+  MX_REQUIRE(n >= 0 && (n == 0 || (experts && tiled)), "mx_layer_set_experts: bad arguments");
+  for (int i = 0; i < n; ++i) {
+    MX_REQUIRE(experts[i] >= 0 && experts[i] < L->cfg.experts, "expert %d outside the layer", experts[i]);
+    MX_REQUIRE(tiled[i] != nullptr && aligned(tiled[i], 256), "tiled expert must be a 256-byte aligned pointer");
+  }
+  for (int base = 0; base < n; base += MX_EXPERT_BATCH) {
+    mx_expert_batch b{};
+    const int m = std::min(MX_EXPERT_BATCH, n - base);
+    for (int i = 0; i < m; ++i) {
+      b.expert[i] = experts[base + i];
+      b.tiled[i] = tiled[base + i];
+    }
+    hipLaunchKernelGGL(set_experts_kernel, dim3(1), dim3(64), 0, as_stream(stream), L->tiles, m, b);
+    MX_LAUNCH_CHECK("set_experts_kernel");
+  }
+  return MX_OK;
+}
+
 int mx_layer_time_stage(mx_layer* L, int32_t stage, int32_t iters, float* us_per_launch, void* stream) {
   MX_REQUIRE(L != nullptr, "layer is closed");
   if (int s = use(L->ctx)) return s;
@@ -1386,6 +1475,62 @@ int mx_expert_forward(mx_ctx* ctx, const mx_expert_ptrs* w, int32_t format, int3
   hipLaunchKernelGGL(gateup_kernel<false>, dim3(I / 32, 1), dim3(256), 0, st, a);
   MX_LAUNCH_CHECK("gateup_kernel");
   hipLaunchKernelGGL(down_kernel<false>, dim3(H / 64, 1), dim3(256), 0, st, a);
+  MX_LAUNCH_CHECK("down_kernel");
+  return MX_OK;
+}
+
+int mx_expert_forward_tiled(mx_ctx* ctx, const void* tiled, int32_t H, int32_t I, const uint16_t* x, int32_t T,
+                            float limit, const float* route_w, uint16_t* y, const mx_expert_stages* stages,
+                            void* stream) {
+  if (int s = use(ctx)) return s;
+  MX_REQUIRE(tiled != nullptr && aligned(tiled, 256), "mx_expert_forward_tiled: 256-byte aligned tiled expert required");
+  MX_REQUIRE(H > 0 && H % 128 == 0 && I > 0 && I % 128 == 0, "expert shapes must be positive multiples of 128");
+  MX_REQUIRE(T >= 0 && T <= kMaxTokens, "token count %d outside [0, %d]", T, kMaxTokens);
+  MX_REQUIRE(std::isfinite(limit) && limit >= 0.f, "Invalid SwiGLU limit");
+  if (T == 0) return MX_OK;
+  MX_REQUIRE(x && y && aligned(x, 16) && aligned(y, 16), "x and y must be 16-byte aligned device pointers");
+  hipStream_t st = as_stream(stream);
+  // scratch: plan | one-entry expert table | xq | xs | dq | ds (stage buffers replace them when supplied)
+  const uint64_t plan_b = (sizeof(Plan) + 255) & ~255ull, table_b = 256;
+  const uint64_t xq_b = ((uint64_t)T * H + 255) & ~255ull, xs_b = ((uint64_t)T * H / 32 + 255) & ~255ull;
+  const uint64_t dq_b = ((uint64_t)T * I + 255) & ~255ull, ds_b = ((uint64_t)T * I / 32 + 255) & ~255ull;
+  void* base = nullptr;
+  if (int s = scratch(ctx, plan_b + table_b + xq_b + xs_b + dq_b + ds_b, &base)) return s;
+  uint8_t* b8 = (uint8_t*)base;
+  Plan* plan = (Plan*)b8;
+  const uint8_t** table = (const uint8_t**)(b8 + plan_b);
+  uint8_t* cur = b8 + plan_b + table_b;
+  uint8_t* xq = (stages && stages->q) ? stages->q : cur;
+  uint8_t* xs = (stages && stages->s) ? stages->s : cur + xq_b;
+  uint8_t* dq = (stages && stages->down_q) ? stages->down_q : cur + xq_b + xs_b;
+  uint8_t* ds = (stages && stages->down_s) ? stages->down_s : cur + xq_b + xs_b + dq_b;
+  MX_REQUIRE(aligned(xq, 16) && aligned(dq, 16) && aligned(xs, 4) && aligned(ds, 4),
+             "stage buffers q/down_q must be 16-byte and s/down_s 4-byte aligned");
+  hipLaunchKernelGGL(set_expert_kernel, dim3(1), dim3(1), 0, st, table, (const uint8_t*)tiled);
+  MX_LAUNCH_CHECK("set_expert_kernel");
+  hipLaunchKernelGGL(single_plan_kernel, dim3(1), dim3(64), 0, st, plan, T, route_w);
+  MX_LAUNCH_CHECK("single_plan_kernel");
+  if (int s = mx_act_quant32(ctx, x, xq, xs, T, H, stream)) return s;
+  ExpertArgs a{};
+  a.tiles = table;
+  a.plan = plan;
+  a.H = H;
+  a.I = I;
+  a.limit = limit;
+  a.xq = xq;
+  a.xs = xs;
+  a.dq = dq;
+  a.ds = ds;
+  a.out = y;
+  if (stages) {
+    a.w1 = stages->w1;
+    a.w3 = stages->w3;
+    a.din = stages->down_input;
+    a.trace = stages->trace;
+  }
+  hipLaunchKernelGGL(gateup_kernel<true>, dim3(I / 32, 1), dim3(256), 0, st, a);
+  MX_LAUNCH_CHECK("gateup_kernel");
+  hipLaunchKernelGGL(down_kernel<true>, dim3(H / 64, 1), dim3(256), 0, st, a);
   MX_LAUNCH_CHECK("down_kernel");
   return MX_OK;
 }

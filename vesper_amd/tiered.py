@@ -1,0 +1,275 @@
+"""Host-pinned expert streaming (mirrors TieredCache / TieredExpertRuntime, src/vesper/cache.py:19-287 and
+src/vesper/tiered.py:130-216, made asynchronous).
+
+* ExpertCache: HBM slots over host-pinned expert bytes (mx_cache_*): LRU, misses copied with hipMemcpyAsync
+  on a side stream, ordered by per-slot release events and a ready event instead of host waits.
+* HostExpertPool: tiled experts in pinned host memory (the RAM tier), filled from reference-layout arrays or
+  from device-generated synthetic experts.
+* TieredExpertRuntime: forward(key "layer:expert", x, w) on the slot the cache gives (the reference's
+  single-expert API); last_event["source_tier"] is "primary_gpu" on a hit, "host_pinned" on a miss.
+* OffloadDecode: several MoE layers whose routed experts live in the pool and are streamed into the cache
+  per step; the shared experts stay resident.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import threading
+import time
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from .config import MoEConfig
+from .layer import TENSORS, ExpertBank, bf16_input, validate_expert_arrays
+
+
+def expert_key(layer: int, expert: int) -> int:
+    """64-bit cache key of (layer, expert)."""
+    if not (0 <= layer < 2 ** 31 and 0 <= expert < 2 ** 32):
+        raise ValueError("layer or expert index outside the key range")
+    return (int(layer) << 32) | int(expert)
+
+
+def parse_key(key: str) -> tuple[int, int]:
+    """The reference's "layer:expert" key (tiered.py:199)."""
+    try:
+        layer, expert = key.split(":")
+        return int(layer), int(expert)
+    except (AttributeError, ValueError):
+        raise ValueError("Expert keys have the form 'layer:expert'") from None
+
+
+class ExpertCache:
+    """`slots` device slots of `slot_bytes` each, keyed by expert_key."""
+
+    def __init__(self, ctx: _lib.Context, slot_bytes: int, slots: int):
+        self.ctx, self.slot_bytes, self.slots = ctx, int(slot_bytes), int(slots)
+        h = C.c_void_p()
+        ctx.lib.cache_create(ctx._h(), self.slot_bytes, self.slots, C.byref(h))
+        self.handle = h
+
+    def register(self, key: int, host_ptr: int):
+        self.ctx.lib.cache_register(self.handle, int(key), C.c_void_p(int(host_ptr)))
+
+    def ensure(self, keys) -> tuple[list[int], np.ndarray]:
+        keys = np.ascontiguousarray(keys, dtype=np.int64)
+        ptrs = (C.c_void_p * max(len(keys), 1))()
+        hits = np.zeros(max(len(keys), 1), np.int32)
+        self.ctx.lib.cache_ensure(self.handle, keys.ctypes.data_as(C.c_void_p), len(keys), ptrs,
+                                  hits.ctypes.data_as(C.c_void_p))
+        return [int(p or 0) for p in ptrs[:len(keys)]], hits[:len(keys)]
+
+    def ready_event(self) -> int:
+        e = C.c_void_p()
+        self.ctx.lib.cache_ready_event(self.handle, C.byref(e))
+        return int(e.value)
+
+    def wait_ready(self, stream=None):
+        """Make `stream` wait for the copies of the last ensure()."""
+        self.ctx.lib.stream_wait_event(self.ctx._h(), _lib._stream(stream), C.c_void_p(self.ready_event()))
+
+    def release(self, keys, stream=None):
+        keys = np.ascontiguousarray(keys, dtype=np.int64)
+        self.ctx.lib.cache_release(self.handle, keys.ctypes.data_as(C.c_void_p), len(keys), _lib._stream(stream))
+
+    def set_timing(self, enable: bool):
+        self.ctx.lib.cache_set_timing(self.handle, int(bool(enable)))
+
+    def stats(self) -> dict:
+        hits, misses, nbytes = C.c_uint64(), C.c_uint64(), C.c_uint64()
+        ms, resident = C.c_double(), C.c_int32()
+        self.ctx.lib.cache_stats(self.handle, C.byref(hits), C.byref(misses), C.byref(nbytes), C.byref(ms),
+                                 C.byref(resident))
+        return {"hits": hits.value, "misses": misses.value, "bytes_copied": nbytes.value, "copy_ms": ms.value,
+                "resident": resident.value}
+
+    def close(self):
+        if self.handle:
+            h, self.handle = self.handle, C.c_void_p()
+            self.ctx.lib.cache_destroy(h)
+
+
+class HostExpertPool:
+    """`count` tiled experts in one pinned host allocation (the RAM tier of the reference's cache)."""
+
+    def __init__(self, ctx: _lib.Context, config: MoEConfig, count: int):
+        self.ctx, self.config, self.count = ctx, config, int(count)
+        self.expert_bytes = int(ctx.lib.cdll.mx_tiled_expert_bytes(config.hidden, config.intermediate))
+        self.base = ctx.host_alloc_pinned(self.expert_bytes * self.count)
+
+    def ptr(self, index: int) -> int:
+        if not 0 <= index < self.count:
+            raise ValueError("pool index outside the pool")
+        return self.base + index * self.expert_bytes
+
+    def fill_from_bank(self, bank: ExpertBank, bank_index: int, index: int):
+        """Copy one tiled expert of a device bank into pool entry `index` (D2H)."""
+        self.ctx.lib.memcpy_d2h(self.ctx._h(), C.c_void_p(self.ptr(index)), C.c_void_p(bank.tiled_ptr(bank_index)),
+                                self.expert_bytes, None)
+
+    def upload_arrays(self, index: int, arrays: dict, staging: ExpertBank):
+        """Reference-layout arrays -> tiled (on the device, via a one-expert staging bank) -> pool entry."""
+        validate_expert_arrays(arrays, self.config)
+        staging.upload(0, arrays)
+        self.fill_from_bank(staging, 0, index)
+
+    def close(self):
+        if self.base:
+            self.ctx.host_free_pinned(self.base)
+            self.base = 0
+
+
+@dataclass(frozen=True)
+class CacheConfig:
+    """Slots of the device cache (the reference's primary slots, tiered.py:21-49); RAM is the pool."""
+    primary_slots: int = 64
+    timing: bool = False
+
+
+class TieredExpertRuntime:
+    """Serial single-expert execution through the cache (tiered.py:130-216): forward(key, x, w)."""
+
+    def __init__(self, ctx: _lib.Context, config: MoEConfig, pool: HostExpertPool, index_of: dict,
+                 cache_config: CacheConfig = CacheConfig(), swiglu_limit: float | None = None):
+        self.ctx, self.config, self.pool, self.index_of = ctx, config, pool, dict(index_of)
+        self.limit = config.swiglu_limit if swiglu_limit is None else float(swiglu_limit)
+        self.cache = ExpertCache(ctx, pool.expert_bytes, cache_config.primary_slots)
+        for key, index in self.index_of.items():
+            self.cache.register(expert_key(*parse_key(key)), pool.ptr(index))
+        self.lock, self.active, self.last_event = threading.Lock(), False, None
+        t, h, i = 16, config.hidden, config.intermediate
+        self.work = {"x": ctx.empty((t, h), np.uint16), "route": ctx.empty((t,), np.float32),
+                     "q": ctx.empty((t, h), np.uint8), "s": ctx.empty((t, h // 32), np.uint8),
+                     "w1": ctx.empty((t, i), np.uint16), "w3": ctx.empty((t, i), np.uint16),
+                     "down_input": ctx.empty((t, i), np.uint16), "trace": ctx.empty((t, i, 5), np.float32),
+                     "down_q": ctx.empty((t, i), np.uint8), "down_s": ctx.empty((t, i // 32), np.uint8),
+                     "w2": ctx.empty((t, h), np.uint16)}
+
+    def forward(self, key: str, x, routing_weight=None) -> dict:
+        if key not in self.index_of:
+            raise KeyError("Requested expert is absent from the pinned native store")
+        bits = bf16_input(x, self.config.hidden)
+        t = bits.shape[0]
+        if not 1 <= t <= 16:
+            raise ValueError("One expert call accepts 1 to 16 tokens")
+        route = None
+        if routing_weight is not None:
+            route = np.broadcast_to(np.asarray(routing_weight, np.float32).reshape(-1), (t,)).copy()
+            if not np.isfinite(route).all():
+                raise ValueError("Routing weight must be finite")
+        with self.lock:
+            if self.active:
+                raise RuntimeError("Nested requests could replace a live compute slot")
+            self.active = True
+            try:
+                started = time.perf_counter()
+                w = self.work
+                self.ctx.copy_h2d(w["x"].ptr, bits)
+                if route is not None:
+                    self.ctx.copy_h2d(w["route"].ptr, route)
+                k = expert_key(*parse_key(key))
+                (ptr,), (hit,) = self.cache.ensure([k])
+                self.cache.wait_ready(None)
+                stages = _lib.MxExpertStages(*[w[n].ptr for n in ("q", "s", "w1", "w3", "down_input", "trace",
+                                                                  "down_q", "down_s")])
+                self.ctx.lib.expert_forward_tiled(self.ctx._h(), C.c_void_p(ptr), self.config.hidden,
+                                                  self.config.intermediate, C.c_void_p(w["x"].ptr), t, self.limit,
+                                                  None if route is None else C.c_void_p(w["route"].ptr),
+                                                  C.c_void_p(w["w2"].ptr), C.byref(stages), None)
+                self.cache.release([k], None)
+                h, i = self.config.hidden, self.config.intermediate
+                layout = {"q": ((t, h), np.uint8), "s": ((t, h // 32), np.uint8), "w1": ((t, i), np.uint16),
+                          "w3": ((t, i), np.uint16), "down_input": ((t, i), np.uint16),
+                          "trace": ((t, i, 5), np.float32), "down_q": ((t, i), np.uint8),
+                          "down_s": ((t, i // 32), np.uint8), "w2": ((t, h), np.uint16)}
+                out = {n: self.ctx.download(w[n].ptr, shape, dt) for n, (shape, dt) in layout.items()}
+                out["down_input"] = (out["down_input"].astype(np.uint32) << 16).view(np.float32)
+                self.last_event = {"key": key, "source_tier": "primary_gpu" if hit else "host_pinned",
+                                   "wall_ms": (time.perf_counter() - started) * 1000}
+                return out
+            finally:
+                self.active = False
+
+    def snapshot(self) -> dict:
+        return self.cache.stats()
+
+    def close(self):
+        self.cache.close()
+        for d in self.work.values():
+            d.free()
+
+
+class OffloadDecode:
+    """`layers` MoE layers sharing one device cache; routed experts stream from host-pinned pools.
+
+    pool_of(layer, expert) -> (pool, index) names each routed expert's host bytes; shared_ptrs[layer] is a
+    resident tiled shared expert (or None). step(x, routing) runs every layer at T tokens with given
+    routing: per layer, ensure its experts (copies on the cache stream), make the compute stream wait,
+    re-point the layer's table (one launch), decode, release the slots -- all asynchronous, so the next
+    layer's copies overlap this layer's compute.
+    """
+
+    def __init__(self, ctx: _lib.Context, config: MoEConfig, layers: int, pool_of, shared_ptrs, cache: ExpertCache,
+                 placeholder_ptr: int):
+        self.ctx, self.config, self.layers, self.cache = ctx, config, int(layers), cache
+        self.lib = ctx.lib
+        self.handles = []
+        self.stream = ctx.stream()
+        self._owned = []
+        cfg = _lib.MxMoeConfig(config.hidden, config.intermediate, config.experts, config.top_k,
+                               _lib.MX_SCORE[config.score_func], config.route_scale, config.swiglu_limit,
+                               _lib.MX_FMT_MXFP4 if config.shared else -1, config.max_tokens)
+        rw = ctx.upload(np.zeros((config.experts, config.hidden), np.float32))   # router unused: routing is given
+        self._owned.append(rw)
+        for layer in range(self.layers):
+            table = (C.c_void_p * config.experts)(*([placeholder_ptr] * config.experts))
+            shared = C.c_void_p(shared_ptrs[layer]) if config.shared else None
+            h = C.c_void_p()
+            self.lib.layer_create(ctx._h(), C.byref(cfg), _lib.vp(rw), None, table, shared, C.byref(h))
+            self.handles.append(h)
+            for e in range(config.experts):
+                pool, index = pool_of(layer, e)
+                cache.register(expert_key(layer, e), pool.ptr(index))
+        t, k = config.max_tokens, config.top_k
+        self.ids = [ctx.empty((t, k), np.int32) for _ in range(self.layers)]
+        self.wts = [ctx.empty((t, k), np.float32) for _ in range(self.layers)]
+        self._owned += self.ids + self.wts
+
+    def load_routing(self, routing):
+        """routing[layer] = (ids [T, k] int32, weights [T, k] FP32), copied to the device (synchronously)."""
+        for layer, (ids, w) in enumerate(routing):
+            self.ctx.copy_h2d(self.ids[layer].ptr, np.ascontiguousarray(ids, np.int32))
+            self.ctx.copy_h2d(self.wts[layer].ptr, np.ascontiguousarray(w, np.float32))
+
+    def step_device(self, x_ptr: int, tokens: int, y_ptrs, routing_host):
+        """Enqueue one step on self.stream; routing_host[layer] = ids [T, k] (host, for the cache keys)."""
+        for layer in range(self.layers):
+            experts = np.unique(routing_host[layer][:tokens])
+            keys = [expert_key(layer, int(e)) for e in experts]
+            ptrs, _ = self.cache.ensure(keys)
+            self.cache.wait_ready(self.stream)
+            arr_e = (C.c_int32 * len(experts))(*[int(e) for e in experts])
+            arr_p = (C.c_void_p * len(experts))(*ptrs)
+            self.lib.layer_set_experts(self.handles[layer], len(experts), arr_e, arr_p, _lib._stream(self.stream))
+            src = x_ptr if layer == 0 else y_ptrs[layer - 1]
+            self.lib.moe_decode_routed(self.handles[layer], C.c_void_p(int(src)), int(tokens),
+                                       C.c_void_p(self.ids[layer].ptr), C.c_void_p(self.wts[layer].ptr),
+                                       C.c_void_p(int(y_ptrs[layer])), _lib._stream(self.stream))
+            self.cache.release(keys, self.stream)
+
+    def close(self):
+        for h in self.handles:
+            self.lib.layer_destroy(h)
+        self.handles = []
+        for d in self._owned:
+            d.free()
+        self._owned = []
+        self.ctx.destroy_stream(self.stream)
+
+
+def decode_routed(layer, x_ptr: int, tokens: int, ids_ptr: int, weights_ptr: int, y_ptr: int, stream=None):
+    """mx_moe_decode_routed on a MoELayer (routing given on the device)."""
+    layer.lib.moe_decode_routed(layer.handle, C.c_void_p(int(x_ptr)), int(tokens), C.c_void_p(int(ids_ptr)),
+                                C.c_void_p(int(weights_ptr)), C.c_void_p(int(y_ptr)), _lib._stream(stream))
