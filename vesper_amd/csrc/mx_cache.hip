@@ -3,7 +3,8 @@
 //
 // The reference promotes an expert with blocking copies and a host sync per request. Here a fixed pool
 // of HBM slots is indexed by an LRU map from 64-bit keys (e.g. layer << 32 | expert) to slots; a miss
-// takes the least recently used slot that the same batch does not need, and its bytes are copied from
+// takes the least recently used slot that the same batch does not need (preferring one that no queued work
+// still reads), and its bytes are copied from
 // the key's registered host-pinned source with hipMemcpyAsync on the cache's own copy stream. Ordering is
 // carried by events, never by host waits:
 //   * each slot has a release event, recorded by the caller on the compute stream after the work that
@@ -12,6 +13,7 @@
 //     the compute stream wait for (mx_cache_ready_event + mx_stream_wait_event).
 // So copies for the next layer run while the current layer computes. Per-copy event pairs (optional)
 // measure the time the copy engine spent on each transfer.
+#include <algorithm>
 #include <cstring>
 #include <list>
 #include <unordered_map>
@@ -137,6 +139,9 @@ int mx_cache_ensure(mx_cache* c, const int64_t* keys, int32_t n, void** dev_ptrs
     c->lru.splice(c->lru.end(), c->lru, it->second.second);
     slot_of[i] = it->second.first;
   }
+  // the batch's keys present in the LRU list: its hits now, plus each miss once inserted (all at the back)
+  int batch_in_lru = 0;
+  for (int i = 0; i < n; ++i) batch_in_lru += slot_of[i] >= 0;
   bool copied = false;
   for (int i = 0; i < n; ++i) {
     if (hit) hit[i] = slot_of[i] >= 0;
@@ -150,10 +155,22 @@ int mx_cache_ensure(mx_cache* c, const int64_t* keys, int32_t n, void** dev_ptrs
       s = c->free_slots.back();
       c->free_slots.pop_back();
     } else {
-      const int64_t victim = c->lru.front();   // least recent; batch keys are all at the back
-      auto vit = c->where.find(victim);
+      // Least recently used first, but skip a slot whose last release is still in flight on the GPU (the
+      // host may run ahead of the device): copying into it would make the copy stream wait for that work.
+      // Batch keys sit at the back and are never reached; with none idle, take the front and wait.
+      auto pick = c->lru.begin();
+      const int candidates = std::min<int>(64, (int)c->lru.size() - batch_in_lru);
+      int scanned = 0;
+      for (auto it = c->lru.begin(); scanned < candidates; ++it, ++scanned) {
+        const int cand = c->where[*it].first;
+        if (!c->release_pending[cand] || hipEventQuery(c->released[cand]) == hipSuccess) {
+          pick = it;
+          break;
+        }
+      }
+      auto vit = c->where.find(*pick);
       s = vit->second.first;
-      c->lru.pop_front();
+      c->lru.erase(pick);
       c->where.erase(vit);
     }
     if (c->release_pending[s]) MX_HIP(hipStreamWaitEvent(c->copy, c->released[s], 0));
@@ -175,6 +192,7 @@ int mx_cache_ensure(mx_cache* c, const int64_t* keys, int32_t n, void** dev_ptrs
     if (c->timing) MX_HIP(hipEventRecord(c->copy_events[c->copy_events_used++], c->copy));
     c->bytes_copied += c->slot_bytes;
     c->owner[s] = keys[i];
+    ++batch_in_lru;
     c->lru.push_back(keys[i]);
     c->where[keys[i]] = {s, std::prev(c->lru.end())};
     slot_of[i] = s;

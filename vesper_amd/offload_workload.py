@@ -1,0 +1,187 @@
+"""Offload-mixed MoE decode, used by bench.py.
+
+  python -m vesper_amd.offload_workload --steps 10 --warmup 4
+
+8 consecutive MoE layers of the BASELINE shapes at T = 4 tokens. A device cache holds 25 % of the routed
+experts (8 x 256 / 4 = 512 slots of 23.4 MB); every routed expert's tiled bytes sit in host pinned memory
+and misses stream over PCIe with hipMemcpyAsync on the cache's side stream, overlapped with compute. The
+expert selection is a seeded trace: each token picks 8 distinct experts at step 0, and at every later step
+keeps 5 of its previous 8 (60 %) and draws 3 new ones. Route weights are uniform positive, normalized,
+times 2.5. Shared experts stay resident.
+
+Synthetic content: one pinned pool of the 256 routed experts serves all 8 layers (key (layer, expert)
+reads pool[expert]); the cache keys stay distinct per layer, so the traffic is that of 8 x 256 experts
+while host memory holds 6 GB instead of 48 GB. The compute-only reference runs the same trace with
+every expert resident.
+
+At most two steps are in flight (the host waits for step s - 2 before enqueuing step s).
+
+Reported: step us (HIP events on the compute stream), copy us per step (a fresh cache replaying the same
+trace with copies only: the same misses, no compute between them), compute-only us per step, overlap = 1 - (t_step - max(t_copy, t_compute)) /
+min(t_copy, t_compute), the pinned H2D rate of one large copy, and cache hits / misses / bytes.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import sys
+
+import numpy as np
+
+
+def trace(rng, steps, layers, tokens, experts, top_k, keep=5, route_scale=2.5):
+    """routing[step][layer] = (ids [T, k] int32, weights [T, k] FP32)."""
+    out = []
+    prev = [[None] * tokens for _ in range(layers)]
+    for _ in range(steps):
+        step = []
+        for layer in range(layers):
+            ids = np.empty((tokens, top_k), np.int32)
+            for t in range(tokens):
+                if prev[layer][t] is None:
+                    ids[t] = rng.choice(experts, top_k, replace=False)
+                else:
+                    kept = rng.choice(prev[layer][t], keep, replace=False)
+                    rest = np.setdiff1d(np.arange(experts), kept)
+                    ids[t] = np.concatenate([kept, rng.choice(rest, top_k - keep, replace=False)])
+                prev[layer][t] = ids[t].copy()
+            raw = rng.uniform(0.05, 1.0, (tokens, top_k)).astype(np.float32)
+            step.append((ids, (raw / raw.sum(1, keepdims=True) * np.float32(route_scale)).astype(np.float32)))
+        out.append(step)
+    return out
+
+
+def run(steps=10, warmup=4, layers=8, tokens=4, resident_frac=0.25, seed=20261018, ctx=None):
+    from . import _lib
+    from .config import BASELINE as cfg
+    from .layer import ExpertBank, MoELayer, bf16_input
+    from .tiered import ExpertCache, HostExpertPool, OffloadDecode, decode_routed, expert_key
+    own = ctx is None
+    ctx = ctx or _lib.Context(0)
+    rng = np.random.default_rng(seed)
+    bank = ExpertBank(ctx, cfg, cfg.experts + 1)         # device copies: pool source and compute-only reference
+    bank.fill_synthetic(seed)
+    pool = HostExpertPool(ctx, cfg, cfg.experts)
+    for e in range(cfg.experts):
+        pool.fill_from_bank(bank, e, e)
+    ctx.sync()
+    # pinned H2D peak: one 1 GiB copy from the pool into the bank's first experts' space
+    n = 1 << 30
+    s0, s1 = ctx.event(), ctx.event()
+    ctx.record(s0)
+    ctx.lib.memcpy_h2d(ctx._h(), C.c_void_p(bank.base), C.c_void_p(pool.base), n, None)
+    ctx.record(s1)
+    h2d_gbs = n / (ctx.elapsed_ms(s0, s1) * 1e-3) / 1e9
+    for e in range(cfg.experts):                         # restore the overwritten experts' bytes
+        ctx.lib.memcpy_h2d(ctx._h(), C.c_void_p(bank.tiled_ptr(e)), C.c_void_p(pool.ptr(e)), pool.expert_bytes, None)
+    ctx.sync()
+    slots = int(resident_frac * layers * cfg.experts)
+    cache = ExpertCache(ctx, pool.expert_bytes, slots)
+    off = OffloadDecode(ctx, cfg, layers, lambda l, e: (pool, e), [bank.tiled_ptr(cfg.experts)] * layers, cache,
+                        bank.tiled_ptr(0))
+    tr = trace(rng, warmup + steps, layers, tokens, cfg.experts, cfg.top_k)
+    x = ctx.upload(bf16_input(rng.standard_normal((tokens, cfg.hidden)).astype(np.float32), cfg.hidden))
+    ys = [ctx.empty((tokens, cfg.hidden), np.uint16) for _ in range(layers)]
+    ids_dev = [[ctx.upload(tr[s][l][0]) for l in range(layers)] for s in range(warmup + steps)]
+    w_dev = [[ctx.upload(tr[s][l][1]) for l in range(layers)] for s in range(warmup + steps)]
+
+    def offload_step(s):
+        for l in range(layers):
+            ctx.copy_d2d(off.ids[l].ptr, ids_dev[s][l].ptr, ids_dev[s][l].nbytes, off.stream)
+            ctx.copy_d2d(off.wts[l].ptr, w_dev[s][l].ptr, w_dev[s][l].nbytes, off.stream)
+        off.step_device(x.ptr, tokens, [y.ptr for y in ys], [tr[s][l][0] for l in range(layers)])
+
+    # at most two steps in flight: before enqueuing step s the host waits for step s - 2 to finish (a serving
+    # loop also waits, for the next step's routing)
+    done = [ctx.event() for _ in range(warmup + steps)]
+
+    def enqueue(s):
+        if s >= 2:
+            ctx.lib.event_sync(ctx._h(), C.c_void_p(done[s - 2]))
+        offload_step(s)
+        ctx.record(done[s], off.stream)
+
+    for s in range(warmup):
+        enqueue(s)
+    ctx.sync(off.stream)
+    cache.set_timing(False)
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.record(e0, off.stream)
+    for s in range(warmup, warmup + steps):
+        enqueue(s)
+    ctx.record(e1, off.stream)
+    t_step = ctx.elapsed_ms(e0, e1) * 1000 / steps
+    st = cache.stats()
+    off.close()
+    cache.close()
+
+    # copy-only: a fresh cache replays the same trace (same misses) with no compute between the copies
+    cache = ExpertCache(ctx, pool.expert_bytes, slots)
+    off = OffloadDecode(ctx, cfg, layers, lambda l, e: (pool, e), [bank.tiled_ptr(cfg.experts)] * layers, cache,
+                        bank.tiled_ptr(0))
+
+    def copy_only(s):
+        for l in range(layers):
+            keys = [expert_key(l, int(e)) for e in np.unique(tr[s][l][0])]
+            cache.ensure(keys)
+            cache.wait_ready(off.stream)
+            cache.release(keys, off.stream)
+
+    for s in range(warmup):
+        copy_only(s)
+    ctx.sync(off.stream)
+    cache.set_timing(False)
+    ctx.record(e0, off.stream)
+    for s in range(warmup, warmup + steps):
+        copy_only(s)
+    ctx.record(e1, off.stream)
+    t_copy = ctx.elapsed_ms(e0, e1) * 1000 / steps
+    assert cache.stats()["misses"] == st["misses"], "the copy-only replay must see the same misses"
+
+    # compute-only: the same layers and trace with every expert resident (table -> bank)
+    layer = MoELayer(ctx, cfg, np.zeros((cfg.experts, cfg.hidden), np.float32), bank)
+    for s in range(warmup):
+        for l in range(layers):
+            decode_routed(layer, x.ptr if l == 0 else ys[l - 1].ptr, tokens, ids_dev[s][l].ptr, w_dev[s][l].ptr,
+                          ys[l].ptr)
+    ctx.sync()
+    ctx.record(e0)
+    for s in range(warmup, warmup + steps):
+        for l in range(layers):
+            decode_routed(layer, x.ptr if l == 0 else ys[l - 1].ptr, tokens, ids_dev[s][l].ptr, w_dev[s][l].ptr,
+                          ys[l].ptr)
+    ctx.record(e1)
+    t_compute = ctx.elapsed_ms(e0, e1) * 1000 / steps
+    raw = 1.0 - (t_step - max(t_copy, t_compute)) / max(min(t_copy, t_compute), 1e-9)
+    overlap = min(1.0, raw)   # above 1 only by run-to-run noise (the step ran faster than copies alone)
+    out = {"layers": layers, "tokens": tokens, "cache_slots": slots, "step_us": round(t_step, 1),
+           "copy_us": round(t_copy, 1), "compute_us": round(t_compute, 1), "overlap": round(overlap, 4), "overlap_raw": round(raw, 4),
+           "h2d_GB_per_s_single_copy": round(h2d_gbs, 1),
+           "streamed_GB_per_s": round(st["bytes_copied"] / steps / (t_step * 1e-6) / 1e9, 1),
+           "misses_per_step": st["misses"] / steps, "hits_per_step": st["hits"] / steps,
+           "bytes_per_step": st["bytes_copied"] // steps}
+    layer.close()
+    off.close()
+    cache.close()
+    for d in [x] + ys + [d for row in ids_dev + w_dev for d in row]:
+        d.free()
+    pool.close()
+    bank.free()
+    if own:
+        ctx.close()
+    return out
+
+
+def main():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=4)
+    args = p.parse_args()
+    print(json.dumps(run(args.steps, args.warmup)), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
