@@ -34,6 +34,8 @@ def parse():
     p.add_argument("--seed", type=int, default=20261018)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--profile-iters", type=int, default=20)
+    p.add_argument("--no-secondary", action="store_true",
+                   help="skip the other BASELINE configurations (prefill, FP8 projections, offload)")
     return p.parse_args()
 
 
@@ -196,11 +198,38 @@ def main():
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle, bounded sample)")
         result["cpu_baseline"] = cpu_baseline(layer, bank, w, x_rows, cfg)
-    print(json.dumps(result), flush=True)
     layer.close()
     bank.free()
+    if not args.no_secondary:
+        result["secondary"] = secondary(ctx)
+    print(json.dumps(result), flush=True)
     ctx.close()
     return 0
+
+
+def secondary(ctx):
+    """The other BASELINE configurations, measured on the same GPU (each a few seconds): 2 = MoE prefill
+    (T = 4096, Zipf(1.1) routing), 3 = FP8 block-128 projections at T = 1, 16, 2048, 4 = 8-layer offload
+    decode at T = 4 with 25 % of the routed experts resident."""
+    from vesper_amd import fp8_workload, offload_workload, prefill_workload
+    out = {}
+    log("configuration 2: prefill")
+    p = prefill_workload.run(4096, 5, ctx=ctx)
+    out["prefill_T4096"] = dict(p, mfma_peak_TFLOP_per_s=5000.0, mfma_frac=round(p["TFLOP_per_s"] / 5000.0, 4))
+    log(f"prefill: {p}")
+    log("configuration 3: FP8 projections")
+    f = fp8_workload.run((1, 16, 2048), 20, ctx=ctx)
+    out["fp8_projections"] = {str(t): {"us": v["us"], "GB_per_s": v["GB_per_s"], "TFLOP_per_s": v["TFLOP_per_s"],
+                                       "hbm_frac": round(v["GB_per_s"] / HBM_PEAK_GBS, 4),
+                                       "mfma_frac": round(v["TFLOP_per_s"] / 5000.0, 4),
+                                       "per_projection_us": {k: p2["us"] for k, p2 in v["projections"].items()}}
+                              for t, v in f.items()}
+    log(f"fp8: {out['fp8_projections']}")
+    log("configuration 4: offload decode")
+    o = offload_workload.run(10, 4, ctx=ctx)
+    out["offload_8layers_T4"] = o
+    log(f"offload: {o}")
+    return out
 
 
 if __name__ == "__main__":

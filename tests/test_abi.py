@@ -67,3 +67,12 @@ def test_expert_keys_round_trip_and_refuse_bad_forms():
             parse_key(bad)
     with pytest.raises(ValueError):
         expert_key(-1, 0)
+
+
+def test_product_package_never_imports_the_oracle():
+    """oracle/ is test infrastructure: the vesper_amd package must not import it (no CPU fallback path)."""
+    import re as _re
+    pkg = ROOT / "vesper_amd"
+    offenders = [p.name for p in pkg.glob("*.py")
+                 if _re.search(r"^\s*(from|import)\s+oracle\b", p.read_text(), flags=_re.M)]
+    assert not offenders, offenders

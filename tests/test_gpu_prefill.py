@@ -10,7 +10,8 @@ order or token would move whole outputs, far outside the tolerance.
 import numpy as np
 import pytest
 
-from oracle.inputs import activations, mxfp4_expert, router_weight, zipf_routing
+from oracle.inputs import activations, mxfp4_expert, router_weight
+from vesper_amd.workloads import zipf_routing
 from oracle.moe import moe_layer, moe_layer_routed
 from tests.helpers import assert_close, max_rel_err
 from vesper_amd import _lib

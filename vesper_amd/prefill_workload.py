@@ -22,8 +22,7 @@ def run(tokens=4096, iters=5, seed=20261018, ctx=None):
     from . import _lib
     from .config import BASELINE as cfg
     from .layer import ExpertBank, MoELayer, bf16_input
-    sys.path.insert(0, str(__import__("pathlib").Path(__file__).resolve().parents[1]))
-    from oracle.inputs import zipf_routing      # the workload's routing generator (seeded)
+    from .workloads import zipf_routing
     own = ctx is None
     ctx = ctx or _lib.Context(0)
     rng = np.random.default_rng(seed)
