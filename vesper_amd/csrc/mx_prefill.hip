@@ -34,6 +34,7 @@ constexpr int kTileRows = 128;   // token rows per GEMM tile
 constexpr int kThreads = 512;    // 8 waves
 constexpr int kWaveTok = 4;      // token tiles of 16 per wave
 constexpr int kLdsRow = 144;     // 128 bytes of a row's K chunk + 16 bytes of bank padding
+constexpr int kDepth = 3;        // chunks of operands in flight per wave
 constexpr int kMaxTopK = 32;
 
 struct PrefillPlan {
@@ -184,6 +185,9 @@ __global__ __launch_bounds__(kThreads) void grouped_kernel(GemmArgs a) {
   const uint8_t* ssrc = kGateUp ? a.xs + (size_t)a.plan.sorted_tok[srow] * (a.H / 32)
                                 : a.ds + (size_t)srow * (a.I / 32);
 
+  // 16-token column tiles past the tile's rows hold padding: their MFMAs (and, for a wave with none left,
+  // its weight loads) are skipped (a wave-uniform branch)
+  const int live_tiles = min(kWaveTok, max(0, (rows - 16 * u0 + 15) / 16));
   auto load_b = [&](int c, uint4 (&bst)[2], uint32_t& sst) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) bst[j] = ldg128(xsrc[j] + (size_t)c * 128);
@@ -195,6 +199,7 @@ __global__ __launch_bounds__(kThreads) void grouped_kernel(GemmArgs a) {
     if (tid < kTileRows) lds_s[stage][tid] = sst;
   };
   auto load_a = [&](int c, uint4 (&am)[4], uint32_t& sw) {
+    if (live_tiles == 0) return;
 #pragma unroll
     for (int t = 0; t < 4; ++t) am[t] = ldg128(wlane + (size_t)c * 4096 + t * 1024);
     sw = ldg32(slane + (size_t)c * 256);
@@ -207,6 +212,7 @@ __global__ __launch_bounds__(kThreads) void grouped_kernel(GemmArgs a) {
   auto compute = [&](int stage, const uint4 (&am)[4], uint32_t sw) {
 #pragma unroll
     for (int u = 0; u < kWaveTok; ++u) {
+      if (u >= live_tiles) break;
       const uint8_t* row = &lds_b[stage][(16 * (u0 + u) + n) * kLdsRow];
       const uint4 b0 = *reinterpret_cast<const uint4*>(row + 16 * q);
       const uint4 b1 = *reinterpret_cast<const uint4*>(row + 64 + 16 * q);
@@ -216,32 +222,36 @@ __global__ __launch_bounds__(kThreads) void grouped_kernel(GemmArgs a) {
     }
   };
 
-  uint4 bst[2];
-  uint32_t sst = 0;
-  uint4 a0[4], a1[4];
-  uint32_t sw0 = 0, sw1 = 0;
-  load_b(0, bst, sst);
-  load_a(0, a0, sw0);
-  store_b(0, bst, sst);
+  // Register ring of kDepth chunks: the loads of chunk c + kDepth are issued right after chunk c's MFMAs,
+  // so about kDepth chunks of weights and gathered activations are in flight per wave while the
+  // activations of chunk c + 1, loaded kDepth - 1 chunks earlier, move into the other LDS stage.
+  uint4 a_ring[kDepth][4];
+  uint32_t sw_ring[kDepth];
+  uint4 b_ring[kDepth][2];
+  uint32_t sx_ring[kDepth];
+#pragma unroll
+  for (int j = 0; j < kDepth; ++j) {
+    const int c = min(j, C - 1);
+    load_a(c, a_ring[j], sw_ring[j]);
+    load_b(c, b_ring[j], sx_ring[j]);
+  }
+  store_b(0, b_ring[0], sx_ring[0]);
   __syncthreads();
-  for (int c = 0; c < C; c += 2) {
-    const bool more1 = c + 1 < C;
-    if (more1) {
-      load_b(c + 1, bst, sst);
-      load_a(c + 1, a1, sw1);
+  for (int base = 0; base < C; base += kDepth) {
+#pragma unroll
+    for (int j = 0; j < kDepth; ++j) {
+      const int c = base + j;
+      if (c < C) {
+        compute(c & 1, a_ring[j], sw_ring[j]);
+        const int jn = (j + 1) % kDepth;
+        if (c + 1 < C) store_b((c + 1) & 1, b_ring[jn], sx_ring[jn]);
+        if (c + kDepth < C) {
+          load_a(c + kDepth, a_ring[j], sw_ring[j]);
+          load_b(c + kDepth, b_ring[j], sx_ring[j]);
+        }
+        __syncthreads();
+      }
     }
-    compute(0, a0, sw0);
-    if (more1) store_b(1, bst, sst);
-    __syncthreads();
-    if (!more1) break;
-    const bool more2 = c + 2 < C;
-    if (more2) {
-      load_b(c + 2, bst, sst);
-      load_a(c + 2, a0, sw0);
-    }
-    compute(1, a1, sw1);
-    if (more2) store_b(0, bst, sst);
-    __syncthreads();
   }
 
   if constexpr (kGateUp) {
