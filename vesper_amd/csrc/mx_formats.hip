@@ -54,6 +54,42 @@ __global__ void act_quant32_kernel(const In* __restrict__ x, uint8_t* __restrict
   }
 }
 
+// BF16 input, 8 values per thread (one 16-byte load), 4 threads per 32-block: the block amax is two
+// xor-shuffles inside the quad, the 8 codes are one 8-byte store. Grid-stride over the groups of 8.
+__global__ __launch_bounds__(256) void act_quant32_v8_kernel(const uint16_t* __restrict__ x, uint8_t* __restrict__ q,
+                                                             uint8_t* __restrict__ s, int64_t groups) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < groups; base += stride) {
+    const int64_t i = base + threadIdx.x;   // quads never straddle the bound: groups is a multiple of 4
+    const bool live = i < groups;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (live) v = reinterpret_cast<const uint4*>(x)[i];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    float f[8];
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f[2 * j] = mx::bf16_value(w[j] & 0xFFFFu);
+      f[2 * j + 1] = mx::bf16_value(w[j] >> 16);
+      amax = fmaxf(amax, fmaxf(fabsf(f[2 * j]), fabsf(f[2 * j + 1])));
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 4));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 4));
+    amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
+    const uint32_t code = mx::act_scale_code(amax);
+    const float sc = mx::e8m0_value(code);
+    if (live) {
+      uint2 out;
+      out.x = mx::act_quant_value(f[0], sc) | (mx::act_quant_value(f[1], sc) << 8) |
+              (mx::act_quant_value(f[2], sc) << 16) | (mx::act_quant_value(f[3], sc) << 24);
+      out.y = mx::act_quant_value(f[4], sc) | (mx::act_quant_value(f[5], sc) << 8) |
+              (mx::act_quant_value(f[6], sc) << 16) | (mx::act_quant_value(f[7], sc) << 24);
+      reinterpret_cast<uint2*>(q)[i] = out;
+      if ((i & 3) == 0) s[i >> 2] = (uint8_t)code;
+    }
+  }
+}
+
 unsigned grid_for(int64_t items, int threads) {
   const int64_t g = (items + threads - 1) / threads;
   return (unsigned)(g < 1 ? 1 : g > 1048576 ? 1048576 : g);
@@ -94,6 +130,15 @@ int mx_act_quant32(mx_ctx* ctx, const uint16_t* x, uint8_t* q, uint8_t* scales, 
   if (!rows) return MX_OK;
   MX_REQUIRE(x && q && scales, "mx_act_quant32: null pointer");
   const int64_t blocks = rows * (width / 32);
+  if (((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 7) == 0) {
+    const int64_t groups = blocks * 4;
+    const int64_t want = (groups + 255) / 256;
+    hipLaunchKernelGGL(act_quant32_v8_kernel, dim3((unsigned)(want < 65536 ? want : 65536)), dim3(256), 0,
+                       as_stream(stream), x, q, scales, groups);
+    MX_LAUNCH_CHECK("act_quant32_v8_kernel");
+    return MX_OK;
+  }
+  MX_REQUIRE(blocks * 32 <= (int64_t)1048576 * 256, "mx_act_quant32: unaligned input limited to 2^28 values");
   hipLaunchKernelGGL(act_quant32_kernel<uint16_t>, dim3(grid_for(blocks * 32, 256)), dim3(256), 0,
                      as_stream(stream), x, q, scales, blocks);
   MX_LAUNCH_CHECK("act_quant32_kernel");
@@ -107,6 +152,7 @@ int mx_act_quant32_f32(mx_ctx* ctx, const float* x, uint8_t* q, uint8_t* scales,
   if (!rows) return MX_OK;
   MX_REQUIRE(x && q && scales, "mx_act_quant32_f32: null pointer");
   const int64_t blocks = rows * (width / 32);
+  MX_REQUIRE(blocks * 32 <= (int64_t)1048576 * 256, "mx_act_quant32_f32: limited to 2^28 values per call");
   hipLaunchKernelGGL(act_quant32_kernel<float>, dim3(grid_for(blocks * 32, 256)), dim3(256), 0, as_stream(stream),
                      x, q, scales, blocks);
   MX_LAUNCH_CHECK("act_quant32_kernel");

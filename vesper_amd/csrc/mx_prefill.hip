@@ -54,9 +54,19 @@ __global__ void zero_i32_kernel(int32_t* p, int n) {
 
 // Routing ids outside [0, E) (the C caller's responsibility) are skipped by every plan step and by the
 // combine, so such input gives wrong rows for its token but never an access out of bounds.
-__global__ void count_kernel(const int32_t* __restrict__ ids, int n, int E, int32_t* __restrict__ counts) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n && ids[i] >= 0 && ids[i] < E) atomicAdd(&counts[ids[i]], 1);
+// Per-workgroup LDS histogram, then one global atomic per nonzero bin (E <= 1024).
+__global__ __launch_bounds__(256) void count_kernel(const int32_t* __restrict__ ids, int n, int E,
+                                                    int32_t* __restrict__ counts) {
+  __shared__ int32_t h[1024];
+  for (int e = threadIdx.x; e < E; e += 256) h[e] = 0;
+  __syncthreads();
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
+    const int e = ids[i];
+    if (e >= 0 && e < E) atomicAdd(&h[e], 1);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += 256)
+    if (h[e]) atomicAdd(&counts[e], h[e]);
 }
 
 // One wave: slot counts -> row offsets and the tile list (ascending slot, shared last).
@@ -308,13 +318,14 @@ __global__ __launch_bounds__(kThreads) void grouped_kernel(GemmArgs a) {
   }
 }
 
-// grid (ceil(H / 512), T), 64 threads, 8 hidden positions per thread.
-__global__ __launch_bounds__(64) void prefill_combine_kernel(PrefillPlan p, const int32_t* __restrict__ ids,
-                                                             const uint16_t* __restrict__ rows, int T, int H, int k,
-                                                             int E, int has_shared, uint16_t* __restrict__ y) {
+// grid (T), 256 threads: one workgroup per token; thread 0 orders the token's rows by expert ID in LDS,
+// then every thread sums 8 hidden positions per step over the rows (shared row last).
+__global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillPlan p, const int32_t* __restrict__ ids,
+                                                              const uint16_t* __restrict__ rows, int T, int H, int k,
+                                                              int E, int has_shared, uint16_t* __restrict__ y) {
   __shared__ int32_t order[kMaxTopK + 1];
   __shared__ int order_n;
-  const int t = blockIdx.y;
+  const int t = blockIdx.x;
   if (threadIdx.x == 0) {
     int32_t es[kMaxTopK], rs[kMaxTopK];
     int m = 0;
@@ -333,31 +344,31 @@ __global__ __launch_bounds__(64) void prefill_combine_kernel(PrefillPlan p, cons
       ++m;
     }
     for (int i = 0; i < m; ++i) order[i] = rs[i];
+    if (has_shared) order[m++] = T * k + t;   // the shared expert's rows follow the routed ones
     order_n = m;
   }
   __syncthreads();
-  const int h = (blockIdx.x * 64 + threadIdx.x) * 8;
-  if (h >= H) return;
-  const int m = order_n, n = m + has_shared;
-  float acc[8];
+  const int n = order_n;
+  for (int h = threadIdx.x * 8; h < H; h += 256 * 8) {
+    float acc[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
-  for (int i = 0; i < n; ++i) {
-    const int r = i < m ? order[i] : T * k + t;   // the shared expert's rows follow the routed ones
-    const uint4 v = *reinterpret_cast<const uint4*>(rows + (size_t)r * H + h);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+    for (int i = 0; i < n; ++i) {
+      const uint4 v = *reinterpret_cast<const uint4*>(rows + (size_t)order[i] * H + h);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      acc[2 * j] = acc[2 * j] + mx::bf16_value(w[j] & 0xFFFFu);
-      acc[2 * j + 1] = acc[2 * j + 1] + mx::bf16_value(w[j] >> 16);
+      for (int j = 0; j < 4; ++j) {
+        acc[2 * j] = acc[2 * j] + mx::bf16_value(w[j] & 0xFFFFu);
+        acc[2 * j + 1] = acc[2 * j + 1] + mx::bf16_value(w[j] >> 16);
+      }
     }
+    uint4 o;
+    o.x = mx::bf16_bits(acc[0]) | (mx::bf16_bits(acc[1]) << 16);
+    o.y = mx::bf16_bits(acc[2]) | (mx::bf16_bits(acc[3]) << 16);
+    o.z = mx::bf16_bits(acc[4]) | (mx::bf16_bits(acc[5]) << 16);
+    o.w = mx::bf16_bits(acc[6]) | (mx::bf16_bits(acc[7]) << 16);
+    *reinterpret_cast<uint4*>(y + (size_t)t * H + h) = o;
   }
-  uint4 o;
-  o.x = mx::bf16_bits(acc[0]) | (mx::bf16_bits(acc[1]) << 16);
-  o.y = mx::bf16_bits(acc[2]) | (mx::bf16_bits(acc[3]) << 16);
-  o.z = mx::bf16_bits(acc[4]) | (mx::bf16_bits(acc[5]) << 16);
-  o.w = mx::bf16_bits(acc[6]) | (mx::bf16_bits(acc[7]) << 16);
-  *reinterpret_cast<uint4*>(y + (size_t)t * H + h) = o;
 }
 
 uint64_t r256(uint64_t b) { return (b + 255) & ~255ull; }
@@ -459,7 +470,7 @@ int mx_moe_prefill(mx_layer* layer, const uint16_t* x, int32_t T, const int32_t*
   hipLaunchKernelGGL(zero_i32_kernel, dim3((E + 1 + 255) / 256), dim3(256), 0, st, p.counts, E + 1);
   MX_LAUNCH_CHECK("zero_i32_kernel");
   const int pairs = T * k;
-  hipLaunchKernelGGL(count_kernel, dim3((pairs + 255) / 256), dim3(256), 0, st, rid, pairs, E, p.counts);
+  hipLaunchKernelGGL(count_kernel, dim3(std::min(64, (pairs + 255) / 256)), dim3(256), 0, st, rid, pairs, E, p.counts);
   MX_LAUNCH_CHECK("count_kernel");
   hipLaunchKernelGGL(offsets_kernel, dim3(1), dim3(64), 0, st, p, E, T, v.has_shared);
   MX_LAUNCH_CHECK("offsets_kernel");
@@ -481,7 +492,7 @@ int mx_moe_prefill(mx_layer* layer, const uint16_t* x, int32_t T, const int32_t*
   MX_LAUNCH_CHECK("grouped_kernel<gate/up>");
   hipLaunchKernelGGL(grouped_kernel<false>, dim3(H / 256, ws.max_tiles), dim3(kThreads), 0, st, a);
   MX_LAUNCH_CHECK("grouped_kernel<down>");
-  hipLaunchKernelGGL(prefill_combine_kernel, dim3((H / 8 + 63) / 64, T), dim3(64), 0, st, p, rid,
+  hipLaunchKernelGGL(prefill_combine_kernel, dim3(T), dim3(256), 0, st, p, rid,
                      (const uint16_t*)a.out, T, H, k, E, v.has_shared, y);
   MX_LAUNCH_CHECK("prefill_combine_kernel");
   return MX_OK;
