@@ -58,6 +58,26 @@ def test_prefill_zipf_routing_matches_oracle(gpu_ctx, tokens, shared):
         bank.free()
 
 
+def test_prefill_narrow_shapes_take_the_smaller_tiles(gpu_ctx):
+    """I % 256 != 0 and H % 512 != 0: gate/up with one 64-row group per wave, down on 8-wave tiles."""
+    cfg = MoEConfig(hidden=768, intermediate=384, experts=16, top_k=4, swiglu_limit=7.0, shared="mxfp4",
+                    max_tokens=16)
+    rng = np.random.default_rng(384)
+    layer, bank, w, arrays = small_layer(gpu_ctx, rng, cfg)
+    try:
+        x = activations(rng, 200, cfg.hidden)
+        ids, wts = zipf_routing(rng, 200, cfg.experts, cfg.top_k)
+        got = layer.prefill(x, ids, wts)
+        ref = moe_layer_routed(x, ids, wts, {e: arrays[e] for e in range(cfg.experts)}, arrays[cfg.experts],
+                               num_experts=cfg.experts, swiglu_limit=cfg.swiglu_limit)
+        assert_close(got, ref["output_bf16"], "prefill narrow")
+        for t in range(200):
+            assert max_rel_err(got[t], ref["output_bf16"][t]) <= 2e-2, t
+    finally:
+        layer.close()
+        bank.free()
+
+
 def test_prefill_through_the_layer_router(gpu_ctx):
     cfg = MoEConfig(hidden=512, intermediate=256, experts=32, top_k=4, swiglu_limit=0.0, shared="mxfp4",
                     max_tokens=16)

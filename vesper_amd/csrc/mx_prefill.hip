@@ -157,10 +157,9 @@ struct GemmArgs {
   uint16_t* out;                 // [rows][H] expert outputs (BF16)
 };
 
-// Grouped GEMM over one 128-row tile of one slot. kGateUp: A = W1/W3 tiles of 4 groups of 32 intermediate
-// rows, B = gathered token rows of xq; else A = W2 tiles of 4 groups of 64 rows, B = the tile's rows of dq.
-template <bool kGateUp>
-__global__ __launch_bounds__(kThreads) void grouped_kernel(GemmArgs a) {
+// Down GEMM over one 128-row tile of one slot for H % 512 != 0: A = W2 tiles of 4 groups of 64 rows,
+// B = the tile's rows of dq; 8 waves, each one group for 64 of the tile's token rows.
+__global__ __launch_bounds__(kThreads) void down_tile_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds_b[2][kTileRows * kLdsRow];
   __shared__ uint32_t lds_s[2][kTileRows];
   const int ti = blockIdx.y;
@@ -170,14 +169,13 @@ __global__ __launch_bounds__(kThreads) void grouped_kernel(GemmArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q = lane >> 4, n = lane & 15;
-  const int K = kGateUp ? a.H : a.I;
-  const int C = K / 128;
+  const int C = a.I / 128;
   const int gg = blockIdx.x * 4 + (wave & 3);
   const int u0 = (wave >> 2) * kWaveTok;
   const uint8_t* blob = a.tiles[slot];
   const TiledOffsets off = tiled_offsets(a.H, a.I);
-  const uint8_t* wlane = blob + (kGateUp ? 0 : off.dn_w) + (size_t)gg * C * 4096 + 16 * lane;
-  const uint8_t* slane = blob + (kGateUp ? off.gu_s : off.dn_s) + (size_t)gg * C * 256 + 4 * lane;
+  const uint8_t* wlane = blob + off.dn_w + (size_t)gg * C * 4096 + 16 * lane;
+  const uint8_t* slane = blob + off.dn_s + (size_t)gg * C * 256 + 4 * lane;
 
   // staging: pieces tid and tid + 512 of the tile's 128 rows x 8 x 16 bytes; rows past the tile repeat
   // its last row (results dropped)
@@ -186,14 +184,10 @@ __global__ __launch_bounds__(kThreads) void grouped_kernel(GemmArgs a) {
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int pc = tid + kThreads * j, r = pc >> 3, part = pc & 7;
-    const int row = row0 + min(r, rows - 1);
-    const uint8_t* src = kGateUp ? a.xq + (size_t)a.plan.sorted_tok[row] * a.H : a.dq + (size_t)row * a.I;
-    xsrc[j] = src + 16 * part;
+    xsrc[j] = a.dq + (size_t)(row0 + min(r, rows - 1)) * a.I + 16 * part;
     ldst[j] = r * kLdsRow + 16 * part;
   }
-  const int srow = row0 + min(tid & (kTileRows - 1), rows - 1);
-  const uint8_t* ssrc = kGateUp ? a.xs + (size_t)a.plan.sorted_tok[srow] * (a.H / 32)
-                                : a.ds + (size_t)srow * (a.I / 32);
+  const uint8_t* ssrc = a.ds + (size_t)(row0 + min(tid & (kTileRows - 1), rows - 1)) * (a.I / 32);
 
   // 16-token column tiles past the tile's rows hold padding: their MFMAs (and, for a wave with none left,
   // its weight loads) are skipped (a wave-uniform branch)
@@ -264,56 +258,200 @@ __global__ __launch_bounds__(kThreads) void grouped_kernel(GemmArgs a) {
     }
   }
 
-  if constexpr (kGateUp) {
-    // D[4q + i][n] of tile t: lanes q < 2 hold W1 rows 32gg + 8t + 4q + i, lane + 32 the matching W3 rows
-    const bool weighted = slot < a.E;
 #pragma unroll
-    for (int u = 0; u < kWaveTok; ++u) {
-      const int r = 16 * (u0 + u) + n;
+  for (int u = 0; u < kWaveTok; ++u) {
+    const int r = 16 * (u0 + u) + n;
+    if (r >= rows) continue;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      uint2 packed;
+      packed.x = mx::bf16_bits(acc[t][u][0]) | (mx::bf16_bits(acc[t][u][1]) << 16);
+      packed.y = mx::bf16_bits(acc[t][u][2]) | (mx::bf16_bits(acc[t][u][3]) << 16);
+      *reinterpret_cast<uint2*>(a.out + (size_t)(row0 + r) * a.H + 64 * gg + 16 * t + 4 * q) = packed;
+    }
+  }
+}
+
+// Grouped GEMM over one 128-row tile of one slot. kGateUp: A = W1/W3 tiles (a group = 32 intermediate rows
+// of W1 and W3, 64 MFMA rows), B = the tile's gathered token rows of xq; else A = W2 tiles (a group = 64
+// hidden rows), B = the tile's rows of dq. 256 threads = 4 waves, each owning kBigGroups groups for all 128
+// token rows, so no weight byte is loaded twice within a workgroup; the accumulators live in the
+// accumulation registers. Operand bytes per MFMA: 256 (one group per wave) or 192 (two), against 384 for
+// down_tile_kernel. Grid x covers 2I / (256 kBigGroups) gate/up or H / (256 kBigGroups) down workgroups.
+constexpr int kBigThreads = 256;
+constexpr int kBigTok = 8;       // token tiles of 16 per wave
+constexpr int kBigDepth = 2;     // chunks in flight
+
+// kBigGroups = groups per wave: 2 where the grid divides (I % 256, H % 512), else 1 (gate/up) or
+// down_tile_kernel (down).
+template <bool kGateUp, int kBigGroups>
+__global__ __launch_bounds__(kBigThreads) void grouped_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds_b[2][kTileRows * kLdsRow];
+  __shared__ uint32_t lds_s[2][kTileRows];
+  const int ti = blockIdx.y;
+  if (ti >= *a.plan.n_tiles) return;
+  const int32_t* info = a.plan.tile_info + (size_t)ti * 4;
+  const int slot = info[0], row0 = info[1], rows = info[2];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q = lane >> 4, n = lane & 15;
+  const int K = kGateUp ? a.H : a.I;
+  const int C = K / 128;
+  const int g0 = blockIdx.x * (4 * kBigGroups) + kBigGroups * wave;
+  const uint8_t* blob = a.tiles[slot];
+  const TiledOffsets off = tiled_offsets(a.H, a.I);
+  const uint8_t* wbase = blob + (kGateUp ? 0 : off.dn_w) + 16 * lane;
+  const uint8_t* sbase = blob + (kGateUp ? off.gu_s : off.dn_s) + 4 * lane;
+  const int live_tiles = min(kBigTok, (rows + 15) / 16);
+
+  // staging: pieces tid + 256 j (j < 4) of the tile's 128 rows x 8 x 16 bytes
+  const uint8_t* xsrc[4];
+  int ldst[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int pc = tid + kBigThreads * j, r = pc >> 3, part = pc & 7;
+    const int row = row0 + min(r, rows - 1);
+    const uint8_t* src = kGateUp ? a.xq + (size_t)a.plan.sorted_tok[row] * a.H : a.dq + (size_t)row * a.I;
+    xsrc[j] = src + 16 * part;
+    ldst[j] = r * kLdsRow + 16 * part;
+  }
+  const int srow = row0 + min(tid & (kTileRows - 1), rows - 1);
+  const uint8_t* ssrc = kGateUp ? a.xs + (size_t)a.plan.sorted_tok[srow] * (a.H / 32)
+                                : a.ds + (size_t)srow * (a.I / 32);
+  auto load_b = [&](int c, uint4 (&bst)[4], uint32_t& sst) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bst[j] = ldg128(xsrc[j] + (size_t)c * 128);
+    sst = ldg32(ssrc + 4 * c);
+  };
+  auto store_b = [&](int stage, const uint4 (&bst)[4], uint32_t sst) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<uint4*>(&lds_b[stage][ldst[j]]) = bst[j];
+    if (tid < kTileRows) lds_s[stage][tid] = sst;
+  };
+  auto load_a = [&](int c, uint4 (&am)[kBigGroups][4], uint32_t (&sw)[kBigGroups]) {
+#pragma unroll
+    for (int gi = 0; gi < kBigGroups; ++gi) {
+      const size_t gb = (size_t)(g0 + gi) * C + c;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) am[gi][t] = ldg128(wbase + gb * 4096 + t * 1024);
+      sw[gi] = ldg32(sbase + gb * 256);
+    }
+  };
+  v4f acc[kBigGroups][4][kBigTok];
+#pragma unroll
+  for (int gi = 0; gi < kBigGroups; ++gi)
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int u = 0; u < kBigTok; ++u) acc[gi][t][u] = v4f{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int stage, const uint4 (&am)[kBigGroups][4], const uint32_t (&sw)[kBigGroups]) {
+#pragma unroll
+    for (int u = 0; u < kBigTok; ++u) {
+      if (u >= live_tiles) break;
+      const uint8_t* row = &lds_b[stage][(16 * u + n) * kLdsRow];
+      const uint4 b0 = *reinterpret_cast<const uint4*>(row + 16 * q);
+      const uint4 b1 = *reinterpret_cast<const uint4*>(row + 64 + 16 * q);
+      const int sx = (int)((lds_s[stage][16 * u + n] >> (8 * q)) & 0xFF);
+#pragma unroll
+      for (int gi = 0; gi < kBigGroups; ++gi)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          acc[gi][t][u] = mfma_fp4_fp8(am[gi][t], b0, b1, acc[gi][t][u], (int)((sw[gi] >> (8 * t)) & 0xFF), sx);
+    }
+  };
+  uint4 a_ring[kBigDepth][kBigGroups][4];
+  uint32_t sw_ring[kBigDepth][kBigGroups];
+  uint4 b_ring[kBigDepth][4];
+  uint32_t sx_ring[kBigDepth];
+#pragma unroll
+  for (int j = 0; j < kBigDepth; ++j) {
+    const int c = min(j, C - 1);
+    load_a(c, a_ring[j], sw_ring[j]);
+    load_b(c, b_ring[j], sx_ring[j]);
+  }
+  store_b(0, b_ring[0], sx_ring[0]);
+  __syncthreads();
+  for (int base = 0; base < C; base += kBigDepth) {
+#pragma unroll
+    for (int j = 0; j < kBigDepth; ++j) {
+      const int c = base + j;
+      if (c < C) {
+        compute(c & 1, a_ring[j], sw_ring[j]);
+        const int jn = (j + 1) % kBigDepth;
+        if (c + 1 < C) store_b((c + 1) & 1, b_ring[jn], sx_ring[jn]);
+        if (c + kBigDepth < C) {
+          load_a(c + kBigDepth, a_ring[j], sw_ring[j]);
+          load_b(c + kBigDepth, b_ring[j], sx_ring[j]);
+        }
+        __syncthreads();
+      }
+    }
+  }
+
+  if constexpr (kGateUp) {
+    const bool weighted = slot < a.E;
+    // The SwiGLU body is too large to unroll eight times, and a rolled loop may not index the accumulator
+    // array by its counter (that would move the array to scratch memory): each pass copies token tile u
+    // out of the array with constant indices and selects (uniform branch-free selects).
+#pragma unroll 1
+    for (int u = 0; u < live_tiles; ++u) {
+      const int r = 16 * u + n;
       const bool live = r < rows;
       const int row = row0 + (live ? r : 0);
       const float rw = a.plan.sorted_w[row];
-      float din[4][4];
-      float amax = 0.f;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float up = __shfl_xor(acc[t][u][i], 32, 64);
-          din[t][i] = mxd::swiglu_element(mx::bf16_bits(acc[t][u][i]), mx::bf16_bits(up), a.limit, weighted, rw,
-                                          nullptr);
-          amax = fmaxf(amax, fabsf(din[t][i]));
-        }
-      }
-      // the token's 32-row block is spread over lanes q = 0 and 1 (16 values each)
-      amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-      amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
-      const uint32_t code = mx::act_scale_code(amax);
-      const float sc = mx::e8m0_value(code);
-      if (q < 2 && live) {
-        uint8_t* dst = a.dq + (size_t)row * a.I + 32 * gg + 4 * q;
+      for (int gi = 0; gi < kBigGroups; ++gi) {
+        const int gg = g0 + gi;
+        v4f cur[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          uint32_t word = 0;
+          cur[t] = acc[gi][t][0];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) word |= mx::act_quant_value(din[t][i], sc) << (8 * i);
-          *reinterpret_cast<uint32_t*>(dst + 8 * t) = word;
+          for (int uu = 1; uu < kBigTok; ++uu) cur[t] = uu == u ? acc[gi][t][uu] : cur[t];
         }
-        if (q == 0) a.ds[(size_t)row * (a.I / 32) + gg] = (uint8_t)code;
+        float din[4][4];
+        float amax = 0.f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float up = __shfl_xor(cur[t][i], 32, 64);
+            din[t][i] = mxd::swiglu_element(mx::bf16_bits(cur[t][i]), mx::bf16_bits(up), a.limit, weighted, rw,
+                                            nullptr);
+            amax = fmaxf(amax, fabsf(din[t][i]));
+          }
+        }
+        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+        amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
+        const uint32_t code = mx::act_scale_code(amax);
+        const float sc = mx::e8m0_value(code);
+        if (q < 2 && live) {
+          uint8_t* dst = a.dq + (size_t)row * a.I + 32 * gg + 4 * q;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) word |= mx::act_quant_value(din[t][i], sc) << (8 * i);
+            *reinterpret_cast<uint32_t*>(dst + 8 * t) = word;
+          }
+          if (q == 0) a.ds[(size_t)row * (a.I / 32) + gg] = (uint8_t)code;
+        }
       }
     }
   } else {
 #pragma unroll
-    for (int u = 0; u < kWaveTok; ++u) {
-      const int r = 16 * (u0 + u) + n;
+    for (int u = 0; u < kBigTok; ++u) {
+      const int r = 16 * u + n;
       if (r >= rows) continue;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        uint2 packed;
-        packed.x = mx::bf16_bits(acc[t][u][0]) | (mx::bf16_bits(acc[t][u][1]) << 16);
-        packed.y = mx::bf16_bits(acc[t][u][2]) | (mx::bf16_bits(acc[t][u][3]) << 16);
-        *reinterpret_cast<uint2*>(a.out + (size_t)(row0 + r) * a.H + 64 * gg + 16 * t + 4 * q) = packed;
-      }
+      for (int gi = 0; gi < kBigGroups; ++gi)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          uint2 packed;
+          packed.x = mx::bf16_bits(acc[gi][t][u][0]) | (mx::bf16_bits(acc[gi][t][u][1]) << 16);
+          packed.y = mx::bf16_bits(acc[gi][t][u][2]) | (mx::bf16_bits(acc[gi][t][u][3]) << 16);
+          *reinterpret_cast<uint2*>(a.out + (size_t)(row0 + r) * a.H + 64 * (g0 + gi) + 16 * t + 4 * q) = packed;
+        }
     }
   }
 }
@@ -488,9 +626,15 @@ int mx_moe_prefill(mx_layer* layer, const uint16_t* x, int32_t T, const int32_t*
   a.dq = b + ws.dq;
   a.ds = b + ws.ds;
   a.out = (uint16_t*)(b + ws.eout);
-  hipLaunchKernelGGL(grouped_kernel<true>, dim3(I / 128, ws.max_tiles), dim3(kThreads), 0, st, a);
+  if (I % 256 == 0)
+    hipLaunchKernelGGL((grouped_kernel<true, 2>), dim3(I / 256, ws.max_tiles), dim3(kBigThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((grouped_kernel<true, 1>), dim3(I / 128, ws.max_tiles), dim3(kBigThreads), 0, st, a);
   MX_LAUNCH_CHECK("grouped_kernel<gate/up>");
-  hipLaunchKernelGGL(grouped_kernel<false>, dim3(H / 256, ws.max_tiles), dim3(kThreads), 0, st, a);
+  if (H % 512 == 0)
+    hipLaunchKernelGGL((grouped_kernel<false, 2>), dim3(H / 512, ws.max_tiles), dim3(kBigThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL(down_tile_kernel, dim3(H / 256, ws.max_tiles), dim3(kThreads), 0, st, a);
   MX_LAUNCH_CHECK("grouped_kernel<down>");
   hipLaunchKernelGGL(prefill_combine_kernel, dim3(T), dim3(256), 0, st, p, rid,
                      (const uint16_t*)a.out, T, H, k, E, v.has_shared, y);
