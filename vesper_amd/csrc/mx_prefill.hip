@@ -7,10 +7,10 @@
 //   plan      count pairs per expert, expert-major row offsets (shared expert last) and 128-row tiles;
 //             a stable per-expert scatter gives each expert's rows in ascending token order
 //             (participation, src/vesper/moe.py:18-30) and each (token, rank) pair its row
-//   gate/up   grid (I/128, tiles), 8 waves: 4 groups of 32 intermediate rows (W1 + W3 interleaved per
-//             MFMA tile, as in the tiled layout) x 2 halves of the tile's 128 tokens; the tokens' E4M3
-//             rows are gathered into LDS per 128-wide K chunk; epilogue SwiGLU + route weight + the
-//             per-token quantization of each 32-row block of the down input
+//   gate/up   grid (I/128, tiles), 4 waves: 4 groups of 32 intermediate rows (W1 + W3 interleaved per
+//             MFMA tile, as in the tiled layout), each wave one group for all 128 tokens of the tile; the
+//             tokens' E4M3 rows are copied global -> LDS per 128-wide K chunk; epilogue SwiGLU + route
+//             weight + the per-token quantization of each 32-row block of the down input
 //   down      grid (H/256, tiles), same shape over W2 with the tile's contiguous down-input rows
 //   combine   per token: its expert rows in ascending expert ID, then the shared row; FP32 from +0,
 //             one BF16 rounding (aggregation_probe.cu:4-25)
@@ -31,10 +31,6 @@ using mxd::TiledOffsets;
 using mxd::v4f;
 
 constexpr int kTileRows = 128;   // token rows per GEMM tile
-constexpr int kThreads = 512;    // 8 waves
-constexpr int kWaveTok = 4;      // token tiles of 16 per wave
-constexpr int kLdsRow = 144;     // 128 bytes of a row's K chunk + 16 bytes of bank padding
-constexpr int kDepth = 3;        // chunks of operands in flight per wave
 constexpr int kMaxTopK = 32;
 
 struct PrefillPlan {
@@ -157,137 +153,110 @@ struct GemmArgs {
   uint16_t* out;                 // [rows][H] expert outputs (BF16)
 };
 
-// Down GEMM over one 128-row tile of one slot for H % 512 != 0: A = W2 tiles of 4 groups of 64 rows,
-// B = the tile's rows of dq; 8 waves, each one group for 64 of the tile's token rows.
-__global__ __launch_bounds__(kThreads) void down_tile_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds_b[2][kTileRows * kLdsRow];
-  __shared__ uint32_t lds_s[2][kTileRows];
-  const int ti = blockIdx.y;
-  if (ti >= *a.plan.n_tiles) return;
-  const int32_t* info = a.plan.tile_info + (size_t)ti * 4;
-  const int slot = info[0], row0 = info[1], rows = info[2];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int q = lane >> 4, n = lane & 15;
-  const int C = a.I / 128;
-  const int gg = blockIdx.x * 4 + (wave & 3);
-  const int u0 = (wave >> 2) * kWaveTok;
-  const uint8_t* blob = a.tiles[slot];
-  const TiledOffsets off = tiled_offsets(a.H, a.I);
-  const uint8_t* wlane = blob + off.dn_w + (size_t)gg * C * 4096 + 16 * lane;
-  const uint8_t* slane = blob + off.dn_s + (size_t)gg * C * 256 + 4 * lane;
+// The s_waitcnt immediate that waits until at most n vector-memory operations of this wave are
+// outstanding (lgkm and export counts left at their maxima: no wait on them).
+constexpr int vm_wait_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-  // staging: pieces tid and tid + 512 of the tile's 128 rows x 8 x 16 bytes; rows past the tile repeat
-  // its last row (results dropped)
-  const uint8_t* xsrc[2];
-  int ldst[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int pc = tid + kThreads * j, r = pc >> 3, part = pc & 7;
-    xsrc[j] = a.dq + (size_t)(row0 + min(r, rows - 1)) * a.I + 16 * part;
-    ldst[j] = r * kLdsRow + 16 * part;
-  }
-  const uint8_t* ssrc = a.ds + (size_t)(row0 + min(tid & (kTileRows - 1), rows - 1)) * (a.I / 32);
-
-  // 16-token column tiles past the tile's rows hold padding: their MFMAs (and, for a wave with none left,
-  // its weight loads) are skipped (a wave-uniform branch)
-  const int live_tiles = min(kWaveTok, max(0, (rows - 16 * u0 + 15) / 16));
-  auto load_b = [&](int c, uint4 (&bst)[2], uint32_t& sst) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) bst[j] = ldg128(xsrc[j] + (size_t)c * 128);
-    sst = ldg32(ssrc + 4 * c);
-  };
-  auto store_b = [&](int stage, const uint4 (&bst)[2], uint32_t sst) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) *reinterpret_cast<uint4*>(&lds_b[stage][ldst[j]]) = bst[j];
-    if (tid < kTileRows) lds_s[stage][tid] = sst;
-  };
-  auto load_a = [&](int c, uint4 (&am)[4], uint32_t& sw) {
-    if (live_tiles == 0) return;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) am[t] = ldg128(wlane + (size_t)c * 4096 + t * 1024);
-    sw = ldg32(slane + (size_t)c * 256);
-  };
-  v4f acc[4][kWaveTok];
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int u = 0; u < kWaveTok; ++u) acc[t][u] = v4f{0.f, 0.f, 0.f, 0.f};
-  auto compute = [&](int stage, const uint4 (&am)[4], uint32_t sw) {
-#pragma unroll
-    for (int u = 0; u < kWaveTok; ++u) {
-      if (u >= live_tiles) break;
-      const uint8_t* row = &lds_b[stage][(16 * (u0 + u) + n) * kLdsRow];
-      const uint4 b0 = *reinterpret_cast<const uint4*>(row + 16 * q);
-      const uint4 b1 = *reinterpret_cast<const uint4*>(row + 64 + 16 * q);
-      const int sx = (int)((lds_s[stage][16 * (u0 + u) + n] >> (8 * q)) & 0xFF);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) acc[t][u] = mfma_fp4_fp8(am[t], b0, b1, acc[t][u], (int)((sw >> (8 * t)) & 0xFF), sx);
-    }
-  };
-
-  // Register ring of kDepth chunks: the loads of chunk c + kDepth are issued right after chunk c's MFMAs,
-  // so about kDepth chunks of weights and gathered activations are in flight per wave while the
-  // activations of chunk c + 1, loaded kDepth - 1 chunks earlier, move into the other LDS stage.
-  uint4 a_ring[kDepth][4];
-  uint32_t sw_ring[kDepth];
-  uint4 b_ring[kDepth][2];
-  uint32_t sx_ring[kDepth];
-#pragma unroll
-  for (int j = 0; j < kDepth; ++j) {
-    const int c = min(j, C - 1);
-    load_a(c, a_ring[j], sw_ring[j]);
-    load_b(c, b_ring[j], sx_ring[j]);
-  }
-  store_b(0, b_ring[0], sx_ring[0]);
-  __syncthreads();
-  for (int base = 0; base < C; base += kDepth) {
-#pragma unroll
-    for (int j = 0; j < kDepth; ++j) {
-      const int c = base + j;
-      if (c < C) {
-        compute(c & 1, a_ring[j], sw_ring[j]);
-        const int jn = (j + 1) % kDepth;
-        if (c + 1 < C) store_b((c + 1) & 1, b_ring[jn], sx_ring[jn]);
-        if (c + kDepth < C) {
-          load_a(c + kDepth, a_ring[j], sw_ring[j]);
-          load_b(c + kDepth, b_ring[j], sx_ring[j]);
-        }
-        __syncthreads();
-      }
-    }
-  }
-
-#pragma unroll
-  for (int u = 0; u < kWaveTok; ++u) {
-    const int r = 16 * (u0 + u) + n;
-    if (r >= rows) continue;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      uint2 packed;
-      packed.x = mx::bf16_bits(acc[t][u][0]) | (mx::bf16_bits(acc[t][u][1]) << 16);
-      packed.y = mx::bf16_bits(acc[t][u][2]) | (mx::bf16_bits(acc[t][u][3]) << 16);
-      *reinterpret_cast<uint2*>(a.out + (size_t)(row0 + r) * a.H + 64 * gg + 16 * t + 4 * q) = packed;
-    }
-  }
+// Asynchronous copies from global memory into LDS of 16 (4) bytes per lane: lane l's bytes land at
+// lds + 16 l (4 l); lds is the wave-uniform LDS byte address. Counted by vmcnt like any other
+// vector-memory load. Inline assembly rather than the compiler builtin: for the builtin the compiler
+// treats every later wait on vmcnt as unordered (copies and register loads mixed) and widens it to
+// vmcnt(0), which drains the copies in flight at each weight-register use; with the copies invisible
+// to it, its waits for the weight loads are exact (and cover a few more copies than needed, as the
+// hardware counter also holds them). The caller orders its LDS reads after the copies with explicit
+// waits. One wait state between the M0 write and the copy.
+__device__ __forceinline__ void global_to_lds16(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds) : "m0");
+}
+__device__ __forceinline__ void global_to_lds4(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" : : "v"(src), "s"(lds) : "m0");
 }
 
-// Grouped GEMM over one 128-row tile of one slot. kGateUp: A = W1/W3 tiles (a group = 32 intermediate rows
-// of W1 and W3, 64 MFMA rows), B = the tile's gathered token rows of xq; else A = W2 tiles (a group = 64
-// hidden rows), B = the tile's rows of dq. 256 threads = 4 waves, each owning kBigGroups groups for all 128
-// token rows, so no weight byte is loaded twice within a workgroup; the accumulators live in the
-// accumulation registers. Operand bytes per MFMA: 256 (one group per wave) or 192 (two), against 384 for
-// down_tile_kernel. Grid x covers 2I / (256 kBigGroups) gate/up or H / (256 kBigGroups) down workgroups.
-constexpr int kBigThreads = 256;
-constexpr int kBigTok = 8;       // token tiles of 16 per wave
-constexpr int kBigDepth = 2;     // chunks in flight
+// Workgroup barrier ordering LDS only: the fences are restricted to the local address space, so the
+// barrier waits for this wave's LDS operations (lgkmcnt) but leaves its global loads in flight. A plain
+// __syncthreads() also waits for every outstanding global load (vmcnt(0)), which would drain the
+// prefetch pipelines below at every K chunk.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
-// kBigGroups = groups per wave: 2 where the grid divides (I % 256, H % 512), else 1 (gate/up) or
-// down_tile_kernel (down).
-template <bool kGateUp, int kBigGroups>
-__global__ __launch_bounds__(kBigThreads) void grouped_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds_b[2][kTileRows * kLdsRow];
-  __shared__ uint32_t lds_s[2][kTileRows];
+// Workgroup barrier for the global->LDS copy pipelines: the caller has already waited for its own copies
+// and LDS reads (s_waitcnt) as far as the barrier must cover. Even the local-only fences of lds_barrier
+// would wait for every copy in flight (the copies write LDS), so the barrier is issued bare; the empty
+// assembly statements with a memory clobber keep the compiler from moving memory operations across it.
+__device__ __forceinline__ void copy_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Two 16-token tiles' MFMA B operands (per tile two 16-byte reads 1 KB apart, the tiles' blocks being
+// consecutive) and their scale words, read from LDS and waited for. Inline assembly: for compiler-visible
+// LDS reads the compiler cannot tell which global->LDS copies they depend on and waits for all of them
+// (vmcnt(0)), draining the copies in flight for later chunks; the caller's explicit vmcnt wait before the
+// barrier orders these reads after the copies they read.
+__device__ __forceinline__ void lds_read_b2(uint32_t addr, uint32_t saddr, uint4 (&b)[4], uint32_t (&sw)[2]) {
+  mxd::u32x4_t x0, x1, x2, x3;
+  uint32_t s0, s1;
+  asm volatile(
+      "ds_read_b128 %0, %6\n\t"
+      "ds_read_b128 %1, %6 offset:1024\n\t"
+      "ds_read_b128 %2, %6 offset:2048\n\t"
+      "ds_read_b128 %3, %6 offset:3072\n\t"
+      "ds_read_b32 %4, %7\n\t"
+      "ds_read_b32 %5, %7 offset:64\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3), "=&v"(s0), "=&v"(s1)
+      : "v"(addr), "v"(saddr));
+  b[0] = uint4{x0.x, x0.y, x0.z, x0.w};
+  b[1] = uint4{x1.x, x1.y, x1.z, x1.w};
+  b[2] = uint4{x2.x, x2.y, x2.z, x2.w};
+  b[3] = uint4{x3.x, x3.y, x3.z, x3.w};
+  sw[0] = s0;
+  sw[1] = s1;
+}
+
+constexpr int kGThreads = 512;   // 8 waves (two per SIMD), one 64-row group of the weights each
+constexpr int kStages = 5;       // activation chunks in LDS: chunk c + 4 is copied in while chunk c multiplies
+constexpr int kADepth = 3;       // weight chunks per wave in registers: chunk c + 3 loads after chunk c
+constexpr int kBCopies = 3;      // per wave and chunk: 2 activation blocks + 1 block of scale words
+constexpr int kALoads = 5;       // per wave and chunk: 4 weight tiles + 1 scale word
+// a stage: 16 activation blocks of 1 KB, then 512 scale words (wave w writes words 64w.., rows 64w +
+// lane; only the first 128 are read)
+constexpr int kStageSB = 16384, kStageBytes = 18432;
+// epilogue tiles in the same LDS: gate and up [128][kEpiRowG] BF16, or the down output [128][kEpiRowD]
+constexpr int kEpiRowG = 256 + 8, kEpiRowD = 512 + 8;
+constexpr int kLdsBytes = 2 * kTileRows * kEpiRowG * 2;
+static_assert(kStages * kStageBytes <= kLdsBytes && kTileRows * kEpiRowD * 2 <= kLdsBytes, "LDS layout");
+
+// Grouped GEMM over one 128-row tile of one slot. kGateUp: A = W1/W3 tiles (a group = 32 intermediate
+// rows of W1 and 32 of W3 as the tiled layout interleaves them, 64 MFMA rows), B = the tile's gathered
+// token rows of xq; else A = W2 tiles (a group = 64 hidden rows), B = the tile's rows of dq. Grid x covers
+// the groups eight per workgroup (ceil(I / 256) gate/up, ceil(H / 512) down), grid y the tiles.
+//
+// Each wave keeps its 64 x 128 output block in 128 accumulator registers and fits in 256 registers, so
+// two waves share a SIMD and one's waits are covered by the other's MFMAs. The weights stream into a
+// register ring kADepth chunks deep. The activations go global -> LDS without registers (global_load_lds,
+// 16 bytes a lane) as 16 blocks of 1 KB per chunk, block 2u + h holding at lane (q, n) the bytes 64h +
+// 16q.. of row 16u + n, which is exactly the MFMA B operand of lane (q, n) for token tile u, so every LDS
+// read is one linear 1 KB wave access. A step: wait for chunk c's activation copies (this wave's) and a
+// barrier (everyone's copies, and everyone done with the stage chunk c + 4 overwrites), start chunk
+// c + 4's copies, multiply chunk c, load chunk c + 3's weights into the register slot chunk c used. Every
+// step issues the same loads (past the end, repeats of chunk C - 1), so the count of operations issued
+// after chunk c's copies is never below kBCopies (kStages - 2) + kALoads kADepth (the first step's).
+//
+// Epilogue: the accumulators go to LDS as BF16 [token][column] and every thread then finishes whole
+// 32-column blocks of one token: gate/up SwiGLU + route weight + the block's E4M3 quantization (32 code
+// bytes and one scale byte), or 16-byte row segments of the down output.
+template <bool kGateUp>
+__global__ __launch_bounds__(kGThreads, 2) void grouped_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsBytes];
   const int ti = blockIdx.y;
   if (ti >= *a.plan.n_tiles) return;
   const int32_t* info = a.plan.tile_info + (size_t)ti * 4;
@@ -297,161 +266,169 @@ __global__ __launch_bounds__(kBigThreads) void grouped_kernel(GemmArgs a) {
   const int q = lane >> 4, n = lane & 15;
   const int K = kGateUp ? a.H : a.I;
   const int C = K / 128;
-  const int g0 = blockIdx.x * (4 * kBigGroups) + kBigGroups * wave;
+  // a wave past the last group (I / 32 or H / 64 groups) still copies its share of the activations and
+  // loads repeats of the last group's weights, but computes and stores nothing
+  const int groups = kGateUp ? a.I / 32 : a.H / 64;
+  const int g = blockIdx.x * 8 + wave;
+  const bool active = g < groups;
+  const int gl = min(g, groups - 1);
   const uint8_t* blob = a.tiles[slot];
   const TiledOffsets off = tiled_offsets(a.H, a.I);
-  const uint8_t* wbase = blob + (kGateUp ? 0 : off.dn_w) + 16 * lane;
-  const uint8_t* sbase = blob + (kGateUp ? off.gu_s : off.dn_s) + 4 * lane;
-  const int live_tiles = min(kBigTok, (rows + 15) / 16);
+  const uint8_t* wl = blob + (kGateUp ? 0 : off.dn_w) + (size_t)gl * C * 4096 + 16 * lane;
+  const uint8_t* sl = blob + (kGateUp ? off.gu_s : off.dn_s) + (size_t)gl * C * 256 + 4 * lane;
+  const int live_tiles = min(8, (rows + 15) / 16);
 
-  // staging: pieces tid + 256 j (j < 4) of the tile's 128 rows x 8 x 16 bytes
-  const uint8_t* xsrc[4];
-  int ldst[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int pc = tid + kBigThreads * j, r = pc >> 3, part = pc & 7;
-    const int row = row0 + min(r, rows - 1);
-    const uint8_t* src = kGateUp ? a.xq + (size_t)a.plan.sorted_tok[row] * a.H : a.dq + (size_t)row * a.I;
-    xsrc[j] = src + 16 * part;
-    ldst[j] = r * kLdsRow + 16 * part;
-  }
-  const int srow = row0 + min(tid & (kTileRows - 1), rows - 1);
-  const uint8_t* ssrc = kGateUp ? a.xs + (size_t)a.plan.sorted_tok[srow] * (a.H / 32)
-                                : a.ds + (size_t)srow * (a.I / 32);
-  auto load_b = [&](int c, uint4 (&bst)[4], uint32_t& sst) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) bst[j] = ldg128(xsrc[j] + (size_t)c * 128);
-    sst = ldg32(ssrc + 4 * c);
+  // this wave's activation blocks 2 wave + h (token tile u = wave) and scale words of rows 64 wave + lane;
+  // rows past the tile repeat its last row. The offsets fit 32 bits (the host bounds the buffers).
+  const uint8_t* bbase = kGateUp ? a.xq : a.dq;
+  const uint8_t* sbbase = kGateUp ? a.xs : a.ds;
+  const int br = row0 + min(16 * wave + n, rows - 1);
+  const uint32_t boff = (kGateUp ? (uint32_t)a.plan.sorted_tok[br] * (uint32_t)a.H : (uint32_t)br * (uint32_t)a.I) + 16 * q;
+  const int sr = row0 + min(64 * wave + lane, rows - 1);
+  const uint32_t soff = kGateUp ? (uint32_t)a.plan.sorted_tok[sr] * (uint32_t)(a.H / 32) : (uint32_t)sr * (uint32_t)(a.I / 32);
+  const uint32_t lds0 = lds_addr(lds);
+  auto copy_b = [&](int c) {
+    const uint32_t st = __builtin_amdgcn_readfirstlane(lds0 + (c % kStages) * kStageBytes + 2048 * wave);
+    global_to_lds16(bbase + (size_t)c * 128 + boff, st);
+    global_to_lds16(bbase + (size_t)c * 128 + boff + 64, st + 1024);
+    global_to_lds4(sbbase + (size_t)c * 4 + soff, st - 2048 * wave + kStageSB + 256 * wave);
   };
-  auto store_b = [&](int stage, const uint4 (&bst)[4], uint32_t sst) {
+  auto load_a = [&](int c, uint4 (&am)[4], uint32_t& sw) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) *reinterpret_cast<uint4*>(&lds_b[stage][ldst[j]]) = bst[j];
-    if (tid < kTileRows) lds_s[stage][tid] = sst;
+    for (int t = 0; t < 4; ++t) am[t] = ldg128(wl + (size_t)c * 4096 + t * 1024);
+    sw = ldg32(sl + (size_t)c * 256);
   };
-  auto load_a = [&](int c, uint4 (&am)[kBigGroups][4], uint32_t (&sw)[kBigGroups]) {
+  v4f acc[4][8];
 #pragma unroll
-    for (int gi = 0; gi < kBigGroups; ++gi) {
-      const size_t gb = (size_t)(g0 + gi) * C + c;
+  for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) am[gi][t] = ldg128(wbase + gb * 4096 + t * 1024);
-      sw[gi] = ldg32(sbase + gb * 256);
-    }
-  };
-  v4f acc[kBigGroups][4][kBigTok];
+    for (int u = 0; u < 8; ++u) acc[t][u] = v4f{0.f, 0.f, 0.f, 0.f};
+  const uint32_t lb = lds0 + 16 * lane;
+  const uint32_t lsb = lds0 + kStageSB + 4 * n;
+  auto compute = [&](int c, const uint4 (&am)[4], uint32_t sw) {
+    const uint32_t so = (c % kStages) * kStageBytes;
 #pragma unroll
-  for (int gi = 0; gi < kBigGroups; ++gi)
+    for (int u = 0; u < 8; u += 2) {
+      if (u >= live_tiles) break;   // wave-uniform
+      uint4 b[4];
+      uint32_t sxw[2];
+      lds_read_b2(lb + so + 2 * u * 1024, lsb + so + 64 * u, b, sxw);
+      const int sx0 = (int)((sxw[0] >> (8 * q)) & 0xFF), sx1 = (int)((sxw[1] >> (8 * q)) & 0xFF);
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int u = 0; u < kBigTok; ++u) acc[gi][t][u] = v4f{0.f, 0.f, 0.f, 0.f};
-  auto compute = [&](int stage, const uint4 (&am)[kBigGroups][4], const uint32_t (&sw)[kBigGroups]) {
-#pragma unroll
-    for (int u = 0; u < kBigTok; ++u) {
-      if (u >= live_tiles) break;
-      const uint8_t* row = &lds_b[stage][(16 * u + n) * kLdsRow];
-      const uint4 b0 = *reinterpret_cast<const uint4*>(row + 16 * q);
-      const uint4 b1 = *reinterpret_cast<const uint4*>(row + 64 + 16 * q);
-      const int sx = (int)((lds_s[stage][16 * u + n] >> (8 * q)) & 0xFF);
-#pragma unroll
-      for (int gi = 0; gi < kBigGroups; ++gi)
+      for (int t = 0; t < 4; ++t) acc[t][u] = mfma_fp4_fp8(am[t], b[0], b[1], acc[t][u], (int)((sw >> (8 * t)) & 0xFF), sx0);
+      if (u + 1 < live_tiles) {
 #pragma unroll
         for (int t = 0; t < 4; ++t)
-          acc[gi][t][u] = mfma_fp4_fp8(am[gi][t], b0, b1, acc[gi][t][u], (int)((sw[gi] >> (8 * t)) & 0xFF), sx);
+          acc[t][u + 1] = mfma_fp4_fp8(am[t], b[2], b[3], acc[t][u + 1], (int)((sw >> (8 * t)) & 0xFF), sx1);
+      }
+      // pins these tiles' MFMAs before the next tiles' reads: the compiler would otherwise sink every MFMA
+      // past the last read and keep all eight tiles' operands live at once
+      asm volatile("" : "+v"(acc[0][u]), "+v"(acc[1][u]), "+v"(acc[2][u]), "+v"(acc[3][u]), "+v"(acc[0][u + 1]),
+                   "+v"(acc[1][u + 1]), "+v"(acc[2][u + 1]), "+v"(acc[3][u + 1]));
     }
   };
-  uint4 a_ring[kBigDepth][kBigGroups][4];
-  uint32_t sw_ring[kBigDepth][kBigGroups];
-  uint4 b_ring[kBigDepth][4];
-  uint32_t sx_ring[kBigDepth];
+
+  uint4 a_ring[kADepth][4];
+  uint32_t sw_ring[kADepth];
 #pragma unroll
-  for (int j = 0; j < kBigDepth; ++j) {
-    const int c = min(j, C - 1);
-    load_a(c, a_ring[j], sw_ring[j]);
-    load_b(c, b_ring[j], sx_ring[j]);
+  for (int j = 0; j < kStages - 1; ++j) copy_b(min(j, C - 1));
+#pragma unroll
+  for (int j = 0; j < kADepth; ++j) load_a(min(j, C - 1), a_ring[j], sw_ring[j]);
+  auto step = [&](int c, int j) {
+    // chunk c's copies are done once at most this many later operations are outstanding (first step:
+    // the copies of chunks 1 .. kStages - 2 and the weight loads of chunks 0 .. kADepth - 1)
+    __builtin_amdgcn_s_waitcnt(vm_wait_imm(kBCopies * (kStages - 2) + kALoads * kADepth) & ~(15 << 8));  // + lgkmcnt(0)
+    copy_barrier();
+    copy_b(min(c + kStages - 1, C - 1));
+    if (active) compute(c, a_ring[j], sw_ring[j]);
+    load_a(min(c + kADepth, C - 1), a_ring[j], sw_ring[j]);
+  };
+  int base = 0;
+  for (; base + kADepth <= C; base += kADepth) {
+#pragma unroll
+    for (int j = 0; j < kADepth; ++j) step(base + j, j);
   }
-  store_b(0, b_ring[0], sx_ring[0]);
+#pragma unroll
+  for (int j = 0; j < kADepth - 1; ++j)
+    if (base + j < C) step(base + j, j);
+  // every copy must land before the LDS is reused below (and before it can be handed to another workgroup)
+  __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));
   __syncthreads();
-  for (int base = 0; base < C; base += kBigDepth) {
-#pragma unroll
-    for (int j = 0; j < kBigDepth; ++j) {
-      const int c = base + j;
-      if (c < C) {
-        compute(c & 1, a_ring[j], sw_ring[j]);
-        const int jn = (j + 1) % kBigDepth;
-        if (c + 1 < C) store_b((c + 1) & 1, b_ring[jn], sx_ring[jn]);
-        if (c + kBigDepth < C) {
-          load_a(c + kBigDepth, a_ring[j], sw_ring[j]);
-          load_b(c + kBigDepth, b_ring[j], sx_ring[j]);
-        }
-        __syncthreads();
-      }
-    }
-  }
 
   if constexpr (kGateUp) {
-    const bool weighted = slot < a.E;
-    // The SwiGLU body is too large to unroll eight times, and a rolled loop may not index the accumulator
-    // array by its counter (that would move the array to scratch memory): each pass copies token tile u
-    // out of the array with constant indices and selects (uniform branch-free selects).
-#pragma unroll 1
-    for (int u = 0; u < live_tiles; ++u) {
-      const int r = 16 * u + n;
-      const bool live = r < rows;
-      const int row = row0 + (live ? r : 0);
-      const float rw = a.plan.sorted_w[row];
+    // D[4q + i][n] of tile t: lanes q < 2 hold W1 rows 32g + 8t + 4q + i, lanes q >= 2 the same W3 rows
+    uint16_t* eg = reinterpret_cast<uint16_t*>(lds);
+    if (active) {
+      uint16_t* dst = eg + (q >> 1) * (kTileRows * kEpiRowG) + n * kEpiRowG + 32 * wave + 4 * (q & 1);
 #pragma unroll
-      for (int gi = 0; gi < kBigGroups; ++gi) {
-        const int gg = g0 + gi;
-        v4f cur[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          cur[t] = acc[gi][t][0];
-#pragma unroll
-          for (int uu = 1; uu < kBigTok; ++uu) cur[t] = uu == u ? acc[gi][t][uu] : cur[t];
-        }
-        float din[4][4];
-        float amax = 0.f;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float up = __shfl_xor(cur[t][i], 32, 64);
-            din[t][i] = mxd::swiglu_element(mx::bf16_bits(cur[t][i]), mx::bf16_bits(up), a.limit, weighted, rw,
-                                            nullptr);
-            amax = fmaxf(amax, fabsf(din[t][i]));
-          }
-        }
-        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-        amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
-        const uint32_t code = mx::act_scale_code(amax);
-        const float sc = mx::e8m0_value(code);
-        if (q < 2 && live) {
-          uint8_t* dst = a.dq + (size_t)row * a.I + 32 * gg + 4 * q;
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            uint32_t word = 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) word |= mx::act_quant_value(din[t][i], sc) << (8 * i);
-            *reinterpret_cast<uint32_t*>(dst + 8 * t) = word;
-          }
-          if (q == 0) a.ds[(size_t)row * (a.I / 32) + gg] = (uint8_t)code;
-        }
-      }
-    }
-  } else {
-#pragma unroll
-    for (int u = 0; u < kBigTok; ++u) {
-      const int r = 16 * u + n;
-      if (r >= rows) continue;
-#pragma unroll
-      for (int gi = 0; gi < kBigGroups; ++gi)
+      for (int u = 0; u < 8; ++u)
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           uint2 packed;
-          packed.x = mx::bf16_bits(acc[gi][t][u][0]) | (mx::bf16_bits(acc[gi][t][u][1]) << 16);
-          packed.y = mx::bf16_bits(acc[gi][t][u][2]) | (mx::bf16_bits(acc[gi][t][u][3]) << 16);
-          *reinterpret_cast<uint2*>(a.out + (size_t)(row0 + r) * a.H + 64 * (g0 + gi) + 16 * t + 4 * q) = packed;
+          packed.x = mx::bf16_bits(acc[t][u][0]) | (mx::bf16_bits(acc[t][u][1]) << 16);
+          packed.y = mx::bf16_bits(acc[t][u][2]) | (mx::bf16_bits(acc[t][u][3]) << 16);
+          *reinterpret_cast<uint2*>(dst + 16 * u * kEpiRowG + 8 * t) = packed;
         }
+    }
+    __syncthreads();
+    const bool weighted = slot < a.E;
+    for (int p = tid; p < kTileRows * 8; p += kGThreads) {
+      const int tok = p >> 3, blk = p & 7, gg = blockIdx.x * 8 + blk;
+      if (tok >= rows || gg >= groups) continue;
+      const int row = row0 + tok;
+      const float rw = a.plan.sorted_w[row];
+      const uint4* gsrc = reinterpret_cast<const uint4*>(eg + tok * kEpiRowG + 32 * blk);
+      const uint4* usrc = reinterpret_cast<const uint4*>(eg + kTileRows * kEpiRowG + tok * kEpiRowG + 32 * blk);
+      float din[32];
+      float amax = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint4 gv = gsrc[j], uv = usrc[j];
+        const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const uint32_t gb = (gw[k >> 1] >> (16 * (k & 1))) & 0xFFFFu, ub = (uw[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
+          din[8 * j + k] = mxd::swiglu_element(gb, ub, a.limit, weighted, rw, nullptr);
+          amax = fmaxf(amax, fabsf(din[8 * j + k]));
+        }
+      }
+      amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
+      const uint32_t code = mx::act_scale_code(amax);
+      const float sc = mx::e8m0_value(code);
+      uint32_t words[8];
+#pragma unroll
+      for (int w = 0; w < 8; ++w) {
+        words[w] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) words[w] |= mx::act_quant_value(din[4 * w + i], sc) << (8 * i);
+      }
+      uint4* dst = reinterpret_cast<uint4*>(a.dq + (size_t)row * a.I + 32 * gg);
+      dst[0] = uint4{words[0], words[1], words[2], words[3]};
+      dst[1] = uint4{words[4], words[5], words[6], words[7]};
+      a.ds[(size_t)row * (a.I / 32) + gg] = (uint8_t)code;
+    }
+  } else {
+    // D[4q + i][n] of tile t: W2 rows 64g + 16t + 4q + i
+    uint16_t* eo = reinterpret_cast<uint16_t*>(lds);
+    if (active) {
+      uint16_t* dst = eo + n * kEpiRowD + 64 * wave + 4 * q;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          uint2 packed;
+          packed.x = mx::bf16_bits(acc[t][u][0]) | (mx::bf16_bits(acc[t][u][1]) << 16);
+          packed.y = mx::bf16_bits(acc[t][u][2]) | (mx::bf16_bits(acc[t][u][3]) << 16);
+          *reinterpret_cast<uint2*>(dst + 16 * u * kEpiRowD + 16 * t) = packed;
+        }
+    }
+    __syncthreads();
+    const int cols = min(512, a.H - 512 * (int)blockIdx.x);
+    for (int p = tid; p < kTileRows * 64; p += kGThreads) {
+      const int tok = p >> 6, seg = p & 63;
+      if (tok >= rows || 8 * seg >= cols) continue;
+      *reinterpret_cast<uint4*>(a.out + (size_t)(row0 + tok) * a.H + 512 * blockIdx.x + 8 * seg) =
+          *reinterpret_cast<const uint4*>(eo + tok * kEpiRowD + 8 * seg);
     }
   }
 }
@@ -576,6 +553,9 @@ int mx_moe_prefill(mx_layer* layer, const uint16_t* x, int32_t T, const int32_t*
   MX_REQUIRE((ids == nullptr) == (weights == nullptr), "routing ids and weights are given together or not at all");
   MX_REQUIRE(c.intermediate % 128 == 0 && c.hidden % 256 == 0, "prefill needs I % 128 == 0 and H % 256 == 0");
   const Workspace ws = workspace_layout(c, T, v.has_shared);
+  MX_REQUIRE((uint64_t)T * c.hidden <= 0xFFFFFFFFull && (uint64_t)ws.rows * c.intermediate <= 0xFFFFFFFFull,
+             "prefill of %d tokens: the gathered activations (T * H and T * (top_k + shared) * I bytes) must stay "
+             "below 4 GiB", T);
   MX_REQUIRE(workspace && ((uintptr_t)workspace & 255) == 0 && workspace_bytes >= ws.total,
              "workspace must be 256-byte aligned and at least mx_prefill_workspace_bytes (%llu) bytes",
              (unsigned long long)ws.total);
@@ -626,15 +606,9 @@ int mx_moe_prefill(mx_layer* layer, const uint16_t* x, int32_t T, const int32_t*
   a.dq = b + ws.dq;
   a.ds = b + ws.ds;
   a.out = (uint16_t*)(b + ws.eout);
-  if (I % 256 == 0)
-    hipLaunchKernelGGL((grouped_kernel<true, 2>), dim3(I / 256, ws.max_tiles), dim3(kBigThreads), 0, st, a);
-  else
-    hipLaunchKernelGGL((grouped_kernel<true, 1>), dim3(I / 128, ws.max_tiles), dim3(kBigThreads), 0, st, a);
+  hipLaunchKernelGGL(grouped_kernel<true>, dim3((I + 255) / 256, ws.max_tiles), dim3(kGThreads), 0, st, a);
   MX_LAUNCH_CHECK("grouped_kernel<gate/up>");
-  if (H % 512 == 0)
-    hipLaunchKernelGGL((grouped_kernel<false, 2>), dim3(H / 512, ws.max_tiles), dim3(kBigThreads), 0, st, a);
-  else
-    hipLaunchKernelGGL(down_tile_kernel, dim3(H / 256, ws.max_tiles), dim3(kThreads), 0, st, a);
+  hipLaunchKernelGGL(grouped_kernel<false>, dim3((H + 511) / 512, ws.max_tiles), dim3(kGThreads), 0, st, a);
   MX_LAUNCH_CHECK("grouped_kernel<down>");
   hipLaunchKernelGGL(prefill_combine_kernel, dim3(T), dim3(256), 0, st, p, rid,
                      (const uint16_t*)a.out, T, H, k, E, v.has_shared, y);
