@@ -38,6 +38,38 @@ __device__ __forceinline__ v4f mfma_fp4_fp8(uint4 a, uint4 b0, uint4 b1, v4f c, 
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 4, 0, 0, sa, 0, sb);
 }
 
+// As mfma_fp4_fp8, with the A scale taken from byte kByte of the word sa4 (the instruction's opsel
+// selects it; checked against the extracted byte on gfx950).
+template <int kByte>
+__device__ __forceinline__ v4f mfma_fp4_fp8_sel(uint4 a, uint4 b0, uint4 b1, v4f c, uint32_t sa4, int sb) {
+  const v8i av = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
+  const v8i bv = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 4, 0, kByte, (int)sa4, 0, sb);
+}
+
+// E4M3 codes of four FP32 values clamped to [-448, 448] (NaN -> 0x7F), packed low value first: equal to
+// mx::e4m3_encode(clamp(v)) for every FP32 input. The gfx950 pair conversion (round to nearest even,
+// OCP E4M3) was checked against mx::e4m3_encode on every FP32 value with |v| <= 448; it encodes NaN as
+// 0xFF, so NaN lanes are patched to the encoder's 0x7F.
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+  auto clamp = [](float y) { return y > 448.f ? 448.f : (y < -448.f ? -448.f : y); };
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(clamp(a), clamp(b), 0, false);
+  uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(clamp(c), clamp(d), (int)lo, true);
+  w = a != a ? (w & 0xFFFFFF00u) | 0x7Fu : w;
+  w = b != b ? (w & 0xFFFF00FFu) | 0x7F00u : w;
+  w = c != c ? (w & 0xFF00FFFFu) | 0x7F0000u : w;
+  w = d != d ? (w & 0x00FFFFFFu) | 0x7F000000u : w;
+  return w;
+}
+
+// mx::bf16_round written with selects only (no divergent branch): round to nearest even, NaN quieted.
+__device__ __forceinline__ float bf16_round_sel(float f) {
+  const uint32_t b = mx::f2u(f);
+  const uint32_t rne = (b + 0x7FFFu + ((b >> 16) & 1u)) & 0xFFFF0000u;
+  const uint32_t qnan = (b & 0xFFFF0000u) | 0x400000u;
+  return mx::u2f((b & 0x7FFFFFFFu) > 0x7F800000u ? qnan : rne);
+}
+
 __device__ __forceinline__ v4f mfma_fp8_fp8(uint4 a0, uint4 a1, uint4 b0, uint4 b1, v4f c, int sa, int sb) {
   const v8i av = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
   const v8i bv = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
@@ -72,6 +104,28 @@ __device__ __forceinline__ float swiglu_element(uint32_t b1, uint32_t b3, float 
     tr[3] = product;
     tr[4] = routed;
   }
+  return mx::bf16_round(routed);
+}
+
+// Entries of the SiLU table: silu_f32 of every BF16 gate value (index = BF16 bits), then of the clamp
+// limit (index kSiluLimit, used when limit > 0 and the gate exceeds it).
+constexpr uint32_t kSiluLimit = 65536, kSiluEntries = 65537;
+
+// swiglu_element with silu_f32(gate) read from the SiLU table: the table holds the same function of the
+// same inputs (the gate is a BF16 value or, clamped, the limit), so the result has the same bits.
+__device__ __forceinline__ float swiglu_table(const float* silu_table, uint32_t b1, uint32_t b3, float limit,
+                                              bool weighted, float rw) {
+  const float gate = mx::bf16_value(b1);
+  float upf = mx::bf16_value(b3);
+  uint32_t idx = b1;
+  if (limit > 0.f) {
+    if (gate > limit) idx = kSiluLimit;
+    if (upf > limit) upf = limit;
+    if (upf < -limit) upf = -limit;
+  }
+  const float silu = ldgf(silu_table + idx);
+  const float product = silu * upf;
+  const float routed = weighted ? rw * product : product;
   return mx::bf16_round(routed);
 }
 

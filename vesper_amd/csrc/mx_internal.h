@@ -52,6 +52,7 @@ struct LayerView {
   const float* bias;
   const uint8_t** tiles;   // device [E + 1] tiled expert blobs, shared last
   int has_shared;
+  const float* silu;       // device [65537]: mxd::silu_f32 of every BF16 gate value, then of the limit
 };
 LayerView layer_view(mx_layer* layer);
 

@@ -1014,6 +1014,13 @@ int check_expert_ptrs(const mx_expert_ptrs& w, const char* who) {
 // ------------------------------------------------------------------------------------------------
 // Layer object
 
+// SiLU table of a layer: silu_f32 of every BF16 value, then of the clamp limit (0 when unclamped).
+__global__ void silu_table_kernel(float* table, float limit) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < mxd::kSiluLimit) table[i] = mxd::silu_f32(mx::bf16_value(i));
+  else if (i == mxd::kSiluLimit) table[i] = limit > 0.f ? mxd::silu_f32(limit) : 0.f;
+}
+
 struct mx_layer {
   mx_ctx* ctx = nullptr;
   mx_moe_config cfg{};
@@ -1028,6 +1035,7 @@ struct mx_layer {
   uint8_t *xq = nullptr, *xs = nullptr, *dq = nullptr, *ds = nullptr;
   uint16_t *w1 = nullptr, *w3 = nullptr, *din = nullptr, *eout = nullptr;
   Plan* plan = nullptr;
+  float* silu = nullptr;   // [mxd::kSiluEntries] SiLU table (prefill epilogue)
   int max_rows = 0;
   // the most recent decode call (mx_layer_time_stage repeats its stages)
   const uint16_t* last_x = nullptr;
@@ -1115,6 +1123,7 @@ LayerView layer_view(mx_layer* L) {
   v.bias = L->bias;
   v.tiles = L->tiles;
   v.has_shared = L->has_shared;
+  v.silu = L->silu;
   return v;
 }
 
@@ -1240,6 +1249,10 @@ int mx_layer_create(mx_ctx* ctx, const mx_moe_config* cfg, const float* router_w
   if ((s = layer_alloc_t(L, R * I, &L->dq))) return fail_out(s);
   if ((s = layer_alloc_t(L, R * I / 32 + 16, &L->ds))) return fail_out(s);
   if ((s = layer_alloc_t(L, R * H, &L->eout))) return fail_out(s);
+  if ((s = layer_alloc_t(L, (uint64_t)mxd::kSiluEntries, &L->silu))) return fail_out(s);
+  hipLaunchKernelGGL(silu_table_kernel, dim3((mxd::kSiluEntries + 255) / 256), dim3(256), 0, nullptr, L->silu,
+                     cfg->swiglu_limit);
+  if (hipError_t e = hipGetLastError(); e != hipSuccess) return fail_out(hip_fail(e, "mx_layer_create: SiLU table"));
   std::vector<const void*> host(E + 1);
   for (int e = 0; e < E; ++e) host[e] = experts[e];
   host[E] = shared ? shared : experts[0];

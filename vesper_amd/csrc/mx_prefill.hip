@@ -146,6 +146,7 @@ struct GemmArgs {
   PrefillPlan plan;
   int H, I, E;
   float limit;
+  const float* silu;             // [mxd::kSiluEntries] the layer's SiLU table
   const uint8_t* xq;             // [T][H] E4M3 codes of the tokens
   const uint8_t* xs;             // [T][H / 32] E8M0
   uint8_t* dq;                   // [rows][I] down-input codes
@@ -197,7 +198,8 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 }
 
 // Two 16-token tiles' MFMA B operands (per tile two 16-byte reads 1 KB apart, the tiles' blocks being
-// consecutive) and their scale words, read from LDS and waited for. Inline assembly: for compiler-visible
+// consecutive) and their scale bytes (saddr: this lane's byte of tile u's scale words, +64 for u + 1),
+// read from LDS and waited for. Inline assembly: for compiler-visible
 // LDS reads the compiler cannot tell which global->LDS copies they depend on and waits for all of them
 // (vmcnt(0)), draining the copies in flight for later chunks; the caller's explicit vmcnt wait before the
 // barrier orders these reads after the copies they read.
@@ -209,8 +211,8 @@ __device__ __forceinline__ void lds_read_b2(uint32_t addr, uint32_t saddr, uint4
       "ds_read_b128 %1, %6 offset:1024\n\t"
       "ds_read_b128 %2, %6 offset:2048\n\t"
       "ds_read_b128 %3, %6 offset:3072\n\t"
-      "ds_read_b32 %4, %7\n\t"
-      "ds_read_b32 %5, %7 offset:64\n\t"
+      "ds_read_u8 %4, %7\n\t"
+      "ds_read_u8 %5, %7 offset:64\n\t"
       "s_waitcnt lgkmcnt(0)"
       : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3), "=&v"(s0), "=&v"(s1)
       : "v"(addr), "v"(saddr));
@@ -304,22 +306,24 @@ __global__ __launch_bounds__(kGThreads, 2) void grouped_kernel(GemmArgs a) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) acc[t][u] = v4f{0.f, 0.f, 0.f, 0.f};
   const uint32_t lb = lds0 + 16 * lane;
-  const uint32_t lsb = lds0 + kStageSB + 4 * n;
+  const uint32_t lsb = lds0 + kStageSB + 4 * n + q;   // byte q (K block q) of token n's scale word
   auto compute = [&](int c, const uint4 (&am)[4], uint32_t sw) {
     const uint32_t so = (c % kStages) * kStageBytes;
 #pragma unroll
     for (int u = 0; u < 8; u += 2) {
       if (u >= live_tiles) break;   // wave-uniform
       uint4 b[4];
-      uint32_t sxw[2];
-      lds_read_b2(lb + so + 2 * u * 1024, lsb + so + 64 * u, b, sxw);
-      const int sx0 = (int)((sxw[0] >> (8 * q)) & 0xFF), sx1 = (int)((sxw[1] >> (8 * q)) & 0xFF);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) acc[t][u] = mfma_fp4_fp8(am[t], b[0], b[1], acc[t][u], (int)((sw >> (8 * t)) & 0xFF), sx0);
+      uint32_t sx[2];
+      lds_read_b2(lb + so + 2 * u * 1024, lsb + so + 64 * u, b, sx);
+      acc[0][u] = mxd::mfma_fp4_fp8_sel<0>(am[0], b[0], b[1], acc[0][u], sw, (int)sx[0]);
+      acc[1][u] = mxd::mfma_fp4_fp8_sel<1>(am[1], b[0], b[1], acc[1][u], sw, (int)sx[0]);
+      acc[2][u] = mxd::mfma_fp4_fp8_sel<2>(am[2], b[0], b[1], acc[2][u], sw, (int)sx[0]);
+      acc[3][u] = mxd::mfma_fp4_fp8_sel<3>(am[3], b[0], b[1], acc[3][u], sw, (int)sx[0]);
       if (u + 1 < live_tiles) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          acc[t][u + 1] = mfma_fp4_fp8(am[t], b[2], b[3], acc[t][u + 1], (int)((sw >> (8 * t)) & 0xFF), sx1);
+        acc[0][u + 1] = mxd::mfma_fp4_fp8_sel<0>(am[0], b[2], b[3], acc[0][u + 1], sw, (int)sx[1]);
+        acc[1][u + 1] = mxd::mfma_fp4_fp8_sel<1>(am[1], b[2], b[3], acc[1][u + 1], sw, (int)sx[1]);
+        acc[2][u + 1] = mxd::mfma_fp4_fp8_sel<2>(am[2], b[2], b[3], acc[2][u + 1], sw, (int)sx[1]);
+        acc[3][u + 1] = mxd::mfma_fp4_fp8_sel<3>(am[3], b[2], b[3], acc[3][u + 1], sw, (int)sx[1]);
       }
       // pins these tiles' MFMAs before the next tiles' reads: the compiler would otherwise sink every MFMA
       // past the last read and keep all eight tiles' operands live at once
@@ -372,6 +376,8 @@ __global__ __launch_bounds__(kGThreads, 2) void grouped_kernel(GemmArgs a) {
     }
     __syncthreads();
     const bool weighted = slot < a.E;
+    // the clamp limit, or +inf when unclamped (no comparison then holds, as with no clamp)
+    const float lim = a.limit > 0.f ? a.limit : __builtin_inff();
     for (int p = tid; p < kTileRows * 8; p += kGThreads) {
       const int tok = p >> 3, blk = p & 7, gg = blockIdx.x * 8 + blk;
       if (tok >= rows || gg >= groups) continue;
@@ -379,8 +385,10 @@ __global__ __launch_bounds__(kGThreads, 2) void grouped_kernel(GemmArgs a) {
       const float rw = a.plan.sorted_w[row];
       const uint4* gsrc = reinterpret_cast<const uint4*>(eg + tok * kEpiRowG + 32 * blk);
       const uint4* usrc = reinterpret_cast<const uint4*>(eg + kTileRows * kEpiRowG + tok * kEpiRowG + 32 * blk);
-      float din[32];
-      float amax = 0.f;
+      // mxd::swiglu_table per element, written as three passes so that the 32 table loads are in flight
+      // together: clamp and table index, loads, then the products
+      uint32_t idx[32];
+      float up[32];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint4 gv = gsrc[j], uv = usrc[j];
@@ -388,20 +396,32 @@ __global__ __launch_bounds__(kGThreads, 2) void grouped_kernel(GemmArgs a) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
           const uint32_t gb = (gw[k >> 1] >> (16 * (k & 1))) & 0xFFFFu, ub = (uw[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
-          din[8 * j + k] = mxd::swiglu_element(gb, ub, a.limit, weighted, rw, nullptr);
-          amax = fmaxf(amax, fabsf(din[8 * j + k]));
+          float upf = mx::bf16_value(ub);
+          upf = upf > lim ? lim : upf;
+          upf = upf < -lim ? -lim : upf;
+          idx[8 * j + k] = mx::bf16_value(gb) > lim ? mxd::kSiluLimit : gb;
+          up[8 * j + k] = upf;
         }
+      }
+      float din[32];
+#pragma unroll
+      for (int k = 0; k < 32; ++k) din[k] = mxd::ldgf(a.silu + idx[k]);
+      float amax = 0.f;
+#pragma unroll
+      for (int k = 0; k < 32; ++k) {
+        const float product = din[k] * up[k];
+        din[k] = mxd::bf16_round_sel(weighted ? rw * product : product);
+        amax = fmaxf(amax, fabsf(din[k]));
       }
       amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
       const uint32_t code = mx::act_scale_code(amax);
-      const float sc = mx::e8m0_value(code);
+      // x / 2^e as x * 2^-e: both are exact or one rounding of the same exact value (code is in
+      // [105, 246] for amax in [1e-4, FLT_MAX], so 2^-e is a normal float)
+      const float inv = mx::u2f((254u - code) << 23);
       uint32_t words[8];
 #pragma unroll
-      for (int w = 0; w < 8; ++w) {
-        words[w] = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) words[w] |= mx::act_quant_value(din[4 * w + i], sc) << (8 * i);
-      }
+      for (int w = 0; w < 8; ++w)
+        words[w] = mxd::e4m3x4(din[4 * w] * inv, din[4 * w + 1] * inv, din[4 * w + 2] * inv, din[4 * w + 3] * inv);
       uint4* dst = reinterpret_cast<uint4*>(a.dq + (size_t)row * a.I + 32 * gg);
       dst[0] = uint4{words[0], words[1], words[2], words[3]};
       dst[1] = uint4{words[4], words[5], words[6], words[7]};
@@ -601,6 +621,7 @@ int mx_moe_prefill(mx_layer* layer, const uint16_t* x, int32_t T, const int32_t*
   a.I = I;
   a.E = E;
   a.limit = c.swiglu_limit;
+  a.silu = v.silu;
   a.xq = b + ws.xq;
   a.xs = b + ws.xs;
   a.dq = b + ws.dq;
