@@ -73,6 +73,11 @@ int mx_copy_kernel(mx_ctx* ctx, void* dst, const void* src, uint64_t bytes, void
 
 /* ---- format hooks (replaces format_probe.cu decode_fp4/encode_fp8/activation32, lines 23-52) ---- */
 
+/* Self-check with no counterpart in the reference: compares the gfx950 hardware E4M3 packing used by the
+ * prefill epilogue with the bit-exact software encoder on every FP32 bit pattern (clamped to +-448 as the
+ * activation quantizers clamp); *mismatches receives the count, 0 when they agree. Synchronous. */
+int mx_check_e4m3_pack(mx_ctx* ctx, uint64_t* mismatches);
+
 /* out[r][k] = E2M1(packed[r][k/2] nibble, low first) * E8M0(scales[r][k/32]); bit-exact. */
 int mx_dequant_mxfp4(mx_ctx* ctx, const uint8_t* packed, const uint8_t* scales, float* out,
                      int64_t rows, int64_t k, void* stream);

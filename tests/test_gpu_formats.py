@@ -92,3 +92,13 @@ def test_block_gemv_random_inputs_close_to_in_order_sum(gpu_ctx):
     got = run_gemv(gpu_ctx, q, sa, w, sw)
     ref = mxfp4_gemv_spec(q, sa, w, sw)
     assert_gemv_close(got, ref, "random GEMV")
+
+
+def test_hardware_e4m3_packing_matches_the_encoder_on_every_float(gpu_ctx):
+    """The prefill epilogue packs E4M3 codes with the gfx950 conversion instruction; on every one of the
+    2^32 FP32 inputs (clamped to +-448 as the quantizers clamp) it must give the software encoder's code,
+    which test_encode_e4m3_conformance_space pins to the oracle."""
+    import ctypes as C
+    mismatches = C.c_uint64(1)
+    gpu_ctx.lib.check_e4m3_pack(gpu_ctx._h(), C.byref(mismatches))
+    assert mismatches.value == 0

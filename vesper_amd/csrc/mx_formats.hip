@@ -4,6 +4,9 @@
 // encode_fp8 and activation32 (src/vesper/kernels/format_probe.cu:23-52). The
 // production path never materialises dequantized weights; these exist so the
 // formats can be checked on the device against the oracle.
+#include <vector>
+
+#include "mx_device.h"
 #include "mx_internal.h"
 #include "mx_numerics.h"
 
@@ -99,7 +102,44 @@ unsigned grid_for(int64_t items, int threads) {
 
 using namespace mxi;
 
+// Exhaustive comparison of the hardware E4M3 packing (mxd::e4m3x4) with the software encoder on every
+// FP32 bit pattern, clamped to [-448, 448] as the activation quantizers clamp: per-thread mismatch counts.
+__global__ __launch_bounds__(256) void e4m3_pack_check_kernel(uint32_t* counts) {
+  const uint32_t tid = blockIdx.x * blockDim.x + threadIdx.x, threads = gridDim.x * blockDim.x;
+  auto clamp = [](float y) { return y > 448.f ? 448.f : (y < -448.f ? -448.f : y); };
+  uint32_t bad = 0;
+  for (uint64_t m = (uint64_t)tid * 4; m < (1ull << 32); m += (uint64_t)threads * 4) {
+    float v[4];
+    uint32_t want = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = mx::u2f((uint32_t)(m + i));
+      want |= mx::e4m3_encode(clamp(v[i])) << (8 * i);
+    }
+    bad += mxd::e4m3x4(v[0], v[1], v[2], v[3]) != want;
+  }
+  counts[tid] = bad;
+}
+
 extern "C" {
+
+int mx_check_e4m3_pack(mx_ctx* ctx, uint64_t* mismatches) {
+  if (int st = use(ctx)) return st;
+  MX_REQUIRE(mismatches != nullptr, "mx_check_e4m3_pack: null output");
+  constexpr int kBlocks = 4096, kThreads = 256;
+  uint32_t* d = nullptr;
+  MX_HIP(hipMalloc(&d, sizeof(uint32_t) * kBlocks * kThreads));
+  std::vector<uint32_t> h(kBlocks * kThreads);
+  hipLaunchKernelGGL(e4m3_pack_check_kernel, dim3(kBlocks), dim3(kThreads), 0, nullptr, d);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) e = hipMemcpy(h.data(), d, sizeof(uint32_t) * h.size(), hipMemcpyDeviceToHost);
+  (void)hipFree(d);
+  if (e != hipSuccess) return hip_fail(e, "mx_check_e4m3_pack");
+  uint64_t total = 0;
+  for (uint32_t c : h) total += c;
+  *mismatches = total;
+  return MX_OK;
+}
 
 int mx_dequant_mxfp4(mx_ctx* ctx, const uint8_t* packed, const uint8_t* scales, float* out, int64_t rows,
                      int64_t k, void* stream) {
