@@ -96,22 +96,39 @@ def run_projection(block, w, sw, x_bits):
         return proj.fp8("p", x_bits)
 
 
-@pytest.mark.parametrize("block", [32, 128])
-@pytest.mark.parametrize("tokens", [1, 5, 16, 21, 40, 200])
-def test_exact_on_representable_inputs(block, tokens):
+def exact_case(block, tokens, rows, width, wmax, xmax, seed):
     """Small-integer codes, power-of-two scales: every partial sum is exact, so any order gives the
     same FP32 result and the trace must equal the oracle bit for bit."""
-    rng = np.random.default_rng(block * 100 + tokens)
-    rows, width = (128, 512) if tokens <= 32 else (320, 640)       # 320 rows: a partial 256-row GEMM tile
-    w = encode_e4m3(rng.integers(-8, 9, (rows, width)).astype(np.float32))
+    rng = np.random.default_rng(seed)
+    w = encode_e4m3(rng.integers(-wmax, wmax + 1, (rows, width)).astype(np.float32))
     if block == 32:
         sw = rng.integers(125, 130, (rows // 32, width // 32), dtype=np.uint8)
-        x = rng.integers(-16, 17, (tokens, width)).astype(np.float32)
+        x = rng.integers(-xmax, xmax + 1, (tokens, width)).astype(np.float32)
         x[:, ::32] = 448.0                                   # per-32 scale 2^0: codes are the integers
     else:
         sw = np.exp2(rng.integers(-8, -2, ((rows + 127) // 128, width // 128))).astype(np.float32)
-        x = rng.integers(-16, 17, (tokens, width)).astype(np.float32)
+        x = rng.integers(-xmax, xmax + 1, (tokens, width)).astype(np.float32)
         x[:, ::128] = 448.0                                  # per-128 scale exactly 1
+    return w, sw, x
+
+
+@pytest.mark.parametrize("block", [32, 128])
+@pytest.mark.parametrize("tokens", [1, 5, 16, 21, 40, 200])
+def test_exact_on_representable_inputs(block, tokens):
+    rows, width = (128, 512) if tokens <= 32 else (320, 640)       # 320 rows: a partial 256-row GEMM tile
+    w, sw, x = exact_case(block, tokens, rows, width, 8, 16, block * 100 + tokens)
+    check_exact(block, w, sw, x)
+
+
+@pytest.mark.parametrize("block", [32, 128])
+def test_exact_through_the_split_k_gemm(block):
+    """200 tokens x 320 rows over K = 2048: the GEMM splits K in two and adds the FP32 partial sums in
+    split order; magnitudes stay small enough (|sum| < 2^16 units of the smallest scale) to be exact."""
+    w, sw, x = exact_case(block, 200, 320, 2048, 1, 2, 7 + block)
+    check_exact(block, w, sw, x)
+
+
+def check_exact(block, w, sw, x):
     bits = bf16_bits(x)
     got = run_projection(block, w, sw, bits)
     ref = fp8_projection(bf16_values(bits), w, sw, block)

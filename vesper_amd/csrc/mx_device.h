@@ -26,6 +26,16 @@ __device__ __forceinline__ float ldgf(const float* p) {
   return *(const __attribute__((address_space(1))) float*)(p);
 }
 
+// Workgroup barrier ordering LDS only: the fences are restricted to the local address space, so the
+// barrier waits for this wave's LDS operations (lgkmcnt) but leaves its global loads in flight. A plain
+// __syncthreads() also waits for every outstanding global load (vmcnt(0)), which drains a kernel's
+// register prefetch rings at every barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // V_MFMA_SCALE_F32_16X16X128_F8F6F4 operand layouts (measured on gfx950 with one-hot probes):
 //   FP4 A (cbsz 4, 4 VGPRs): lane l = row l % 16, K = 32 (l / 16) + nibble j, low nibble first.
 //   FP8 A (cbsz 0) and FP8 B (blgp 0), 8 VGPRs: lane l = row / column l % 16; bytes 0-15 hold

@@ -250,7 +250,8 @@ __global__ void fp8_splitk_reduce_kernel(const float* __restrict__ partial, int 
 // same bytes in step, the second from L2). The workgroup's 128 tokens x 128 K of activation codes (and
 // their scales) are staged in LDS, double-buffered, and shared by the 8 waves. Each wave accumulates
 // 4 row tiles x 4 token tiles of 16 x 16 in registers; A for the next chunk is prefetched into a second
-// register set while the current chunk's 16 MFMAs run.
+// register set while the current chunk's 16 MFMAs run. The barriers order LDS only (mxd::lds_barrier),
+// so the prefetched loads stay in flight across them.
 constexpr int kGemmTok = 128;                 // tokens per workgroup
 constexpr int kGemmThreads = 512;
 constexpr int kWaveTiles = 4;                 // token tiles per wave
@@ -263,7 +264,10 @@ __global__ __launch_bounds__(kGemmThreads) void fp8_gemm_kernel(Fp8Args a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q = lane >> 4, n = lane & 15;
-  const int C = a.K / 128;
+  // split K (grid z): this workgroup's chunks [c0, c0 + C)
+  const int chunks = a.K / 128, per = (chunks + gridDim.z - 1) / gridDim.z;
+  const int c0 = blockIdx.z * per;
+  const int C = min(per, chunks - c0);
   const int groups = a.N / 64;
   const int g_raw = blockIdx.x * 4 + (wave & 3);
   const bool has_rows = g_raw < groups;
@@ -271,9 +275,9 @@ __global__ __launch_bounds__(kGemmThreads) void fp8_gemm_kernel(Fp8Args a) {
   const int u0 = (wave >> 2) * kWaveTiles;
   const int m0 = blockIdx.y * kGemmTok;
   const Fp8Blob off = fp8_blob(a.N, a.K, kBlock);
-  const uint8_t* wlane = a.blob + (size_t)g * C * 8192 + 16 * lane;
-  const uint8_t* slane = a.blob + off.scales + (size_t)g * C * 256 + 4 * lane;
-  const float* swrow = reinterpret_cast<const float*>(a.blob + off.scales) + (size_t)((64 * g) / 128) * C;
+  const uint8_t* wlane = a.blob + (size_t)g * chunks * 8192 + 16 * lane;
+  const uint8_t* slane = a.blob + off.scales + (size_t)g * chunks * 256 + 4 * lane;
+  const float* swrow = reinterpret_cast<const float*>(a.blob + off.scales) + (size_t)((64 * g) / 128) * chunks;
 
   // staging: thread tid moves pieces tid and tid + 512 (token = piece / 8, 16-byte part = piece % 8)
   const uint8_t* xsrc[2];
@@ -287,18 +291,20 @@ __global__ __launch_bounds__(kGemmThreads) void fp8_gemm_kernel(Fp8Args a) {
   }
   const int stok = min(m0 + (tid & (kGemmTok - 1)), a.T - 1);
 
-  auto load_b = [&](int c, uint4 (&bst)[2], uint32_t& sst) {
+  auto load_b = [&](int cl, uint4 (&bst)[2], uint32_t& sst) {
+    const int c = c0 + cl;
 #pragma unroll
     for (int j = 0; j < 2; ++j) bst[j] = ldg128(xsrc[j] + (size_t)c * 128);
     if constexpr (kBlock == 32) sst = ldg32((const uint8_t*)a.xs + (size_t)stok * (a.K / 32) + 4 * c);
-    else sst = __float_as_uint(ldgf((const float*)a.xs + (size_t)stok * C + c));
+    else sst = __float_as_uint(ldgf((const float*)a.xs + (size_t)stok * chunks + c));
   };
   auto store_b = [&](int stage, const uint4 (&bst)[2], uint32_t sst) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) *reinterpret_cast<uint4*>(&lds_b[stage][ldst[j]]) = bst[j];
     if (tid < kGemmTok) lds_s[stage][tid] = sst;
   };
-  auto load_a = [&](int c, uint4 (&am)[kTiles][2], uint32_t& sw) {
+  auto load_a = [&](int cl, uint4 (&am)[kTiles][2], uint32_t& sw) {
+    const int c = c0 + cl;
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) {
       am[t][0] = ldg128(wlane + (size_t)c * 8192 + t * 2048);
@@ -345,7 +351,7 @@ __global__ __launch_bounds__(kGemmThreads) void fp8_gemm_kernel(Fp8Args a) {
   load_b(0, bst, sst);
   load_a(0, a0, sw0);
   store_b(0, bst, sst);
-  __syncthreads();
+  mxd::lds_barrier();
   // two chunks per iteration so the A register sets alternate with static indices
   for (int c = 0; c < C; c += 2) {
     const bool more1 = c + 1 < C;
@@ -355,7 +361,7 @@ __global__ __launch_bounds__(kGemmThreads) void fp8_gemm_kernel(Fp8Args a) {
     }
     compute(0, a0, sw0);
     if (more1) store_b(1, bst, sst);
-    __syncthreads();
+    mxd::lds_barrier();
     if (!more1) break;
     const bool more2 = c + 2 < C;
     if (more2) {
@@ -364,7 +370,7 @@ __global__ __launch_bounds__(kGemmThreads) void fp8_gemm_kernel(Fp8Args a) {
     }
     compute(1, a1, sw1);
     if (more2) store_b(0, bst, sst);
-    __syncthreads();
+    mxd::lds_barrier();
   }
   if (!has_rows) return;
 #pragma unroll
@@ -374,12 +380,16 @@ __global__ __launch_bounds__(kGemmThreads) void fp8_gemm_kernel(Fp8Args a) {
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) {
       const size_t o = (size_t)tok * a.N + 64 * g + 16 * t + 4 * q;
+      const float4 v = make_float4(acc[t][u][0], acc[t][u][1], acc[t][u][2], acc[t][u][3]);
+      if (gridDim.z > 1) {
+        *reinterpret_cast<float4*>(a.partial + (size_t)blockIdx.z * a.T * a.N + o) = v;
+        continue;
+      }
       uint2 packed;
-      packed.x = mx::bf16_bits(acc[t][u][0]) | (mx::bf16_bits(acc[t][u][1]) << 16);
-      packed.y = mx::bf16_bits(acc[t][u][2]) | (mx::bf16_bits(acc[t][u][3]) << 16);
+      packed.x = mx::bf16_bits(v.x) | (mx::bf16_bits(v.y) << 16);
+      packed.y = mx::bf16_bits(v.z) | (mx::bf16_bits(v.w) << 16);
       *reinterpret_cast<uint2*>(a.y + o) = packed;
-      if (a.trace)
-        *reinterpret_cast<float4*>(a.trace + o) = make_float4(acc[t][u][0], acc[t][u][1], acc[t][u][2], acc[t][u][3]);
+      if (a.trace) *reinterpret_cast<float4*>(a.trace + o) = v;
     }
   }
 }
@@ -391,15 +401,22 @@ int check_fp8_shape(int N, int K, int block, const char* who) {
   return MX_OK;
 }
 
-// K splits of the decode GEMV: about 1024 workgroups, every wave keeping at least one chunk.
+// K splits. Decode GEMV: about 1024 workgroups, every wave keeping at least one chunk. GEMM: only when
+// the rows and tokens alone give fewer workgroups than CUs (the partial sums cost a write and a read of
+// splits x T x N floats), then about 512, every split keeping 8 chunks.
 int fp8_splits(int N, int K, int T) {
-  if (T > kGemvMaxTokens) return 1;
+  if (T > kGemvMaxTokens) {
+    const int base_wgs = ((N / 64 + 3) / 4) * ((T + kGemmTok - 1) / kGemmTok);
+    if (base_wgs >= 256) return 1;
+    return std::max(1, std::min({8, (K / 128) / 8, (512 + base_wgs - 1) / base_wgs}));
+  }
   const int base_wgs = (N / 64) * ((T + kTok - 1) / kTok);
   return std::max(1, std::min({16, (K / 128) / 4, (1024 + base_wgs - 1) / base_wgs}));
 }
 
-// The product on quantized activations: GEMV (T <= 32, split K + ordered reduce into `partial`, which
-// holds fp8_splits(N, K, T) * T * N floats) or the tiled GEMM.
+// The product on quantized activations: GEMV (T <= 32) or the tiled GEMM, either with its K split over
+// fp8_splits(N, K, T) workgroups whose FP32 partial sums go to `partial` (fp8_splits * T * N floats) and
+// are added in split order by fp8_splitk_reduce_kernel.
 int launch_fp8_product(const uint8_t* blob, int N, int K, int block, const uint8_t* q, const void* sc, int T,
                        uint16_t* y, float* trace, float* partial, hipStream_t st) {
   Fp8Args a{};
@@ -425,10 +442,17 @@ int launch_fp8_product(const uint8_t* blob, int N, int K, int block, const uint8
       MX_LAUNCH_CHECK("fp8_splitk_reduce_kernel");
     }
   } else {
-    const dim3 grid((N / 64 + 3) / 4, (T + kGemmTok - 1) / kGemmTok);
+    const int splits = fp8_splits(N, K, T);
+    const dim3 grid((N / 64 + 3) / 4, (T + kGemmTok - 1) / kGemmTok, splits);
     if (block == 32) hipLaunchKernelGGL(fp8_gemm_kernel<32>, grid, dim3(kGemmThreads), 0, st, a);
     else hipLaunchKernelGGL(fp8_gemm_kernel<128>, grid, dim3(kGemmThreads), 0, st, a);
     MX_LAUNCH_CHECK("fp8_gemm_kernel");
+    if (splits > 1) {
+      const int64_t count = (int64_t)T * N;
+      hipLaunchKernelGGL(fp8_splitk_reduce_kernel, dim3((unsigned)((count / 4 + 255) / 256)), dim3(256), 0, st,
+                         (const float*)partial, splits, count, y, trace);
+      MX_LAUNCH_CHECK("fp8_splitk_reduce_kernel");
+    }
   }
   return MX_OK;
 }

@@ -173,16 +173,6 @@ __device__ __forceinline__ void global_to_lds4(const void* src, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" : : "v"(src), "s"(lds) : "m0");
 }
 
-// Workgroup barrier ordering LDS only: the fences are restricted to the local address space, so the
-// barrier waits for this wave's LDS operations (lgkmcnt) but leaves its global loads in flight. A plain
-// __syncthreads() also waits for every outstanding global load (vmcnt(0)), which would drain the
-// prefetch pipelines below at every K chunk.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // Workgroup barrier for the global->LDS copy pipelines: the caller has already waited for its own copies
 // and LDS reads (s_waitcnt) as far as the barrier must cover. Even the local-only fences of lds_barrier
 // would wait for every copy in flight (the copies write LDS), so the barrier is issued bare; the empty
