@@ -13,7 +13,8 @@
 //             weight + the per-token quantization of each 32-row block of the down input
 //   down      grid (H/256, tiles), same shape over W2 with the tile's contiguous down-input rows
 //   combine   per token: its expert rows in ascending expert ID, then the shared row; FP32 from +0,
-//             one BF16 rounding (aggregation_probe.cu:4-25)
+//             one BF16 rounding (aggregation_probe.cu:4-25). The down GEMM writes each row to the
+//             token's contiguous [k + 1][H] block in that order, so the combine streams it.
 #include <algorithm>
 #include <cmath>
 
@@ -41,6 +42,8 @@ struct PrefillPlan {
   int32_t* sorted_tok;  // [rows] token of each row
   float* sorted_w;      // [rows] route weight of each row
   int32_t* pair_row;    // [T * k] row of pair (t, rank)
+  int32_t* row_dest;    // [rows] where the combine reads the row: t (k + 1) + j, j = the row's place in
+                        // the token's ascending-expert order (the shared expert's row: j = k)
 };
 
 __global__ void zero_i32_kernel(int32_t* p, int n) {
@@ -113,6 +116,7 @@ __global__ __launch_bounds__(1024) void scatter_kernel(PrefillPlan p, const int3
     for (int t = tid; t < T; t += 1024) {
       p.sorted_tok[base_row + t] = t;
       p.sorted_w[base_row + t] = 1.0f;
+      p.row_dest[base_row + t] = t * (k + 1) + k;
     }
     return;
   }
@@ -141,6 +145,25 @@ __global__ __launch_bounds__(1024) void scatter_kernel(PrefillPlan p, const int3
   }
 }
 
+// One thread per (token, rank) pair with a valid expert: the row's place in the combine's token-major
+// layout, t (k + 1) + j with j = its position among the token's valid pairs ordered by (expert, rank).
+__global__ __launch_bounds__(256) void dest_kernel(PrefillPlan p, const int32_t* __restrict__ ids, int T, int k,
+                                                   int E) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= T * k) return;
+  const int e = ids[i];
+  if (e < 0 || e >= E) return;
+  const int t = i / k, rank = i - t * k;
+  const int32_t* tok_ids = ids + (size_t)t * k;
+  int j = 0;
+#pragma unroll 8
+  for (int r = 0; r < k; ++r) {
+    const int f = tok_ids[r];
+    j += f >= 0 && f < E && (f < e || (f == e && r < rank));
+  }
+  p.row_dest[p.pair_row[i]] = t * (k + 1) + j;
+}
+
 struct GemmArgs {
   const uint8_t* const* tiles;   // [E + 1] tiled expert blobs
   PrefillPlan plan;
@@ -151,7 +174,7 @@ struct GemmArgs {
   const uint8_t* xs;             // [T][H / 32] E8M0
   uint8_t* dq;                   // [rows][I] down-input codes
   uint8_t* ds;                   // [rows][I / 32]
-  uint16_t* out;                 // [rows][H] expert outputs (BF16)
+  uint16_t* out;                 // [T][k + 1][H] expert outputs (BF16), token-major (plan.row_dest)
 };
 
 // The s_waitcnt immediate that waits until at most n vector-memory operations of this wave are
@@ -433,58 +456,65 @@ __global__ __launch_bounds__(kGThreads, 2) void grouped_kernel(GemmArgs a) {
         }
     }
     __syncthreads();
+    // thread tid copies segment tid % 64 of rows tid / 64 + 8 i (i < 16); their destinations are loaded
+    // together first
     const int cols = min(512, a.H - 512 * (int)blockIdx.x);
-    for (int p = tid; p < kTileRows * 64; p += kGThreads) {
-      const int tok = p >> 6, seg = p & 63;
-      if (tok >= rows || 8 * seg >= cols) continue;
-      *reinterpret_cast<uint4*>(a.out + (size_t)(row0 + tok) * a.H + 512 * blockIdx.x + 8 * seg) =
-          *reinterpret_cast<const uint4*>(eo + tok * kEpiRowD + 8 * seg);
+    const int seg = tid & 63, tok0 = tid >> 6;
+    int dest[kTileRows / 8];
+#pragma unroll
+    for (int i = 0; i < kTileRows / 8; ++i) dest[i] = a.plan.row_dest[row0 + min(tok0 + 8 * i, rows - 1)];
+    if (8 * seg < cols) {
+#pragma unroll
+      for (int i = 0; i < kTileRows / 8; ++i) {
+        const int tok = tok0 + 8 * i;
+        if (tok < rows)
+          *reinterpret_cast<uint4*>(a.out + (size_t)dest[i] * a.H + 512 * blockIdx.x + 8 * seg) =
+              *reinterpret_cast<const uint4*>(eo + tok * kEpiRowD + 8 * seg);
+      }
     }
   }
 }
 
-// grid (T), 256 threads: one workgroup per token; thread 0 orders the token's rows by expert ID in LDS,
-// then every thread sums 8 hidden positions per step over the rows (shared row last).
-__global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillPlan p, const int32_t* __restrict__ ids,
+// Grid-stride over (token, 8 hidden positions) items, 256 threads a workgroup. The down GEMM stored each
+// token's rows contiguously in ascending expert order (row_dest), the shared expert's at place k; an item
+// sums its 8 positions over them in that order, loading up to 9 rows at once.
+__global__ __launch_bounds__(256) void prefill_combine_kernel(const int32_t* __restrict__ ids,
                                                               const uint16_t* __restrict__ rows, int T, int H, int k,
                                                               int E, int has_shared, uint16_t* __restrict__ y) {
-  __shared__ int32_t order[kMaxTopK + 1];
-  __shared__ int order_n;
-  const int t = blockIdx.x;
-  if (threadIdx.x == 0) {
-    int32_t es[kMaxTopK], rs[kMaxTopK];
-    int m = 0;
+  const int per_tok = H / 8;
+  const int64_t items = (int64_t)T * per_tok;
+  constexpr int kBatch = 9;
+  for (int64_t it = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; it < items; it += (int64_t)gridDim.x * blockDim.x) {
+    const int t = (int)(it / per_tok), h = (int)(it - (int64_t)t * per_tok) * 8;
+    int m = 0;   // the token's valid routed pairs
     for (int i = 0; i < k; ++i) {
       const int e = ids[t * k + i];
-      if (e < 0 || e >= E) continue;
-      const int r = p.pair_row[t * k + i];
-      int j = m - 1;
-      while (j >= 0 && es[j] > e) {
-        es[j + 1] = es[j];
-        rs[j + 1] = rs[j];
-        --j;
-      }
-      es[j + 1] = e;
-      rs[j + 1] = r;
-      ++m;
+      m += e >= 0 && e < E;
     }
-    for (int i = 0; i < m; ++i) order[i] = rs[i];
-    if (has_shared) order[m++] = T * k + t;   // the shared expert's rows follow the routed ones
-    order_n = m;
-  }
-  __syncthreads();
-  const int n = order_n;
-  for (int h = threadIdx.x * 8; h < H; h += 256 * 8) {
+    const int n = m + (has_shared ? 1 : 0);
+    const uint16_t* base = rows + (size_t)t * (k + 1) * H + h;
     float acc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] = 0.f;
-    for (int i = 0; i < n; ++i) {
-      const uint4 v = *reinterpret_cast<const uint4*>(rows + (size_t)order[i] * H + h);
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    for (int i0 = 0; i0 < n; i0 += kBatch) {
+      // all of a batch's loads first (places past n repeat the last one), then the sums in order
+      uint4 v[kBatch];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        acc[2 * j] = acc[2 * j] + mx::bf16_value(w[j] & 0xFFFFu);
-        acc[2 * j + 1] = acc[2 * j + 1] + mx::bf16_value(w[j] >> 16);
+      for (int b = 0; b < kBatch; ++b) {
+        const int j = min(i0 + b, n - 1);
+        v[b] = *reinterpret_cast<const uint4*>(base + (size_t)(j < m ? j : k) * H);
+      }
+      // no early exit: a fully unrolled loop keeps v[] in registers (a break would index it dynamically)
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        if (i0 + b < n) {
+          const uint32_t w[4] = {v[b].x, v[b].y, v[b].z, v[b].w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc[2 * j] = acc[2 * j] + mx::bf16_value(w[j] & 0xFFFFu);
+            acc[2 * j + 1] = acc[2 * j + 1] + mx::bf16_value(w[j] >> 16);
+          }
+        }
       }
     }
     uint4 o;
@@ -501,7 +531,7 @@ uint64_t r256(uint64_t b) { return (b + 255) & ~255ull; }
 // Workspace layout (each piece 256-byte aligned).
 struct Workspace {
   uint64_t logits, scores, selection, ids, w, xq, xs, counts, row0, tile_info, n_tiles, sorted_tok, sorted_w,
-      pair_row, dq, ds, eout, total;
+      pair_row, row_dest, dq, ds, eout, total;
   int max_tiles, rows;
 };
 
@@ -531,9 +561,10 @@ Workspace workspace_layout(const mx_moe_config& c, int T, int has_shared) {
   w.sorted_tok = take((uint64_t)w.rows * 4);
   w.sorted_w = take((uint64_t)w.rows * 4);
   w.pair_row = take(pairs * 4);
+  w.row_dest = take((uint64_t)w.rows * 4);
   w.dq = take((uint64_t)w.rows * I);
   w.ds = take((uint64_t)w.rows * I / 32);
-  w.eout = take((uint64_t)w.rows * H * 2);
+  w.eout = take((uint64_t)T * (k + 1) * H * 2);   // token-major: [T][k + 1][H]
   w.total = o;
   return w;
 }
@@ -595,6 +626,7 @@ int mx_moe_prefill(mx_layer* layer, const uint16_t* x, int32_t T, const int32_t*
   p.sorted_tok = (int32_t*)(b + ws.sorted_tok);
   p.sorted_w = (float*)(b + ws.sorted_w);
   p.pair_row = (int32_t*)(b + ws.pair_row);
+  p.row_dest = (int32_t*)(b + ws.row_dest);
   hipLaunchKernelGGL(zero_i32_kernel, dim3((E + 1 + 255) / 256), dim3(256), 0, st, p.counts, E + 1);
   MX_LAUNCH_CHECK("zero_i32_kernel");
   const int pairs = T * k;
@@ -604,6 +636,8 @@ int mx_moe_prefill(mx_layer* layer, const uint16_t* x, int32_t T, const int32_t*
   MX_LAUNCH_CHECK("offsets_kernel");
   hipLaunchKernelGGL(scatter_kernel, dim3(E + 1), dim3(1024), 0, st, p, rid, rw, T, k, E, v.has_shared);
   MX_LAUNCH_CHECK("scatter_kernel");
+  hipLaunchKernelGGL(dest_kernel, dim3((pairs + 255) / 256), dim3(256), 0, st, p, rid, T, k, E);
+  MX_LAUNCH_CHECK("dest_kernel");
   GemmArgs a{};
   a.tiles = v.tiles;
   a.plan = p;
@@ -621,8 +655,9 @@ int mx_moe_prefill(mx_layer* layer, const uint16_t* x, int32_t T, const int32_t*
   MX_LAUNCH_CHECK("grouped_kernel<gate/up>");
   hipLaunchKernelGGL(grouped_kernel<false>, dim3((H + 511) / 512, ws.max_tiles), dim3(kGThreads), 0, st, a);
   MX_LAUNCH_CHECK("grouped_kernel<down>");
-  hipLaunchKernelGGL(prefill_combine_kernel, dim3(T), dim3(256), 0, st, p, rid,
-                     (const uint16_t*)a.out, T, H, k, E, v.has_shared, y);
+  const int64_t items = (int64_t)T * (H / 8);
+  hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)std::min<int64_t>(2048, (items + 255) / 256)), dim3(256), 0,
+                     st, rid, (const uint16_t*)a.out, T, H, k, E, v.has_shared, y);
   MX_LAUNCH_CHECK("prefill_combine_kernel");
   return MX_OK;
 }
