@@ -50,7 +50,9 @@ def arrays_for(layout, block, rng, layer=0):
     return arrays
 
 
-def test_act_quant128_bit_exact(gpu_ctx):
+@pytest.mark.parametrize("offset", [0, 2])
+def test_act_quant128_bit_exact(gpu_ctx, offset):
+    """offset 0: 16-byte aligned buffers (8 values per lane); offset 2 values: the 4-byte aligned path."""
     rng = np.random.default_rng(7)
     x = rng.standard_normal((9, 1024)).astype(np.float32)
     x *= np.ldexp(np.ones((9, 1), np.float32), rng.integers(-30, 10, (9, 1)))
@@ -58,13 +60,15 @@ def test_act_quant128_bit_exact(gpu_ctx):
     x[1, :128] = 448.0
     x[2, 256:384] = -1e-7
     bits = bf16_bits(x)
-    xd = gpu_ctx.upload(bits)
-    q = gpu_ctx.empty((9, 1024), np.uint8)
+    padded = np.concatenate([np.zeros(offset, np.uint16), bits.ravel()])
+    xd = gpu_ctx.upload(padded)
+    q = gpu_ctx.empty((9 * 1024 + 2 * offset,), np.uint8)
     s = gpu_ctx.empty((9, 8), np.float32)
-    gpu_ctx.lib.act_quant128(gpu_ctx._h(), _lib.vp(xd), _lib.vp(q), _lib.vp(s), 9, 1024, None)
+    gpu_ctx.lib.act_quant128(gpu_ctx._h(), _lib.vp(xd.ptr + 2 * offset), _lib.vp(q.ptr + 2 * offset), _lib.vp(s), 9,
+                             1024, None)
     q_ref, s_ref = quantize_activation_128(bf16_values(bits))
     np.testing.assert_array_equal(s.download().view(np.uint32), s_ref.view(np.uint32))
-    np.testing.assert_array_equal(q.download(), q_ref)
+    np.testing.assert_array_equal(q.download()[2 * offset:].reshape(9, 1024), q_ref)
     for d in (xd, q, s):
         d.free()
 
