@@ -132,6 +132,26 @@ def test_exact_through_the_split_k_gemm(block):
     check_exact(block, w, sw, x)
 
 
+@pytest.mark.parametrize("block", [32, 128])
+@pytest.mark.parametrize("tokens", [1, 21])
+def test_exact_through_the_split_k_gemv(block, tokens):
+    """K = 2048 splits the GEMV's K four ways; the last workgroup of each tile adds the partial sums in
+    split order. Three calls in a row on one weight set, each with new activations, each exact: a tile
+    counter left behind by one call would leave the next call's outputs unwritten."""
+    w, sw, _ = exact_case(block, tokens, 192, 2048, 4, 8, 31 + block + tokens)
+    rows, width = w.shape
+    arrays = {"layers.0.attn.p.weight": w, "layers.0.attn.p.scale": sw}
+    with NativeProjections(arrays, block=block, layout={"p": (rows, width)}) as proj:
+        for call in range(3):
+            _, _, x = exact_case(block, tokens, rows, width, 4, 8, 100 * call + block + tokens)
+            bits = bf16_bits(x)
+            got = proj.fp8("p", bits)
+            ref = fp8_projection(bf16_values(bits), w, sw, block)
+            np.testing.assert_array_equal(got["output_fp32"].view(np.uint32), ref["output_fp32"].view(np.uint32),
+                                          err_msg=f"call {call}")
+            np.testing.assert_array_equal(got["output_bf16"], ref["output_bf16"], err_msg=f"call {call}")
+
+
 def check_exact(block, w, sw, x):
     bits = bf16_bits(x)
     got = run_projection(block, w, sw, bits)

@@ -31,6 +31,10 @@ using mxd::v4f;
 constexpr int kTiles = 4;   // 16-row MFMA tiles per workgroup: 64 weight rows
 constexpr int kTok = 16;    // token columns per MFMA
 constexpr int kGemvMaxTokens = 32;   // above this the tiled GEMM reuses each weight tile for 128 tokens
+// The GEMV's last workgroup per tile adds the split-K partial sums when they total at most this many
+// bytes. Above it (the 7168- and 24576-row projections at 16 tokens, measured on MI355X) the
+// device-coherent round trip through one workgroup per tile costs more than fp8_splitk_reduce_kernel.
+constexpr uint64_t kTicketPartialBytes = 2u << 20;
 
 struct Fp8Blob {
   size_t scales;   // byte offset of the scale section
@@ -134,6 +138,8 @@ struct Fp8Args {
   uint16_t* y;         // [T][N] BF16
   float* trace;        // [T][N] FP32 sums, nullable
   float* partial;      // split K: [splits][T][N] FP32 partial sums (the GEMV writes these instead of y)
+  uint32_t* tickets;   // split-K GEMV: arrival counter per (row group, token tile), zero between launches;
+                       // null = partial sums only, added by fp8_splitk_reduce_kernel
 };
 
 template <int kBlock>
@@ -187,7 +193,9 @@ __device__ __forceinline__ void fp8_mma(const Fp8Chunk<kBlock>& r, v4f (&acc)[kT
 // grid (N / 64, ceil(T / 16), splits), 256 threads: 64 weight rows x 16 tokens x one K range per
 // workgroup. Wave w streams its quarter of the workgroup's K chunks (P = 2 chunks of 8 KB in flight), the
 // quarters are summed through LDS in wave order, then wave t writes tile t: BF16 (and the FP32 trace)
-// when K is not split, else its FP32 partial sums for fp8_splitk_reduce_kernel.
+// when K is not split, else its FP32 partial sums. With K split and a.tickets set, the last workgroup of
+// the (row group, token tile) to arrive adds the partial sums in split order (fp8_splitk_reduce_kernel's
+// arithmetic) and writes the outputs; without tickets fp8_splitk_reduce_kernel does it.
 template <int kBlock>
 __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
   constexpr int P = 2;
@@ -237,12 +245,52 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     out[i] = ((red[0][wave][lane][i] + red[1][wave][lane][i]) + red[2][wave][lane][i]) + red[3][wave][lane][i];
-  if (live) {
-    const size_t o = (size_t)tok * a.N + 64 * g + 16 * wave + 4 * q;
-    if (S > 1) {
-      *reinterpret_cast<float4*>(a.partial + (size_t)z * a.T * a.N + o) = make_float4(out[0], out[1], out[2], out[3]);
+  const size_t o = (size_t)tok * a.N + 64 * g + 16 * wave + 4 * q;
+  if (S > 1) {
+    float* part = a.partial + (size_t)z * a.T * a.N + o;
+    if (!a.tickets) {
+      if (live) *reinterpret_cast<float4*>(part) = make_float4(out[0], out[1], out[2], out[3]);
       return;
     }
+    // Device-coherent partial sums; once every wave's stores have completed (s_waitcnt 0, then the
+    // barrier) one relaxed atomic takes the tile's ticket. The last of the S arrivals reads all partial
+    // sums back, device-coherent, and adds them in split order.
+    if (live) {
+      mxd::store_device(part, out[0], out[1]);
+      mxd::store_device(part + 2, out[2], out[3]);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __shared__ uint32_t arrived;
+    __syncthreads();
+    uint32_t* ticket = a.tickets + (size_t)blockIdx.y * gridDim.x + g;
+    if (tid == 0) arrived = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (arrived != (uint32_t)(S - 1)) return;
+    if (tid == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!live) return;
+    const size_t stride = (size_t)a.T * a.N;
+    float2 p[16][2];
+#pragma unroll
+    for (int zz = 0; zz < 16; ++zz)
+      if (zz < S) {
+        p[zz][0] = mxd::load_device(a.partial + (size_t)zz * stride + o);
+        p[zz][1] = mxd::load_device(a.partial + (size_t)zz * stride + o + 2);
+      }
+    float4 t = make_float4(p[0][0].x, p[0][0].y, p[0][1].x, p[0][1].y);
+#pragma unroll
+    for (int zz = 1; zz < 16; ++zz)
+      if (zz < S) {
+        t.x = t.x + p[zz][0].x;
+        t.y = t.y + p[zz][0].y;
+        t.z = t.z + p[zz][1].x;
+        t.w = t.w + p[zz][1].y;
+      }
+    out[0] = t.x;
+    out[1] = t.y;
+    out[2] = t.z;
+    out[3] = t.w;
+  }
+  if (live) {
     uint2 packed;
     packed.x = mx::bf16_bits(out[0]) | (mx::bf16_bits(out[1]) << 16);
     packed.y = mx::bf16_bits(out[2]) | (mx::bf16_bits(out[3]) << 16);
@@ -445,9 +493,10 @@ int fp8_splits(int N, int K, int T) {
 
 // The product on quantized activations: GEMV (T <= 32) or the tiled GEMM, either with its K split over
 // fp8_splits(N, K, T) workgroups whose FP32 partial sums go to `partial` (fp8_splits * T * N floats) and
-// are added in split order by fp8_splitk_reduce_kernel.
+// are added in split order: by the GEMV's last workgroup per tile (`tickets`, the context's arrival
+// counters) or by fp8_splitk_reduce_kernel.
 int launch_fp8_product(const uint8_t* blob, int N, int K, int block, const uint8_t* q, const void* sc, int T,
-                       uint16_t* y, float* trace, float* partial, hipStream_t st) {
+                       uint16_t* y, float* trace, float* partial, uint32_t* tickets, hipStream_t st) {
   Fp8Args a{};
   a.blob = blob;
   a.N = N;
@@ -461,10 +510,13 @@ int launch_fp8_product(const uint8_t* blob, int N, int K, int block, const uint8
   if (T <= kGemvMaxTokens) {
     const int splits = fp8_splits(N, K, T);
     const dim3 grid(N / 64, (T + kTok - 1) / kTok, splits);
+    if (splits > 1 && (size_t)grid.x * grid.y <= MX_TICKETS &&
+        (uint64_t)splits * T * N * sizeof(float) <= kTicketPartialBytes)
+      a.tickets = tickets;
     if (block == 32) hipLaunchKernelGGL(fp8_gemv_kernel<32>, grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL(fp8_gemv_kernel<128>, grid, dim3(256), 0, st, a);
     MX_LAUNCH_CHECK("fp8_gemv_kernel");
-    if (splits > 1) {
+    if (splits > 1 && !a.tickets) {
       const int64_t count = (int64_t)T * N;
       hipLaunchKernelGGL(fp8_splitk_reduce_kernel, dim3((unsigned)((count / 4 + 255) / 256)), dim3(256), 0, st,
                          (const float*)partial, splits, count, y, trace);
@@ -569,7 +621,7 @@ int mx_fp8_projection(mx_ctx* ctx, const void* tiled, int32_t N, int32_t K, int3
     if (int s = mx_act_quant128(ctx, x, q, (float*)sc, T, K, stream)) return s;
   }
   return launch_fp8_product((const uint8_t*)tiled, N, K, block, q, sc, T, y, trace,
-                            (float*)((uint8_t*)base + q_b + s_b), st);
+                            (float*)((uint8_t*)base + q_b + s_b), ctx->tickets, st);
 }
 
 int mx_fp8_expert_forward(mx_ctx* ctx, const void* w1, const void* w3, const void* w2, int32_t H, int32_t I,
@@ -615,14 +667,14 @@ int mx_fp8_expert_forward(mx_ctx* ctx, const void* w1, const void* w3, const voi
                  ((uintptr_t)ds & 3) == 0,
              "stage buffers: q/down_q 16-byte, w1/w3 8-byte, scales and down_input 4-byte aligned");
   if (int e = mx_act_quant32(ctx, x, q, s, T, H, stream)) return e;
-  if (int e = launch_fp8_product((const uint8_t*)w1, I, H, 32, q, s, T, b1, nullptr, partial, st)) return e;
-  if (int e = launch_fp8_product((const uint8_t*)w3, I, H, 32, q, s, T, b3, nullptr, partial, st)) return e;
+  if (int e = launch_fp8_product((const uint8_t*)w1, I, H, 32, q, s, T, b1, nullptr, partial, ctx->tickets, st)) return e;
+  if (int e = launch_fp8_product((const uint8_t*)w3, I, H, 32, q, s, T, b3, nullptr, partial, ctx->tickets, st)) return e;
   const int64_t n = (int64_t)T * I;
   hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (const uint16_t*)b1,
                      (const uint16_t*)b3, T, I, limit, route_w, din, trace);
   MX_LAUNCH_CHECK("swiglu_kernel");
   if (int e = mx_act_quant32(ctx, din, dq, ds, T, I, stream)) return e;
-  return launch_fp8_product((const uint8_t*)w2, H, I, 32, dq, ds, T, y, nullptr, partial, st);
+  return launch_fp8_product((const uint8_t*)w2, H, I, 32, dq, ds, T, y, nullptr, partial, ctx->tickets, st);
 }
 
 }  // extern "C"

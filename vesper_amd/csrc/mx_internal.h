@@ -20,7 +20,12 @@ struct mx_ctx {
   std::unordered_map<void*, uint64_t> pinned;       // host pinned allocations
   void* scratch = nullptr;                          // small reusable device scratch
   uint64_t scratch_bytes = 0;
+  uint32_t* tickets = nullptr;                      // [MX_TICKETS] arrival counters, zero between launches
 };
+
+// Arrival counters of split-K kernels: the last workgroup of an output tile to arrive finishes the tile
+// and puts its counter back to zero, so the array is zero again whenever the launch has ended.
+#define MX_TICKETS 16384
 
 // By-value kernel argument of mx_layer_set_experts: up to 64 table entries per launch.
 #define MX_EXPERT_BATCH 64

@@ -68,9 +68,17 @@ int mx_create(int device, uint64_t cap_bytes, mx_ctx** out) {
   MX_REQUIRE(device >= 0 && device < n, "mx_create: device %d not present (%d visible)", device, n);
   MX_HIP(hipSetDevice(device));
   MX_HIP(hipFree(nullptr));  // initialise the device's primary context now
+  uint32_t* tickets = nullptr;
+  MX_HIP(hipMalloc(&tickets, MX_TICKETS * sizeof(uint32_t)));
+  if (hipMemset(tickets, 0, MX_TICKETS * sizeof(uint32_t)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+    const hipError_t err = hipGetLastError();
+    (void)hipFree(tickets);
+    return hip_fail(err, "mx_create: clear the arrival counters");
+  }
   mx_ctx* ctx = new mx_ctx();
   ctx->device = device;
   ctx->cap = cap_bytes;
+  ctx->tickets = tickets;
   *out = ctx;
   return MX_OK;
 }
@@ -83,6 +91,7 @@ int mx_destroy(mx_ctx* ctx) {
     for (auto& kv : ctx->owned) (void)hipFree(kv.first);
     for (auto& kv : ctx->pinned) (void)hipHostFree(kv.first);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->tickets) (void)hipFree(ctx->tickets);
   }
   delete ctx;
   return status;
