@@ -5,8 +5,12 @@ SwiGLU experts of 7168 x 2048, ordered combine) at each batch size T in {1, 4, 1
 resident in HBM. Expert weights are synthetic (uniform nibbles, E8M0 codes uniform in
 [118, 126]) generated in HBM; W_r ~ N(0, 0.02); x ~ N(0, 1) rounded to BF16.
 
+Consecutive decode calls go to consecutive layers of LAYERS independently generated ones (own 257
+experts and router each, 6 GB per layer), as in a model: no call finds the weights of the call before
+in the GPU's caches (256 MB Infinity Cache), which a single layer re-run with one routing would allow.
+
 value = whole-step weight-stream throughput: algorithmic bytes (distinct selected experts + shared
-+ router + activations, counted from the seeded routing) / step time. Prints one JSON line.
++ router + activations, counted from each call's seeded routing) / step time. Prints one JSON line.
 """
 
 from __future__ import annotations
@@ -22,6 +26,7 @@ import numpy as np
 
 HBM_PEAK_GBS = 8000.0
 TOKENS = (1, 4, 16)
+LAYERS = 4
 ROOT = os.path.dirname(os.path.abspath(__file__))
 TRAFFIC = os.path.join(ROOT, "profiles", "gateup_T16_traffic.json")
 
@@ -118,71 +123,88 @@ def main():
     ctx = _lib.Context(0)
     name, arch = ctx.device_name()
     log(f"device {name} {arch}")
+    # layer 0 (and x) as in vesper_amd.profile_workload, so their counter runs describe its kernels
     rng = np.random.default_rng(args.seed)
-    bank = ExpertBank(ctx, cfg, cfg.experts + 1)
-    bank.fill_synthetic(args.seed)
-    w = (rng.standard_normal((cfg.experts, cfg.hidden)) * 0.02).astype(np.float32)
-    layer = MoELayer(ctx, cfg, w, bank)
-    x_rows = rng.standard_normal((max(TOKENS), cfg.hidden)).astype(np.float32)
+    banks, routers, layers = [], [], []
+    for li in range(LAYERS):
+        bank = ExpertBank(ctx, cfg, cfg.experts + 1)
+        bank.fill_synthetic(args.seed + li)
+        r = rng if li == 0 else np.random.default_rng(args.seed + li)
+        w = (r.standard_normal((cfg.experts, cfg.hidden)) * 0.02).astype(np.float32)
+        banks.append(bank)
+        routers.append(w)
+        layers.append(MoELayer(ctx, cfg, w, bank))
+        if li == 0:
+            x_rows = rng.standard_normal((max(TOKENS), cfg.hidden)).astype(np.float32)
     bits = x_rows.view(np.uint32).astype(np.uint64)
     bits = ((bits + 0x7FFF + ((bits >> 16) & 1)) >> 16).astype(np.uint16)
     xs = {t: ctx.upload(bits[:t].copy()) for t in TOKENS}
     ys = {t: ctx.empty((t, cfg.hidden), np.uint16) for t in TOKENS}
     stream = ctx.stream()
     ctx.sync()
-    log("weights resident; warming up")
+    log(f"weights of {LAYERS} layers resident; warming up")
 
     plans, per_t = {}, {}
-    for t in TOKENS:
-        layer.decode_device(xs[t].ptr, t, ys[t].ptr, stream)
-        ctx.sync(stream)
-        plans[t] = layer.plan()
-    for _ in range(args.warmup):
+    for li, layer in enumerate(layers):
         for t in TOKENS:
             layer.decode_device(xs[t].ptr, t, ys[t].ptr, stream)
+            ctx.sync(stream)
+            plans[li, t] = layer.plan()
+    calls = 0
+    for _ in range(args.warmup):
+        for t in TOKENS:
+            layers[calls % LAYERS].decode_device(xs[t].ptr, t, ys[t].ptr, stream)
+            calls += 1
     ctx.sync(stream)
 
-    # timed region: K steps, each a decode layer at T = 1, 4, 16
+    # timed region: K steps, each a decode layer at T = 1, 4, 16, consecutive calls on consecutive layers
     start, stop = ctx.event(), ctx.event()
     ctx.sync()
+    timed_bytes = 0
     ctx.record(start, stream)
     for _ in range(args.steps):
         for t in TOKENS:
-            layer.decode_device(xs[t].ptr, t, ys[t].ptr, stream)
+            li = calls % LAYERS
+            layers[li].decode_device(xs[t].ptr, t, ys[t].ptr, stream)
+            timed_bytes += algorithmic_bytes(cfg, plans[li, t], t)
+            calls += 1
     ctx.record(stop, stream)
     total_ms = ctx.elapsed_ms(start, stop)
     ctx.sync()
     ms_per_step = total_ms / args.steps
     log(f"timed {args.steps} steps: {ms_per_step * 1000:.1f} us/step")
 
-    # per-T latency and per-kernel timing (HIP events between the kernels on the launch stream)
-    step_bytes = 0
+    # per-T latency (calls rotating over the layers) and per-kernel timing of layer 0 (each stage
+    # re-launched back to back on the launch stream, HIP events around the loop)
     for t in TOKENS:
+        t_bytes = 0
         ctx.record(start, stream)
-        for _ in range(args.steps):
-            layer.decode_device(xs[t].ptr, t, ys[t].ptr, stream)
+        for i in range(args.steps):
+            layers[i % LAYERS].decode_device(xs[t].ptr, t, ys[t].ptr, stream)
+            t_bytes += algorithmic_bytes(cfg, plans[i % LAYERS, t], t)
         ctx.record(stop, stream)
         us = ctx.elapsed_ms(start, stop) / args.steps * 1000
-        b = algorithmic_bytes(cfg, plans[t], t)
-        step_bytes += b
-        # each stage re-launched back to back on the launch stream, HIP events around the loop
-        layer.decode_device(xs[t].ptr, t, ys[t].ptr, stream)
-        kernel_us = {stage: layer.time_stage(stage, args.profile_iters, stream) for stage in layer.STAGES}
-        per_t[t] = {"us_per_layer": us, "distinct_experts": plans[t]["n_routed"], "bytes": b,
+        b = t_bytes / args.steps
+        layers[0].decode_device(xs[t].ptr, t, ys[t].ptr, stream)
+        kernel_us = {stage: layers[0].time_stage(stage, args.profile_iters, stream) for stage in MoELayer.STAGES}
+        distinct = [plans[li, t]["n_routed"] for li in range(LAYERS)]
+        per_t[t] = {"us_per_layer": us, "distinct_experts": float(np.mean(distinct)),
+                    "distinct_experts_per_layer": distinct, "bytes": b,
                     "GB_per_s": b / (us * 1e-6) / 1e9, "hbm_frac": b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-                    "kernel_us": kernel_us, "gateup_bytes": gateup_bytes(cfg, plans[t], t)}
-        log(f"T={t}: {us:.1f} us/layer, {per_t[t]['GB_per_s']:.0f} GB/s, kernels {per_t[t]['kernel_us']}")
+                    "kernel_us_layer0": kernel_us, "gateup_bytes_layer0": gateup_bytes(cfg, plans[0, t], t)}
+        log(f"T={t}: {us:.1f} us/layer, {per_t[t]['GB_per_s']:.0f} GB/s, layer-0 kernels {kernel_us}")
 
-    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    value = timed_bytes / (total_ms * 1e-3) / 1e9
     head = per_t[16]
-    gu_us = head["kernel_us"]["gateup"]
-    achieved = head["gateup_bytes"] / (gu_us * 1e-6) / 1e9
+    gu_us = head["kernel_us_layer0"]["gateup"]
+    achieved = head["gateup_bytes_layer0"] / (gu_us * 1e-6) / 1e9
     result = {
         "metric": "MoE decode-layer us + MXFP4 weight-stream GB/s (% HBM peak), top-8 of 256",
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "mxfp4xe4m3->f32", "data": "synthetic (seeded; weights generated in HBM)",
         "config": {"workload": "BASELINE config 1: routed MoE decode layer, T in {1,4,16} per step",
+                   "layers_rotated": LAYERS,
                    "hidden": cfg.hidden, "intermediate": cfg.intermediate, "experts": cfg.experts,
                    "top_k": cfg.top_k, "shared": cfg.shared, "score_func": cfg.score_func,
                    "route_scale": cfg.route_scale, "tokens_per_step": list(TOKENS)},
@@ -191,15 +213,16 @@ def main():
                       for t, d in per_t.items()},
         "roofline": {"kernel": "gateup_kernel (T=16)", "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(head["gateup_bytes"]), "launch_us": round(gu_us, 2),
-                     "algorithmic_bytes": head["gateup_bytes"]},
+                     "traffic": measured_traffic(head["gateup_bytes_layer0"]), "launch_us": round(gu_us, 2),
+                     "algorithmic_bytes": head["gateup_bytes_layer0"]},
         "device": {"name": name, "arch": arch},
     }
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle, bounded sample)")
-        result["cpu_baseline"] = cpu_baseline(layer, bank, w, x_rows, cfg)
-    layer.close()
-    bank.free()
+        result["cpu_baseline"] = cpu_baseline(layers[0], banks[0], routers[0], x_rows, cfg)
+    for layer, bank in zip(layers, banks):
+        layer.close()
+        bank.free()
     if not args.no_secondary:
         result["secondary"] = secondary(ctx)
     print(json.dumps(result), flush=True)

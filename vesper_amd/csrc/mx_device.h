@@ -22,6 +22,17 @@ __device__ __forceinline__ uint4 ldg128(const uint8_t* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Non-temporal (streaming) loads, the `nt` bit: for data read once per call, such as expert weights
+// in decode. A plain blocked read of 2 GiB on MI355X runs at 7.3 TB/s with them, 6.5 TB/s without.
+__device__ __forceinline__ uint32_t ldg32_nt(const uint8_t* p) {
+  return __builtin_nontemporal_load((const __attribute__((address_space(1))) uint32_t*)(p));
+}
+
+__device__ __forceinline__ uint4 ldg128_nt(const uint8_t* p) {
+  const u32x4_t v = __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4_t*)(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ float ldgf(const float* p) {
   return *(const __attribute__((address_space(1))) float*)(p);
 }
