@@ -80,6 +80,32 @@ def measured_traffic(algorithmic):
     return rec.get("traffic_bytes")
 
 
+def read_ceiling(ctx, stream, nbytes=2 << 30, reps=7):
+    """HBM read rate of the fastest plain read kernel measured on this part (mx_read_kernel: 4096
+    workgroups over contiguous ranges, non-temporal 16-byte loads), median of `reps` launches of
+    `nbytes`, HIP events on the launch stream."""
+    from vesper_amd import _lib
+    import ctypes as C
+    src = ctx.malloc(nbytes)
+    out = ctx.empty((4 * 4096,), np.uint32)
+    start, stop = ctx.event(), ctx.event()
+    times = []
+    for i in range(reps + 2):
+        ctx.record(start, stream)
+        ctx.lib.read_kernel(ctx._h(), C.c_void_p(src), nbytes, _lib.vp(out), _lib._stream(stream))
+        ctx.record(stop, stream)
+        ms = ctx.elapsed_ms(start, stop)
+        if i >= 2:
+            times.append(ms)
+    ctx.free(src)
+    out.free()
+    gbs = nbytes / (float(np.median(times)) * 1e-3) / 1e9
+    return {"GB_per_s": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes,
+            "kernel": "read_ceiling_kernel (mx_read_kernel): 4096 workgroups over contiguous ranges, "
+                      "non-temporal 16-byte loads, 3 x 4 KB in flight per wave; median of "
+                      f"{reps} launches"}
+
+
 def cpu_baseline(layer, bank, w, x_rows, cfg):
     """The NumPy oracle's layer at T=1 on the host cores, single-threaded BLAS, bounded sample."""
     import threadpoolctl
@@ -194,6 +220,8 @@ def main():
                     "kernel_us_layer0": kernel_us, "gateup_bytes_layer0": gateup_bytes(cfg, plans[0, t], t)}
         log(f"T={t}: {us:.1f} us/layer, {per_t[t]['GB_per_s']:.0f} GB/s, layer-0 kernels {kernel_us}")
 
+    ceiling = read_ceiling(ctx, stream)
+    log(f"read ceiling: {ceiling['GB_per_s']} GB/s")
     value = timed_bytes / (total_ms * 1e-3) / 1e9
     head = per_t[16]
     gu_us = head["kernel_us_layer0"]["gateup"]
@@ -214,7 +242,10 @@ def main():
         "roofline": {"kernel": "gateup_kernel (T=16)", "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(head["gateup_bytes_layer0"]), "launch_us": round(gu_us, 2),
-                     "algorithmic_bytes": head["gateup_bytes_layer0"]},
+                     "algorithmic_bytes": head["gateup_bytes_layer0"],
+                     "read_ceiling_GB_s": ceiling["GB_per_s"],
+                     "frac_of_read_ceiling": round(achieved / ceiling["GB_per_s"], 4)},
+        "hbm_read_ceiling": ceiling,
         "device": {"name": name, "arch": arch},
     }
     if not args.no_cpu_baseline:

@@ -71,6 +71,13 @@ int mx_fill_uniform_u8(mx_ctx* ctx, void* dst, uint64_t bytes, uint64_t seed, ui
  * calibrate the profiler's HBM byte counters. Pointers 16-byte aligned, bytes a multiple of 16. */
 int mx_copy_kernel(mx_ctx* ctx, void* dst, const void* src, uint64_t bytes, void* stream);
 
+/* Streaming read of `bytes` (a multiple of 16 MiB, 16-byte aligned source) by the fastest plain read
+ * kernel measured on MI355X (4096 workgroups of contiguous ranges, non-temporal 16-byte loads, three
+ * 4 KB steps in flight per wave): the HBM read rate the weight-streaming kernels are compared with.
+ * out[4 * 4096] receives the XOR of the 32-bit words each wave read. No reference counterpart: a
+ * measurement workload. */
+int mx_read_kernel(mx_ctx* ctx, const void* src, uint64_t bytes, uint32_t* out, void* stream);
+
 /* ---- format hooks (replaces format_probe.cu decode_fp4/encode_fp8/activation32, lines 23-52) ---- */
 
 /* Self-check with no counterpart in the reference: compares the gfx950 hardware E4M3 packing used by the

@@ -126,6 +126,7 @@ SIGNATURES = {
     "mx_fp8_expert_forward": ([_P, _P, _P, _P, _I32, _I32, _P, _I32, _F, _P, _P, C.POINTER(MxExpertStages), _P],
                               C.c_int),
     "mx_copy_kernel": ([_P, _P, _P, _U64, _P], C.c_int),
+    "mx_read_kernel": ([_P, _P, _U64, _P, _P], C.c_int),
     "mx_check_e4m3_pack": ([_P, C.POINTER(_U64)], C.c_int),
 }
 

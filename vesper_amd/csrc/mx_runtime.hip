@@ -3,6 +3,7 @@
 // Replaces the reference's ctypes Driver/Device layer (src/vesper/cuda.py:28-222):
 // an explicit-allocation map with a byte cap, pinned host buffers, copies, and
 // device-wide errors surfaced as status codes plus a thread-local message.
+#include "mx_device.h"
 #include "mx_internal.h"
 
 namespace mxi {
@@ -296,6 +297,55 @@ extern "C" int mx_fill_uniform_u8(mx_ctx* ctx, void* dst, uint64_t bytes, uint64
 __global__ void copy_u8x16_kernel(uint4* __restrict__ dst, const uint4* __restrict__ src, uint64_t n16) {
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
+}
+
+// Streaming read at the best rate measured for a plain kernel on MI355X: workgroup g owns the bytes
+// [g * per, (g + 1) * per); wave w of 4 reads 4 KB steps w, w + 4, ... (four 1 KB loads, 16 bytes per
+// lane), three steps in flight, with non-temporal loads. Each wave writes the XOR of the 32-bit words
+// it read, so the launch cannot be elided and its coverage can be checked.
+constexpr int kReadWorkgroups = 4096;
+constexpr int kReadDepth = 3;
+
+__global__ __launch_bounds__(256) void read_ceiling_kernel(const uint8_t* __restrict__ src, uint64_t per,
+                                                           uint32_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint8_t* base = src + (uint64_t)blockIdx.x * per + 16 * lane;
+  const uint64_t steps = per / 4096;
+  uint32_t acc = 0;
+  uint64_t s0 = wave;
+  for (; s0 + 4 * (kReadDepth - 1) < steps; s0 += 4 * kReadDepth) {
+    uint4 v[kReadDepth][4];
+#pragma unroll
+    for (int s = 0; s < kReadDepth; ++s)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) v[s][t] = mxd::ldg128_nt(base + (s0 + 4 * s) * 4096 + t * 1024);
+#pragma unroll
+    for (int s = 0; s < kReadDepth; ++s)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc ^= v[s][t].x ^ v[s][t].y ^ v[s][t].z ^ v[s][t].w;
+  }
+  for (; s0 < steps; s0 += 4)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint4 v = mxd::ldg128_nt(base + s0 * 4096 + t * 1024);
+      acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, m, 64);
+  if (lane == 0) out[blockIdx.x * 4 + wave] = acc;
+}
+
+extern "C" int mx_read_kernel(mx_ctx* ctx, const void* src, uint64_t bytes, uint32_t* out, void* stream) {
+  if (int s = use(ctx)) return s;
+  MX_REQUIRE(src != nullptr && out != nullptr, "mx_read_kernel: null pointer");
+  const uint64_t unit = (uint64_t)kReadWorkgroups * 4096;
+  MX_REQUIRE(((uintptr_t)src & 15) == 0 && bytes > 0 && bytes % unit == 0,
+             "mx_read_kernel: 16-byte aligned source and a positive multiple of %llu bytes required",
+             (unsigned long long)unit);
+  hipLaunchKernelGGL(read_ceiling_kernel, dim3(kReadWorkgroups), dim3(256), 0, as_stream(stream),
+                     (const uint8_t*)src, bytes / kReadWorkgroups, out);
+  MX_LAUNCH_CHECK("read_ceiling_kernel");
+  return MX_OK;
 }
 
 extern "C" int mx_copy_kernel(mx_ctx* ctx, void* dst, const void* src, uint64_t bytes, void* stream) {
