@@ -321,23 +321,32 @@ __global__ void fp8_splitk_reduce_kernel(const float* __restrict__ partial, int 
 
 // ---- GEMM for many tokens ------------------------------------------------------------------------
 //
-// grid (ceil(N / 256), ceil(T / 128)), 512 threads = 8 waves. Wave w owns the 64-row group
-// 4 * blockIdx.x + (w % 4) and the token half w / 4 (64 tokens = 4 MFMA column tiles); it reads its A
-// operands straight from the tiled blob (1 KB contiguous per load; the two waves of a row group read the
-// same bytes in step, the second from L2). The workgroup's 128 tokens x 128 K of activation codes (and
-// their scales) are staged in LDS, double-buffered, and shared by the 8 waves. Each wave accumulates
-// 4 row tiles x 4 token tiles of 16 x 16 in registers; A for the next chunk is prefetched into a second
-// register set while the current chunk's 16 MFMAs run. The barriers order LDS only (mxd::lds_barrier),
-// so the prefetched loads stay in flight across them.
+// grid (ceil(N / 256), ceil(T / 128), K splits), 512 threads = 8 waves. Wave w owns the 64-row group
+// 4 * blockIdx.x + (w % 4) and the token half w / 4 (64 tokens = 4 MFMA column tiles), accumulating
+// 4 row tiles x 4 token tiles of 16 x 16. Every operand of a 128-wide K chunk reaches LDS by direct
+// global->LDS copies (no registers) into a 3-stage ring: the 4 row groups' weight chunks (32 KB, copied
+// 1 KB per wave instruction in the tiled blob's MFMA operand order, so both token halves read the
+// weights from LDS), the 128 tokens' activation codes (16 KB, block 2u + h holding at lane (q, n) the
+// bytes 64h + 16q.. of token 16u + n: the MFMA B operand of token tile u), the tokens' activation
+// scales and the row groups' weight scales. Each wave issues the same 8 copies per chunk, so a step
+// waits until only the next chunk's 8 are outstanding, meets the others at a bare barrier, starts the
+// copies of the chunk two ahead and multiplies. The loop has no compiler-visible global loads, so the
+// compiler adds no vmcnt waits that would drain the ring.
 constexpr int kGemmTok = 128;                 // tokens per workgroup
 constexpr int kGemmThreads = 512;
 constexpr int kWaveTiles = 4;                 // token tiles per wave
-constexpr int kLdsRow = 144;                  // 128 bytes of a token's K chunk + 16 bytes of bank padding
+constexpr int kGemmStages = 3;
+constexpr int kGemmCopies = 8;                // copies per wave and chunk: 4 weight, 2 activation, 2 scale
+constexpr int kGemmA = 32768;                 // stage layout: weights,
+constexpr int kGemmB = 16384;                 //   activation codes,
+constexpr int kGemmSA = 512;                  //   activation scales (4 bytes per token),
+constexpr int kGemmSW = 2048;                 //   weight scales (256 bytes per wave)
+constexpr int kGemmStage = kGemmA + kGemmB + kGemmSA + kGemmSW;
+static_assert(kGemmStages * kGemmStage <= 160 * 1024, "GEMM LDS ring");
 
 template <int kBlock>
 __global__ __launch_bounds__(kGemmThreads) void fp8_gemm_kernel(Fp8Args a) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds_b[2][kGemmTok * kLdsRow];
-  __shared__ uint32_t lds_s[2][kGemmTok];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kGemmStages * kGemmStage];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q = lane >> 4, n = lane & 15;
@@ -352,43 +361,34 @@ __global__ __launch_bounds__(kGemmThreads) void fp8_gemm_kernel(Fp8Args a) {
   const int u0 = (wave >> 2) * kWaveTiles;
   const int m0 = blockIdx.y * kGemmTok;
   const Fp8Blob off = fp8_blob(a.N, a.K, kBlock);
-  const uint8_t* wlane = a.blob + (size_t)g * chunks * 8192 + 16 * lane;
-  const uint8_t* slane = a.blob + off.scales + (size_t)g * chunks * 256 + 4 * lane;
-  const float* swrow = reinterpret_cast<const float*>(a.blob + off.scales) + (size_t)((64 * g) / 128) * chunks;
 
-  // staging: thread tid moves pieces tid and tid + 512 (token = piece / 8, 16-byte part = piece % 8)
-  const uint8_t* xsrc[2];
-  int ldst[2];
+  // this wave's copies: weight pieces 4 wave .. 4 wave + 3 (row group wave / 2, pieces 4 (wave % 2) ..),
+  // activation blocks 2 wave, 2 wave + 1 (token tile wave), the scales of tokens 16 wave .. 16 wave + 15,
+  // and its own row group's weight scales. Rows past N and tokens past T repeat valid ones.
+  const int ga = min(blockIdx.x * 4 + (wave >> 1), groups - 1);
+  const uint8_t* wsrc = a.blob + (size_t)ga * chunks * 8192 + (size_t)(4 * (wave & 1)) * 1024 + 16 * lane;
+  const int btok = min(m0 + 16 * wave + n, a.T - 1);
+  const uint8_t* bsrc = a.xq + (size_t)btok * a.K + 16 * q;
+  const int stok = min(m0 + 16 * wave + (lane & 15), a.T - 1);
+  const uint8_t* sasrc = kBlock == 32 ? (const uint8_t*)a.xs + (size_t)stok * (a.K / 32)
+                                      : (const uint8_t*)a.xs + (size_t)stok * chunks * 4;
+  const uint8_t* swsrc = kBlock == 32 ? a.blob + off.scales + (size_t)g * chunks * 256 + 4 * lane
+                                      : a.blob + off.scales + ((size_t)((64 * g) / 128) * chunks) * 4;
+  const uint32_t lds0 = mxd::lds_addr(lds);
+  auto copy = [&](int cl) {
+    const int c = c0 + min(cl, C - 1);   // past the end: repeats of the last chunk, so the count stays fixed
+    const uint32_t st = lds0 + (uint32_t)(cl % kGemmStages) * kGemmStage;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int p = tid + kGemmThreads * j, tok = p >> 3, part = p & 7;
-    const int tc = min(m0 + tok, a.T - 1);
-    xsrc[j] = a.xq + (size_t)tc * a.K + 16 * part;
-    ldst[j] = tok * kLdsRow + 16 * part;
-  }
-  const int stok = min(m0 + (tid & (kGemmTok - 1)), a.T - 1);
-
-  auto load_b = [&](int cl, uint4 (&bst)[2], uint32_t& sst) {
-    const int c = c0 + cl;
+    for (int i = 0; i < 4; ++i)
+      mxd::global_to_lds16(wsrc + (size_t)c * 8192 + i * 1024, __builtin_amdgcn_readfirstlane(st + (4 * wave + i) * 1024));
 #pragma unroll
-    for (int j = 0; j < 2; ++j) bst[j] = ldg128(xsrc[j] + (size_t)c * 128);
-    if constexpr (kBlock == 32) sst = ldg32((const uint8_t*)a.xs + (size_t)stok * (a.K / 32) + 4 * c);
-    else sst = __float_as_uint(ldgf((const float*)a.xs + (size_t)stok * chunks + c));
-  };
-  auto store_b = [&](int stage, const uint4 (&bst)[2], uint32_t sst) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) *reinterpret_cast<uint4*>(&lds_b[stage][ldst[j]]) = bst[j];
-    if (tid < kGemmTok) lds_s[stage][tid] = sst;
-  };
-  auto load_a = [&](int cl, uint4 (&am)[kTiles][2], uint32_t& sw) {
-    const int c = c0 + cl;
-#pragma unroll
-    for (int t = 0; t < kTiles; ++t) {
-      am[t][0] = ldg128(wlane + (size_t)c * 8192 + t * 2048);
-      am[t][1] = ldg128(wlane + (size_t)c * 8192 + t * 2048 + 1024);
-    }
-    if constexpr (kBlock == 32) sw = ldg32(slane + (size_t)c * 256);
-    else sw = __float_as_uint(ldgf(swrow + c));
+    for (int h = 0; h < 2; ++h)
+      mxd::global_to_lds16(bsrc + (size_t)c * 128 + 64 * h,
+                           __builtin_amdgcn_readfirstlane(st + kGemmA + (2 * wave + h) * 1024));
+    const uint32_t sa_lds = __builtin_amdgcn_readfirstlane(st + kGemmA + kGemmB + 64 * wave);
+    if (lane < 16) mxd::global_to_lds4(sasrc + (size_t)c * 4, sa_lds);
+    const uint32_t sw_lds = __builtin_amdgcn_readfirstlane(st + kGemmA + kGemmB + kGemmSA + 256 * wave);
+    if (kBlock == 32 || lane == 0) mxd::global_to_lds4(swsrc + (size_t)c * (kBlock == 32 ? 256 : 4), sw_lds);
   };
 
   v4f acc[kTiles][kWaveTiles];
@@ -397,58 +397,75 @@ __global__ __launch_bounds__(kGemmThreads) void fp8_gemm_kernel(Fp8Args a) {
 #pragma unroll
     for (int u = 0; u < kWaveTiles; ++u) acc[t][u] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int stage, const uint4 (&am)[kTiles][2], uint32_t sw) {
+  auto compute = [&](int cl) {
+    const uint8_t* st = lds + (cl % kGemmStages) * kGemmStage;
+    uint4 am[kTiles][2];
 #pragma unroll
-    for (int u = 0; u < kWaveTiles; ++u) {
-      const uint8_t* row = &lds_b[stage][(16 * (u0 + u) + n) * kLdsRow];
-      const uint4 b0 = *reinterpret_cast<const uint4*>(row + 16 * q);
-      const uint4 b1 = *reinterpret_cast<const uint4*>(row + 64 + 16 * q);
-      const uint32_t sx = lds_s[stage][16 * (u0 + u) + n];
-      if constexpr (kBlock == 32) {
-        const int sxb = (int)((sx >> (8 * q)) & 0xFF);
+    for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        am[t][h] = *reinterpret_cast<const uint4*>(st + (8 * (wave & 3) + 2 * t + h) * 1024 + 16 * lane);
+    const uint32_t swv = *reinterpret_cast<const uint32_t*>(st + kGemmA + kGemmB + kGemmSA + 256 * wave +
+                                                            (kBlock == 32 ? 4 * lane : 0));
+    uint4 b[kWaveTiles][2];
+    uint32_t sx[kWaveTiles];
+    auto read_b = [&](int u) {
+      const int tile = u0 + u;
+      b[u][0] = *reinterpret_cast<const uint4*>(st + kGemmA + (2 * tile) * 1024 + 16 * lane);
+      b[u][1] = *reinterpret_cast<const uint4*>(st + kGemmA + (2 * tile + 1) * 1024 + 16 * lane);
+      sx[u] = *reinterpret_cast<const uint32_t*>(st + kGemmA + kGemmB + 4 * (16 * tile + n));
+    };
+    if constexpr (kBlock == 32) {
+#pragma unroll
+      for (int u = 0; u < kWaveTiles; ++u) read_b(u);
+#pragma unroll
+      for (int u = 0; u < kWaveTiles; ++u) {
+        const int sxb = (int)((sx[u] >> (8 * q)) & 0xFF);
 #pragma unroll
         for (int t = 0; t < kTiles; ++t)
-          acc[t][u] = mfma_fp8_fp8(am[t][0], am[t][1], b0, b1, acc[t][u], (int)((sw >> (8 * t)) & 0xFF), sxb);
-      } else {
-        const float sa = __uint_as_float(sx), swf = __uint_as_float(sw);
+          acc[t][u] = mfma_fp8_fp8(am[t][0], am[t][1], b[u][0], b[u][1], acc[t][u], (int)((swv >> (8 * t)) & 0xFF),
+                                   sxb);
+      }
+    } else {
+      // Per chunk the MFMA gives the block dot d (unit scales) and acc += (d * sa) * sw follows in FP32. MFMA
+      // k + 1 is issued before the 12 FP32 operations that scale MFMA k, so they run while it executes;
+      // the scheduling fences keep the compiler from pairing each MFMA with its own scaling instead (which
+      // waits for every result). Token tile u + 2's operands are read from LDS while tile u multiplies.
+      const float swf = __uint_as_float(swv);
+      constexpr int kSteps = kTiles * kWaveTiles;
+      read_b(0);
+      read_b(1);
+      v4f d[2];
+      d[0] = mfma_fp8_fp8(am[0][0], am[0][1], b[0][0], b[0][1], v4f{0.f, 0.f, 0.f, 0.f}, 127, 127);
 #pragma unroll
-        for (int t = 0; t < kTiles; ++t) {
-          const v4f d = mfma_fp8_fp8(am[t][0], am[t][1], b0, b1, v4f{0.f, 0.f, 0.f, 0.f}, 127, 127);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[t][u][i] = acc[t][u][i] + (d[i] * sa) * swf;
+      for (int k = 0; k < kSteps; ++k) {
+        const int t = k % kTiles, u = k / kTiles;
+        if (t == 1 && u + 2 < kWaveTiles) read_b(u + 2);
+        if (k + 1 < kSteps) {
+          const int t1 = (k + 1) % kTiles, u1 = (k + 1) / kTiles;
+          d[(k + 1) & 1] = mfma_fp8_fp8(am[t1][0], am[t1][1], b[u1][0], b[u1][1], v4f{0.f, 0.f, 0.f, 0.f}, 127, 127);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        const float sa = __uint_as_float(sx[u]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[t][u][i] = acc[t][u][i] + (d[k & 1][i] * sa) * swf;
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
 
-  uint4 bst[2];
-  uint32_t sst = 0;
-  uint4 a0[kTiles][2], a1[kTiles][2];
-  uint32_t sw0 = 0, sw1 = 0;
-  load_b(0, bst, sst);
-  load_a(0, a0, sw0);
-  store_b(0, bst, sst);
-  mxd::lds_barrier();
-  // two chunks per iteration so the A register sets alternate with static indices
-  for (int c = 0; c < C; c += 2) {
-    const bool more1 = c + 1 < C;
-    if (more1) {
-      load_b(c + 1, bst, sst);
-      load_a(c + 1, a1, sw1);
-    }
-    compute(0, a0, sw0);
-    if (more1) store_b(1, bst, sst);
-    mxd::lds_barrier();
-    if (!more1) break;
-    const bool more2 = c + 2 < C;
-    if (more2) {
-      load_b(c + 2, bst, sst);
-      load_a(c + 2, a0, sw0);
-    }
-    compute(1, a1, sw1);
-    if (more2) store_b(0, bst, sst);
-    mxd::lds_barrier();
+#pragma unroll
+  for (int j = 0; j < kGemmStages - 1; ++j) copy(j);
+  for (int c = 0; c < C; ++c) {
+    // chunk c's copies are done once only chunk c + 1's are outstanding; the barrier waits for everyone's
+    // (and for everyone to have finished chunk c - 1, whose stage chunk c + 2 takes)
+    __builtin_amdgcn_s_waitcnt(mxd::vm_wait_imm(kGemmCopies * (kGemmStages - 2)));
+    mxd::copy_barrier();
+    copy(c + kGemmStages - 1);
+    compute(c);
   }
+  // every copy must land before the workgroup ends (its LDS may be handed to another workgroup)
+  __builtin_amdgcn_s_waitcnt(mxd::vm_wait_imm(0));
   if (!has_rows) return;
 #pragma unroll
   for (int u = 0; u < kWaveTiles; ++u) {

@@ -177,38 +177,11 @@ struct GemmArgs {
   uint16_t* out;                 // [T][k + 1][H] expert outputs (BF16), token-major (plan.row_dest)
 };
 
-// The s_waitcnt immediate that waits until at most n vector-memory operations of this wave are
-// outstanding (lgkm and export counts left at their maxima: no wait on them).
-constexpr int vm_wait_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-
-// Asynchronous copies from global memory into LDS of 16 (4) bytes per lane: lane l's bytes land at
-// lds + 16 l (4 l); lds is the wave-uniform LDS byte address. Counted by vmcnt like any other
-// vector-memory load. Inline assembly rather than the compiler builtin: for the builtin the compiler
-// treats every later wait on vmcnt as unordered (copies and register loads mixed) and widens it to
-// vmcnt(0), which drains the copies in flight at each weight-register use; with the copies invisible
-// to it, its waits for the weight loads are exact (and cover a few more copies than needed, as the
-// hardware counter also holds them). The caller orders its LDS reads after the copies with explicit
-// waits. One wait state between the M0 write and the copy.
-__device__ __forceinline__ void global_to_lds16(const void* src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds) : "m0");
-}
-__device__ __forceinline__ void global_to_lds4(const void* src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" : : "v"(src), "s"(lds) : "m0");
-}
-
-// Workgroup barrier for the global->LDS copy pipelines: the caller has already waited for its own copies
-// and LDS reads (s_waitcnt) as far as the barrier must cover. Even the local-only fences of lds_barrier
-// would wait for every copy in flight (the copies write LDS), so the barrier is issued bare; the empty
-// assembly statements with a memory clobber keep the compiler from moving memory operations across it.
-__device__ __forceinline__ void copy_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
+using mxd::copy_barrier;
+using mxd::global_to_lds16;
+using mxd::global_to_lds4;
+using mxd::lds_addr;
+using mxd::vm_wait_imm;
 
 // Two 16-token tiles' MFMA B operands (per tile two 16-byte reads 1 KB apart, the tiles' blocks being
 // consecutive) and their scale bytes (saddr: this lane's byte of tile u's scale words, +64 for u + 1),
