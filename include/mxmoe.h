@@ -9,6 +9,13 @@
  *
  * The reference binds CUDA probe kernels through ctypes (src/vesper/cuda.py);
  * each declaration below names the reference interface it replaces.
+ *
+ * A context keeps small reusable device buffers (scratch, and the arrival
+ * counters of split-K kernels, which are zero between launches), and a layer
+ * keeps its per-call buffers: calls on one context, or on one layer, must not
+ * run concurrently on different streams. Use one context per stream that runs
+ * alongside others, as the reference serialises calls per Device
+ * (src/vesper/connected.py:131-133).
  */
 #ifndef MXMOE_H
 #define MXMOE_H
