@@ -161,6 +161,54 @@ def test_exact_through_the_split_k_gemv(block, tokens):
             np.testing.assert_array_equal(got["output_bf16"], ref["output_bf16"], err_msg=f"call {call}")
 
 
+def project_both_ways(proj, ctx, name, bits, rows, width):
+    """One projection of BF16 `bits` with the activation codes and scales requested (the quantizer kernel
+    runs first) and without them (block 128 at <= 4 tokens: the GEMV quantizes in LDS). Returns
+    (trace, y) of each."""
+    tokens = bits.shape[0]
+    x = ctx.upload(bits)
+    q = ctx.empty((tokens, width), np.uint8)
+    s = ctx.empty((tokens, width // 128), np.float32)
+    outs = []
+    try:
+        for with_codes in (True, False):
+            trace = ctx.empty((tokens, rows), np.float32)
+            y = ctx.empty((tokens, rows), np.uint16)
+            proj.project_device(name, x.ptr, tokens, y.ptr, trace_ptr=trace, q_ptr=q if with_codes else None,
+                                s_ptr=s if with_codes else None)
+            outs.append((trace.download(), y.download()))
+            trace.free()
+            y.free()
+    finally:
+        for d in (x, q, s):
+            d.free()
+    return outs
+
+
+@pytest.mark.parametrize("tokens", [1, 3, 4])
+@pytest.mark.parametrize("rows,width", [(256, 1024), (128, 2048), (576, 7168)])
+def test_gemv_quantizing_in_lds_equals_the_quantizer_path(gpu_ctx, tokens, rows, width):
+    """Block 128 at <= 4 tokens without requested codes: the GEMV quantizes its own K range with the
+    quantizer kernel's arithmetic, so FP32 sums and BF16 outputs equal the two-launch path bit for bit
+    (random inputs), and the oracle's exactly on representable inputs."""
+    rng = np.random.default_rng(tokens * 1000 + rows + width)
+    w, sw = fp8_weights(rng, rows, width, 128)
+    arrays = {"layers.0.attn.p.weight": w, "layers.0.attn.p.scale": sw}
+    with NativeProjections(arrays, block=128, layout={"p": (rows, width)}) as proj:
+        bits = bf16_bits(rng.standard_normal((tokens, width)).astype(np.float32))
+        (t_q, y_q), (t_f, y_f) = project_both_ways(proj, gpu_ctx, "p", bits, rows, width)
+        np.testing.assert_array_equal(t_f.view(np.uint32), t_q.view(np.uint32))
+        np.testing.assert_array_equal(y_f, y_q)
+    w, sw, x = exact_case(128, tokens, rows, width, 2, 4, 7 * tokens + rows)   # sums below 2^24 units of 2^-8
+    arrays = {"layers.0.attn.p.weight": w, "layers.0.attn.p.scale": sw}
+    with NativeProjections(arrays, block=128, layout={"p": (rows, width)}) as proj:
+        bits = bf16_bits(x)
+        ref = fp8_projection(bf16_values(bits), w, sw, 128)
+        (_, _), (t_f, y_f) = project_both_ways(proj, gpu_ctx, "p", bits, rows, width)
+        np.testing.assert_array_equal(t_f.view(np.uint32), ref["output_fp32"].view(np.uint32))
+        np.testing.assert_array_equal(y_f, ref["output_bf16"])
+
+
 def check_exact(block, w, sw, x):
     bits = bf16_bits(x)
     got = run_projection(block, w, sw, bits)

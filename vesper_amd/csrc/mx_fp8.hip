@@ -140,7 +140,16 @@ struct Fp8Args {
   float* partial;      // split K: [splits][T][N] FP32 partial sums (the GEMV writes these instead of y)
   uint32_t* tickets;   // split-K GEMV: arrival counter per (row group, token tile), zero between launches;
                        // null = partial sums only, added by fp8_splitk_reduce_kernel
+  const uint16_t* x;   // fused GEMV (block 128, few tokens): the BF16 input [T][K], quantized in the kernel
 };
+
+// Fused per-128 quantization in the GEMV (block 128, up to kFusedMaxTokens tokens, up to kFusedChunks K
+// chunks per workgroup): each workgroup quantizes its own chunks of its tokens into LDS, [chunk][token]
+// rows of 128 codes + 16 bytes of padding, with act_quant128_v8_kernel's arithmetic, and the MFMAs read
+// the B operand and the activation scale from there. Saves the quantizer launch for decode-size calls.
+constexpr int kFusedMaxTokens = 4;
+constexpr int kFusedChunks = 8;
+constexpr int kFusedRow = 144;
 
 template <int kBlock>
 struct Fp8Chunk {
@@ -148,9 +157,10 @@ struct Fp8Chunk {
   uint4 b0, b1;
   uint32_t sw;   // block 32: scale word (byte t = tile t); block 128: FP32 bits of the weight block scale
   uint32_t sx;   // block 32: 4 activation E8M0 codes of the chunk; block 128: FP32 bits of the act scale
+  int c;         // the chunk (fused: its activations are read from LDS at the MFMA)
 };
 
-template <int kBlock>
+template <int kBlock, bool kFused>
 __device__ __forceinline__ void fp8_load(Fp8Chunk<kBlock>& r, const Fp8Args& a, const uint8_t* wlane,
                                          const uint8_t* slane, const float* swrow, const uint8_t* xrow, int tok,
                                          int c, int q) {
@@ -158,6 +168,11 @@ __device__ __forceinline__ void fp8_load(Fp8Chunk<kBlock>& r, const Fp8Args& a, 
   for (int t = 0; t < kTiles; ++t) {
     r.a[t][0] = ldg128(wlane + (size_t)c * 8192 + t * 2048);
     r.a[t][1] = ldg128(wlane + (size_t)c * 8192 + t * 2048 + 1024);
+  }
+  r.c = c;
+  if constexpr (kFused) {
+    r.sw = __float_as_uint(ldgf(swrow + c));
+    return;
   }
   r.b0 = ldg128(xrow + (size_t)c * 128 + 16 * q);
   r.b1 = ldg128(xrow + (size_t)c * 128 + 64 + 16 * q);
@@ -170,8 +185,17 @@ __device__ __forceinline__ void fp8_load(Fp8Chunk<kBlock>& r, const Fp8Args& a, 
   }
 }
 
-template <int kBlock>
-__device__ __forceinline__ void fp8_mma(const Fp8Chunk<kBlock>& r, v4f (&acc)[kTiles], int q, uint32_t keep) {
+// qrow: fused, this lane's token row of the workgroup's quantized activations in LDS (chunk cb at offset 0),
+// qs its scale column; unused otherwise.
+template <int kBlock, bool kFused>
+__device__ __forceinline__ void fp8_mma(Fp8Chunk<kBlock> r, v4f (&acc)[kTiles], int q, uint32_t keep,
+                                        const uint8_t* qrow, const float* qs, int cb) {
+  if constexpr (kFused) {
+    const uint8_t* row = qrow + (size_t)(r.c - cb) * kTok * kFusedRow;
+    r.b0 = *reinterpret_cast<const uint4*>(row + 16 * q);
+    r.b1 = *reinterpret_cast<const uint4*>(row + 64 + 16 * q);
+    r.sx = __float_as_uint(qs[(r.c - cb) * kTok]);
+  }
   const uint4 b0 = make_uint4(r.b0.x & keep, r.b0.y & keep, r.b0.z & keep, r.b0.w & keep);
   const uint4 b1 = make_uint4(r.b1.x & keep, r.b1.y & keep, r.b1.z & keep, r.b1.w & keep);
   if constexpr (kBlock == 32) {
@@ -196,7 +220,7 @@ __device__ __forceinline__ void fp8_mma(const Fp8Chunk<kBlock>& r, v4f (&acc)[kT
 // when K is not split, else its FP32 partial sums. With K split and a.tickets set, the last workgroup of
 // the (row group, token tile) to arrive adds the partial sums in split order (fp8_splitk_reduce_kernel's
 // arithmetic) and writes the outputs; without tickets fp8_splitk_reduce_kernel does it.
-template <int kBlock>
+template <int kBlock, bool kFused>
 __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
   constexpr int P = 2;
   const int g = blockIdx.x;
@@ -219,21 +243,72 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
   const int cb = (C * z) / S, cw = (C * (z + 1)) / S - cb;   // this workgroup's chunk range
   const int c0 = cb + (cw * wave) / 4;
   const int cn = cb + (cw * (wave + 1)) / 4 - c0;
-  if (cn > 0) {
-    const uint32_t keep = live ? 0xFFFFFFFFu : 0u;
-    Fp8Chunk<kBlock> buf[P];
+  // fused: this workgroup's quantized activations, [chunk][token] rows (tokens past T read token ntok - 1's
+  // row: finite scale, codes masked at the MFMA)
+  __shared__ __attribute__((aligned(16))) uint8_t qx[kFused ? kFusedChunks * kTok * kFusedRow : 16];
+  __shared__ float qsc[kFused ? kFusedChunks * kTok : 1];
+  const int ntok = min(kTok, a.T - (int)blockIdx.y * kTok);
+  const int nq = min(n, ntok - 1);
+  const int sub = tid & 15, grp = tid >> 4;
+  uint4 xv[kFusedMaxTokens];
+  if constexpr (kFused) {
+    // block bi = grp + 16 j: token bi / cw, chunk cb + bi % cw; 16 lanes of 8 values each
 #pragma unroll
-    for (int j = 0; j < P; ++j) fp8_load(buf[j], a, wlane, slane, swrow, xrow, rtok, c0 + min(j, cn - 1), q);
+    for (int j = 0; j < kFusedMaxTokens; ++j) {
+      const int bi = grp + 16 * j;
+      xv[j] = bi < ntok * cw
+                  ? ldg128(reinterpret_cast<const uint8_t*>(a.x + (size_t)(blockIdx.y * kTok + bi / cw) * a.K +
+                                                            (size_t)(cb + bi % cw) * 128 + 8 * sub))
+                  : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  const uint32_t keep = live ? 0xFFFFFFFFu : 0u;
+  Fp8Chunk<kBlock> buf[P];
+  if (cn > 0) {
+#pragma unroll
+    for (int j = 0; j < P; ++j)
+      fp8_load<kBlock, kFused>(buf[j], a, wlane, slane, swrow, xrow, rtok, c0 + min(j, cn - 1), q);
+  }
+  if constexpr (kFused) {
+#pragma unroll
+    for (int j = 0; j < kFusedMaxTokens; ++j) {
+      const int bi = grp + 16 * j;
+      if (bi < ntok * cw) {   // uniform over the 16 lanes of a block
+        const uint32_t w[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+        float v[8];
+        float amax = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[2 * i] = mx::bf16_value(w[i] & 0xFFFFu);
+          v[2 * i + 1] = mx::bf16_value(w[i] >> 16);
+          amax = fmaxf(amax, fmaxf(fabsf(v[2 * i]), fabsf(v[2 * i + 1])));
+        }
+#pragma unroll
+        for (int m = 8; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+        const float sc = mx::act128_scale(amax);
+        uint2 codes;
+        codes.x = mxd::e4m3x4(v[0] / sc, v[1] / sc, v[2] / sc, v[3] / sc);
+        codes.y = mxd::e4m3x4(v[4] / sc, v[5] / sc, v[6] / sc, v[7] / sc);
+        const int slot = (bi % cw) * kTok + bi / cw;
+        *reinterpret_cast<uint2*>(qx + slot * kFusedRow + 8 * sub) = codes;
+        if (sub == 0) qsc[slot] = sc;
+      }
+    }
+    mxd::lds_barrier();   // LDS only: the weight loads above stay in flight
+  }
+  if (cn > 0) {
+    const uint8_t* qrow = qx + nq * kFusedRow;
+    const float* qs = qsc + nq;
     int i = 0;
     for (; i + P < cn; i += P) {
 #pragma unroll
       for (int j = 0; j < P; ++j) {
-        fp8_mma(buf[j], acc, q, keep);
-        fp8_load(buf[j], a, wlane, slane, swrow, xrow, rtok, c0 + min(i + j + P, cn - 1), q);
+        fp8_mma<kBlock, kFused>(buf[j], acc, q, keep, qrow, qs, cb);
+        fp8_load<kBlock, kFused>(buf[j], a, wlane, slane, swrow, xrow, rtok, c0 + min(i + j + P, cn - 1), q);
       }
     }
 #pragma unroll
-    for (int j = 0; j < P; ++j) fp8_mma(buf[j], acc, q, i + j < cn ? keep : 0u);
+    for (int j = 0; j < P; ++j) fp8_mma<kBlock, kFused>(buf[j], acc, q, i + j < cn ? keep : 0u, qrow, qs, cb);
   }
   __shared__ float red[4][kTiles][64][4];
 #pragma unroll
@@ -508,12 +583,22 @@ int fp8_splits(int N, int K, int T) {
   return std::max(1, std::min({16, (K / 128) / 4, (1024 + base_wgs - 1) / base_wgs}));
 }
 
+// Whether the block-128 GEMV can quantize its own activations: few tokens, and every workgroup's K range
+// (ceil(chunks / splits)) within its LDS buffer.
+bool fp8_fused_ok(int N, int K, int T, int block) {
+  if (block != 128 || T > kFusedMaxTokens || T > kGemvMaxTokens) return false;
+  const int chunks = K / 128, splits = fp8_splits(N, K, T);
+  return (chunks + splits - 1) / splits <= kFusedChunks;
+}
+
 // The product on quantized activations: GEMV (T <= 32) or the tiled GEMM, either with its K split over
 // fp8_splits(N, K, T) workgroups whose FP32 partial sums go to `partial` (fp8_splits * T * N floats) and
 // are added in split order: by the GEMV's last workgroup per tile (`tickets`, the context's arrival
 // counters) or by fp8_splitk_reduce_kernel.
+// x_fused: the BF16 input when the GEMV quantizes it itself (fp8_fused_ok), else null (q and sc given).
 int launch_fp8_product(const uint8_t* blob, int N, int K, int block, const uint8_t* q, const void* sc, int T,
-                       uint16_t* y, float* trace, float* partial, uint32_t* tickets, hipStream_t st) {
+                       uint16_t* y, float* trace, float* partial, uint32_t* tickets, hipStream_t st,
+                       const uint16_t* x_fused = nullptr) {
   Fp8Args a{};
   a.blob = blob;
   a.N = N;
@@ -524,14 +609,17 @@ int launch_fp8_product(const uint8_t* blob, int N, int K, int block, const uint8
   a.y = y;
   a.trace = trace;
   a.partial = partial;
+  a.x = x_fused;
+  if (x_fused) a.xq = reinterpret_cast<const uint8_t*>(x_fused);   // not read: B comes from LDS
   if (T <= kGemvMaxTokens) {
     const int splits = fp8_splits(N, K, T);
     const dim3 grid(N / 64, (T + kTok - 1) / kTok, splits);
     if (splits > 1 && (size_t)grid.x * grid.y <= MX_TICKETS &&
         (uint64_t)splits * T * N * sizeof(float) <= kTicketPartialBytes)
       a.tickets = tickets;
-    if (block == 32) hipLaunchKernelGGL(fp8_gemv_kernel<32>, grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL(fp8_gemv_kernel<128>, grid, dim3(256), 0, st, a);
+    if (block == 32) hipLaunchKernelGGL((fp8_gemv_kernel<32, false>), grid, dim3(256), 0, st, a);
+    else if (x_fused) hipLaunchKernelGGL((fp8_gemv_kernel<128, true>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((fp8_gemv_kernel<128, false>), grid, dim3(256), 0, st, a);
     MX_LAUNCH_CHECK("fp8_gemv_kernel");
     if (splits > 1 && !a.tickets) {
       const int64_t count = (int64_t)T * N;
@@ -632,13 +720,16 @@ int mx_fp8_projection(mx_ctx* ctx, const void* tiled, int32_t N, int32_t K, int3
   uint8_t* q = q_out ? q_out : (uint8_t*)base;
   void* sc = s_out ? s_out : (void*)((uint8_t*)base + q_b);
   MX_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)sc & 3) == 0, "mx_fp8_projection: q 16-byte, s 4-byte aligned");
+  float* partial = (float*)((uint8_t*)base + q_b + s_b);
+  if (!q_out && !s_out && fp8_fused_ok(N, K, T, block))   // the GEMV quantizes x itself
+    return launch_fp8_product((const uint8_t*)tiled, N, K, block, nullptr, nullptr, T, y, trace, partial,
+                              ctx->tickets, st, x);
   if (block == 32) {
     if (int s = mx_act_quant32(ctx, x, q, (uint8_t*)sc, T, K, stream)) return s;
   } else {
     if (int s = mx_act_quant128(ctx, x, q, (float*)sc, T, K, stream)) return s;
   }
-  return launch_fp8_product((const uint8_t*)tiled, N, K, block, q, sc, T, y, trace,
-                            (float*)((uint8_t*)base + q_b + s_b), ctx->tickets, st);
+  return launch_fp8_product((const uint8_t*)tiled, N, K, block, q, sc, T, y, trace, partial, ctx->tickets, st);
 }
 
 int mx_fp8_expert_forward(mx_ctx* ctx, const void* w1, const void* w3, const void* w2, int32_t H, int32_t I,
