@@ -146,7 +146,8 @@ struct Fp8Args {
 // Fused per-128 quantization in the GEMV (block 128, up to kFusedMaxTokens tokens, up to kFusedChunks K
 // chunks per workgroup): each workgroup quantizes its own chunks of its tokens into LDS, [chunk][token]
 // rows of 128 codes + 16 bytes of padding, with act_quant128_v8_kernel's arithmetic, and the MFMAs read
-// the B operand and the activation scale from there. Saves the quantizer launch for decode-size calls.
+// the B operand and the activation scale from there. Saves the quantizer launch for decode-size calls;
+// at 16 tokens the repeated quantization in every workgroup costs more than the launch (measured).
 constexpr int kFusedMaxTokens = 4;
 constexpr int kFusedChunks = 8;
 constexpr int kFusedRow = 144;
