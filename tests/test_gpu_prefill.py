@@ -137,6 +137,33 @@ def test_prefill_baseline_shapes_sampled_tokens(gpu_ctx):
         bank.free()
 
 
+def test_prefill_reference_shapes_sampled_tokens(gpu_ctx):
+    """The reference model's shapes (384 experts x (5120 x 2304), top-6, clamp 10, shared expert): K runs
+    of 40 and 18 chunks (not multiples of the weight ring's depth), 9 gate/up and 10 down row blocks;
+    Zipf routing over 600 tokens, four tokens against the oracle."""
+    from vesper_amd.config import REFERENCE as cfg
+    rng = np.random.default_rng(5120)
+    bank = ExpertBank(gpu_ctx, cfg, cfg.experts + 1)
+    bank.fill_synthetic(seed=11)
+    w = router_weight(rng, cfg.experts, cfg.hidden)
+    layer = MoELayer(gpu_ctx, cfg, w, bank)
+    try:
+        T = 600
+        x = activations(rng, T, cfg.hidden)
+        ids, wts = zipf_routing(rng, T, cfg.experts, cfg.top_k)
+        assert np.bincount(ids.ravel()).max() > 128                # a multi-tile expert
+        got = layer.prefill(x, ids, wts)
+        sample = np.array([0, 233, 417, T - 1])
+        needed = sorted({int(e) for e in ids[sample].ravel()})
+        experts = {e: bank.download(e) for e in needed}
+        ref = moe_layer_routed(x, ids, wts, experts, bank.download(cfg.experts), num_experts=cfg.experts,
+                               swiglu_limit=cfg.swiglu_limit, tokens=sample)
+        assert_close(got[sample], ref["output_bf16"], "prefill reference shapes")
+    finally:
+        layer.close()
+        bank.free()
+
+
 def test_prefill_refuses_bad_routing(gpu_ctx):
     cfg = MoEConfig(hidden=512, intermediate=256, experts=16, top_k=2, shared=None, max_tokens=16)
     rng = np.random.default_rng(3)
