@@ -59,6 +59,53 @@ def test_postprocess_matches_oracle_bit_exactly(score_func, experts, k, scale):
     assert [bool(v) for v in got["tied"]] == [tie_flag(ref["selection"][t], k) for t in range(40)]
 
 
+def test_untied_and_edge_selections_against_the_oracle():
+    """Untied selections are ranked by the threshold rounds themselves; a zero among the winners (where
+    +0 and -0 are distinct keys but equal floats, so the sorting network decides their order), ties,
+    negative values, subnormals and winners one ULP apart are covered too: indices, weights and the tie
+    flag bit-exact against the oracle in every case."""
+    from oracle.router import route_weights, topk_indices
+    rng = np.random.default_rng(3131)
+    k, scale = 8, 2.5
+    rows = []
+    for case in range(12):
+        sel = rng.standard_normal(256).astype(np.float32)
+        if case in (1, 2, 3):
+            sel = -np.abs(sel)
+            lo, hi = (4, 9) if case != 2 else (9, 4)
+            sel[lo] = np.float32(0.0)              # +0 and -0 both win; by key +0 ranks first
+            sel[hi] = np.float32(-0.0)
+            if case == 3:
+                sel[hi] = sel[lo]                  # a single zero among the winners
+        elif case == 4:
+            sel = -np.abs(sel)                     # all negative
+        elif case == 5:
+            sel = (sel * np.float32(1e-39)).astype(np.float32)    # subnormals of both signs
+        elif case == 6:
+            top = np.argsort(sel)[::-1][:9]
+            v = np.float32(0.75)
+            for e in top:                          # nine winners one ULP apart, descending by ID order
+                sel[e] = v
+                v = np.nextafter(v, np.float32(0.0), dtype=np.float32)
+        elif case == 7:
+            top = np.argsort(sel)[::-1]
+            sel[top[8]] = sel[top[7]]              # the k-th value shared with an unselected expert
+        elif case == 8:
+            top = np.argsort(sel)[::-1]
+            sel[top[3]] = sel[top[1]]              # a tie inside the winners
+        rows.append(sel)
+    selection = np.stack(rows)
+    scores = rng.uniform(0.01, 1.0, selection.shape).astype(np.float32)
+    with RouterProbe(experts=256, top_k=k, score_func="sigmoid", route_scale=scale) as probe:
+        got = probe.inspect_selection(scores, selection)
+    for row in range(len(rows)):
+        ids = topk_indices(selection[row], k)
+        _, _, weights = route_weights(scores[row], ids, scale)
+        assert got["indices"][row].tolist() == ids.tolist(), row
+        np.testing.assert_array_equal(got["weights"][row].view(np.uint32), weights.view(np.uint32), err_msg=str(row))
+        assert bool(got["tied"][row]) == tie_flag(selection[row], k), row
+
+
 def test_gate_projection_matches_float64_oracle():
     rng = np.random.default_rng(9)
     w = router_weight(rng, 256, 7168)

@@ -62,6 +62,10 @@ __device__ __forceinline__ uint32_t ordered_key(float v) {
   return b ^ ((b & 0x80000000u) ? 0xFFFFFFFFu : 0x80000000u);
 }
 
+// ordered_key of +0, -0, +inf and -inf
+constexpr uint32_t kKeyPosZero = 0x80000000u, kKeyNegZero = 0x7FFFFFFFu, kKeyPosInf = 0xFF800000u,
+                   kKeyNegInf = 0x007FFFFFu;
+
 // FP32 score of one logit: exp/log1p in float64 rounded once to FP32 (the oracle does the same).
 __device__ __forceinline__ float score_of(float z, int score_func) {
   if (score_func == MX_SCORE_SIGMOID) {
@@ -174,10 +178,16 @@ __device__ void topk_token_wave_t(const float* __restrict__ selection, const flo
     scr[j] = ok ? scores[e] : 0.f;
     key[j] = ok ? ordered_key(sel[j]) : 0u;
   }
-  // 1. threshold search
+  // 1. threshold search. Each round finds the next distinct key and how many experts hold it: lanes
+  //    holding at least 1, 2, ... kPer of their keys at that value, counted by ballots.
   uint64_t bound = 1ull << 32;   // exclusive upper bound on keys still to rank
   int taken = 0, tied = 0;
   uint32_t thr = 0;
+  // While every round finds exactly one expert at a nonzero, non-NaN value, the rounds themselves are
+  // the selection in descending order (float order equals key order there), which is what the sorting
+  // network below produces for distinct values; lane r keeps round r's expert.
+  bool distinct = true;
+  int32_t round_id = 0;
   for (int round = 0; round < k; ++round) {
     uint32_t m = 0;
     bool any = false;
@@ -188,72 +198,92 @@ __device__ void topk_token_wave_t(const float* __restrict__ selection, const flo
     }
     // lanes without a candidate contribute key 0; a real key 0 (-NaN pattern) is excluded upstream
     const uint32_t best = wave_max_u(any ? m : 0u);
-    int c = 0;
+    int cj = 0, jhit = 0;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
       const int e = lane * per + j;
-      c += (e < E && key[j] == best) ? 1 : 0;
+      if (e < E && key[j] == best) {
+        ++cj;
+        jhit = j;
+      }
     }
-    c = wave_sum_i(c);
+    const uint64_t holders = __ballot(cj >= 1);
+    int c = __popcll(holders);
+#pragma unroll
+    for (int mm = 2; mm <= kPer; ++mm) c += __popcll(__ballot(cj >= mm));
     tied |= c >= 2;
     taken += c;
     thr = best;
+    const int hit = holders ? __builtin_ctzll(holders) : 0;
+    const int32_t id = hit * per + __builtin_amdgcn_readlane(jhit, hit);
+    distinct = distinct && c == 1 && best != kKeyPosZero && best != kKeyNegZero && best <= kKeyPosInf &&
+               best >= kKeyNegInf;
+    if (lane == round) round_id = id;
     if (taken >= k) break;
     bound = best;
   }
-  // 2. gather by ascending ID: lane-major then j (experts are laid out contiguously per lane)
-  int n_gt = 0, n_eq = 0;
+  const int slot = lane & 31;
+  float kv;
+  int32_t iv;
+  int vv;
+  if (distinct) {
+    kv = 0.f;
+    iv = round_id;
+    vv = slot < k;
+  } else {
+    // 2. gather by ascending ID: lane-major then j (experts are laid out contiguously per lane)
+    int n_gt = 0, n_eq = 0;
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int e = lane * per + j;
-    if (e < E) {
-      n_gt += key[j] > thr;
-      n_eq += key[j] == thr;
-    }
-  }
-  const int inc_gt = wave_scan_i(n_gt, lane);
-  const int inc_eq = wave_scan_i(n_eq, lane);
-  const int total_gt = __builtin_amdgcn_readlane(inc_gt, 63);
-  int pos_gt = inc_gt - n_gt, pos_eq = total_gt + inc_eq - n_eq;
-  __shared__ float s_key[kRouteWaves][32];
-  __shared__ int32_t s_id[kRouteWaves][32];
-  const int wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int e = lane * per + j;
-    if (e < E) {
-      if (key[j] > thr) {
-        if (pos_gt < k) { s_key[wave][pos_gt] = sel[j]; s_id[wave][pos_gt] = e; }
-        ++pos_gt;
-      } else if (key[j] == thr) {
-        if (pos_eq < k) { s_key[wave][pos_eq] = sel[j]; s_id[wave][pos_eq] = e; }
-        ++pos_eq;
+    for (int j = 0; j < kPer; ++j) {
+      const int e = lane * per + j;
+      if (e < E) {
+        n_gt += key[j] > thr;
+        n_eq += key[j] == thr;
       }
     }
+    const int inc_gt = wave_scan_i(n_gt, lane);
+    const int inc_eq = wave_scan_i(n_eq, lane);
+    const int total_gt = __builtin_amdgcn_readlane(inc_gt, 63);
+    int pos_gt = inc_gt - n_gt, pos_eq = total_gt + inc_eq - n_eq;
+    __shared__ float s_key[kRouteWaves][32];
+    __shared__ int32_t s_id[kRouteWaves][32];
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int e = lane * per + j;
+      if (e < E) {
+        if (key[j] > thr) {
+          if (pos_gt < k) { s_key[wave][pos_gt] = sel[j]; s_id[wave][pos_gt] = e; }
+          ++pos_gt;
+        } else if (key[j] == thr) {
+          if (pos_eq < k) { s_key[wave][pos_eq] = sel[j]; s_id[wave][pos_eq] = e; }
+          ++pos_eq;
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // 3. bitonic network on lanes 0..31 (lanes 32..63 mirror them and are ignored)
+    kv = slot < k ? s_key[wave][slot] : 0.f;
+    iv = slot < k ? s_id[wave][slot] : 0;
+    vv = slot < k;
+    bitonic_stage<2, 1>(kv, iv, vv, slot);
+    bitonic_stage<4, 2>(kv, iv, vv, slot);
+    bitonic_stage<4, 1>(kv, iv, vv, slot);
+    bitonic_stage<8, 4>(kv, iv, vv, slot);
+    bitonic_stage<8, 2>(kv, iv, vv, slot);
+    bitonic_stage<8, 1>(kv, iv, vv, slot);
+    bitonic_stage<16, 8>(kv, iv, vv, slot);
+    bitonic_stage<16, 4>(kv, iv, vv, slot);
+    bitonic_stage<16, 2>(kv, iv, vv, slot);
+    bitonic_stage<16, 1>(kv, iv, vv, slot);
+    bitonic_stage<32, 16>(kv, iv, vv, slot);
+    bitonic_stage<32, 8>(kv, iv, vv, slot);
+    bitonic_stage<32, 4>(kv, iv, vv, slot);
+    bitonic_stage<32, 2>(kv, iv, vv, slot);
+    bitonic_stage<32, 1>(kv, iv, vv, slot);
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  // 3. bitonic network on lanes 0..31 (lanes 32..63 mirror them and are ignored)
-  const int slot = lane & 31;
-  float kv = slot < k ? s_key[wave][slot] : 0.f;
-  int32_t iv = slot < k ? s_id[wave][slot] : 0;
-  int vv = slot < k;
-  bitonic_stage<2, 1>(kv, iv, vv, slot);
-  bitonic_stage<4, 2>(kv, iv, vv, slot);
-  bitonic_stage<4, 1>(kv, iv, vv, slot);
-  bitonic_stage<8, 4>(kv, iv, vv, slot);
-  bitonic_stage<8, 2>(kv, iv, vv, slot);
-  bitonic_stage<8, 1>(kv, iv, vv, slot);
-  bitonic_stage<16, 8>(kv, iv, vv, slot);
-  bitonic_stage<16, 4>(kv, iv, vv, slot);
-  bitonic_stage<16, 2>(kv, iv, vv, slot);
-  bitonic_stage<16, 1>(kv, iv, vv, slot);
-  bitonic_stage<32, 16>(kv, iv, vv, slot);
-  bitonic_stage<32, 8>(kv, iv, vv, slot);
-  bitonic_stage<32, 4>(kv, iv, vv, slot);
-  bitonic_stage<32, 2>(kv, iv, vv, slot);
-  bitonic_stage<32, 1>(kv, iv, vv, slot);
   // 4. raw scores, tree denominator, weights
   // expert iv's raw score lives in lane iv / kPer, register iv % kPer
   float raw = 0.f;
@@ -831,6 +861,54 @@ __device__ __forceinline__ v4f reduce_tiles(const v4f (&acc)[kTiles], int wave, 
   return out;
 }
 
+// SwiGLU epilogue of gate/up tile t of row group g once its 4 partial tiles are summed: in `mine`, lanes
+// with q < 2 hold W1 rows 4q + i of the tile (D[4q + i][n]) and lane + 32 the matching W3 rows. Writes
+// the down input of token column n to s_din[n][8t + 4q + i] (and the diagnostic copies when requested).
+__device__ __forceinline__ void gateup_tile_epilogue(const ExpertArgs& a, int s, int g, int t, const v4f& mine,
+                                                     int q, int n, int ntok, float (*s_din)[32]) {
+  const Plan* __restrict__ plan = a.plan;
+  float upv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) upv[i] = __shfl_xor(mine[i], 32, 64);
+  if (q < 2 && n < ntok) {
+    const int row0 = plan->slot_row0[s];
+    const bool weighted = plan->slot_weighted[s] != 0;
+    const float rw = plan->slot_w[s][n];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int li = t * 8 + 4 * q + i;           // row within the 32-row block
+      const int gi = g * 32 + li;                 // intermediate index
+      const uint32_t b1 = mx::bf16_bits(mine[i]);
+      const uint32_t b3 = mx::bf16_bits(upv[i]);
+      const size_t o2 = (size_t)(row0 + n) * a.I + gi;
+      const float din = mxd::swiglu_element(b1, b3, a.limit, weighted, rw, a.trace ? a.trace + o2 * 5 : nullptr);
+      s_din[n][li] = din;
+      if (a.w1) a.w1[o2] = (uint16_t)b1;
+      if (a.w3) a.w3[o2] = (uint16_t)b3;
+      if (a.din) a.din[o2] = (uint16_t)mx::bf16_bits(din);
+    }
+  }
+}
+
+// Per-token quantization of row group g's 32-row block of the down input (one E8M0 block per token):
+// 16 consecutive threads j2 = 0..15 take token tn, 2 values each.
+__device__ __forceinline__ void gateup_quantize_block(const ExpertArgs& a, int s, int g, int tn, int j2, int ntok,
+                                                      const float (*s_din)[32]) {
+  if (tn >= ntok) return;
+  const int I = a.I;
+  const float v0 = s_din[tn][2 * j2], v1 = s_din[tn][2 * j2 + 1];
+  float amax = fmaxf(fabsf(v0), fabsf(v1));
+#pragma unroll
+  for (int mm = 8; mm >= 1; mm >>= 1) amax = fmaxf(amax, __shfl_xor(amax, mm, 16));
+  amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
+  const uint32_t code = mx::act_scale_code(amax);
+  const float sc = mx::e8m0_value(code);
+  const uint32_t q0 = mx::act_quant_value(v0, sc), q1 = mx::act_quant_value(v1, sc);
+  const size_t r = (size_t)(a.plan->slot_row0[s] + tn);
+  *reinterpret_cast<uint16_t*>(a.dq + r * I + g * 32 + 2 * j2) = (uint16_t)(q0 | (q1 << 8));
+  if (j2 == 0) a.ds[r * (I / 32) + g] = (uint8_t)code;
+}
+
 // grid (I/32, slots), 256 threads. The workgroup computes intermediate rows [32g, 32g + 32) of W1 and
 // W3 for the slot's tokens: tile t holds W1 rows 32g + 8t + (0..7) as MFMA rows 0-7 and the same W3
 // rows as MFMA rows 8-15. After the cross-wave sum, wave t owns tile t, applies the SwiGLU epilogue,
@@ -876,44 +954,9 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
   __shared__ float red[4][kTiles][64][4];
   __shared__ float s_din[kMaxTokens][32];
   const v4f mine = reduce_tiles(acc, wave, lane, red);
-  // D[4q + i][n] of tile `wave`: lanes q < 2 hold W1 rows 4q+i; lane + 32 holds the matching W3 rows.
-  float upv[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) upv[i] = __shfl_xor(mine[i], 32, 64);
-  if (q < 2 && n < ntok) {
-    const int row0 = plan->slot_row0[s];
-    const bool weighted = plan->slot_weighted[s] != 0;
-    const float rw = plan->slot_w[s][n];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int li = wave * 8 + 4 * q + i;        // row within the 32-row block
-      const int gi = g * 32 + li;                 // intermediate index
-      const uint32_t b1 = mx::bf16_bits(mine[i]);
-      const uint32_t b3 = mx::bf16_bits(upv[i]);
-      const size_t o2 = (size_t)(row0 + n) * I + gi;
-      const float din = mxd::swiglu_element(b1, b3, a.limit, weighted, rw, a.trace ? a.trace + o2 * 5 : nullptr);
-      s_din[n][li] = din;
-      if (a.w1) a.w1[o2] = (uint16_t)b1;
-      if (a.w3) a.w3[o2] = (uint16_t)b3;
-      if (a.din) a.din[o2] = (uint16_t)mx::bf16_bits(din);
-    }
-  }
+  gateup_tile_epilogue(a, s, g, wave, mine, q, n, ntok, s_din);
   __syncthreads();
-  // per-token quantization of the 32-row block: 16 threads per token, 2 values each
-  const int tn = tid >> 4, j2 = tid & 15;
-  if (tn < ntok) {
-    const float v0 = s_din[tn][2 * j2], v1 = s_din[tn][2 * j2 + 1];
-    float amax = fmaxf(fabsf(v0), fabsf(v1));
-#pragma unroll
-    for (int mm = 8; mm >= 1; mm >>= 1) amax = fmaxf(amax, __shfl_xor(amax, mm, 16));
-    amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
-    const uint32_t code = mx::act_scale_code(amax);
-    const float sc = mx::e8m0_value(code);
-    const uint32_t q0 = mx::act_quant_value(v0, sc), q1 = mx::act_quant_value(v1, sc);
-    const size_t r = (size_t)(plan->slot_row0[s] + tn);
-    *reinterpret_cast<uint16_t*>(a.dq + r * I + g * 32 + 2 * j2) = (uint16_t)(q0 | (q1 << 8));
-    if (j2 == 0) a.ds[r * (I / 32) + g] = (uint8_t)code;
-  }
+  gateup_quantize_block(a, s, g, tid >> 4, tid & 15, ntok, s_din);
 }
 
 // grid (H/64, slots), 256 threads: output rows [64b, 64b + 64) of W2 as 4 tiles of 16 rows; after
