@@ -23,7 +23,7 @@ __device__ __forceinline__ uint4 ldg128(const uint8_t* p) {
 }
 
 // Non-temporal (streaming) loads, the `nt` bit: for data read once per call, such as expert weights
-// in decode. A plain blocked read of 2 GiB on MI355X runs at 7.3 TB/s with them, 6.5 TB/s without.
+// in decode. A plain blocked read of 2 GiB on MI355X runs at 6.9-7.0 TB/s with them, 6.0-6.2 TB/s without.
 __device__ __forceinline__ uint32_t ldg32_nt(const uint8_t* p) {
   return __builtin_nontemporal_load((const __attribute__((address_space(1))) uint32_t*)(p));
 }
