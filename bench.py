@@ -264,8 +264,9 @@ def main():
 def secondary(ctx):
     """The other BASELINE configurations, measured on the same GPU (each a few seconds): 2 = MoE prefill
     (T = 4096, Zipf(1.1) routing), 3 = FP8 block-128 projections at T = 1, 16, 2048, 4 = 8-layer offload
-    decode at T = 4 with 25 % of the routed experts resident."""
-    from vesper_amd import fp8_workload, offload_workload, prefill_workload
+    decode at T = 4 with 25 % of the routed experts resident; and the SHA-256 admission audit of expert
+    slots (one expert, and the 1 GiB maximum payload)."""
+    from vesper_amd import fp8_workload, integrity_workload, offload_workload, prefill_workload
     out = {}
     log("configuration 2: prefill")
     p = prefill_workload.run(4096, 5, ctx=ctx)
@@ -283,6 +284,9 @@ def secondary(ctx):
     o = offload_workload.run(10, 4, ctx=ctx)
     out["offload_8layers_T4"] = o
     log(f"offload: {o}")
+    log("cache admission audit: SHA-256 per 4 KiB chunk")
+    out["integrity_sha256"] = integrity_workload.run(20, ctx=ctx)
+    log(f"integrity: {out['integrity_sha256']}")
     return out
 
 

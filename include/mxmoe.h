@@ -55,6 +55,10 @@ int mx_device_name(mx_ctx* ctx, char* name, size_t name_bytes, char* arch, size_
 int mx_malloc(mx_ctx* ctx, uint64_t bytes, void** dptr);       /* Device.allocate (cuda.py:121-138) */
 int mx_free(mx_ctx* ctx, void* dptr);                           /* Device.free                        */
 int mx_owned_bytes(mx_ctx* ctx, uint64_t* live, uint64_t* peak);/* Device.peak / allocations          */
+/* Size of the allocation this context owns at base pointer `dptr` (0 when it owns none): the
+ * allocation lookup of Device.allocations, src/vesper/cuda.py:121-138, that DeviceIntegrity.digests
+ * uses to refuse unowned sources (src/vesper/integrity.py:53-54). */
+int mx_owned_size(mx_ctx* ctx, const void* dptr, uint64_t* bytes);
 int mx_host_alloc_pinned(mx_ctx* ctx, uint64_t bytes, void** hptr); /* Pinned (cuda.py:200-222)       */
 int mx_host_free_pinned(mx_ctx* ctx, void* hptr);
 int mx_memcpy_h2d(mx_ctx* ctx, void* dst, const void* src, uint64_t bytes, void* stream); /* Device.upload   */
@@ -77,6 +81,13 @@ int mx_fill_uniform_u8(mx_ctx* ctx, void* dst, uint64_t bytes, uint64_t seed, ui
 /* Device-side copy by a plain streaming kernel (16 B per thread): the known-size workload used to
  * calibrate the profiler's HBM byte counters. Pointers 16-byte aligned, bytes a multiple of 16. */
 int mx_copy_kernel(mx_ctx* ctx, void* dst, const void* src, uint64_t bytes, void* stream);
+
+/* SHA-256 of every consecutive 4 KiB chunk of `bytes` device bytes (0 < bytes <= 2^30): digests
+ * receives ceil(bytes / 4096) x 32 bytes, chunk c's digest at 32 c; the last chunk may be short.
+ * Replaces the sha256_chunks kernel (src/vesper/kernels/integrity_probe.cu) launched by
+ * DeviceIntegrity.digests (src/vesper/integrity.py:44-66) for the cache's admission audit
+ * (src/vesper/tiered.py:78-95). data and digests 16-byte aligned and not overlapping. */
+int mx_sha256_chunks(mx_ctx* ctx, const void* data, uint64_t bytes, void* digests, void* stream);
 
 /* Streaming read of `bytes` (a multiple of 16 MiB, 16-byte aligned source) by the fastest plain read
  * kernel measured on MI355X (4096 workgroups of contiguous ranges, non-temporal 16-byte loads, three

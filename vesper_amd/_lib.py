@@ -127,6 +127,8 @@ SIGNATURES = {
                               C.c_int),
     "mx_copy_kernel": ([_P, _P, _P, _U64, _P], C.c_int),
     "mx_read_kernel": ([_P, _P, _U64, _P, _P], C.c_int),
+    "mx_sha256_chunks": ([_P, _P, _U64, _P, _P], C.c_int),
+    "mx_owned_size": ([_P, _P, C.POINTER(_U64)], C.c_int),
     "mx_check_e4m3_pack": ([_P, C.POINTER(_U64)], C.c_int),
 }
 
@@ -259,6 +261,12 @@ class Context:
 
     def free(self, p: int):
         self.lib.free(self._h(), C.c_void_p(int(p)))
+
+    def owned_size(self, p: int) -> int:
+        """Bytes of the allocation this context owns at base pointer p (0 if none)."""
+        size = C.c_uint64()
+        self.lib.owned_size(self._h(), C.c_void_p(int(p)), C.byref(size))
+        return size.value
 
     def owned_bytes(self):
         live, peak = C.c_uint64(), C.c_uint64()

@@ -1,0 +1,184 @@
+// SHA-256 admission audit of device bytes: one digest per consecutive 4 KiB chunk
+// (integrity.py:9-27 digest layout, kernels/integrity_probe.cu sha256_chunks), written from
+// FIPS 180-4 (sections 4.1.2 functions, 4.2.2 constants, 5.1.1 padding, 5.3.3 initial value,
+// 6.2.2 computation).
+//
+// Chunks are independent and each chunk's 65 compressions are a dependent chain, so one lane owns
+// one chunk: a wave hashes 64 chunks side by side. Per 64-byte block a lane runs about 1,500 integer
+// VALU instructions against 64 bytes of loads, so the kernel is bound by the VALU issue rate (about
+// 1.4-1.5 TB/s of hashed bytes over the whole chip), not by HBM; a lane's next block is loaded while
+// the current one is compressed, and the padding block of a full chunk is built from constants.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "mx_internal.h"
+
+namespace {
+
+constexpr uint32_t kChunkBytes = 4096;
+constexpr uint64_t kMaxPayload = 1ull << 30;   // integrity.py:15-17
+
+// FIPS 180-4 section 4.2.2: first 32 bits of the fractional parts of the cube roots of the first 64 primes.
+constexpr uint32_t kRound[64] = {
+    0x428a2f98u, 0x71374491u, 0xb5c0fbcfu, 0xe9b5dba5u, 0x3956c25bu, 0x59f111f1u, 0x923f82a4u, 0xab1c5ed5u,
+    0xd807aa98u, 0x12835b01u, 0x243185beu, 0x550c7dc3u, 0x72be5d74u, 0x80deb1feu, 0x9bdc06a7u, 0xc19bf174u,
+    0xe49b69c1u, 0xefbe4786u, 0x0fc19dc6u, 0x240ca1ccu, 0x2de92c6fu, 0x4a7484aau, 0x5cb0a9dcu, 0x76f988dau,
+    0x983e5152u, 0xa831c66du, 0xb00327c8u, 0xbf597fc7u, 0xc6e00bf3u, 0xd5a79147u, 0x06ca6351u, 0x14292967u,
+    0x27b70a85u, 0x2e1b2138u, 0x4d2c6dfcu, 0x53380d13u, 0x650a7354u, 0x766a0abbu, 0x81c2c92eu, 0x92722c85u,
+    0xa2bfe8a1u, 0xa81a664bu, 0xc24b8b70u, 0xc76c51a3u, 0xd192e819u, 0xd6990624u, 0xf40e3585u, 0x106aa070u,
+    0x19a4c116u, 0x1e376c08u, 0x2748774cu, 0x34b0bcb5u, 0x391c0cb3u, 0x4ed8aa4au, 0x5b9cca4fu, 0x682e6ff3u,
+    0x748f82eeu, 0x78a5636fu, 0x84c87814u, 0x8cc70208u, 0x90befffau, 0xa4506cebu, 0xbef9a3f7u, 0xc67178f2u};
+
+// Section 5.3.3: first 32 bits of the fractional parts of the square roots of the first 8 primes.
+constexpr uint32_t kInitial[8] = {0x6a09e667u, 0xbb67ae85u, 0x3c6ef372u, 0xa54ff53au,
+                                  0x510e527fu, 0x9b05688cu, 0x1f83d9abu, 0x5be0cd19u};
+
+// rotate right by n (0 < n < 32): one v_alignbit_b32
+__device__ __forceinline__ uint32_t rotr(uint32_t x, int n) { return __builtin_amdgcn_alignbit(x, x, n); }
+
+// Three-input bitwise functions as one v_bitop3_b32 each; both truth tables are symmetric in their
+// inputs (odd parity 0x96, at least two set 0xE8), so the operand order of the encoding does not matter.
+__device__ __forceinline__ uint32_t xor3(uint32_t x, uint32_t y, uint32_t z) {
+  return __builtin_amdgcn_bitop3_b32(x, y, z, 0x96);
+}
+__device__ __forceinline__ uint32_t majority3(uint32_t x, uint32_t y, uint32_t z) {
+  return __builtin_amdgcn_bitop3_b32(x, y, z, 0xE8);
+}
+
+// One compression (section 6.2.2) of the block in w (big-endian words); w is consumed as the rolling
+// 16-word message schedule. Fully unrolled so every index and round constant is static.
+__device__ __forceinline__ void compress(uint32_t (&h)[8], uint32_t (&w)[16]) {
+  uint32_t a = h[0], b = h[1], c = h[2], d = h[3], e = h[4], f = h[5], g = h[6], k = h[7];
+#pragma unroll
+  for (int i = 0; i < 64; ++i) {
+    if (i >= 16) {
+      const uint32_t x = w[(i - 15) & 15], y = w[(i - 2) & 15];
+      const uint32_t sigma0 = xor3(rotr(x, 7), rotr(x, 18), x >> 3);
+      const uint32_t sigma1 = xor3(rotr(y, 17), rotr(y, 19), y >> 10);
+      w[i & 15] = w[i & 15] + sigma0 + w[(i - 7) & 15] + sigma1;
+    }
+    const uint32_t big1 = xor3(rotr(e, 6), rotr(e, 11), rotr(e, 25));
+    const uint32_t choose = (e & f) | (~e & g);
+    const uint32_t t1 = k + big1 + choose + kRound[i] + w[i & 15];
+    const uint32_t big0 = xor3(rotr(a, 2), rotr(a, 13), rotr(a, 22));
+    const uint32_t majority = majority3(a, b, c);
+    const uint32_t t2 = big0 + majority;
+    k = g;
+    g = f;
+    f = e;
+    e = d + t1;
+    d = c;
+    c = b;
+    b = a;
+    a = t1 + t2;
+  }
+  h[0] += a;
+  h[1] += b;
+  h[2] += c;
+  h[3] += d;
+  h[4] += e;
+  h[5] += f;
+  h[6] += g;
+  h[7] += k;
+}
+
+// 64 message bytes at p (16-byte aligned, inside the payload) as four 16-byte loads
+__device__ __forceinline__ void load_block(uint4 (&v)[4], const uint8_t* p) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = *reinterpret_cast<const uint4*>(p + 16 * i);
+}
+
+// little-endian loads -> the block's big-endian message words
+__device__ __forceinline__ void to_words(uint32_t (&w)[16], const uint4 (&v)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w[4 * i + 0] = __builtin_bswap32(v[i].x);
+    w[4 * i + 1] = __builtin_bswap32(v[i].y);
+    w[4 * i + 2] = __builtin_bswap32(v[i].z);
+    w[4 * i + 3] = __builtin_bswap32(v[i].w);
+  }
+}
+
+// grid ceil(chunks / 256) x 256 threads: lane c hashes bytes [4096 c, min(4096 (c + 1), bytes)) and
+// writes its 32-byte digest (the eight state words big-endian) to digests + 32 c.
+__global__ __launch_bounds__(256) void sha256_chunks_kernel(const uint8_t* __restrict__ data,
+                                                            uint8_t* __restrict__ digests, uint64_t bytes,
+                                                            uint32_t chunks) {
+  const uint32_t chunk = blockIdx.x * 256u + threadIdx.x;
+  if (chunk >= chunks) return;
+  const uint64_t start = (uint64_t)chunk * kChunkBytes;
+  const uint32_t len = (uint32_t)(bytes - start < kChunkBytes ? bytes - start : kChunkBytes);
+  const uint8_t* src = data + start;
+  uint32_t h[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) h[i] = kInitial[i];
+
+  // Blocks wholly inside the chunk's bytes come from memory (block b + 1 is in flight while block b is
+  // compressed). Padding (section 5.1.1) follows: the rem = len % 64 remaining bytes, the 0x80 marker,
+  // zeros, and the 64-bit message length in bits in the last two words, with one more block when
+  // rem >= 56. For a whole 4 KiB chunk rem = 0 and the padding block is constant. One loop over all
+  // blocks keeps a single copy of the unrolled compression in the kernel.
+  const uint32_t whole = len / 64;
+  const uint32_t rem = len - 64 * whole;
+  const uint32_t total = whole + (rem < 56 ? 1 : 2);
+  const uint8_t* tail = src + 64 * whole;
+  const uint32_t bits = len * 8;   // len <= 4096: the high word of the length is zero
+  uint4 cur[4], next[4];
+  if (whole > 0) load_block(cur, src);
+  for (uint32_t b = 0; b < total; ++b) {
+    uint32_t w[16];
+    if (b < whole) {
+      if (b + 1 < whole) load_block(next, src + 64 * (b + 1));
+      to_words(w, cur);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) cur[i] = next[i];
+    } else if (b == whole) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        uint32_t word = 0;
+        if (4 * j <= rem) {   // data bytes or the marker: assemble the word byte by byte
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const uint32_t p = 4 * j + t;
+            const uint32_t byte = p < rem ? tail[p] : (p == rem ? 0x80u : 0u);
+            word |= byte << (24 - 8 * t);
+          }
+        }
+        w[j] = word;
+      }
+      if (rem < 56) w[15] = bits;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 15; ++j) w[j] = 0;
+      w[15] = bits;
+    }
+    compress(h, w);
+  }
+  uint4* out = reinterpret_cast<uint4*>(digests + (size_t)chunk * 32);
+  out[0] = make_uint4(__builtin_bswap32(h[0]), __builtin_bswap32(h[1]), __builtin_bswap32(h[2]),
+                      __builtin_bswap32(h[3]));
+  out[1] = make_uint4(__builtin_bswap32(h[4]), __builtin_bswap32(h[5]), __builtin_bswap32(h[6]),
+                      __builtin_bswap32(h[7]));
+}
+
+}  // namespace
+
+using namespace mxi;
+
+extern "C" int mx_sha256_chunks(mx_ctx* ctx, const void* data, uint64_t bytes, void* digests, void* stream) {
+  if (int s = use(ctx)) return s;
+  MX_REQUIRE(data != nullptr && digests != nullptr, "mx_sha256_chunks: null pointer");
+  MX_REQUIRE(bytes > 0 && bytes <= kMaxPayload, "Invalid bounded integrity payload size");
+  MX_REQUIRE(((uintptr_t)data & 15) == 0 && ((uintptr_t)digests & 15) == 0,
+             "mx_sha256_chunks: data and digests must be 16-byte aligned");
+  const uint64_t chunks = (bytes + kChunkBytes - 1) / kChunkBytes;
+  const uint8_t* d = (const uint8_t*)data;
+  uint8_t* o = (uint8_t*)digests;
+  MX_REQUIRE(o + chunks * 32 <= d || d + bytes <= o, "Digest destination must not overwrite source bytes");
+  hipLaunchKernelGGL(sha256_chunks_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0,
+                     as_stream(stream), d, o, bytes, (uint32_t)chunks);
+  MX_LAUNCH_CHECK("sha256_chunks_kernel");
+  return MX_OK;
+}

@@ -136,6 +136,15 @@ int mx_free(mx_ctx* ctx, void* dptr) {
   return MX_OK;
 }
 
+int mx_owned_size(mx_ctx* ctx, const void* dptr, uint64_t* bytes) {
+  MX_REQUIRE(ctx != nullptr, "mx_owned_size: context is closed");
+  MX_REQUIRE(bytes != nullptr, "mx_owned_size: null output");
+  std::lock_guard<std::mutex> g(ctx->lock);
+  auto it = ctx->owned.find(const_cast<void*>(dptr));
+  *bytes = it == ctx->owned.end() ? 0 : it->second;
+  return MX_OK;
+}
+
 int mx_owned_bytes(mx_ctx* ctx, uint64_t* live, uint64_t* peak) {
   MX_REQUIRE(ctx != nullptr, "mx_owned_bytes: context is closed");
   std::lock_guard<std::mutex> g(ctx->lock);
