@@ -280,6 +280,9 @@ def secondary(ctx):
                                        "per_projection_us": {k: p2["us"] for k, p2 in v["projections"].items()}}
                               for t, v in f.items()}
     log(f"fp8: {out['fp8_projections']}")
+    g = fp8_workload.run_grouped((1, 8), 20, ctx=ctx)
+    out["wo_a_grouped"] = {str(t): dict(v, hbm_frac=round(v["GB_per_s"] / HBM_PEAK_GBS, 4)) for t, v in g.items()}
+    log(f"wo_a grouped: {out['wo_a_grouped']}")
     log("configuration 4: offload decode")
     o = offload_workload.run(10, 4, ctx=ctx)
     out["offload_8layers_T4"] = o

@@ -114,6 +114,11 @@ int mx_act_quant32(mx_ctx* ctx, const uint16_t* x_bf16, uint8_t* q, uint8_t* sca
 /* Same quantizer over FP32 input (BF16-rounded first), the activation32 signature. */
 int mx_act_quant32_f32(mx_ctx* ctx, const float* x, uint8_t* q, uint8_t* scales,
                        int64_t rows, int64_t width, void* stream);
+/* Per-32 quantize-dequantize of `count` BF16 values (a multiple of 32): E4M3 codes, E8M0 scales (the
+ * mx_act_quant32 arithmetic) and the round trip rounded = BF16(E4M3(code) x 2^(scale - 127)). Replaces
+ * kv_round32 (src/vesper/kernels/kv_probe.cu:4-25). x and rounded 16-byte, codes 8-byte aligned. */
+int mx_kv_round32(mx_ctx* ctx, const uint16_t* x, int64_t count, uint16_t* rounded, uint8_t* codes, uint8_t* scales,
+                  void* stream);
 
 /* ---- expert arithmetic ---- */
 
@@ -250,6 +255,15 @@ int mx_act_quant128(mx_ctx* ctx, const uint16_t* x_bf16, uint8_t* q, float* s, i
  * ([T][K/32] E8M0 or [T][K/128] FP32) -- the stage dict of projections.py:146-154. */
 int mx_fp8_projection(mx_ctx* ctx, const void* tiled, int32_t n, int32_t k, int32_t block, const uint16_t* x_bf16,
                       int32_t tokens, uint16_t* y_bf16, float* trace, uint8_t* q_out, void* s_out, void* stream);
+
+/* Grouped block-32 FP8 projection (the attention output projection wo_a): weight rows [g rows, (g + 1)
+ * rows) of `tiled` (mx_fp8_tile, block 32, groups x rows by K) multiply activation group g, so
+ * y[t][g rows + r] = sum_k W[g rows + r][k] x[t][g][k] with x given as per-32 E4M3 codes q[T][groups][K]
+ * and E8M0 scales s[T][groups][K/32] (mx_kv_round32). Replaces the dequantize-to-BF16 + batched BF16
+ * GEMM of NativeProjections.grouped (src/vesper/projections.py:60-67,156-171): the weights stay E4M3 and
+ * the scaled MFMA applies both block scales. 1 <= T <= 32 tokens, rows a multiple of 64. */
+int mx_fp8_grouped_projection(mx_ctx* ctx, const void* tiled, int32_t groups, int32_t rows, int32_t K,
+                              const uint8_t* q, const uint8_t* s, int32_t T, uint16_t* y, float* trace, void* stream);
 
 /* FP8 block-32 expert (the shared expert's format, src/vesper/shared.py:20-24,141-170 with
  * gemv_fp8_shared, shared_probe.cu:4-49): the MXFP4 expert's stage sequence with E4M3 weights and E8M0

@@ -110,3 +110,39 @@ def fp8_weights(rng, rows, width, block: int):
     else:
         scales = rng.integers(118, 127, (rows // 32, width // 32), dtype=np.uint8)
     return codes, scales
+
+
+def kv_round32(values_bits):
+    """kv_round32 (kv_probe.cu:4-25): per-32 E4M3 codes and E8M0 scales of the BF16 values (the
+    activation32 quantizer, formats.quantize_activation) and the round trip
+    rounded = BF16(E4M3(code) x 2^(scale - 127)), exact in FP32 and in BF16.
+    Returns (rounded BF16 bits, codes, scales)."""
+    from .formats import bf16_bits, bf16_values, e4m3_values, e8m0_values, quantize_activation
+    codes, scales = quantize_activation(bf16_values(np.asarray(values_bits, np.uint16)))
+    vals = e4m3_values(codes).astype(np.float32).reshape(*codes.shape[:-1], -1, 32) * e8m0_values(scales)[..., None]
+    return bf16_bits(vals.reshape(codes.shape).astype(np.float32)), codes, scales
+
+
+def dequant_block32(weight_codes, weight_scales) -> np.ndarray:
+    """E4M3 codes x E8M0 of their 32 x 32 block, as float64 (projection_dequant_wo_a; every value is exact
+    in BF16, so the reference's BF16 conversion keeps it)."""
+    from .formats import e4m3_values, e8m0_values
+    s = np.repeat(np.repeat(e8m0_values(weight_scales).astype(np.float64), 32, axis=0), 32, axis=1)
+    return e4m3_values(weight_codes).astype(np.float64) * s
+
+
+def wo_a_grouped(values_bits, weight_codes, weight_scales, groups: int = 8) -> dict:
+    """NativeProjections.grouped (projections.py:60-67,156-171): kv_round32 of the [T, groups, K] input,
+    then per group g out[t, g, r] = BF16(sum_k W[g R + r, k] x rounded[t, g, k]) with R = rows / groups,
+    W the exactly dequantized weight. The reference runs a batched BF16 GEMM with FP32 accumulation in
+    an order the library does not specify; the sum here is evaluated in float64 (exact products) and
+    rounded once to FP32."""
+    from .formats import bf16_bits, bf16_values
+    values_bits = np.asarray(values_bits, np.uint16)
+    t = int(np.prod(values_bits.shape[:-2]))
+    rounded, codes, scales = kv_round32(values_bits)
+    x = bf16_values(rounded).astype(np.float64).reshape(t, groups, -1)
+    w = dequant_block32(weight_codes, weight_scales).reshape(groups, -1, x.shape[-1])
+    out = np.einsum("grk,tgk->tgr", w, x).astype(np.float32)
+    return {"rounded_bf16": rounded, "input_fp8": codes, "scale_e8m0": scales, "output_fp32": out,
+            "output_bf16": bf16_bits(out).reshape(*values_bits.shape[:-1], -1)}

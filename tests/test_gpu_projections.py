@@ -268,3 +268,69 @@ def test_reference_shapes_block32_and_refusals():
     bad["layers.0.attn.wkv.scale"] = np.full((16, 160), 255, np.uint8)
     with pytest.raises(ValueError):
         NativeProjections(bad, block=32)
+
+
+def wo_a_arrays(w, sw):
+    """The grouped projection's weights beside one tiny block-32 projection (the runtime tiles both)."""
+    rng = np.random.default_rng(0)
+    arrays = arrays_for({"p": (64, 128)}, 32, rng)
+    arrays["layers.0.attn.wo_a.weight"] = w
+    arrays["layers.0.attn.wo_a.scale"] = sw
+    return arrays
+
+
+def test_kv_round32_and_window_rounding_bit_exact():
+    from oracle.projections import kv_round32
+    rng = np.random.default_rng(512)
+    v = rng.standard_normal((2, 7, 512)).astype(np.float32) * np.exp2(rng.integers(-12, 8, (2, 7, 1)))
+    v[0, 3] = 0.0                                                # zero blocks: the floor scale
+    v[1, 2, :32] = np.float32(1e-30)                              # below the floor
+    bits = bf16_bits(v)
+    w, sw = fp8_weights(rng, 8192, 4096, 32)
+    with NativeProjections(wo_a_arrays(w, sw), block=32, layout={"p": (64, 128)}) as proj:
+        got = proj.round_window(bits)
+        with pytest.raises(ValueError, match="window"):
+            proj.round_window(np.concatenate([bits, bits[:1]]))      # a batch of 3
+    rounded, q, s = kv_round32(bits)
+    np.testing.assert_array_equal(got["rounded_bf16"], rounded)
+    np.testing.assert_array_equal(got["codes_fp8"], q)
+    np.testing.assert_array_equal(got["scales_e8m0"], s)
+
+
+def test_grouped_projection_exact_on_representable_inputs():
+    """Small-integer weight codes with power-of-two block scales, and activations whose per-32 scale is
+    2^0 (each block holds 448): every partial sum is exact in FP32, so the BF16 outputs equal the oracle's
+    bit for bit -- and each group reads its own activations (distinct per group)."""
+    from oracle.projections import wo_a_grouped
+    rng = np.random.default_rng(4096)
+    w = encode_e4m3(rng.integers(-8, 9, (8192, 4096)).astype(np.float32))
+    sw = rng.integers(125, 130, (256, 128), dtype=np.uint8)
+    for tokens in (1, 5):
+        x = rng.integers(-16, 17, (tokens, 8, 4096)).astype(np.float32)
+        x[..., ::32] = 448.0
+        bits = bf16_bits(x)
+        with NativeProjections(wo_a_arrays(w, sw), block=32, layout={"p": (64, 128)}) as proj:
+            got = proj.grouped(bits)
+        ref = wo_a_grouped(bits, w, sw)
+        np.testing.assert_array_equal(got["input_fp8"], ref["input_fp8"])
+        np.testing.assert_array_equal(got["scale_e8m0"], ref["scale_e8m0"])
+        np.testing.assert_array_equal(got["rounded_bf16"], ref["rounded_bf16"])
+        np.testing.assert_array_equal(got["output_bf16"], ref["output_bf16"].reshape(tokens, 8, 1024))
+
+
+@pytest.mark.parametrize("lead", [(1,), (8,), (2, 3)])
+def test_grouped_projection_random_within_tolerance(lead):
+    from oracle.projections import wo_a_grouped
+    rng = np.random.default_rng(sum(lead) + 17)
+    w, sw = fp8_weights(rng, 8192, 4096, 32)
+    bits = bf16_bits(rng.standard_normal((*lead, 8, 4096)).astype(np.float32))
+    with NativeProjections(wo_a_arrays(w, sw), block=32, layout={"p": (64, 128)}) as proj:
+        got = proj.grouped(bits)
+        with pytest.raises(ValueError):
+            proj.grouped(bits[..., :2048].copy())
+        with pytest.raises(ValueError):
+            proj.grouped(np.zeros((33, 8, 4096), np.uint16))
+    ref = wo_a_grouped(bits, w, sw)
+    assert got["output_bf16"].shape == (*lead, 8, 1024)
+    np.testing.assert_array_equal(got["rounded_bf16"], ref["rounded_bf16"])
+    assert_close(got["output_bf16"].reshape(-1, 8192), ref["output_bf16"].reshape(-1, 8192), "wo_a grouped")

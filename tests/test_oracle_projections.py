@@ -104,3 +104,43 @@ def test_config3_layout_and_weights():
     w, s = fp8_weights(np.random.default_rng(0), 576, 256, 128)
     assert s.shape == (5, 2) and np.all((w & 0x7F) != 0x7F)
     assert np.all((s >= 2.0 ** -8) & (s <= 2.0 ** -2))
+
+
+def test_kv_round32_round_trips_representable_blocks():
+    """A block built as E4M3 values x 2^k with its largest code 448 x 2^k present is recovered exactly:
+    codes, the scale 127 + k and the rounded values equal the input; an all-zero block keeps zeros with
+    the floor's scale (105)."""
+    from oracle.formats import bf16_bits, e4m3_values, encode_e4m3
+    from oracle.projections import kv_round32
+    rng = np.random.default_rng(32)
+    codes = rng.integers(0, 126, (4, 32)).astype(np.uint8) | (rng.integers(0, 2, (4, 32)).astype(np.uint8) << 7)
+    codes[:, 5] = 0x7E                                           # 448
+    k = np.array([-6, 0, 3, -20])
+    x = (e4m3_values(codes).astype(np.float64) * np.exp2(k)[:, None]).astype(np.float32)
+    x = np.concatenate([x, np.zeros((1, 32), np.float32)])
+    rounded, q, s = kv_round32(bf16_bits(x))
+    np.testing.assert_array_equal(q[:4], codes)
+    np.testing.assert_array_equal(s[:4, 0], 127 + k)
+    np.testing.assert_array_equal(rounded, bf16_bits(x))
+    assert s[4, 0] == 105 and not q[4].any()
+    assert (encode_e4m3(np.float32(448.0)) == 0x7E).all()
+
+
+def test_wo_a_grouped_indexes_groups_and_rows():
+    """One-hot weights: row r of group g reads element (r + 3 g) mod K of activation group g, so every
+    output is a known rounded input value times the weight's block scale."""
+    from oracle.formats import bf16_bits, bf16_values
+    from oracle.projections import kv_round32, wo_a_grouped
+    groups, rows, width, t = 4, 64, 128, 3
+    rng = np.random.default_rng(8)
+    codes = np.zeros((groups * rows, width), np.uint8)
+    r = np.arange(groups * rows)
+    col = (r % rows + 3 * (r // rows)) % width
+    codes[r, col] = 0x38                                         # E4M3 1.0
+    scales = rng.integers(124, 130, (groups * rows // 32, width // 32), dtype=np.uint8)
+    x = bf16_bits(rng.standard_normal((t, groups, width)).astype(np.float32))
+    out = wo_a_grouped(x, codes, scales, groups=groups)
+    rounded = bf16_values(kv_round32(x)[0]).reshape(t, groups, width)
+    ws = np.exp2(scales.astype(np.float64) - 127)[r // 32, col // 32]
+    want = rounded[:, r // rows, col] * ws[None, :]
+    np.testing.assert_array_equal(out["output_bf16"].reshape(t, -1), bf16_bits(want.astype(np.float32)))

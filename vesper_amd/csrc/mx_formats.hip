@@ -59,8 +59,10 @@ __global__ void act_quant32_kernel(const In* __restrict__ x, uint8_t* __restrict
 
 // BF16 input, 8 values per thread (one 16-byte load), 4 threads per 32-block: the block amax is two
 // xor-shuffles inside the quad, the 8 codes are one 8-byte store. Grid-stride over the groups of 8.
+// rounded (nullable): the quantize-dequantize round trip BF16(E4M3(code) x scale), one 16-byte store.
 __global__ __launch_bounds__(256) void act_quant32_v8_kernel(const uint16_t* __restrict__ x, uint8_t* __restrict__ q,
-                                                             uint8_t* __restrict__ s, int64_t groups) {
+                                                             uint8_t* __restrict__ s, int64_t groups,
+                                                             uint16_t* __restrict__ rounded) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < groups; base += stride) {
     const int64_t i = base + threadIdx.x;   // quads never straddle the bound: groups is a multiple of 4
@@ -89,6 +91,18 @@ __global__ __launch_bounds__(256) void act_quant32_v8_kernel(const uint16_t* __r
               (mx::act_quant_value(f[6], sc) << 16) | (mx::act_quant_value(f[7], sc) << 24);
       reinterpret_cast<uint2*>(q)[i] = out;
       if ((i & 3) == 0) s[i >> 2] = (uint8_t)code;
+      if (rounded) {
+        // E4M3 value x power of two is exact in FP32 and has at most 4 significant bits: the BF16
+        // rounding keeps it exactly
+        uint32_t r[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t lo = mx::bf16_bits(mx::e4m3_value((j < 2 ? out.x : out.y) >> (16 * (j & 1)) & 0xFFu) * sc);
+          const uint32_t hi = mx::bf16_bits(mx::e4m3_value((j < 2 ? out.x : out.y) >> (16 * (j & 1) + 8) & 0xFFu) * sc);
+          r[j] = lo | (hi << 16);
+        }
+        reinterpret_cast<uint4*>(rounded)[i] = make_uint4(r[0], r[1], r[2], r[3]);
+      }
     }
   }
 }
@@ -174,7 +188,7 @@ int mx_act_quant32(mx_ctx* ctx, const uint16_t* x, uint8_t* q, uint8_t* scales, 
     const int64_t groups = blocks * 4;
     const int64_t want = (groups + 255) / 256;
     hipLaunchKernelGGL(act_quant32_v8_kernel, dim3((unsigned)(want < 65536 ? want : 65536)), dim3(256), 0,
-                       as_stream(stream), x, q, scales, groups);
+                       as_stream(stream), x, q, scales, groups, (uint16_t*)nullptr);
     MX_LAUNCH_CHECK("act_quant32_v8_kernel");
     return MX_OK;
   }
@@ -182,6 +196,22 @@ int mx_act_quant32(mx_ctx* ctx, const uint16_t* x, uint8_t* q, uint8_t* scales, 
   hipLaunchKernelGGL(act_quant32_kernel<uint16_t>, dim3(grid_for(blocks * 32, 256)), dim3(256), 0,
                      as_stream(stream), x, q, scales, blocks);
   MX_LAUNCH_CHECK("act_quant32_kernel");
+  return MX_OK;
+}
+
+int mx_kv_round32(mx_ctx* ctx, const uint16_t* x, int64_t count, uint16_t* rounded, uint8_t* codes, uint8_t* scales,
+                  void* stream) {
+  if (int st = use(ctx)) return st;
+  MX_REQUIRE(count >= 0 && count % 32 == 0, "mx_kv_round32: the value count must be a multiple of 32");
+  if (!count) return MX_OK;
+  MX_REQUIRE(x && rounded && codes && scales, "mx_kv_round32: null pointer");
+  MX_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)rounded & 15) == 0 && ((uintptr_t)codes & 7) == 0,
+             "mx_kv_round32: x and rounded 16-byte, codes 8-byte alignment required");
+  const int64_t groups = count / 8;
+  const int64_t want = (groups + 255) / 256;
+  hipLaunchKernelGGL(act_quant32_v8_kernel, dim3((unsigned)(want < 65536 ? want : 65536)), dim3(256), 0,
+                     as_stream(stream), x, codes, scales, groups, rounded);
+  MX_LAUNCH_CHECK("act_quant32_v8_kernel");
   return MX_OK;
 }
 

@@ -141,6 +141,9 @@ struct Fp8Args {
   uint32_t* tickets;   // split-K GEMV: arrival counter per (row group, token tile), zero between launches;
                        // null = partial sums only, added by fp8_splitk_reduce_kernel
   const uint16_t* x;   // fused GEMV (block 128, few tokens): the BF16 input [T][K], quantized in the kernel
+  int64_t x_stride;    // activation elements per token: K, or groups x K when grouped
+  int x_group_rows;    // grouped activations (block-32 GEMV): weight rows [g R, (g + 1) R) multiply
+                       // activation group g, codes at xq + tok x_stride + g K; 0 = one group
 };
 
 // Fused per-128 quantization in the GEMV (block 128, up to kFusedMaxTokens tokens, up to kFusedChunks K
@@ -161,10 +164,11 @@ struct Fp8Chunk {
   int c;         // the chunk (fused: its activations are read from LDS at the MFMA)
 };
 
+// xsrow: this lane's token's activation scales (block 32: E8M0 bytes, block 128: FP32), chunk 0 first.
 template <int kBlock, bool kFused>
 __device__ __forceinline__ void fp8_load(Fp8Chunk<kBlock>& r, const Fp8Args& a, const uint8_t* wlane,
-                                         const uint8_t* slane, const float* swrow, const uint8_t* xrow, int tok,
-                                         int c, int q) {
+                                         const uint8_t* slane, const float* swrow, const uint8_t* xrow,
+                                         const uint8_t* xsrow, int c, int q) {
 #pragma unroll
   for (int t = 0; t < kTiles; ++t) {
     r.a[t][0] = ldg128(wlane + (size_t)c * 8192 + t * 2048);
@@ -179,10 +183,10 @@ __device__ __forceinline__ void fp8_load(Fp8Chunk<kBlock>& r, const Fp8Args& a, 
   r.b1 = ldg128(xrow + (size_t)c * 128 + 64 + 16 * q);
   if constexpr (kBlock == 32) {
     r.sw = ldg32(slane + (size_t)c * 256);
-    r.sx = ldg32((const uint8_t*)a.xs + (size_t)tok * (a.K / 32) + 4 * c);
+    r.sx = ldg32(xsrow + 4 * c);
   } else {
     r.sw = __float_as_uint(ldgf(swrow + c));
-    r.sx = __float_as_uint(ldgf((const float*)a.xs + (size_t)tok * (a.K / 128) + c));
+    r.sx = __float_as_uint(ldgf(reinterpret_cast<const float*>(xsrow) + c));
   }
 }
 
@@ -236,7 +240,12 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
   const uint8_t* wlane = a.blob + (size_t)g * C * 8192 + 16 * lane;
   const uint8_t* slane = a.blob + off.scales + (size_t)g * C * 256 + 4 * lane;
   const float* swrow = reinterpret_cast<const float*>(a.blob + off.scales) + (size_t)((64 * g) / 128) * C;
-  const uint8_t* xrow = a.xq + (size_t)rtok * a.K;
+  // grouped activations: the row group's 64 rows lie in one activation group (x_group_rows % 64 == 0)
+  const int xgroup = a.x_group_rows ? (64 * g) / a.x_group_rows : 0;
+  const uint8_t* xrow = a.xq + (size_t)rtok * a.x_stride + (size_t)xgroup * a.K;
+  const uint8_t* xsrow =
+      kBlock == 32 ? (const uint8_t*)a.xs + (size_t)rtok * (a.x_stride / 32) + (size_t)xgroup * (a.K / 32)
+                   : reinterpret_cast<const uint8_t*>((const float*)a.xs + (size_t)rtok * (a.K / 128));
   v4f acc[kTiles];
 #pragma unroll
   for (int t = 0; t < kTiles; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -268,7 +277,7 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
   if (cn > 0) {
 #pragma unroll
     for (int j = 0; j < P; ++j)
-      fp8_load<kBlock, kFused>(buf[j], a, wlane, slane, swrow, xrow, rtok, c0 + min(j, cn - 1), q);
+      fp8_load<kBlock, kFused>(buf[j], a, wlane, slane, swrow, xrow, xsrow, c0 + min(j, cn - 1), q);
   }
   if constexpr (kFused) {
 #pragma unroll
@@ -305,7 +314,7 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
 #pragma unroll
       for (int j = 0; j < P; ++j) {
         fp8_mma<kBlock, kFused>(buf[j], acc, q, keep, qrow, qs, cb);
-        fp8_load<kBlock, kFused>(buf[j], a, wlane, slane, swrow, xrow, rtok, c0 + min(i + j + P, cn - 1), q);
+        fp8_load<kBlock, kFused>(buf[j], a, wlane, slane, swrow, xrow, xsrow, c0 + min(i + j + P, cn - 1), q);
       }
     }
 #pragma unroll
@@ -599,12 +608,14 @@ bool fp8_fused_ok(int N, int K, int T, int block) {
 // x_fused: the BF16 input when the GEMV quantizes it itself (fp8_fused_ok), else null (q and sc given).
 int launch_fp8_product(const uint8_t* blob, int N, int K, int block, const uint8_t* q, const void* sc, int T,
                        uint16_t* y, float* trace, float* partial, uint32_t* tickets, hipStream_t st,
-                       const uint16_t* x_fused = nullptr) {
+                       const uint16_t* x_fused = nullptr, int x_group_rows = 0) {
   Fp8Args a{};
   a.blob = blob;
   a.N = N;
   a.K = K;
   a.T = T;
+  a.x_group_rows = x_group_rows;
+  a.x_stride = x_group_rows ? (int64_t)K * (N / x_group_rows) : K;
   a.xq = q;
   a.xs = sc;
   a.y = y;
@@ -731,6 +742,26 @@ int mx_fp8_projection(mx_ctx* ctx, const void* tiled, int32_t N, int32_t K, int3
     if (int s = mx_act_quant128(ctx, x, q, (float*)sc, T, K, stream)) return s;
   }
   return launch_fp8_product((const uint8_t*)tiled, N, K, block, q, sc, T, y, trace, partial, ctx->tickets, st);
+}
+
+int mx_fp8_grouped_projection(mx_ctx* ctx, const void* tiled, int32_t groups, int32_t rows, int32_t K,
+                              const uint8_t* q, const uint8_t* s, int32_t T, uint16_t* y, float* trace, void* stream) {
+  if (int st = use(ctx)) return st;
+  MX_REQUIRE(groups >= 1 && groups <= 64 && rows > 0 && rows % 64 == 0 && rows <= (1 << 20),
+             "mx_fp8_grouped_projection: 1 to 64 groups of a positive multiple of 64 rows required");
+  const int N = groups * rows;
+  if (int st = check_fp8_shape(N, K, 32, "mx_fp8_grouped_projection")) return st;
+  MX_REQUIRE(T >= 0 && T <= kGemvMaxTokens, "mx_fp8_grouped_projection: token count %d outside [0, %d]", T,
+             kGemvMaxTokens);
+  if (!T) return MX_OK;
+  MX_REQUIRE(tiled && q && s && y, "mx_fp8_grouped_projection: null pointer");
+  MX_REQUIRE(((uintptr_t)tiled & 255) == 0 && ((uintptr_t)q & 15) == 0 && ((uintptr_t)s & 3) == 0 &&
+                 ((uintptr_t)y & 7) == 0 && ((uintptr_t)trace & 15) == 0,
+             "mx_fp8_grouped_projection: tiled 256-byte, q 16-byte, s 4-byte, y 8-byte, trace 16-byte alignment");
+  void* base = nullptr;
+  if (int st = scratch(ctx, (uint64_t)fp8_splits(N, K, T) * T * N * 4 + 256, &base)) return st;
+  return launch_fp8_product((const uint8_t*)tiled, N, K, 32, q, s, T, y, trace, (float*)base, ctx->tickets,
+                            as_stream(stream), nullptr, rows);
 }
 
 int mx_fp8_expert_forward(mx_ctx* ctx, const void* w1, const void* w3, const void* w2, int32_t H, int32_t I,

@@ -94,12 +94,74 @@ def run(tokens=(1, 16, 2048), iters=20, seed=20261018, ctx=None):
     return out
 
 
+def run_grouped(tokens=(1, 8), iters=20, seed=20261018, ctx=None):
+    """The grouped output projection wo_a (8 groups x 1024 rows over 4096, block-32 E4M3, the reference's
+    own shapes) per call: mx_kv_round32 of the [T, 8, 4096] input, then mx_fp8_grouped_projection, with
+    weights rotated over at least ROTATE_BYTES of copies. Bytes: E4M3 weights + E8M0 scales, the BF16 input
+    read once, rounded / codes / scales written, and the BF16 output."""
+    from . import _lib
+    own = ctx is None
+    ctx = ctx or _lib.Context(0)
+    lib = ctx.lib
+    rows, width, groups = 8192, 4096, 8
+    rng = np.random.default_rng(seed)
+    size = int(lib.cdll.mx_fp8_tiled_bytes(rows, width, 32))
+    w = ctx.malloc(rows * width)
+    ctx.fill_uniform_u8(w, rows * width, seed * 7, 0, 126)
+    swd = ctx.upload(rng.integers(118, 127, (rows // 32, width // 32), dtype=np.uint8))
+    copies = [ctx.malloc(size) for _ in range(max(2, -(-ROTATE_BYTES // size)))]
+    lib.fp8_tile(ctx._h(), C.c_void_p(w), _lib.vp(swd), rows, width, 32, C.c_void_p(copies[0]), None)
+    for c in copies[1:]:
+        ctx.copy_d2d(c, copies[0], size)
+    ctx.sync()
+    ctx.free(w)
+    swd.free()
+    tmax = max(tokens)
+    x = rng.standard_normal((tmax, groups, width)).astype(np.float32)
+    b = x.view(np.uint32).astype(np.uint64)
+    xd = ctx.upload(((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16))
+    rd = ctx.empty((tmax, groups, width), np.uint16)
+    qd = ctx.empty((tmax, groups, width), np.uint8)
+    sd = ctx.empty((tmax, groups, width // 32), np.uint8)
+    yd = ctx.empty((tmax, rows), np.uint16)
+    start, stop = ctx.event(), ctx.event()
+    out = {}
+    try:
+        for t in tokens:
+            def call(i):
+                lib.kv_round32(ctx._h(), _lib.vp(xd), t * groups * width, _lib.vp(rd), _lib.vp(qd), _lib.vp(sd), None)
+                lib.fp8_grouped_projection(ctx._h(), C.c_void_p(copies[i % len(copies)]), groups, rows // groups,
+                                           width, _lib.vp(qd), _lib.vp(sd), t, _lib.vp(yd), None, None)
+            for i in range(3):
+                call(i)
+            ctx.sync()
+            ctx.record(start)
+            for i in range(iters):
+                call(3 + i)
+            ctx.record(stop)
+            us = ctx.elapsed_ms(start, stop) * 1000 / iters
+            nbytes = rows * width + (rows // 32) * (width // 32) + t * groups * width * (2 + 2 + 1) + t * groups * 128 \
+                + t * rows * 2
+            out[t] = {"us": round(us, 2), "GB_per_s": round(nbytes / us / 1e3, 1),
+                      "TFLOP_per_s": round(2 * t * rows * width / us / 1e6, 3), "bytes": nbytes,
+                      "bf16_weight_bytes_avoided": rows * width}
+    finally:
+        for c in copies:
+            ctx.free(c)
+        for d in (xd, rd, qd, sd, yd):
+            d.free()
+        if own:
+            ctx.close()
+    return out
+
+
 def main():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--tokens", type=int, nargs="+", default=[1, 16, 2048])
     p.add_argument("--iters", type=int, default=20)
     args = p.parse_args()
     print(json.dumps(run(tuple(args.tokens), args.iters)), flush=True)
+    print(json.dumps({"wo_a_grouped": run_grouped(iters=args.iters)}), flush=True)
     return 0
 
 

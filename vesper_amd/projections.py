@@ -23,6 +23,9 @@ import numpy as np
 from . import _lib
 
 FP8_LAYOUT = {"wq_a": (1280, 5120), "wq_b": (32768, 1280), "wkv": (512, 5120), "wo_b": (5120, 8192)}
+WO_A = (8192, 4096)          # the grouped output projection: 8 groups of 1024 rows over 4096 (projections.py:34)
+WO_A_GROUPS = 8
+GROUPED_MAX_TOKENS = 32      # grouped calls run on the decode GEMV
 CONFIG3_LAYOUT = {"q_a": (1536, 7168), "q_b": (24576, 1536), "kv_a": (576, 7168), "o": (7168, 16384)}
 MAX_ROWS = 1 << 16
 
@@ -65,6 +68,10 @@ class NativeProjections:
             if rows % 64 or width % 128:
                 raise ValueError("projection rows must be a multiple of 64 and width of 128")
         validate_projection_weights(arrays, layer, self.layout, block)
+        # wo_a (block 32 only) is optional: present, it enables grouped()
+        self.has_wo_a = block == 32 and f"layers.{layer}.attn.wo_a.weight" in arrays
+        if self.has_wo_a:
+            validate_projection_weights(arrays, layer, {"wo_a": WO_A}, 32)
         self.arrays, self.ordinal, self.layer, self.block = arrays, ordinal, layer, block
         self.lock, self.opened, self.ctx = threading.Lock(), False, None
         self.tiled = {}
@@ -76,7 +83,8 @@ class NativeProjections:
             self.ctx = _lib.Context(self.ordinal, 0)
             try:
                 lib = self.ctx.lib
-                for name, (rows, width) in self.layout.items():
+                tiled_layout = dict(self.layout, **({"wo_a": WO_A} if self.has_wo_a else {}))
+                for name, (rows, width) in tiled_layout.items():
                     w = self.ctx.upload(self.arrays[f"layers.{self.layer}.attn.{name}.weight"])
                     s = self.ctx.upload(self.arrays[f"layers.{self.layer}.attn.{name}.scale"])
                     nbytes = int(lib.cdll.mx_fp8_tiled_bytes(rows, width, self.block))
@@ -87,7 +95,7 @@ class NativeProjections:
                     w.free()
                     s.free()
                 self.resident_bytes = sum(int(lib.cdll.mx_fp8_tiled_bytes(r, c, self.block))
-                                          for r, c in self.layout.values())
+                                          for r, c in tiled_layout.values())
                 self.opened = True
                 return self
             except BaseException:
@@ -130,6 +138,57 @@ class NativeProjections:
                         "output_bf16": out.download().reshape(*lead, rows)}
             finally:
                 for d in (x, q, s, trace, out):
+                    d.free()
+
+    def grouped(self, values):
+        """The grouped output projection (projections.py:156-171): values [..., 8, 4096] BF16 ->
+        rounded_bf16, input_fp8, scale_e8m0 [..., 8, 128] and output_bf16 [..., 8, 1024]. kv_round32's
+        codes and scales feed the scaled MFMA directly (the E4M3 weights are never widened to BF16)."""
+        with self.lock:
+            self._ready()
+            if not self.has_wo_a:
+                raise ValueError("grouped() needs the block-32 wo_a weights")
+            if (not isinstance(values, np.ndarray) or values.ndim not in (3, 4) or values.shape[-2:] != (8, 4096)
+                    or not values.flags.c_contiguous):
+                raise ValueError("Expected original eight-group BF16 output-projection input")
+            tokens = validate_values(values.reshape(*values.shape[:-2], 32768), 32768)
+            if tokens > GROUPED_MAX_TOKENS:
+                raise ValueError(f"grouped() takes at most {GROUPED_MAX_TOKENS} tokens per call")
+            rows, width = WO_A
+            x = self.ctx.upload(values)
+            rounded = self.ctx.empty(values.shape, np.uint16)
+            q = self.ctx.empty(values.shape, np.uint8)
+            s = self.ctx.empty((*values.shape[:-1], width // 32), np.uint8)
+            out = self.ctx.empty((tokens, rows), np.uint16)
+            lib, h = self.ctx.lib, self.ctx._h()
+            try:
+                lib.kv_round32(h, _lib.vp(x), values.size, _lib.vp(rounded), _lib.vp(q), _lib.vp(s), None)
+                lib.fp8_grouped_projection(h, C.c_void_p(self.tiled["wo_a"]), WO_A_GROUPS, rows // WO_A_GROUPS, width,
+                                           _lib.vp(q), _lib.vp(s), tokens, _lib.vp(out), None, None)
+                return {"rounded_bf16": rounded.download(), "input_fp8": q.download(), "scale_e8m0": s.download(),
+                        "output_bf16": out.download().reshape(*values.shape[:-2], WO_A_GROUPS, rows // WO_A_GROUPS)}
+            finally:
+                for d in (x, rounded, q, s, out):
+                    d.free()
+
+    def round_window(self, values):
+        """Per-32 post-RoPE FP8 rounding of window KV rows [1 or 2, S, 512] (kv_round32, projections.py:
+        173-188): rounded_bf16, codes_fp8 and scales_e8m0 [B, S, 16]."""
+        with self.lock:
+            self._ready()
+            validate_values(values, 512)
+            if values.ndim != 3 or values.shape[0] not in (1, 2):
+                raise ValueError("Expected bounded window KV rows")
+            x = self.ctx.upload(values)
+            rounded = self.ctx.empty(values.shape, np.uint16)
+            q = self.ctx.empty(values.shape, np.uint8)
+            s = self.ctx.empty((*values.shape[:2], 16), np.uint8)
+            try:
+                self.ctx.lib.kv_round32(self.ctx._h(), _lib.vp(x), values.size, _lib.vp(rounded), _lib.vp(q),
+                                        _lib.vp(s), None)
+                return {"rounded_bf16": rounded.download(), "codes_fp8": q.download(), "scales_e8m0": s.download()}
+            finally:
+                for d in (x, rounded, q, s):
                     d.free()
 
     def __exit__(self, *_):
