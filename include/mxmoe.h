@@ -335,6 +335,10 @@ int mx_cache_destroy(mx_cache* cache);
 int mx_cache_register(mx_cache* cache, int64_t key, const void* host_src);
 /* dev_ptrs[i] <- slot of keys[i] (n <= slots, distinct registered keys); hit[i] (nullable) = 1 if resident. */
 int mx_cache_ensure(mx_cache* cache, const int64_t* keys, int32_t n, void** dev_ptrs, int32_t* hit);
+/* Drop `key`'s slot so it is never served (a slot whose admission audit failed): the key becomes a miss
+ * again and the slot free. The reference publishes a slot only after its audit (src/vesper/cache.py:
+ * 131-146). No-op when the key is not resident. */
+int mx_cache_forget(mx_cache* c, int64_t key);
 int mx_cache_ready_event(mx_cache* cache, void** event);
 int mx_cache_release(mx_cache* cache, const int64_t* keys, int32_t n, void* stream);
 int mx_cache_copy_stream(mx_cache* cache, void** stream);

@@ -97,6 +97,52 @@ def test_tiered_runtime_matches_resident_expert(gpu_ctx):
         pool.close()
 
 
+def test_gpu_sha256_admission_audit(gpu_ctx):
+    """integrity_mode "gpu-sha256": every admitted slot is hashed on the device against its source's digest
+    table before the expert runs. A source byte flipped after its table was taken makes the next admission
+    fail (ValueError) and the slot is dropped, never served; with the byte restored the key is admitted
+    afresh and computes what the resident expert computes."""
+    cfg = MoEConfig(hidden=512, intermediate=256, experts=3, top_k=1, swiglu_limit=10.0, shared=None)
+    rng = np.random.default_rng(21)
+    arrays = [mxfp4_expert(rng, cfg.hidden, cfg.intermediate) for _ in range(3)]
+    pool = HostExpertPool(gpu_ctx, cfg, 3)
+    staging = ExpertBank(gpu_ctx, cfg, 1)
+    try:
+        for i, arr in enumerate(arrays):
+            pool.upload_arrays(i, arr, staging)
+        gpu_ctx.sync()
+        with pytest.raises(ValueError):
+            CacheConfig(integrity_mode="readback")
+        rt = TieredExpertRuntime(gpu_ctx, cfg, pool, {f"0:{i}": i for i in range(3)},
+                                 CacheConfig(primary_slots=2, integrity_mode="gpu-sha256"))
+        x = activations(rng, 2, cfg.hidden)
+        try:
+            for key in ("0:1", "0:0", "0:2"):                   # 0:1 admitted, then evicted
+                rt.forward(key, x, 0.5)
+            snap = rt.snapshot()
+            assert snap["integrity_failures"] == 0 and snap["gpu_audit_payload_bytes"] == 3 * pool.expert_bytes
+            src = np.ctypeslib.as_array((C.c_uint8 * pool.expert_bytes).from_address(pool.ptr(1)))
+            offset = pool.expert_bytes // 3
+            src[offset] ^= 0x10
+            with pytest.raises(ValueError, match="differ"):
+                rt.forward("0:1", x, 0.5)
+            assert rt.snapshot()["integrity_failures"] == 1
+            src[offset] ^= 0x10
+            got = rt.forward("0:1", x, 0.5)
+            assert rt.last_event["source_tier"] == "host_pinned"   # the failed slot was not kept
+            with ResidentExpert(arrays[1], swiglu_limit=10.0, hidden=cfg.hidden, intermediate=cfg.intermediate) as ref:
+                want = ref.forward(x, 0.5)
+            np.testing.assert_array_equal(np.asarray(got["w2"]), np.asarray(want["w2"]))
+            rt.forward("0:1", x, 0.5)
+            assert rt.last_event["source_tier"] == "primary_gpu"   # hits are not re-audited
+            assert rt.snapshot()["gpu_audit_payload_bytes"] == 4 * pool.expert_bytes
+        finally:
+            rt.close()
+    finally:
+        staging.free()
+        pool.close()
+
+
 def test_offload_decode_equals_resident_layers(gpu_ctx):
     cfg = MoEConfig(hidden=512, intermediate=256, experts=16, top_k=4, swiglu_limit=10.0, shared="mxfp4",
                     max_tokens=4)

@@ -58,7 +58,7 @@ def test_closed_or_unowned_input_is_rejected_before_the_kernel():
         checker.digests(123)
     checker.pointer = 456
     owned = {123: 32}
-    checker.ctx = SimpleNamespace(owned_size=lambda p: owned.get(int(p), 0))
+    checker.allocation_size = lambda p: owned.get(int(p), 0)
     with pytest.raises(ValueError, match="owned source"):
         checker.digests(123, size=33)
     with pytest.raises(ValueError, match="owned source"):

@@ -113,6 +113,7 @@ SIGNATURES = {
     "mx_cache_register": ([_P, C.c_int64, _P], C.c_int),
     "mx_cache_ensure": ([_P, _P, _I32, _P, _P], C.c_int),
     "mx_cache_ready_event": ([_P, C.POINTER(_P)], C.c_int),
+    "mx_cache_forget": ([_P, C.c_int64], C.c_int),
     "mx_cache_release": ([_P, _P, _I32, _P], C.c_int),
     "mx_cache_copy_stream": ([_P, C.POINTER(_P)], C.c_int),
     "mx_cache_stats": ([_P, C.POINTER(_U64), C.POINTER(_U64), C.POINTER(_U64), C.POINTER(C.c_double),

@@ -205,6 +205,18 @@ int mx_cache_ensure(mx_cache* c, const int64_t* keys, int32_t n, void** dev_ptrs
   return MX_OK;
 }
 
+int mx_cache_forget(mx_cache* c, int64_t key) {
+  MX_REQUIRE(c != nullptr, "cache is closed");
+  auto it = c->where.find(key);
+  if (it == c->where.end()) return MX_OK;
+  const int s = it->second.first;
+  c->lru.erase(it->second.second);
+  c->where.erase(it);
+  c->owner[s] = -1;
+  c->free_slots.push_back(s);   // its release event, if pending, still orders the next copy into it
+  return MX_OK;
+}
+
 int mx_cache_ready_event(mx_cache* c, void** event) {
   MX_REQUIRE(c != nullptr && event != nullptr, "mx_cache_ready_event: bad arguments");
   *event = c->ready;

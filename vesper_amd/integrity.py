@@ -43,9 +43,12 @@ def hash_chunks(data: np.ndarray, target: np.ndarray):
 class DeviceIntegrity:
     """Owns one bounded device digest table (integrity.py:34-112); the caller owns the context."""
 
-    def __init__(self, ctx: "_lib.Context", size, timings=None):
+    def __init__(self, ctx: "_lib.Context", size, timings=None, allocation_size=None):
+        """allocation_size(pointer) -> bytes owned at that base (default: the context's allocations; the
+        tiered runtime adds its cache slots)."""
         self.shape = digest_shape(size)
         self.ctx, self.size = ctx, size
+        self.allocation_size = allocation_size or ctx.owned_size
         self.timings = timings or Timings()
         self.table = ctx.empty(self.shape, np.uint8)
         self.pointer = self.table.ptr
@@ -58,7 +61,7 @@ class DeviceIntegrity:
         shape = digest_shape(size)
         if size > self.size:
             raise ValueError("Integrity payload exceeds the fixed buffer scope")
-        if self.ctx.owned_size(pointer) < size:
+        if self.allocation_size(pointer) < size:
             raise ValueError("Integrity read exceeds an owned source allocation")
         if target is not None and (target.dtype != np.uint8 or target.shape != shape
                                    or not target.flags.c_contiguous or not target.flags.writeable):

@@ -70,6 +70,10 @@ class ExpertCache:
         """Make `stream` wait for the copies of the last ensure()."""
         self.ctx.lib.stream_wait_event(self.ctx._h(), _lib._stream(stream), C.c_void_p(self.ready_event()))
 
+    def forget(self, key: int):
+        """Drop a key's slot (never served again until copied anew), e.g. after a failed audit."""
+        self.ctx.lib.cache_forget(self.handle, int(key))
+
     def release(self, keys, stream=None):
         keys = np.ascontiguousarray(keys, dtype=np.int64)
         self.ctx.lib.cache_release(self.handle, keys.ctypes.data_as(C.c_void_p), len(keys), _lib._stream(stream))
@@ -121,11 +125,24 @@ class HostExpertPool:
             self.base = 0
 
 
+INTEGRITY_MODES = ("none", "gpu-sha256")
+
+
 @dataclass(frozen=True)
 class CacheConfig:
-    """Slots of the device cache (the reference's primary slots, tiered.py:21-49); RAM is the pool."""
+    """Slots of the device cache (the reference's primary slots, tiered.py:21-49); RAM is the pool.
+
+    integrity_mode "gpu-sha256" audits every admitted slot on the device against the SHA-256 digest table
+    of its pinned source bytes before the expert runs (the reference's gpu-sha256 mode, tiered.py:78-95,
+    cache.py:131-146); "none" admits slots unaudited (the asynchronous offload path's default). The
+    reference's host "readback" mode is not offered."""
     primary_slots: int = 64
     timing: bool = False
+    integrity_mode: str = "none"
+
+    def __post_init__(self):
+        if self.integrity_mode not in INTEGRITY_MODES:
+            raise ValueError(f"integrity_mode must be one of {INTEGRITY_MODES}")
 
 
 class TieredExpertRuntime:
@@ -138,6 +155,15 @@ class TieredExpertRuntime:
         self.cache = ExpertCache(ctx, pool.expert_bytes, cache_config.primary_slots)
         for key, index in self.index_of.items():
             self.cache.register(expert_key(*parse_key(key)), pool.ptr(index))
+        self.audit = cache_config.integrity_mode == "gpu-sha256"
+        self.expected, self.slot_ptrs = {}, set()
+        self.audit_stats = {"integrity_failures": 0, "gpu_audit_payload_bytes": 0, "gpu_audit_digest_d2h_bytes": 0}
+        self.verifier = None
+        if self.audit:
+            from .integrity import DeviceIntegrity
+            size = pool.expert_bytes
+            self.verifier = DeviceIntegrity(ctx, size, allocation_size=lambda p: size if int(p) in self.slot_ptrs
+                                            else ctx.owned_size(p))
         self.lock, self.active, self.last_event = threading.Lock(), False, None
         t, h, i = 16, config.hidden, config.intermediate
         self.work = {"x": ctx.empty((t, h), np.uint16), "route": ctx.empty((t,), np.float32),
@@ -172,6 +198,8 @@ class TieredExpertRuntime:
                 k = expert_key(*parse_key(key))
                 (ptr,), (hit,) = self.cache.ensure([k])
                 self.cache.wait_ready(None)
+                if self.audit and not hit:
+                    self._admit(key, k, ptr)
                 stages = _lib.MxExpertStages(*[w[n].ptr for n in ("q", "s", "w1", "w3", "down_input", "trace",
                                                                   "down_q", "down_s")])
                 self.ctx.lib.expert_forward_tiled(self.ctx._h(), C.c_void_p(ptr), self.config.hidden,
@@ -192,10 +220,33 @@ class TieredExpertRuntime:
             finally:
                 self.active = False
 
+    def _admit(self, key, k, ptr):
+        """Audit a freshly copied slot against its source's digest table; on a mismatch the slot is
+        dropped before anything reads it and ValueError propagates."""
+        from .integrity import digest_shape, hash_chunks
+        if key not in self.expected:
+            size = self.pool.expert_bytes
+            src = np.ctypeslib.as_array((C.c_uint8 * size).from_address(self.pool.ptr(self.index_of[key])))
+            table = np.empty(digest_shape(size), np.uint8)
+            hash_chunks(src, table)
+            self.expected[key] = table
+        self.slot_ptrs.add(int(ptr))
+        try:
+            nbytes = self.verifier.verify(ptr, self.expected[key])
+        except ValueError:
+            self.cache.forget(k)
+            self.audit_stats["integrity_failures"] += 1
+            raise
+        self.audit_stats["gpu_audit_payload_bytes"] += self.pool.expert_bytes
+        self.audit_stats["gpu_audit_digest_d2h_bytes"] += nbytes
+
     def snapshot(self) -> dict:
-        return self.cache.stats()
+        return dict(self.cache.stats(), integrity_mode="gpu-sha256" if self.audit else "none", **self.audit_stats)
 
     def close(self):
+        if self.verifier is not None:
+            self.verifier.close()
+            self.verifier = None
         self.cache.close()
         for d in self.work.values():
             d.free()
