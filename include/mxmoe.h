@@ -89,6 +89,16 @@ int mx_copy_kernel(mx_ctx* ctx, void* dst, const void* src, uint64_t bytes, void
  * (src/vesper/tiered.py:78-95). data and digests 16-byte aligned and not overlapping. */
 int mx_sha256_chunks(mx_ctx* ctx, const void* data, uint64_t bytes, void* digests, void* stream);
 
+/* Batched admission audit: for each of the n slots (device pointers, `bytes` each) hash every 4 KiB chunk
+ * as mx_sha256_chunks does, compare with expected[i] (device digest table, ceil(bytes / 4096) x 32 bytes)
+ * and add slot i's count of differing chunks to mismatches[counters[i]] (device; counters NULL = i). The
+ * counters are not cleared, so several admissions in flight can accumulate into per-expert counters that
+ * the host reads and clears after synchronising. One launch per 64 slots on `stream` (e.g. the cache's
+ * copy stream right after the copies it audits). The batched, asynchronous form of DeviceIntegrity.verify
+ * (src/vesper/integrity.py:67-94); each slot must hold `bytes`. */
+int mx_sha256_verify(mx_ctx* ctx, const void* const* slots, const void* const* expected, const int32_t* counters,
+                     int32_t n, uint64_t bytes, uint32_t* mismatches, void* stream);
+
 /* Streaming read of `bytes` (a multiple of 16 MiB, 16-byte aligned source) by the fastest plain read
  * kernel measured on MI355X (4096 workgroups of contiguous ranges, non-temporal 16-byte loads, three
  * 4 KB steps in flight per wave): the HBM read rate the weight-streaming kernels are compared with.

@@ -143,7 +143,11 @@ def test_gpu_sha256_admission_audit(gpu_ctx):
         pool.close()
 
 
-def test_offload_decode_equals_resident_layers(gpu_ctx):
+@pytest.mark.parametrize("audit", [False, True])
+def test_offload_decode_equals_resident_layers(gpu_ctx, audit):
+    """With audit=True every admitted slot is also verified on the copy stream (mx_sha256_verify) against
+    digest tables taken on the device from the pinned sources: a clean run passes check_audit, and a source
+    byte flipped before a forced admission is reported, dropped from the cache, and passes once restored."""
     cfg = MoEConfig(hidden=512, intermediate=256, experts=16, top_k=4, swiglu_limit=10.0, shared="mxfp4",
                     max_tokens=4)
     L, T, steps = 3, 4, 3
@@ -162,7 +166,8 @@ def test_offload_decode_equals_resident_layers(gpu_ctx):
             banks.append(bank)
             layers.append(MoELayer(gpu_ctx, cfg, np.zeros((cfg.experts, cfg.hidden), np.float32), bank))
         off = OffloadDecode(gpu_ctx, cfg, L, lambda l, e: (pool, l * cfg.experts + e),
-                            [banks[l].tiled_ptr(cfg.experts) for l in range(L)], cache, banks[0].tiled_ptr(0))
+                            [banks[l].tiled_ptr(cfg.experts) for l in range(L)], cache, banks[0].tiled_ptr(0),
+                            audit=audit)
         x = gpu_ctx.upload(bf16_bits(activations(rng, T, cfg.hidden)))
         ys = [gpu_ctx.empty((T, cfg.hidden), np.uint16) for _ in range(L)]
         ref_ys = [gpu_ctx.empty((T, cfg.hidden), np.uint16) for _ in range(L)]
@@ -184,6 +189,21 @@ def test_offload_decode_equals_resident_layers(gpu_ctx):
                     np.testing.assert_array_equal(ys[l].download(), ref_ys[l].download(), err_msg=f"step {step} layer {l}")
             st = cache.stats()
             assert st["misses"] > 20 and st["hits"] > 0
+            if audit:
+                off.check_audit()
+                assert off.audited_slots == st["misses"]
+                ids = np.tile(np.array([3, 5, 7, 9], np.int32), (T, 1))
+                routing = [(ids, np.full((T, cfg.top_k), 0.25, np.float32))] * L
+                off.load_routing(routing)
+                src = np.ctypeslib.as_array((C.c_uint8 * pool.expert_bytes).from_address(pool.ptr(5)))   # layer 0, expert 5
+                src[777] ^= 0x01
+                cache.forget(expert_key(0, 5))
+                off.step_device(x.ptr, T, [y.ptr for y in ys], [r[0] for r in routing])
+                with pytest.raises(ValueError, match="0:5"):
+                    off.check_audit()
+                src[777] ^= 0x01
+                off.step_device(x.ptr, T, [y.ptr for y in ys], [r[0] for r in routing])
+                off.check_audit()
         finally:
             off.close()
             for d in [x] + ys + ref_ys:

@@ -131,6 +131,7 @@ SIGNATURES = {
     "mx_fp8_grouped_projection": ([_P, _P, _I32, _I32, _I32, _P, _P, _I32, _P, _P, _P], C.c_int),
     "mx_kv_round32": ([_P, _P, _I64, _P, _P, _P, _P], C.c_int),
     "mx_sha256_chunks": ([_P, _P, _U64, _P, _P], C.c_int),
+    "mx_sha256_verify": ([_P, C.POINTER(_P), C.POINTER(_P), _P, _I32, _U64, _P, _P], C.c_int),
     "mx_owned_size": ([_P, _P, C.POINTER(_U64)], C.c_int),
     "mx_check_e4m3_pack": ([_P, C.POINTER(_U64)], C.c_int),
 }

@@ -101,20 +101,10 @@ __device__ __forceinline__ void to_words(uint32_t (&w)[16], const uint4 (&v)[4])
   }
 }
 
-// grid ceil(chunks / 256) x 256 threads: lane c hashes bytes [4096 c, min(4096 (c + 1), bytes)) and
-// writes its 32-byte digest (the eight state words big-endian) to digests + 32 c.
-__global__ __launch_bounds__(256) void sha256_chunks_kernel(const uint8_t* __restrict__ data,
-                                                            uint8_t* __restrict__ digests, uint64_t bytes,
-                                                            uint32_t chunks) {
-  const uint32_t chunk = blockIdx.x * 256u + threadIdx.x;
-  if (chunk >= chunks) return;
-  const uint64_t start = (uint64_t)chunk * kChunkBytes;
-  const uint32_t len = (uint32_t)(bytes - start < kChunkBytes ? bytes - start : kChunkBytes);
-  const uint8_t* src = data + start;
-  uint32_t h[8];
+// SHA-256 of the len (1..4096) bytes at src into h (the eight state words).
+__device__ __forceinline__ void hash_chunk(const uint8_t* src, uint32_t len, uint32_t (&h)[8]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) h[i] = kInitial[i];
-
   // Blocks wholly inside the chunk's bytes come from memory (block b + 1 is in flight while block b is
   // compressed). Padding (section 5.1.1) follows: the rem = len % 64 remaining bytes, the 0x80 marker,
   // zeros, and the 64-bit message length in bits in the last two words, with one more block when
@@ -156,11 +146,56 @@ __global__ __launch_bounds__(256) void sha256_chunks_kernel(const uint8_t* __res
     }
     compress(h, w);
   }
+}
+
+// the digest bytes (state words big-endian) as two 16-byte vectors
+__device__ __forceinline__ void digest_words(const uint32_t (&h)[8], uint4& d0, uint4& d1) {
+  d0 = make_uint4(__builtin_bswap32(h[0]), __builtin_bswap32(h[1]), __builtin_bswap32(h[2]), __builtin_bswap32(h[3]));
+  d1 = make_uint4(__builtin_bswap32(h[4]), __builtin_bswap32(h[5]), __builtin_bswap32(h[6]), __builtin_bswap32(h[7]));
+}
+
+// grid ceil(chunks / 256) x 256 threads: lane c hashes bytes [4096 c, min(4096 (c + 1), bytes)) and
+// writes its 32-byte digest to digests + 32 c.
+__global__ __launch_bounds__(256) void sha256_chunks_kernel(const uint8_t* __restrict__ data,
+                                                            uint8_t* __restrict__ digests, uint64_t bytes,
+                                                            uint32_t chunks) {
+  const uint32_t chunk = blockIdx.x * 256u + threadIdx.x;
+  if (chunk >= chunks) return;
+  const uint64_t start = (uint64_t)chunk * kChunkBytes;
+  const uint32_t len = (uint32_t)(bytes - start < kChunkBytes ? bytes - start : kChunkBytes);
+  uint32_t h[8];
+  hash_chunk(data + start, len, h);
   uint4* out = reinterpret_cast<uint4*>(digests + (size_t)chunk * 32);
-  out[0] = make_uint4(__builtin_bswap32(h[0]), __builtin_bswap32(h[1]), __builtin_bswap32(h[2]),
-                      __builtin_bswap32(h[3]));
-  out[1] = make_uint4(__builtin_bswap32(h[4]), __builtin_bswap32(h[5]), __builtin_bswap32(h[6]),
-                      __builtin_bswap32(h[7]));
+  digest_words(h, out[0], out[1]);
+}
+
+// Admission audit of up to kVerifyBatch slots in one launch: the slots' device bytes and their expected
+// digest tables (device memory, chunk c's 32 bytes at 32 c).
+constexpr int kVerifyBatch = 64;
+struct VerifyBatch {
+  const uint8_t* slot[kVerifyBatch];
+  const uint8_t* expected[kVerifyBatch];
+  int32_t counter[kVerifyBatch];   // the mismatch counter each slot adds to
+};
+
+// grid ceil(n x chunks / 256) x 256 threads: lane i hashes chunk i % chunks of slot i / chunks, compares
+// the digest with the expected one and counts a difference in mismatches[counter[slot]] (a vector atomic).
+__global__ __launch_bounds__(256) void sha256_verify_kernel(VerifyBatch batch, int n, uint64_t bytes, uint32_t chunks,
+                                                            uint32_t* __restrict__ mismatches) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  const uint32_t s = (uint32_t)(i / chunks), chunk = (uint32_t)(i % chunks);
+  if (s >= (uint32_t)n) return;
+  const uint64_t start = (uint64_t)chunk * kChunkBytes;
+  const uint32_t len = (uint32_t)(bytes - start < kChunkBytes ? bytes - start : kChunkBytes);
+  uint32_t h[8];
+  hash_chunk(batch.slot[s] + start, len, h);
+  uint4 d0, d1;
+  digest_words(h, d0, d1);
+  const uint4* want = reinterpret_cast<const uint4*>(batch.expected[s] + (size_t)chunk * 32);
+  const uint4 w0 = want[0], w1 = want[1];
+  const bool same = d0.x == w0.x && d0.y == w0.y && d0.z == w0.z && d0.w == w0.w && d1.x == w1.x && d1.y == w1.y &&
+                    d1.z == w1.z && d1.w == w1.w;
+  if (!same) atomicAdd(mismatches + batch.counter[s], 1u);
 }
 
 }  // namespace
@@ -180,5 +215,36 @@ extern "C" int mx_sha256_chunks(mx_ctx* ctx, const void* data, uint64_t bytes, v
   hipLaunchKernelGGL(sha256_chunks_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0,
                      as_stream(stream), d, o, bytes, (uint32_t)chunks);
   MX_LAUNCH_CHECK("sha256_chunks_kernel");
+  return MX_OK;
+}
+
+extern "C" int mx_sha256_verify(mx_ctx* ctx, const void* const* slots, const void* const* expected,
+                                const int32_t* counters, int32_t n, uint64_t bytes, uint32_t* mismatches,
+                                void* stream) {
+  if (int s = use(ctx)) return s;
+  MX_REQUIRE(n >= 0, "mx_sha256_verify: negative slot count");
+  if (n == 0) return MX_OK;
+  MX_REQUIRE(slots && expected && mismatches, "mx_sha256_verify: null pointer");
+  MX_REQUIRE(bytes > 0 && bytes <= kMaxPayload, "Invalid bounded integrity payload size");
+  for (int i = 0; i < n; ++i) {
+    MX_REQUIRE(slots[i] && expected[i] && ((uintptr_t)slots[i] & 15) == 0 && ((uintptr_t)expected[i] & 15) == 0,
+               "mx_sha256_verify: slot %d: 16-byte aligned device pointers required", i);
+    MX_REQUIRE(!counters || counters[i] >= 0, "mx_sha256_verify: slot %d: negative counter index", i);
+  }
+  const uint64_t chunks = (bytes + kChunkBytes - 1) / kChunkBytes;
+  hipStream_t st = as_stream(stream);
+  for (int base = 0; base < n; base += kVerifyBatch) {
+    VerifyBatch b{};
+    const int m = n - base < kVerifyBatch ? n - base : kVerifyBatch;
+    for (int i = 0; i < m; ++i) {
+      b.slot[i] = (const uint8_t*)slots[base + i];
+      b.expected[i] = (const uint8_t*)expected[base + i];
+      b.counter[i] = counters ? counters[base + i] : base + i;
+    }
+    const uint64_t lanes = (uint64_t)m * chunks;
+    hipLaunchKernelGGL(sha256_verify_kernel, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, st, b, m, bytes,
+                       (uint32_t)chunks, mismatches);
+    MX_LAUNCH_CHECK("sha256_verify_kernel");
+  }
   return MX_OK;
 }

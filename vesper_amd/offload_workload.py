@@ -16,6 +16,10 @@ every expert resident.
 
 At most two steps are in flight (the host waits for step s - 2 before enqueuing step s).
 
+Audited replay: the same trace through a fresh cache with the gpu-sha256 admission audit on (each layer's
+admitted slots hashed on the copy stream and compared with digest tables in HBM before the compute
+stream may use them); reported as audited step us and its overhead over the unaudited step.
+
 Reported: step us (HIP events on the compute stream), copy us per step (a fresh cache replaying the same
 trace with copies only: the same misses, no compute between them), compute-only us per step, overlap = 1 - (t_step - max(t_copy, t_compute)) /
 min(t_copy, t_compute), the pinned H2D rate of one large copy, and cache hits / misses / bytes.
@@ -117,6 +121,24 @@ def run(steps=10, warmup=4, layers=8, tokens=4, resident_frac=0.25, seed=2026101
     off.close()
     cache.close()
 
+    # audited: the same trace through a fresh cache, every admitted slot verified on the copy stream against
+    # digest tables held in HBM (the reference's gpu-sha256 admission mode), checked once at the end
+    cache = ExpertCache(ctx, pool.expert_bytes, slots)
+    off = OffloadDecode(ctx, cfg, layers, lambda l, e: (pool, e), [bank.tiled_ptr(cfg.experts)] * layers, cache,
+                        bank.tiled_ptr(0), audit=True)
+    for s in range(warmup):
+        enqueue(s)
+    ctx.sync(off.stream)
+    ctx.record(e0, off.stream)
+    for s in range(warmup, warmup + steps):
+        enqueue(s)
+    ctx.record(e1, off.stream)
+    t_audited = ctx.elapsed_ms(e0, e1) * 1000 / steps
+    off.check_audit()
+    audited_per_step = off.audited_slots / (warmup + steps)
+    off.close()
+    cache.close()
+
     # copy-only: a fresh cache replays the same trace (same misses) with no compute between the copies
     cache = ExpertCache(ctx, pool.expert_bytes, slots)
     off = OffloadDecode(ctx, cfg, layers, lambda l, e: (pool, e), [bank.tiled_ptr(cfg.experts)] * layers, cache,
@@ -161,7 +183,9 @@ def run(steps=10, warmup=4, layers=8, tokens=4, resident_frac=0.25, seed=2026101
            "h2d_GB_per_s_single_copy": round(h2d_gbs, 1),
            "streamed_GB_per_s": round(st["bytes_copied"] / steps / (t_step * 1e-6) / 1e9, 1),
            "misses_per_step": st["misses"] / steps, "hits_per_step": st["hits"] / steps,
-           "bytes_per_step": st["bytes_copied"] // steps}
+           "bytes_per_step": st["bytes_copied"] // steps,
+           "audited_step_us": round(t_audited, 1), "audit_overhead_frac": round(t_audited / t_step - 1.0, 4),
+           "audited_slots_per_step": audited_per_step}
     layer.close()
     off.close()
     cache.close()

@@ -260,10 +260,17 @@ class OffloadDecode:
     routing: per layer, ensure its experts (copies on the cache stream), make the compute stream wait,
     re-point the layer's table (one launch), decode, release the slots -- all asynchronous, so the next
     layer's copies overlap this layer's compute.
+
+    audit=True is the reference's gpu-sha256 admission mode for this asynchronous path: every expert's
+    digest table is taken once from its pinned source bytes (hashed on the device) and kept in HBM; the
+    slots a layer admits are verified in one launch on an audit stream that waits for their copies, and
+    the compute stream waits for the audit (so no expert runs unverified) while the copy stream goes on
+    with the next layer's copies; differing chunks accumulate in per-expert counters. check_audit() (after a synchronisation) refuses the steps since the last check if any
+    admitted slot differed, and drops those slots from the cache.
     """
 
     def __init__(self, ctx: _lib.Context, config: MoEConfig, layers: int, pool_of, shared_ptrs, cache: ExpertCache,
-                 placeholder_ptr: int):
+                 placeholder_ptr: int, audit: bool = False):
         self.ctx, self.config, self.layers, self.cache = ctx, config, int(layers), cache
         self.lib = ctx.lib
         self.handles = []
@@ -287,6 +294,26 @@ class OffloadDecode:
         self.ids = [ctx.empty((t, k), np.int32) for _ in range(self.layers)]
         self.wts = [ctx.empty((t, k), np.float32) for _ in range(self.layers)]
         self._owned += self.ids + self.wts
+        self.audit = bool(audit)
+        if self.audit:
+            from .integrity import digest_shape
+            self.slot_bytes = cache.slot_bytes
+            self.table_bytes = digest_shape(self.slot_bytes)[0] * 32
+            self.tables = ctx.empty((self.layers * config.experts, self.table_bytes), np.uint8)
+            self.mismatch = ctx.upload(np.zeros((self.layers, config.experts), np.uint32))
+            self._owned += [self.tables, self.mismatch]
+            for layer in range(self.layers):
+                for e in range(config.experts):
+                    pool, index = pool_of(layer, e)
+                    self.lib.sha256_chunks(ctx._h(), C.c_void_p(pool.ptr(index)), self.slot_bytes,
+                                           C.c_void_p(self._table(layer, e)), _lib._stream(self.stream))
+            ctx.sync(self.stream)
+            self.audit_stream = ctx.stream()
+            self.audit_done = ctx.event()
+            self.audited_slots = 0
+
+    def _table(self, layer: int, expert: int) -> int:
+        return self.tables.ptr + (layer * self.config.experts + expert) * self.table_bytes
 
     def load_routing(self, routing):
         """routing[layer] = (ids [T, k] int32, weights [T, k] FP32), copied to the device (synchronously)."""
@@ -299,7 +326,20 @@ class OffloadDecode:
         for layer in range(self.layers):
             experts = np.unique(routing_host[layer][:tokens])
             keys = [expert_key(layer, int(e)) for e in experts]
-            ptrs, _ = self.cache.ensure(keys)
+            ptrs, hits = self.cache.ensure(keys)
+            if self.audit:
+                miss = [i for i in range(len(keys)) if not hits[i]]
+                if miss:
+                    n = len(miss)
+                    slots = (C.c_void_p * n)(*[ptrs[i] for i in miss])
+                    tables = (C.c_void_p * n)(*[self._table(layer, int(experts[i])) for i in miss])
+                    counters = (C.c_int32 * n)(*[layer * self.config.experts + int(experts[i]) for i in miss])
+                    self.cache.wait_ready(self.audit_stream)
+                    self.lib.sha256_verify(self.ctx._h(), slots, tables, counters, n, self.slot_bytes,
+                                           C.c_void_p(self.mismatch.ptr), _lib._stream(self.audit_stream))
+                    self.ctx.record(self.audit_done, self.audit_stream)
+                    self.lib.stream_wait_event(self.ctx._h(), _lib._stream(self.stream), C.c_void_p(self.audit_done))
+                    self.audited_slots += n
             self.cache.wait_ready(self.stream)
             arr_e = (C.c_int32 * len(experts))(*[int(e) for e in experts])
             arr_p = (C.c_void_p * len(experts))(*ptrs)
@@ -310,7 +350,27 @@ class OffloadDecode:
                                        C.c_void_p(int(y_ptrs[layer])), _lib._stream(self.stream))
             self.cache.release(keys, self.stream)
 
+    def check_audit(self):
+        """After a synchronisation: raise ValueError if any slot admitted since the last check differed from
+        its source's digests (those keys are dropped from the cache and the counters cleared)."""
+        if not self.audit:
+            return
+        self.ctx.sync()
+        counts = self.mismatch.download()
+        bad = np.argwhere(counts > 0)
+        if len(bad):
+            for layer, e in bad:
+                self.cache.forget(expert_key(int(layer), int(e)))
+            self.mismatch.upload(np.zeros_like(counts))
+            raise ValueError("GPU expert bytes differ from verified original SHA-256 chunks: "
+                             + ", ".join(f"{int(l)}:{int(e)}" for l, e in bad))
+
     def close(self):
+        if self.audit:
+            self.ctx.sync(self.audit_stream)
+            self.ctx.destroy_stream(self.audit_stream)
+            self.ctx.destroy_event(self.audit_done)
+            self.audit = False
         for h in self.handles:
             self.lib.layer_destroy(h)
         self.handles = []
