@@ -67,3 +67,12 @@ def test_closed_or_unowned_input_is_rejected_before_the_kernel():
         checker.digests(123, size=4097)
     with pytest.raises(ValueError, match="complete digest table"):
         checker.digests(123, size=32, target=np.zeros((2, 32), np.uint8))
+
+
+def test_cache_config_accepts_only_the_supported_integrity_modes():
+    from vesper_amd.tiered import CacheConfig
+    assert CacheConfig().integrity_mode == "none"
+    assert CacheConfig(integrity_mode="gpu-sha256").integrity_mode == "gpu-sha256"
+    for bad in ("readback", "", "sha256", None):
+        with pytest.raises(ValueError):
+            CacheConfig(integrity_mode=bad)
