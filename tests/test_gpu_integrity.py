@@ -91,3 +91,45 @@ def test_entry_point_refusals(gpu_ctx):
     finally:
         src.free()
         out.free()
+
+
+def test_batched_verify_counts_differing_chunks_per_slot(gpu_ctx):
+    """mx_sha256_verify over 70 slots (two launches of up to 64): with counters NULL slot i adds its count of
+    differing chunks to mismatches[i]; explicit counters map slots onto shared counters, which accumulate
+    across calls (the call does not clear them)."""
+    n, size = 70, 3 * 4096 + 100                               # three whole chunks and a short one
+    rng = np.random.default_rng(70)
+    data = rng.integers(0, 256, (n, size), dtype=np.uint8)
+    tables = np.stack([digest_table(row) for row in data])       # [n, 4, 32]
+    stride = (size + 255) // 256 * 256
+    slots = gpu_ctx.empty((n, stride), np.uint8)
+    exp = gpu_ctx.upload(tables)
+    counts = gpu_ctx.upload(np.zeros(n, np.uint32))
+    try:
+        host = np.zeros((n, stride), np.uint8)
+        host[:, :size] = data
+        host[3, 5000] ^= 0x80                                   # slot 3, chunk 1
+        host[67, 1] ^= 0x01                                     # slot 67 (second launch), chunk 0
+        host[67, size - 1] ^= 0x01                              # and its short last chunk
+        slots.upload(host)
+        ptrs = (C.c_void_p * n)(*[slots.ptr + i * stride for i in range(n)])
+        tabs = (C.c_void_p * n)(*[exp.ptr + i * tables[0].nbytes for i in range(n)])
+        lib = gpu_ctx.lib
+        lib.sha256_verify(gpu_ctx._h(), ptrs, tabs, None, n, size, _lib.vp(counts), None)
+        gpu_ctx.sync()
+        want = np.zeros(n, np.uint32)
+        want[3], want[67] = 1, 2
+        np.testing.assert_array_equal(counts.download(), want)
+        to_zero = (C.c_int32 * n)(*([0] * n))
+        lib.sha256_verify(gpu_ctx._h(), ptrs, tabs, to_zero, n, size, _lib.vp(counts), None)
+        gpu_ctx.sync()
+        want[0] += 3
+        np.testing.assert_array_equal(counts.download(), want)
+        with pytest.raises(ValueError):
+            lib.sha256_verify(gpu_ctx._h(), ptrs, tabs, None, n, 0, _lib.vp(counts), None)
+        bad = (C.c_int32 * n)(*([-1] + [0] * (n - 1)))
+        with pytest.raises(ValueError):
+            lib.sha256_verify(gpu_ctx._h(), ptrs, tabs, bad, n, size, _lib.vp(counts), None)
+    finally:
+        for d in (slots, exp, counts):
+            d.free()
