@@ -52,7 +52,7 @@ __global__ void act_quant32_kernel(const In* __restrict__ x, uint8_t* __restrict
   amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
   const uint32_t code = mx::act_scale_code(amax);
   if (live) {
-    q[block * 32 + lane] = (uint8_t)mx::act_quant_value(v, mx::e8m0_value(code));
+    q[block * 32 + lane] = (uint8_t)mx::act_quant_pow2(v, 1.0f / mx::e8m0_value(code));
     if (lane == 0) s[block] = (uint8_t)code;
   }
 }
@@ -85,10 +85,11 @@ __global__ __launch_bounds__(256) void act_quant32_v8_kernel(const uint16_t* __r
     const float sc = mx::e8m0_value(code);
     if (live) {
       uint2 out;
-      out.x = mx::act_quant_value(f[0], sc) | (mx::act_quant_value(f[1], sc) << 8) |
-              (mx::act_quant_value(f[2], sc) << 16) | (mx::act_quant_value(f[3], sc) << 24);
-      out.y = mx::act_quant_value(f[4], sc) | (mx::act_quant_value(f[5], sc) << 8) |
-              (mx::act_quant_value(f[6], sc) << 16) | (mx::act_quant_value(f[7], sc) << 24);
+      const float r = 1.0f / sc;   // exact: sc is a power of two
+      out.x = mx::act_quant_pow2(f[0], r) | (mx::act_quant_pow2(f[1], r) << 8) |
+              (mx::act_quant_pow2(f[2], r) << 16) | (mx::act_quant_pow2(f[3], r) << 24);
+      out.y = mx::act_quant_pow2(f[4], r) | (mx::act_quant_pow2(f[5], r) << 8) |
+              (mx::act_quant_pow2(f[6], r) << 16) | (mx::act_quant_pow2(f[7], r) << 24);
       reinterpret_cast<uint2*>(q)[i] = out;
       if ((i & 3) == 0) s[i >> 2] = (uint8_t)code;
       if (rounded) {

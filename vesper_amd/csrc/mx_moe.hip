@@ -604,7 +604,7 @@ __global__ __launch_bounds__(256) void router_kernel(RouterArgs a) {
       for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
       amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
       const uint32_t code = mx::act_scale_code(amax);
-      a.xq[(size_t)b * 32 + l32] = (uint8_t)mx::act_quant_value(v, mx::e8m0_value(code));
+      a.xq[(size_t)b * 32 + l32] = (uint8_t)mx::act_quant_pow2(v, 1.0f / mx::e8m0_value(code));
       if (l32 == 0) a.xs[b] = (uint8_t)code;
     }
   }
@@ -903,7 +903,8 @@ __device__ __forceinline__ void gateup_quantize_block(const ExpertArgs& a, int s
   amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
   const uint32_t code = mx::act_scale_code(amax);
   const float sc = mx::e8m0_value(code);
-  const uint32_t q0 = mx::act_quant_value(v0, sc), q1 = mx::act_quant_value(v1, sc);
+  const float inv = 1.0f / sc;   // exact: sc is a power of two
+  const uint32_t q0 = mx::act_quant_pow2(v0, inv), q1 = mx::act_quant_pow2(v1, inv);
   const size_t r = (size_t)(a.plan->slot_row0[s] + tn);
   *reinterpret_cast<uint16_t*>(a.dq + r * I + g * 32 + 2 * j2) = (uint16_t)(q0 | (q1 << 8));
   if (j2 == 0) a.ds[r * (I / 32) + g] = (uint8_t)code;

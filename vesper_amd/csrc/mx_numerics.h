@@ -114,6 +114,15 @@ MX_HD uint32_t act_quant_value(float x, float s) {
   return e4m3_encode(y);
 }
 
+// act_quant_value for a power-of-two scale s = 2^e (an E8M0 value), given inv_s = 1 / s = 2^-e: x * 2^-e
+// and x / 2^e are the same exact value, correctly rounded by either operation (in the subnormal range
+// too), so the codes are identical; a multiply replaces an IEEE division per value.
+MX_HD uint32_t act_quant_pow2(float x, float inv_s) {
+  float y = x * inv_s;
+  y = y > 448.f ? 448.f : (y < -448.f ? -448.f : y);
+  return e4m3_encode(y);
+}
+
 // FP32 scale of one per-token 128-wide activation block (the FP32-scale FP8 profile):
 // s = f32(max(amax, 1e-4)) / 448 with one IEEE division; the codes are then act_quant_value(x, s).
 MX_HD float act128_scale(float amax) {
