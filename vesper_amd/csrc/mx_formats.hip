@@ -85,11 +85,11 @@ __global__ __launch_bounds__(256) void act_quant32_v8_kernel(const uint16_t* __r
     const float sc = mx::e8m0_value(code);
     if (live) {
       uint2 out;
-      const float r = 1.0f / sc;   // exact: sc is a power of two
-      out.x = mx::act_quant_pow2(f[0], r) | (mx::act_quant_pow2(f[1], r) << 8) |
-              (mx::act_quant_pow2(f[2], r) << 16) | (mx::act_quant_pow2(f[3], r) << 24);
-      out.y = mx::act_quant_pow2(f[4], r) | (mx::act_quant_pow2(f[5], r) << 8) |
-              (mx::act_quant_pow2(f[6], r) << 16) | (mx::act_quant_pow2(f[7], r) << 24);
+      // act_quant_pow2 of the 8 values: x * (1 / sc) is exact scaling (sc a power of two), and the
+      // hardware pair conversion equals mx::e4m3_encode of the clamped value for every FP32 input
+      const float r = 1.0f / sc;
+      out.x = mxd::e4m3x4(f[0] * r, f[1] * r, f[2] * r, f[3] * r);
+      out.y = mxd::e4m3x4(f[4] * r, f[5] * r, f[6] * r, f[7] * r);
       reinterpret_cast<uint2*>(q)[i] = out;
       if ((i & 3) == 0) s[i >> 2] = (uint8_t)code;
       if (rounded) {
