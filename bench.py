@@ -138,7 +138,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the MoE path is single-GPU here "
-                                   "(expert-parallel sharding is described in DESIGN.md, not run)",
+                                   "(expert-parallel sharding is designed, not run)",
                           "n_gpus": args.gpus}))
         return 2
     from vesper_amd import _lib

@@ -13,8 +13,8 @@ The routing weight multiplies the FP32 product before W2 (docs/moe-arithmetic-va
 exp is evaluated in float64 and rounded once to FP32; the HIP kernel does the
 same, so both agree bit for bit except where two float64 exp results straddle
 an FP32 rounding boundary (probability ~2^-28 per element). The reference's
-CUDA expf is not correctly rounded, which is why SURVEY marks these stages
-tolerance-only against the reference itself.
+CUDA expf is not correctly rounded, which is why these stages are compared with
+a tolerance against the reference itself.
 """
 
 from __future__ import annotations

@@ -719,7 +719,7 @@ struct ExpertArgs {
   float* trace;
 };
 
-// Operand layout of V_MFMA_SCALE_F32_16X16X128_F8F6F4 (measured on gfx950):
+// Operand layout of V_MFMA_SCALE_F32_16X16X128_F8F6F4 (measured on gfx950 with one-hot probe kernels):
 //   A (FP4, 4 VGPRs): lane l holds row l%16, K = 32*(l/16) + j for nibble j (low nibble first),
 //                     i.e. one whole 16-byte MX block of the reference layout.
 //   B (FP8, 8 VGPRs): lane l holds column l%16; bytes 0-15 are K = 16*(l/16) + j and bytes 16-31
