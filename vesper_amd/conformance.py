@@ -14,18 +14,24 @@ from . import _lib
 
 
 def compare(expected: np.ndarray, actual: np.ndarray, label: str) -> dict:
-    if expected.shape != actual.shape or expected.dtype != actual.dtype:
+    """Exact-bit comparison report with the reference's result keys (src/vesper/conformance.py:15-28).
+
+    Floating arrays are compared as their storage words, so signed zeros differ; two NaNs of any payload
+    count as equal. Other dtypes compare storage values directly."""
+    if (expected.shape, expected.dtype) != (actual.shape, actual.dtype):
         return {"check": label, "status": "fail", "reason": "shape_or_dtype_mismatch"}
-    if expected.dtype == np.float32:
-        same = (expected.view(np.uint32) == actual.view(np.uint32)) | (np.isnan(expected) & np.isnan(actual))
-        semantics = "exact_float32_bits_with_NaN_classification; signed_zero_preserved"
+    floating = expected.dtype.kind == "f"
+    if floating:
+        word = np.dtype(f"u{expected.dtype.itemsize}")
+        differs = np.not_equal(expected.view(word), actual.view(word))
+        np.logical_and(differs, ~np.logical_and(np.isnan(expected), np.isnan(actual)), out=differs)
     else:
-        same = expected == actual
-        semantics = "exact_storage_bits"
-    mismatches = int(np.count_nonzero(~same))
-    return {"check": label, "status": "pass" if not mismatches else "fail", "elements": int(expected.size),
-            "mismatches": mismatches, "comparison": semantics,
-            "first_mismatch_indices": np.flatnonzero(~same)[:8].tolist()}
+        differs = np.not_equal(expected, actual)
+    where = np.flatnonzero(differs)
+    semantics = (f"exact_float{8 * expected.dtype.itemsize}_bits_with_NaN_classification; signed_zero_preserved"
+                 if floating else "exact_storage_bits")
+    return {"check": label, "status": "fail" if where.size else "pass", "elements": int(expected.size),
+            "mismatches": int(where.size), "comparison": semantics, "first_mismatch_indices": where[:8].tolist()}
 
 
 def decode_fp4(ctx: _lib.Context, packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
