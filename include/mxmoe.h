@@ -99,6 +99,15 @@ int mx_sha256_chunks(mx_ctx* ctx, const void* data, uint64_t bytes, void* digest
 int mx_sha256_verify(mx_ctx* ctx, const void* const* slots, const void* const* expected, const int32_t* counters,
                      int32_t n, uint64_t bytes, uint32_t* mismatches, void* stream);
 
+/* Audit gate for outputs computed from audited slots: if any of counters[index[i]] (device mismatch counters
+ * as mx_sha256_verify fills them, n_counters of them; index a host array, n <= 512) is nonzero, the `count`
+ * BF16 values at y are overwritten with NaN, ordered on `stream` after the work that wrote y. Placed after
+ * each layer that read audited slots, it keeps an output computed from bytes that failed their audit from
+ * passing as a number until the host has read the counters and dropped the slots -- the asynchronous
+ * counterpart of the reference's refusal before a failing slot is used (src/vesper/cache.py:131-146). */
+int mx_audit_gate(mx_ctx* ctx, const uint32_t* counters, int32_t n_counters, const int32_t* index, int32_t n,
+                  uint16_t* y, uint64_t count, void* stream);
+
 /* Streaming read of `bytes` (a multiple of 16 MiB, 16-byte aligned source) by the fastest plain read
  * kernel measured on MI355X (4096 workgroups of contiguous ranges, non-temporal 16-byte loads, three
  * 4 KB steps in flight per wave): the HBM read rate the weight-streaming kernels are compared with.
@@ -203,6 +212,7 @@ int mx_untile_expert(mx_ctx* ctx, const void* tiled, int32_t hidden, int32_t int
 int mx_expert_forward_tiled(mx_ctx* ctx, const void* tiled, int32_t hidden, int32_t intermediate,
                             const uint16_t* x_bf16, int32_t tokens, float swiglu_limit, const float* route_w,
                             uint16_t* y_bf16, const mx_expert_stages* stages, void* stream);
+
 
 /* ---- router (replaces GateProjection.project + RouterProbe, src/vesper/gate.py:133-147,
  *      src/vesper/router.py:227-264, routing_probe.cu:5-86) ---- */
@@ -321,10 +331,17 @@ int mx_moe_decode(mx_layer* layer, const uint16_t* x_bf16, int32_t tokens, uint1
                   int32_t diagnostics, void* stream);
 
 /* Decode with routing decided elsewhere (a seeded trace, an expert-parallel dispatcher): ids [T][k] and
- * weights [T][k] on the device replace the router; an id outside [0, E) or repeated within a token is
- * replaced (smallest expert the token does not name, weight 0) so the call stays in bounds. */
+ * weights [T][k] on the device replace the router. An id outside [0, E) or repeated within a token is
+ * replaced (smallest expert the token does not name, weight 0) so the call stays in bounds, and counted in
+ * the layer's routing error word (mx_layer_route_errors): the reference refuses such routing before any
+ * device work (participation, src/vesper/moe.py:18-30), so a caller that cannot validate ids on the host
+ * must read the word after the call and discard the output when it is nonzero. */
 int mx_moe_decode_routed(mx_layer* layer, const uint16_t* x_bf16, int32_t tokens, const int32_t* ids,
                          const float* weights, uint16_t* y_bf16, void* stream);
+/* Routing ids that mx_moe_decode_routed and mx_moe_prefill replaced since the last clear (see above).
+ * Synchronises `stream` and reads the count into *count; clear != 0 then resets it, ordered on `stream`.
+ * The device-side form of participation's refusals (src/vesper/moe.py:18-30). */
+int mx_layer_route_errors(mx_layer* layer, uint32_t* count, int32_t clear, void* stream);
 /* Re-point n experts at once (one launch per 64), ordered on `stream`: experts[i] -> tiled[i]. */
 int mx_layer_set_experts(mx_layer* layer, int32_t n, const int32_t* experts, const void* const* tiled, void* stream);
 
@@ -360,7 +377,8 @@ int mx_cache_set_timing(mx_cache* cache, int32_t enable);
 /* Prefill: T tokens through the layer (routed experts + shared) as token-sorted grouped GEMMs on the
  * scaled MXFP4 MFMA; same per-token arithmetic as mx_moe_decode.
  * ids [T][k] (device int32, distinct per token) and weights [T][k] (device FP32) give the routing, or both
- * NULL to run the layer's router on x. The caller provides a device workspace of at least
+ * NULL to run the layer's router on x. Invalid given ids are replaced and counted as in
+ * mx_moe_decode_routed. The caller provides a device workspace of at least
  * mx_prefill_workspace_bytes(layer, T) bytes, 256-byte aligned (no allocation inside the call).
  * H % 256 == 0. Replaces the reference's per-token ConnectedMoE.forward loop (connected.py:125-186). */
 uint64_t mx_prefill_workspace_bytes(mx_layer* layer, int32_t tokens);

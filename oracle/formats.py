@@ -113,6 +113,27 @@ def bf16_round(values) -> np.ndarray:
     return bf16_values(bf16_bits(values))
 
 
+def fma_f32(a, b, c) -> np.ndarray:
+    """f32(a * b + c) with one rounding (an IEEE fused multiply-add in FP32), for finite FP32 arrays whose
+    results are normal. a * b is exact in float64 (24 + 24 bits); the float64 sum s = a b + c is rounded,
+    and its rounding error e is recovered exactly (Knuth's two-sum). Rounding s to FP32 is then the correct
+    rounding of the exact value except when s lies exactly halfway between two FP32 values and e != 0: the
+    exact value is then on e's side of the halfway point, and the result moves one FP32 step that way."""
+    a, b, c = (np.asarray(v, dtype=np.float32) for v in (a, b, c))
+    p = a.astype(np.float64) * b.astype(np.float64)
+    c64 = c.astype(np.float64)
+    s = p + c64
+    bb = s - p
+    e = (p - (s - bb)) + (c64 - bb)
+    r = s.astype(np.float32)
+    halfway = (s.view(np.uint64) & np.uint64((1 << 29) - 1)) == np.uint64(1 << 28)
+    r64 = r.astype(np.float64)
+    up = halfway & (e > 0) & (r64 < s)
+    down = halfway & (e < 0) & (r64 > s)
+    r = np.where(up, np.nextafter(r, np.float32(np.inf)), r)
+    return np.where(down, np.nextafter(r, np.float32(-np.inf)), r).astype(np.float32)
+
+
 def quantize_activation(values, block: int = 32) -> tuple[np.ndarray, np.ndarray]:
     """BF16-round, then per-block E4M3 codes with E8M0 scales (formats.py:80-94).
 

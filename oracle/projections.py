@@ -12,11 +12,15 @@ Two scale profiles of the same arithmetic:
 * block 128 (DeepSeek-style FP8): FP32 weight scales
   per 128 x 128 block ([ceil(N/128), K/128]) and per-token per-128 FP32
   activation scales s = f32(max(amax, 1e-4)) / 448, codes E4M3(clip(x / s)).
-  Same order: per 128-wide K group d = exact dot, sum = sum + (d * sa) * sw.
-  The reference has no block-128 path; this profile restates the configuration
-  with the reference's operation order and amax floor. Parity unpinned beyond
-  its closed form: pinned by exact-arithmetic checks (designed representable
-  inputs) and by the block-32 profile sharing the order.
+  Per 128-wide K group d = exact dot rounded once to FP32, then
+  sum = fma(d, f32(sa * sw), sum): one rounding per output and group (the
+  kernels' fused multiply-add; formats.fma_f32 restates it exactly). The
+  reference has no block-128 path (its only FP8 projection has power-of-two
+  block-32 scales, where every order of the scaling gives the same sums); this
+  profile restates the configuration with the reference's amax floor and this
+  build's accumulation order. Parity unpinned beyond its closed form: pinned by
+  exact-arithmetic checks (designed representable inputs), an exact-rational
+  check of the per-group scaling, and the exact-rational pin of fma_f32.
 
 E4M3 x E4M3 products are multiples of 2^-18 below 2^18, so a 128-term dot is
 exact in float64 and is rounded once to FP32.
@@ -26,8 +30,8 @@ from __future__ import annotations
 
 import numpy as np
 
-from .formats import (AMAX_FLOOR, bf16_bits, bf16_values, e4m3_values, encode_e4m3, fp8_block32_gemv_fp32,
-                      quantize_activation)
+from .formats import (AMAX_FLOOR, bf16_bits, bf16_values, e4m3_values, encode_e4m3, fma_f32,
+                      fp8_block32_gemv_fp32, quantize_activation)
 
 # Projection shapes [rows, width] (DeepSeek low-rank attention).
 CONFIG3_LAYOUT = {"q_a": (1536, 7168), "q_b": (24576, 1536), "kv_a": (576, 7168), "o": (7168, 16384)}
@@ -61,13 +65,16 @@ def fp8_block128_gemm_fp32(act_codes, act_scales, weight_codes, weight_scales) -
     g = k // 128
     if q.shape[1] != k or sa.shape != (t, g) or sw.shape != ((n + 127) // 128, g):
         raise ValueError("Mismatched FP8 block-128 dimensions")
-    a = e4m3_values(q).astype(np.float64).reshape(t, g, 128)
-    b = e4m3_values(w).astype(np.float64).reshape(n, g, 128)
-    dots = np.einsum("tgk,ngk->tng", a, b).astype(np.float32)                   # exact, rounded once
+    lut = e4m3_values(np.arange(256, dtype=np.uint8)).astype(np.float64)
     row_scale = sw[np.arange(n) // 128]                                          # [N, G]
     acc = np.zeros((t, n), np.float32)
     for j in range(g):
-        acc = (acc + (dots[:, :, j] * sa[:, j:j + 1]).astype(np.float32) * row_scale[None, :, j]).astype(np.float32)
+        cols = slice(128 * j, 128 * (j + 1))
+        # the block dot: 128 products, each a multiple of 2^-18 below 2^18, so the float64 sum is exact in
+        # any order (BLAS is free to reorder) and is rounded once to FP32
+        d = (lut[q[:, cols]] @ lut[w[:, cols]].T).astype(np.float32)
+        scale = (sa[:, j:j + 1] * row_scale[None, :, j]).astype(np.float32)    # f32(sa * sw)
+        acc = fma_f32(d, scale, acc)                                             # acc = f32(d * scale + acc)
     return acc
 
 

@@ -3,8 +3,9 @@
 * The per-128 activation quantizer: bit-exact against the oracle (codes and FP32 scales).
 * The tiled weight layout: against an independent NumPy construction from its definition.
 * The product: exact on designed inputs whose every partial sum is representable (both profiles), so
-  the operand layouts, scale placement and the (d * sa) * sw order are pinned bit for bit; random
-  inputs within the GEMV bar; configuration-3 and reference shapes within the north-star tolerance.
+  the operand layouts and scale placement are pinned bit for bit; random inputs within the GEMV bar;
+  configuration-3 shapes at T = 1, 16, 300 and 2048 (the GEMM and split-K branches the benchmark times,
+  sampled tokens) and the reference shapes within the north-star tolerance.
 """
 
 import ctypes as C
@@ -246,6 +247,27 @@ def test_config3_projections_within_tolerance(tokens):
             assert got["output_bf16"].shape == (tokens, rows)
             np.testing.assert_array_equal(got["input_fp8"], ref["input_fp8"])
             assert_close(got["output_bf16"], ref["output_bf16"], name)
+
+
+def test_config3_T2048_sampled_tokens_within_tolerance():
+    """All four configuration-3 projections at the benchmark's 2048 tokens: the whole batch runs through the
+    GEMM (q_a and kv_a with K split too), and 64 sampled tokens (first and last included, spread over every
+    128-token tile) are compared with the oracle: codes bit-exact, outputs within the north-star bar."""
+    tokens = 2048
+    rng = np.random.default_rng(20262048)
+    arrays = arrays_for(CONFIG3_LAYOUT, 128, rng)
+    sample = np.unique(np.concatenate([[0, tokens - 1], rng.choice(tokens, 62, replace=False)]))
+    with NativeProjections(arrays, block=128) as proj:
+        for name, (rows, width) in CONFIG3_LAYOUT.items():
+            x = bf16_bits(rng.standard_normal((tokens, width)).astype(np.float32))
+            got = proj.fp8(name, x)
+            ref = fp8_projection(bf16_values(x[sample]), arrays[f"layers.0.attn.{name}.weight"],
+                                 arrays[f"layers.0.attn.{name}.scale"], 128)
+            assert got["output_bf16"].shape == (tokens, rows)
+            np.testing.assert_array_equal(got["input_fp8"][sample], ref["input_fp8"])
+            np.testing.assert_array_equal(got["scale_f32"][sample].view(np.uint32), ref["scale"].view(np.uint32))
+            assert_close(got["output_bf16"][sample], ref["output_bf16"], f"{name} T={tokens}")
+            assert_gemv_close(got["output_bf16"][sample], ref["output_bf16"], f"{name} T={tokens}", min_equal=0.90)
 
 
 def test_reference_shapes_block32_and_refusals():

@@ -199,11 +199,22 @@ def test_offload_decode_equals_resident_layers(gpu_ctx, audit):
                 src[777] ^= 0x01
                 cache.forget(expert_key(0, 5))
                 off.step_device(x.ptr, T, [y.ptr for y in ys], [r[0] for r in routing])
+                gpu_ctx.sync()
+                assert np.all(ys[0].download() == 0x7FC0), "the audit gate did not poison layer 0"
+                for l in range(1, L):   # later layers inherit the NaN through their inputs
+                    v = ys[l].download()
+                    assert np.all(((v & 0x7F80) == 0x7F80) & ((v & 0x7F) != 0)), f"layer {l} output is not NaN"
                 with pytest.raises(ValueError, match="0:5"):
                     off.check_audit()
                 src[777] ^= 0x01
                 off.step_device(x.ptr, T, [y.ptr for y in ys], [r[0] for r in routing])
                 off.check_audit()
+                assert not np.any((ys[-1].download() & 0x7F80) == 0x7F80)
+            off.check_routes()
+            with pytest.raises(ValueError, match="outside the pinned model"):
+                off.load_routing([(np.full((T, cfg.top_k), cfg.experts, np.int32), np.ones((T, cfg.top_k), np.float32))] * L)
+            with pytest.raises(ValueError, match="differs from the routing loaded"):
+                off.step_device(x.ptr, T, [y.ptr for y in ys], [r[0] + 1 for r in routing])
         finally:
             off.close()
             for d in [x] + ys + ref_ys:
@@ -218,8 +229,9 @@ def test_offload_decode_equals_resident_layers(gpu_ctx, audit):
 
 
 def test_decode_routed_repairs_invalid_routing(gpu_ctx):
-    """Out-of-range and repeated ids are replaced (weight 0) so the call stays in bounds: the result equals the
-    call with the repaired routing."""
+    """Out-of-range and repeated ids are replaced (weight 0) so the call stays in bounds and counted in the
+    layer's routing error word: the result equals the call with the repaired routing, the word reads 2 after
+    the bad call and 0 after the good one, and prefill counts the same replacements."""
     cfg = MoEConfig(hidden=512, intermediate=256, experts=8, top_k=2, shared=None, max_tokens=4)
     rng = np.random.default_rng(4)
     bank = ExpertBank(gpu_ctx, cfg, cfg.experts)
@@ -233,10 +245,24 @@ def test_decode_routed_repairs_invalid_routing(gpu_ctx):
         good = gpu_ctx.upload(np.array([[3, 0], [0, 5]], np.int32))
         w_good = gpu_ctx.upload(np.array([[0.5, 0.0], [0.0, 0.9]], np.float32))
         y1, y2 = gpu_ctx.empty((2, cfg.hidden), np.uint16), gpu_ctx.empty((2, cfg.hidden), np.uint16)
+        assert layer.route_errors() == 0
         decode_routed(layer, x.ptr, 2, bad.ptr, w.ptr, y1.ptr)
+        assert layer.route_errors() == 2
         decode_routed(layer, x.ptr, 2, good.ptr, w_good.ptr, y2.ptr)
+        assert layer.route_errors() == 0
         gpu_ctx.sync()
         np.testing.assert_array_equal(y1.download(), y2.download())
+        nbytes = layer.workspace_bytes(2)
+        ws = gpu_ctx.malloc(nbytes)
+        try:
+            layer.prefill_device(x.ptr, 2, y1.ptr, ws, nbytes, bad.ptr, w.ptr)
+            assert layer.route_errors() == 2
+            layer.prefill_device(x.ptr, 2, y2.ptr, ws, nbytes, good.ptr, w_good.ptr)
+            assert layer.route_errors(clear=False) == 0
+            gpu_ctx.sync()
+            np.testing.assert_array_equal(y1.download(), y2.download())
+        finally:
+            gpu_ctx.free(ws)
         for d in (x, bad, w, good, w_good, y1, y2):
             d.free()
     finally:

@@ -5,9 +5,41 @@ from fractions import Fraction
 import numpy as np
 import pytest
 
-from oracle.formats import e4m3_values, encode_e4m3, fp8_block32_gemv_fp32
+from oracle.formats import e4m3_values, encode_e4m3, fma_f32, fp8_block32_gemv_fp32
 from oracle.projections import (CONFIG3_LAYOUT, fp8_block128_gemm_fp32, fp8_projection, fp8_reference_fp32,
                                 fp8_weights, quantize_activation_128)
+
+
+def round_f32(value: Fraction) -> np.float32:
+    """The FP32 nearest to an exact rational (ties to the even significand), by exact comparison of the
+    neighbours of a first guess -- independent of any floating-point rounding chain."""
+    guess = np.float32(float(value))
+    candidates = [np.nextafter(guess, np.float32(-np.inf)), guess, np.nextafter(guess, np.float32(np.inf))]
+    def key(c):
+        return (abs(Fraction(float(c)) - value), int(np.array(c).view(np.uint32)) & 1)
+    return min(candidates, key=key)
+
+
+def test_fma_f32_is_the_correctly_rounded_fused_result():
+    """fma_f32 against exact rational arithmetic: random operands over many magnitudes, and two designed
+    cases where the float64 sum lands exactly halfway between two FP32 values while the exact value does
+    not (the naive double rounding would round the tie to even, the wrong way)."""
+    rng = np.random.default_rng(77)
+    a = (rng.standard_normal(4000) * np.exp2(rng.integers(-20, 20, 4000))).astype(np.float32)
+    b = (rng.standard_normal(4000) * np.exp2(rng.integers(-20, 20, 4000))).astype(np.float32)
+    c = (rng.standard_normal(4000) * np.exp2(rng.integers(-40, 40, 4000))).astype(np.float32)
+    lo, hi = np.float32(1 - 2.0 ** -20), np.float32(1 + 2.0 ** -20)       # lo * hi = 1 - 2^-40 exactly
+    big = np.float32(2.0 ** 24 + 2)
+    a = np.concatenate([a, [lo, lo]]).astype(np.float32)
+    b = np.concatenate([b, [-hi, hi]]).astype(np.float32)
+    c = np.concatenate([c, [big, big]]).astype(np.float32)
+    got = fma_f32(a, b, c)
+    for i in range(len(a)):
+        want = round_f32(Fraction(float(a[i])) * Fraction(float(b[i])) + Fraction(float(c[i])))
+        assert got[i] == want, (i, a[i], b[i], c[i], got[i], want)
+    assert got[-2] == np.float32(2.0 ** 24 + 2) and got[-1] == np.float32(2.0 ** 24 + 2)
+    naive = (a[-2:].astype(np.float64) * b[-2:] + c[-2:]).astype(np.float32)
+    assert list(naive) == [np.float32(2.0 ** 24), np.float32(2.0 ** 24 + 4)]   # what the fix corrects
 
 
 def small_int_codes(rng, shape, lo=-8, hi=8):
@@ -45,26 +77,31 @@ def test_block128_gemm_equals_integer_matmul_on_unit_scales():
 
 
 def test_block128_scaling_is_per_block_and_in_order():
-    """One nonzero K block per weight row: the result is the exact rational ((d * sa) * sw) rounded
-    at each step, computed here with Fractions."""
+    """Each weight row has one or two nonzero K blocks: the result is, per block in K order, the exact
+    rational d * f32(sa * sw) added to the running FP32 sum with one rounding -- computed here with
+    Fractions and an exact nearest-FP32 search."""
     rng = np.random.default_rng(3)
     t, n, k = 2, 130, 256
     q = encode_e4m3(rng.standard_normal((t, k)).astype(np.float32))
     w = np.zeros((n, k), np.uint8)
-    blocks = rng.integers(0, 2, n)
+    used = rng.integers(1, 4, n)                          # bit g set: block g is nonzero
     for r in range(n):
-        w[r, 128 * blocks[r]:128 * blocks[r] + 128] = encode_e4m3(rng.standard_normal(128).astype(np.float32))
+        for g in range(2):
+            if used[r] >> g & 1:
+                w[r, 128 * g:128 * g + 128] = encode_e4m3(rng.standard_normal(128).astype(np.float32))
     sa = np.exp2(rng.integers(-6, 6, (t, 2))).astype(np.float32) * np.float32(1.5)
     sw = np.exp2(rng.uniform(-8, -2, (2, 2))).astype(np.float32)
     got = fp8_block128_gemm_fp32(q, sa, w, sw)
     for i in range(t):
         for r in range(n):
-            g = blocks[r]
-            d = sum(Fraction(float(a)) * Fraction(float(b)) for a, b in
-                    zip(e4m3_values(q[i, 128 * g:128 * g + 128]), e4m3_values(w[r, 128 * g:128 * g + 128])))
-            d32 = np.float32(float(d))
-            want = np.float32(np.float32(d32 * sa[i, g]) * sw[r // 128, g])
-            assert got[i, r] == want
+            acc = np.float32(0.0)
+            for g in range(2):
+                d = sum(Fraction(float(a)) * Fraction(float(b)) for a, b in
+                        zip(e4m3_values(q[i, 128 * g:128 * g + 128]), e4m3_values(w[r, 128 * g:128 * g + 128])))
+                d32 = round_f32(d)
+                scale = round_f32(Fraction(float(sa[i, g])) * Fraction(float(sw[r // 128, g])))
+                acc = round_f32(Fraction(float(d32)) * Fraction(float(scale)) + Fraction(float(acc)))
+            assert got[i, r] == acc
 
 
 def test_profiles_agree_on_unit_scales_and_exact_inputs():

@@ -108,6 +108,7 @@ SIGNATURES = {
     "mx_moe_decode_routed": ([_P, _P, _I32, _P, _P, _P, _P], C.c_int),
     "mx_expert_forward_tiled": ([_P, _P, _I32, _I32, _P, _I32, _F, _P, _P, C.POINTER(MxExpertStages), _P], C.c_int),
     "mx_layer_set_experts": ([_P, _I32, _P, _P, _P], C.c_int),
+    "mx_layer_route_errors": ([_P, C.POINTER(C.c_uint32), _I32, _P], C.c_int),
     "mx_cache_create": ([_P, _U64, _I32, C.POINTER(_P)], C.c_int),
     "mx_cache_destroy": ([_P], C.c_int),
     "mx_cache_register": ([_P, C.c_int64, _P], C.c_int),
@@ -132,6 +133,7 @@ SIGNATURES = {
     "mx_kv_round32": ([_P, _P, _I64, _P, _P, _P, _P], C.c_int),
     "mx_sha256_chunks": ([_P, _P, _U64, _P, _P], C.c_int),
     "mx_sha256_verify": ([_P, C.POINTER(_P), C.POINTER(_P), _P, _I32, _U64, _P, _P], C.c_int),
+    "mx_audit_gate": ([_P, _P, _I32, _P, _I32, _P, _U64, _P], C.c_int),
     "mx_owned_size": ([_P, _P, C.POINTER(_U64)], C.c_int),
     "mx_check_e4m3_pack": ([_P, C.POINTER(_U64)], C.c_int),
 }

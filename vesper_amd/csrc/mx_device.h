@@ -95,6 +95,23 @@ __device__ __forceinline__ float2 load_device(const float* p) {
   return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
 }
 
+// Handoff buffers between workgroups (the split-K GEMV's partial sums) hold this FP32 pattern wherever no
+// value is published: a signalling NaN, which FP32 arithmetic never produces (its NaN results are quiet).
+constexpr uint32_t kHandoffEmpty = 0x7FA0DEADu;
+constexpr int kHandoffPolls = 1 << 16;
+
+// The pair `first` read from p, re-read until it is no longer the empty pattern (a pair is published by one
+// 64-bit atomic, so its halves arrive together); at most kHandoffPolls reads, then NaN instead of a hang.
+__device__ __forceinline__ float2 await_pair(float2 first, const float* p) {
+  float2 v = first;
+  for (int i = 0; __float_as_uint(v.x) == kHandoffEmpty; ++i) {
+    if (i == kHandoffPolls) return make_float2(__builtin_nanf(""), __builtin_nanf(""));
+    __builtin_amdgcn_s_sleep(1);
+    v = load_device(p);
+  }
+  return v;
+}
+
 // V_MFMA_SCALE_F32_16X16X128_F8F6F4 operand layouts (measured on gfx950 with one-hot probes):
 //   FP4 A (cbsz 4, 4 VGPRs): lane l = row l % 16, K = 32 (l / 16) + nibble j, low nibble first.
 //   FP8 A (cbsz 0) and FP8 B (blgp 0), 8 VGPRs: lane l = row / column l % 16; bytes 0-15 hold
@@ -218,6 +235,30 @@ __host__ __device__ __forceinline__ TiledOffsets tiled_offsets(int H, int I) {
   o.dn_s = o.dn_w + ih / 2;
   o.total = o.dn_s + ih / 32;
   return o;
+}
+
+// One token's routing list made valid in place: an id outside [0, E) or equal to an earlier id of the token
+// is replaced by the smallest expert the token does not name, with route weight 0, so every later step sees
+// k distinct in-range experts and stays in bounds. Returns how many ids were replaced (the caller counts
+// them in the layer's routing error word; the host refuses the call's output when it is nonzero).
+__device__ __forceinline__ int repair_token_routes(int32_t* ids, float* w, int k, int E) {
+  int replaced = 0;
+  for (int i = 0; i < k; ++i) {
+    bool bad = ids[i] < 0 || ids[i] >= E;
+    for (int j = 0; j < i && !bad; ++j) bad = ids[j] == ids[i];
+    if (!bad) continue;
+    for (int e = 0; e < E; ++e) {
+      bool used = false;
+      for (int j = 0; j < k && !used; ++j) used = j != i && ids[j] == e;
+      if (!used) {
+        ids[i] = e;
+        break;
+      }
+    }
+    w[i] = 0.f;
+    ++replaced;
+  }
+  return replaced;
 }
 
 }  // namespace mxd

@@ -7,8 +7,10 @@
 //             scaled MFMA, which applies them exactly.
 //   block 128 (DeepSeek-style FP32 scales): weight FP32 per 128 x 128 block
 //             [ceil(N/128)][K/128], activations per-token per-128 FP32. Per 128-wide chunk the MFMA gives
-//             the block dot d (unit scales) and the kernel accumulates acc += (d * sa) * sw in FP32,
-//             the reference's order.
+//             the block dot d (unit scales) and the kernel accumulates acc = fma(d, f32(sa * sw), acc):
+//             one rounding per output and chunk. (The reference's only FP8 projection has power-of-two
+//             block-32 scales, where every order gives the same sums; this profile's order is this
+//             build's own.)
 //
 // Weights are held in a device-native tiled layout (mx_fp8_tile): for each group of 64 rows and each
 // 128-wide K chunk, 4 tiles of 16 rows x 2 KB, each stored as two 1 KB halves of 16 bytes per lane in
@@ -34,7 +36,7 @@ constexpr int kGemvMaxTokens = 32;   // above this the tiled GEMM reuses each we
 // The GEMV's last workgroup per tile adds the split-K partial sums when they total at most this many
 // bytes. Above it (the 7168- and 24576-row projections at 16 tokens, measured on MI355X) the
 // device-coherent round trip through one workgroup per tile costs more than fp8_splitk_reduce_kernel.
-constexpr uint64_t kTicketPartialBytes = 2u << 20;
+constexpr uint64_t kTicketPartialBytes = MX_HANDOFF_BYTES;   // the context's handoff buffer
 
 struct Fp8Blob {
   size_t scales;   // byte offset of the scale section
@@ -140,6 +142,10 @@ struct Fp8Args {
   float* partial;      // split K: [splits][T][N] FP32 partial sums (the GEMV writes these instead of y)
   uint32_t* tickets;   // split-K GEMV: arrival counter per (row group, token tile), zero between launches;
                        // null = partial sums only, added by fp8_splitk_reduce_kernel
+  float* handoff;      // with tickets: [splits][T][N] partial sums in this launch's half of the context's
+                       // handoff buffer, which holds the empty pattern wherever this launch reads
+  uint4* restore;      // with tickets: the other half, whose first restore_n 16-byte words the previous
+  int64_t restore_n;   // launch wrote: every workgroup puts back the empty pattern over its share
   const uint16_t* x;   // fused GEMV (block 128, few tokens): the BF16 input [T][K], quantized in the kernel
   int64_t x_stride;    // activation elements per token: K, or groups x K when grouped
   int x_group_rows;    // grouped activations (block-32 GEMV): weight rows [g R, (g + 1) R) multiply
@@ -209,12 +215,13 @@ __device__ __forceinline__ void fp8_mma(Fp8Chunk<kBlock> r, v4f (&acc)[kTiles], 
     for (int t = 0; t < kTiles; ++t)
       acc[t] = mfma_fp8_fp8(r.a[t][0], r.a[t][1], b0, b1, acc[t], (int)((r.sw >> (8 * t)) & 0xFF), sx);
   } else {
-    const float sa = __uint_as_float(r.sx), sw = __uint_as_float(r.sw);
+    // the chunk's combined scale f32(sa * sw), then one fused multiply-add per output
+    const float s = __uint_as_float(r.sx) * __uint_as_float(r.sw);
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) {
       const v4f d = mfma_fp8_fp8(r.a[t][0], r.a[t][1], b0, b1, v4f{0.f, 0.f, 0.f, 0.f}, 127, 127);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[t][i] = acc[t][i] + (d[i] * sa) * sw;
+      for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(d[i], s, acc[t][i]);
     }
   }
 }
@@ -246,6 +253,15 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
   const uint8_t* xsrow =
       kBlock == 32 ? (const uint8_t*)a.xs + (size_t)rtok * (a.x_stride / 32) + (size_t)xgroup * (a.K / 32)
                    : reinterpret_cast<const uint8_t*>((const float*)a.xs + (size_t)rtok * (a.K / 128));
+  if (a.restore_n) {
+    // this workgroup's share of the other handoff half (plain stores: the kernel boundary publishes them
+    // to the launch that uses that half next)
+    const int64_t wg = ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+    const int64_t wgs = (int64_t)gridDim.x * gridDim.y * gridDim.z;
+    const int64_t per = (a.restore_n + wgs - 1) / wgs;
+    const uint4 empty = make_uint4(mxd::kHandoffEmpty, mxd::kHandoffEmpty, mxd::kHandoffEmpty, mxd::kHandoffEmpty);
+    for (int64_t i = wg * per + tid; i < min((wg + 1) * per, a.restore_n); i += 256) a.restore[i] = empty;
+  }
   v4f acc[kTiles];
 #pragma unroll
   for (int t = 0; t < kTiles; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -337,12 +353,22 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
       if (live) *reinterpret_cast<float4*>(part) = make_float4(out[0], out[1], out[2], out[3]);
       return;
     }
-    // Device-coherent partial sums; once every wave's stores have completed (s_waitcnt 0, then the
-    // barrier) one relaxed atomic takes the tile's ticket. The last of the S arrivals reads all partial
-    // sums back, device-coherent, and adds them in split order.
+    // The partial sums go to this launch's half of the context's handoff buffer (a.handoff, [S][T][N] FP32),
+    // which holds the kHandoffEmpty pattern wherever this launch reads (the launch before restored it):
+    // each pair of sums is published as one 64-bit agent-scope atomic, a relaxed atomic ticket per tile
+    // elects the last of the S arrivals, and that workgroup reads every split's pairs, re-reading any
+    // location that still holds the empty pattern until the published pair is visible, and adds them in
+    // split order. In a launch a location only ever holds the empty pattern or this launch's pair, so
+    // correctness rests on per-location coherence of the atomics (and the kernel boundaries between
+    // launches) -- not on an order between different locations, which would need agent-scope fences: each
+    // release fence writes back the XCD's whole L2, tens of microseconds over a launch. The stores have
+    // completed before the ticket is taken (s_waitcnt 0, then the barrier), so the first read normally finds
+    // them; the re-reads are bounded, and a pair still missing at the bound becomes NaN instead of a hang.
+    const size_t stride = (size_t)a.T * a.N;
+    float* hand = a.handoff + o;
     if (live) {
-      mxd::store_device(part, out[0], out[1]);
-      mxd::store_device(part + 2, out[2], out[3]);
+      mxd::store_device(hand + (size_t)z * stride, out[0], out[1]);
+      mxd::store_device(hand + (size_t)z * stride + 2, out[2], out[3]);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __shared__ uint32_t arrived;
@@ -353,14 +379,28 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
     if (arrived != (uint32_t)(S - 1)) return;
     if (tid == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (!live) return;
-    const size_t stride = (size_t)a.T * a.N;
     float2 p[16][2];
 #pragma unroll
     for (int zz = 0; zz < 16; ++zz)
       if (zz < S) {
-        p[zz][0] = mxd::load_device(a.partial + (size_t)zz * stride + o);
-        p[zz][1] = mxd::load_device(a.partial + (size_t)zz * stride + o + 2);
+        p[zz][0] = mxd::load_device(hand + (size_t)zz * stride);
+        p[zz][1] = mxd::load_device(hand + (size_t)zz * stride + 2);
       }
+    // one check over every pair first; the re-reads are the rare path
+    bool missing = false;
+#pragma unroll
+    for (int zz = 0; zz < 16; ++zz)
+      if (zz < S)
+        missing |= (__float_as_uint(p[zz][0].x) == mxd::kHandoffEmpty) |
+                    (__float_as_uint(p[zz][1].x) == mxd::kHandoffEmpty);
+    if (missing) {
+#pragma unroll
+      for (int zz = 0; zz < 16; ++zz)
+        if (zz < S) {   // unrolled: p stays in registers
+          p[zz][0] = mxd::await_pair(p[zz][0], hand + (size_t)zz * stride);
+          p[zz][1] = mxd::await_pair(p[zz][1], hand + (size_t)zz * stride + 2);
+        }
+    }
     float4 t = make_float4(p[0][0].x, p[0][0].y, p[0][1].x, p[0][1].y);
 #pragma unroll
     for (int zz = 1; zz < 16; ++zz)
@@ -512,10 +552,11 @@ __global__ __launch_bounds__(kGemmThreads) void fp8_gemm_kernel(Fp8Args a) {
                                    sxb);
       }
     } else {
-      // Per chunk the MFMA gives the block dot d (unit scales) and acc += (d * sa) * sw follows in FP32. MFMA
-      // k + 1 is issued before the 12 FP32 operations that scale MFMA k, so they run while it executes;
-      // the scheduling fences keep the compiler from pairing each MFMA with its own scaling instead (which
-      // waits for every result). Token tile u + 2's operands are read from LDS while tile u multiplies.
+      // Per chunk the MFMA gives the block dot d (unit scales) and acc = fma(d, f32(sa * sw), acc) follows in
+      // FP32: one rounding per output. MFMA k + 1 is issued before the 4 fused multiply-adds that scale MFMA k,
+      // so they run while it executes; the scheduling fences keep the compiler from pairing each MFMA with its
+      // own scaling instead (which waits for every result). Token tile u + 2's operands are read from LDS
+      // while tile u multiplies.
       const float swf = __uint_as_float(swv);
       constexpr int kSteps = kTiles * kWaveTiles;
       read_b(0);
@@ -531,9 +572,9 @@ __global__ __launch_bounds__(kGemmThreads) void fp8_gemm_kernel(Fp8Args a) {
           d[(k + 1) & 1] = mfma_fp8_fp8(am[t1][0], am[t1][1], b[u1][0], b[u1][1], v4f{0.f, 0.f, 0.f, 0.f}, 127, 127);
         }
         __builtin_amdgcn_sched_barrier(0);
-        const float sa = __uint_as_float(sx[u]);
+        const float sc = __uint_as_float(sx[u]) * swf;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[t][u][i] = acc[t][u][i] + (d[k & 1][i] * sa) * swf;
+        for (int i = 0; i < 4; ++i) acc[t][u][i] = fmaf(d[k & 1][i], sc, acc[t][u][i]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -605,12 +646,13 @@ bool fp8_fused_ok(int N, int K, int T, int block) {
 }
 
 // The product on quantized activations: GEMV (T <= 32) or the tiled GEMM, either with its K split over
-// fp8_splits(N, K, T) workgroups whose FP32 partial sums go to `partial` (fp8_splits * T * N floats) and
-// are added in split order: by the GEMV's last workgroup per tile (`tickets`, the context's arrival
-// counters) or by fp8_splitk_reduce_kernel.
+// fp8_splits(N, K, T) workgroups whose FP32 partial sums are added in split order: by the GEMV's last
+// workgroup per tile through the context's arrival counters and handoff buffer when they fit it
+// (kTicketPartialBytes), else written to `partial` (fp8_splits * T * N floats) and added by
+// fp8_splitk_reduce_kernel.
 // x_fused: the BF16 input when the GEMV quantizes it itself (fp8_fused_ok), else null (q and sc given).
 int launch_fp8_product(const uint8_t* blob, int N, int K, int block, const uint8_t* q, const void* sc, int T,
-                       uint16_t* y, float* trace, float* partial, uint32_t* tickets, hipStream_t st,
+                       uint16_t* y, float* trace, float* partial, mx_ctx* ctx, hipStream_t st,
                        const uint16_t* x_fused = nullptr, int x_group_rows = 0) {
   Fp8Args a{};
   a.blob = blob;
@@ -630,8 +672,17 @@ int launch_fp8_product(const uint8_t* blob, int N, int K, int block, const uint8
     const int splits = fp8_splits(N, K, T);
     const dim3 grid(N / 64, (T + kTok - 1) / kTok, splits);
     if (splits > 1 && (size_t)grid.x * grid.y <= MX_TICKETS &&
-        (uint64_t)splits * T * N * sizeof(float) <= kTicketPartialBytes)
-      a.tickets = tickets;
+        (uint64_t)splits * T * N * sizeof(float) <= kTicketPartialBytes) {
+      // this launch's half, and the other half's extent the previous launch wrote (restored by this launch)
+      const int h = ctx->handoff_half;
+      a.tickets = ctx->tickets;
+      a.handoff = ctx->handoff + (size_t)h * (MX_HANDOFF_BYTES / 4);
+      a.restore = reinterpret_cast<uint4*>(ctx->handoff + (size_t)(1 - h) * (MX_HANDOFF_BYTES / 4));
+      a.restore_n = (int64_t)(ctx->handoff_dirty[1 - h] / 16);
+      ctx->handoff_dirty[1 - h] = 0;
+      ctx->handoff_dirty[h] = ((uint64_t)splits * T * N * sizeof(float) + 15) / 16 * 16;
+      ctx->handoff_half = 1 - h;
+    }
     if (block == 32) hipLaunchKernelGGL((fp8_gemv_kernel<32, false>), grid, dim3(256), 0, st, a);
     else if (x_fused) hipLaunchKernelGGL((fp8_gemv_kernel<128, true>), grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL((fp8_gemv_kernel<128, false>), grid, dim3(256), 0, st, a);
@@ -737,14 +788,14 @@ int mx_fp8_projection(mx_ctx* ctx, const void* tiled, int32_t N, int32_t K, int3
   MX_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)sc & 3) == 0, "mx_fp8_projection: q 16-byte, s 4-byte aligned");
   float* partial = (float*)((uint8_t*)base + q_b + s_b);
   if (!q_out && !s_out && fp8_fused_ok(N, K, T, block))   // the GEMV quantizes x itself
-    return launch_fp8_product((const uint8_t*)tiled, N, K, block, nullptr, nullptr, T, y, trace, partial,
-                              ctx->tickets, st, x);
+    return launch_fp8_product((const uint8_t*)tiled, N, K, block, nullptr, nullptr, T, y, trace, partial, ctx, st,
+                              x);
   if (block == 32) {
     if (int s = mx_act_quant32(ctx, x, q, (uint8_t*)sc, T, K, stream)) return s;
   } else {
     if (int s = mx_act_quant128(ctx, x, q, (float*)sc, T, K, stream)) return s;
   }
-  return launch_fp8_product((const uint8_t*)tiled, N, K, block, q, sc, T, y, trace, partial, ctx->tickets, st);
+  return launch_fp8_product((const uint8_t*)tiled, N, K, block, q, sc, T, y, trace, partial, ctx, st);
 }
 
 int mx_fp8_grouped_projection(mx_ctx* ctx, const void* tiled, int32_t groups, int32_t rows, int32_t K,
@@ -763,7 +814,7 @@ int mx_fp8_grouped_projection(mx_ctx* ctx, const void* tiled, int32_t groups, in
              "mx_fp8_grouped_projection: tiled 256-byte, q 16-byte, s 4-byte, y 8-byte, trace 16-byte alignment");
   void* base = nullptr;
   if (int st = scratch(ctx, (uint64_t)fp8_splits(N, K, T) * T * N * 4 + 256, &base)) return st;
-  return launch_fp8_product((const uint8_t*)tiled, N, K, 32, q, s, T, y, trace, (float*)base, ctx->tickets,
+  return launch_fp8_product((const uint8_t*)tiled, N, K, 32, q, s, T, y, trace, (float*)base, ctx,
                             as_stream(stream), nullptr, rows);
 }
 
@@ -810,14 +861,14 @@ int mx_fp8_expert_forward(mx_ctx* ctx, const void* w1, const void* w3, const voi
                  ((uintptr_t)ds & 3) == 0,
              "stage buffers: q/down_q 16-byte, w1/w3 8-byte, scales and down_input 4-byte aligned");
   if (int e = mx_act_quant32(ctx, x, q, s, T, H, stream)) return e;
-  if (int e = launch_fp8_product((const uint8_t*)w1, I, H, 32, q, s, T, b1, nullptr, partial, ctx->tickets, st)) return e;
-  if (int e = launch_fp8_product((const uint8_t*)w3, I, H, 32, q, s, T, b3, nullptr, partial, ctx->tickets, st)) return e;
+  if (int e = launch_fp8_product((const uint8_t*)w1, I, H, 32, q, s, T, b1, nullptr, partial, ctx, st)) return e;
+  if (int e = launch_fp8_product((const uint8_t*)w3, I, H, 32, q, s, T, b3, nullptr, partial, ctx, st)) return e;
   const int64_t n = (int64_t)T * I;
   hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (const uint16_t*)b1,
                      (const uint16_t*)b3, T, I, limit, route_w, din, trace);
   MX_LAUNCH_CHECK("swiglu_kernel");
   if (int e = mx_act_quant32(ctx, din, dq, ds, T, I, stream)) return e;
-  return launch_fp8_product((const uint8_t*)w2, H, I, 32, dq, ds, T, y, nullptr, partial, ctx->tickets, st);
+  return launch_fp8_product((const uint8_t*)w2, H, I, 32, dq, ds, T, y, nullptr, partial, ctx, st);
 }
 
 }  // extern "C"

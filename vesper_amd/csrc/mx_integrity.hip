@@ -198,9 +198,45 @@ __global__ __launch_bounds__(256) void sha256_verify_kernel(VerifyBatch batch, i
   if (!same) atomicAdd(mismatches + batch.counter[s], 1u);
 }
 
+// Audit gate: the counters of up to kGateBatch audited experts; when any is nonzero, every workgroup of the
+// grid overwrites its share of y with BF16 NaN, so nothing computed from a slot that failed its audit can
+// pass as a number.
+constexpr int kGateBatch = 512;
+struct GateBatch {
+  int32_t index[kGateBatch];
+};
+
+__global__ __launch_bounds__(256) void audit_gate_kernel(const uint32_t* __restrict__ counters, GateBatch g, int n,
+                                                         uint16_t* __restrict__ y, uint64_t count) {
+  int flagged = 0;
+  for (int i = threadIdx.x; i < n; i += 256) flagged |= counters[g.index[i]] != 0u;
+  if (!__syncthreads_or(flagged)) return;
+  for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < count; i += (uint64_t)gridDim.x * 256u)
+    y[i] = 0x7FC0u;
+}
+
 }  // namespace
 
 using namespace mxi;
+
+extern "C" int mx_audit_gate(mx_ctx* ctx, const uint32_t* counters, int32_t n_counters, const int32_t* index,
+                             int32_t n, uint16_t* y, uint64_t count, void* stream) {
+  if (int s = use(ctx)) return s;
+  MX_REQUIRE(n >= 0 && n <= kGateBatch, "mx_audit_gate: 0 to %d counters per call", kGateBatch);
+  if (n == 0 || count == 0) return MX_OK;
+  MX_REQUIRE(counters && index && y, "mx_audit_gate: null pointer");
+  GateBatch g{};
+  for (int i = 0; i < n; ++i) {
+    MX_REQUIRE(index[i] >= 0 && index[i] < n_counters, "mx_audit_gate: counter index %d outside [0, %d)", index[i],
+               n_counters);
+    g.index[i] = index[i];
+  }
+  const uint64_t blocks = (count + 255) / 256;
+  hipLaunchKernelGGL(audit_gate_kernel, dim3((unsigned)(blocks < 256 ? blocks : 256)), dim3(256), 0, as_stream(stream),
+                     counters, g, n, y, count);
+  MX_LAUNCH_CHECK("audit_gate_kernel");
+  return MX_OK;
+}
 
 extern "C" int mx_sha256_chunks(mx_ctx* ctx, const void* data, uint64_t bytes, void* digests, void* stream) {
   if (int s = use(ctx)) return s;

@@ -21,11 +21,18 @@ struct mx_ctx {
   void* scratch = nullptr;                          // small reusable device scratch
   uint64_t scratch_bytes = 0;
   uint32_t* tickets = nullptr;                      // [MX_TICKETS] arrival counters, zero between launches
+  float* handoff = nullptr;                         // 2 halves of MX_HANDOFF_BYTES, used on alternate launches
+  int handoff_half = 0;                             // the half the next single-launch split-K GEMV uses
+  uint64_t handoff_dirty[2] = {0, 0};               // bytes of each half a launch wrote and nobody restored yet
 };
 
 // Arrival counters of split-K kernels: the last workgroup of an output tile to arrive finishes the tile
 // and puts its counter back to zero, so the array is zero again whenever the launch has ended.
 #define MX_TICKETS 16384
+// The split-K GEMV's partial sums on its single-launch path, per half. A launch writes its partial sums into
+// one half, which holds the empty pattern (mxd::kHandoffEmpty) everywhere it reads, and restores the pattern
+// over what the previous launch wrote into the other half; the next launch then uses that half.
+#define MX_HANDOFF_BYTES (2u << 20)
 
 // By-value kernel argument of mx_layer_set_experts: up to 64 table entries per launch.
 #define MX_EXPERT_BATCH 64
@@ -47,6 +54,7 @@ int use(mx_ctx* ctx);
 // Context-owned scratch of at least `bytes` (grows; never shrinks until destroy).
 int scratch(mx_ctx* ctx, uint64_t bytes, void** out);
 
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 // What other translation units need of a decode layer (defined with the layer in mx_moe.hip).
@@ -58,6 +66,7 @@ struct LayerView {
   const uint8_t** tiles;   // device [E + 1] tiled expert blobs, shared last
   int has_shared;
   const float* silu;       // device [65537]: mxd::silu_f32 of every BF16 gate value, then of the limit
+  uint32_t* route_errors;  // device word: routing ids replaced by routed decode / prefill since the last clear
 };
 LayerView layer_view(mx_layer* layer);
 

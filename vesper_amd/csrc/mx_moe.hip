@@ -20,6 +20,7 @@
 #include "mx_internal.h"
 #include "mx_numerics.h"
 
+
 namespace {
 
 using mxd::ldg128;
@@ -638,12 +639,13 @@ __global__ __launch_bounds__(kRouteThreads) void route_plan_kernel(const float* 
 }
 
 // Plan from given routing (decode with routing decided elsewhere): ids [T][k] and weights [T][k] are
-// staged in LDS, each token's list is made valid first -- an id outside [0, E) or repeated within the
-// token is replaced by the smallest expert the token does not name, with weight 0 -- so any input keeps
-// the plan's invariants (k distinct experts per token) and every access in bounds.
+// staged in LDS and each token's list is made valid first (mxd::repair_token_routes: an id outside [0, E)
+// or repeated within the token becomes the smallest expert the token does not name, with weight 0), so any
+// input keeps the plan's invariants (k distinct experts per token) and every access in bounds; the number
+// of replaced ids is added to `errors`, which the host reads to refuse the call.
 __global__ __launch_bounds__(kRouteThreads) void routed_plan_kernel(const int32_t* ids, const float* w, int T, int k,
                                                                     int E, int32_t* out_ids, float* out_w, Plan* plan,
-                                                                    int has_shared) {
+                                                                    int has_shared, uint32_t* errors) {
   __shared__ int32_t s_idx[kMaxTokens * kMaxTopK];
   __shared__ float s_w[kMaxTokens * kMaxTopK];
   for (int i = threadIdx.x; i < T * k; i += blockDim.x) {
@@ -652,22 +654,8 @@ __global__ __launch_bounds__(kRouteThreads) void routed_plan_kernel(const int32_
   }
   __syncthreads();
   if (threadIdx.x < T) {
-    int32_t* row = s_idx + threadIdx.x * k;
-    float* wr = s_w + threadIdx.x * k;
-    for (int i = 0; i < k; ++i) {
-      bool bad = row[i] < 0 || row[i] >= E;
-      for (int j = 0; j < i && !bad; ++j) bad = row[j] == row[i];
-      if (!bad) continue;
-      for (int e = 0; e < E; ++e) {
-        bool used = false;
-        for (int j = 0; j < k && !used; ++j) used = (j != i) && row[j] == e;
-        if (!used) {
-          row[i] = e;
-          break;
-        }
-      }
-      wr[i] = 0.f;
-    }
+    const int replaced = mxd::repair_token_routes(s_idx + threadIdx.x * k, s_w + threadIdx.x * k, k, E);
+    if (replaced) atomicAdd(errors, (uint32_t)replaced);
   }
   __syncthreads();
   for (int i = threadIdx.x; i < T * k; i += blockDim.x) {
@@ -676,6 +664,8 @@ __global__ __launch_bounds__(kRouteThreads) void routed_plan_kernel(const int32_
   }
   build_plan(plan, s_idx, s_w, T, k, E, has_shared);
 }
+
+__global__ void set_u32_kernel(uint32_t* p, uint32_t v) { *p = v; }
 
 __global__ void set_experts_kernel(const uint8_t** table, int n, mx_expert_batch b) {
   const int i = threadIdx.x;
@@ -1173,6 +1163,7 @@ struct mx_layer {
   uint16_t *w1 = nullptr, *w3 = nullptr, *din = nullptr, *eout = nullptr;
   Plan* plan = nullptr;
   float* silu = nullptr;   // [mxd::kSiluEntries] SiLU table (prefill epilogue)
+  uint32_t* route_errors = nullptr;   // routing ids replaced by routed decode / prefill since the last clear
   int max_rows = 0;
   // the most recent decode call (mx_layer_time_stage repeats its stages)
   const uint16_t* last_x = nullptr;
@@ -1261,6 +1252,7 @@ LayerView layer_view(mx_layer* L) {
   v.tiles = L->tiles;
   v.has_shared = L->has_shared;
   v.silu = L->silu;
+  v.route_errors = L->route_errors;
   return v;
 }
 
@@ -1387,6 +1379,7 @@ int mx_layer_create(mx_ctx* ctx, const mx_moe_config* cfg, const float* router_w
   if ((s = layer_alloc_t(L, R * I / 32 + 16, &L->ds))) return fail_out(s);
   if ((s = layer_alloc_t(L, R * H, &L->eout))) return fail_out(s);
   if ((s = layer_alloc_t(L, (uint64_t)mxd::kSiluEntries, &L->silu))) return fail_out(s);
+  if ((s = layer_alloc_t(L, 64, &L->route_errors))) return fail_out(s);
   hipLaunchKernelGGL(silu_table_kernel, dim3((mxd::kSiluEntries + 255) / 256), dim3(256), 0, nullptr, L->silu,
                      cfg->swiglu_limit);
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return fail_out(hip_fail(e, "mx_layer_create: SiLU table"));
@@ -1395,6 +1388,7 @@ int mx_layer_create(mx_ctx* ctx, const mx_moe_config* cfg, const float* router_w
   host[E] = shared ? shared : experts[0];
   hipError_t err = hipMemcpy(L->tiles, host.data(), sizeof(void*) * (E + 1), hipMemcpyHostToDevice);
   if (err == hipSuccess) err = hipMemset(L->plan, 0, sizeof(Plan));
+  if (err == hipSuccess) err = hipMemset(L->route_errors, 0, 64 * sizeof(uint32_t));
   if (err == hipSuccess) err = hipDeviceSynchronize();
   if (err != hipSuccess) return fail_out(hip_fail(err, "mx_layer_create: table upload"));
   *out = L;
@@ -1515,7 +1509,7 @@ int mx_moe_decode_routed(mx_layer* L, const uint16_t* x, int32_t T, const int32_
   hipStream_t st = as_stream(stream);
   if (int s = mx_act_quant32(L->ctx, x, L->xq, L->xs, T, c.hidden, stream)) return s;
   hipLaunchKernelGGL(routed_plan_kernel, dim3(1), dim3(64 * T), 0, st, ids, weights, T, c.top_k, c.experts, L->indices,
-                     L->weights, L->plan, L->has_shared);
+                     L->weights, L->plan, L->has_shared, L->route_errors);
   MX_LAUNCH_CHECK("routed_plan_kernel");
   L->last_x = x;
   L->last_y = y;
@@ -1523,6 +1517,20 @@ int mx_moe_decode_routed(mx_layer* L, const uint16_t* x, int32_t T, const int32_
   L->last_diag = false;
   for (int stage = MX_STAGE_GATEUP; stage <= MX_STAGE_COMBINE; ++stage)
     if (int s = launch_stage(L, stage, st)) return s;
+  return MX_OK;
+}
+
+int mx_layer_route_errors(mx_layer* L, uint32_t* count, int32_t clear, void* stream) {
+  MX_REQUIRE(L != nullptr, "layer is closed");
+  if (int s = use(L->ctx)) return s;
+  MX_REQUIRE(count != nullptr, "mx_layer_route_errors: null output");
+  hipStream_t st = as_stream(stream);
+  MX_HIP(hipMemcpyAsync(count, L->route_errors, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+  MX_HIP(hipStreamSynchronize(st));
+  if (clear) {
+    hipLaunchKernelGGL(set_u32_kernel, dim3(1), dim3(1), 0, st, L->route_errors, 0u);
+    MX_LAUNCH_CHECK("set_u32_kernel");
+  }
   return MX_OK;
 }
 
@@ -1593,7 +1601,7 @@ int mx_expert_forward(mx_ctx* ctx, const mx_expert_ptrs* w, int32_t format, int3
   const uint64_t xq_b = ((uint64_t)T * H + 255) & ~255ull, xs_b = ((uint64_t)T * H / 32 + 255) & ~255ull;
   const uint64_t dq_b = ((uint64_t)T * I + 255) & ~255ull, ds_b = ((uint64_t)T * I / 32 + 255) & ~255ull;
   void* base = nullptr;
-  if (int s = scratch(ctx, plan_b + xq_b + xs_b + dq_b + ds_b, &base)) return s;
+  if (int s = mxi::scratch(ctx, plan_b + xq_b + xs_b + dq_b + ds_b, &base)) return s;
   uint8_t* b8 = (uint8_t*)base;
   Plan* plan = (Plan*)b8;
   uint8_t* xq = (stages && stages->q) ? stages->q : b8 + plan_b;
@@ -1629,24 +1637,33 @@ int mx_expert_forward(mx_ctx* ctx, const mx_expert_ptrs* w, int32_t format, int3
   return MX_OK;
 }
 
-int mx_expert_forward_tiled(mx_ctx* ctx, const void* tiled, int32_t H, int32_t I, const uint16_t* x, int32_t T,
-                            float limit, const float* route_w, uint16_t* y, const mx_expert_stages* stages,
-                            void* stream) {
-  if (int s = use(ctx)) return s;
-  MX_REQUIRE(tiled != nullptr && aligned(tiled, 256), "mx_expert_forward_tiled: 256-byte aligned tiled expert required");
-  MX_REQUIRE(H > 0 && H % 128 == 0 && I > 0 && I % 128 == 0, "expert shapes must be positive multiples of 128");
-  MX_REQUIRE(T >= 0 && T <= kMaxTokens, "token count %d outside [0, %d]", T, kMaxTokens);
-  MX_REQUIRE(std::isfinite(limit) && limit >= 0.f, "Invalid SwiGLU limit");
-  if (T == 0) return MX_OK;
-  MX_REQUIRE(x && y && aligned(x, 16) && aligned(y, 16), "x and y must be 16-byte aligned device pointers");
-  hipStream_t st = as_stream(stream);
-  // scratch: plan | one-entry expert table | xq | xs | dq | ds (stage buffers replace them when supplied)
+// Bytes of device scratch one tiled expert call needs: plan | one-entry expert table | xq | xs | dq | ds.
+static uint64_t tiled_call_scratch_bytes(int32_t H, int32_t I, int32_t T) {
   const uint64_t plan_b = (sizeof(Plan) + 255) & ~255ull, table_b = 256;
   const uint64_t xq_b = ((uint64_t)T * H + 255) & ~255ull, xs_b = ((uint64_t)T * H / 32 + 255) & ~255ull;
   const uint64_t dq_b = ((uint64_t)T * I + 255) & ~255ull, ds_b = ((uint64_t)T * I / 32 + 255) & ~255ull;
-  void* base = nullptr;
-  if (int s = scratch(ctx, plan_b + table_b + xq_b + xs_b + dq_b + ds_b, &base)) return s;
-  uint8_t* b8 = (uint8_t*)base;
+  return plan_b + table_b + xq_b + xs_b + dq_b + ds_b;
+}
+
+static int check_tiled_call(const char* what, const void* tiled, int32_t H, int32_t I, const uint16_t* x, int32_t T,
+                            float limit, uint16_t* y) {
+  MX_REQUIRE(tiled != nullptr && aligned(tiled, 256), "%s: 256-byte aligned tiled expert required", what);
+  MX_REQUIRE(H > 0 && H % 128 == 0 && I > 0 && I % 128 == 0, "expert shapes must be positive multiples of 128");
+  MX_REQUIRE(T >= 0 && T <= kMaxTokens, "token count %d outside [0, %d]", T, kMaxTokens);
+  MX_REQUIRE(std::isfinite(limit) && limit >= 0.f, "Invalid SwiGLU limit");
+  MX_REQUIRE(T == 0 || (x && y && aligned(x, 16) && aligned(y, 16)), "x and y must be 16-byte aligned device pointers");
+  return MX_OK;
+}
+
+// The tiled expert call on a given scratch region of tiled_call_scratch_bytes(H, I, T) bytes, 256-byte
+// aligned.
+static int tiled_call_on(mx_ctx* ctx, uint8_t* b8, const void* tiled, int32_t H, int32_t I, const uint16_t* x,
+                         int32_t T, float limit, const float* route_w, uint16_t* y, const mx_expert_stages* stages,
+                         void* stream) {
+  hipStream_t st = as_stream(stream);
+  const uint64_t plan_b = (sizeof(Plan) + 255) & ~255ull, table_b = 256;
+  const uint64_t xq_b = ((uint64_t)T * H + 255) & ~255ull, xs_b = ((uint64_t)T * H / 32 + 255) & ~255ull;
+  const uint64_t dq_b = ((uint64_t)T * I + 255) & ~255ull;
   Plan* plan = (Plan*)b8;
   const uint8_t** table = (const uint8_t**)(b8 + plan_b);
   uint8_t* cur = b8 + plan_b + table_b;
@@ -1685,6 +1702,17 @@ int mx_expert_forward_tiled(mx_ctx* ctx, const void* tiled, int32_t H, int32_t I
   return MX_OK;
 }
 
+int mx_expert_forward_tiled(mx_ctx* ctx, const void* tiled, int32_t H, int32_t I, const uint16_t* x, int32_t T,
+                            float limit, const float* route_w, uint16_t* y, const mx_expert_stages* stages,
+                            void* stream) {
+  if (int s = use(ctx)) return s;
+  if (int s = check_tiled_call("mx_expert_forward_tiled", tiled, H, I, x, T, limit, y)) return s;
+  if (T == 0) return MX_OK;
+  void* base = nullptr;
+  if (int s = mxi::scratch(ctx, tiled_call_scratch_bytes(H, I, T), &base)) return s;
+  return tiled_call_on(ctx, (uint8_t*)base, tiled, H, I, x, T, limit, route_w, y, stages, stream);
+}
+
 int mx_gemv_mxfp4(mx_ctx* ctx, const uint8_t* q, const uint8_t* sa, const uint8_t* w, const uint8_t* sw,
                   uint16_t* y, int32_t T, int32_t N, int32_t K, void* stream) {
   if (int s = use(ctx)) return s;
@@ -1696,7 +1724,7 @@ int mx_gemv_mxfp4(mx_ctx* ctx, const uint8_t* q, const uint8_t* sa, const uint8_
              "mx_gemv_mxfp4: q/w 16-byte, scales 4-byte and y 8-byte alignment required");
   hipStream_t st = as_stream(stream);
   void* base = nullptr;
-  if (int s = scratch(ctx, sizeof(Plan), &base)) return s;
+  if (int s = mxi::scratch(ctx, sizeof(Plan), &base)) return s;
   Plan* plan = (Plan*)base;
   hipLaunchKernelGGL(single_plan_kernel, dim3(1), dim3(64), 0, st, plan, T, (const float*)nullptr);
   MX_LAUNCH_CHECK("single_plan_kernel");
@@ -1774,7 +1802,7 @@ int mx_router(mx_ctx* ctx, const float* W, const float* bias, const uint16_t* x,
   float *scores = out->scores, *selection = out->selection;
   if (!scores || !selection) {
     void* base = nullptr;
-    if (int s = scratch(ctx, (uint64_t)T * E * 8, &base)) return s;
+    if (int s = mxi::scratch(ctx, (uint64_t)T * E * 8, &base)) return s;
     if (!scores) scores = (float*)base;
     if (!selection) selection = (float*)base + (uint64_t)T * E;
   }
@@ -1829,7 +1857,7 @@ int mx_router_postprocess(mx_ctx* ctx, const float* logits, const float* bias, i
   float *scores = out->scores, *selection = out->selection;
   if (!scores || !selection) {
     void* base = nullptr;
-    if (int s = scratch(ctx, (uint64_t)T * E * 8, &base)) return s;
+    if (int s = mxi::scratch(ctx, (uint64_t)T * E * 8, &base)) return s;
     if (!scores) scores = (float*)base;
     if (!selection) selection = (float*)base + (uint64_t)T * E;
   }

@@ -7,11 +7,12 @@
 //   plan      count pairs per expert, expert-major row offsets (shared expert last) and 128-row tiles;
 //             a stable per-expert scatter gives each expert's rows in ascending token order
 //             (participation, src/vesper/moe.py:18-30) and each (token, rank) pair its row
-//   gate/up   grid (I/128, tiles), 4 waves: 4 groups of 32 intermediate rows (W1 + W3 interleaved per
-//             MFMA tile, as in the tiled layout), each wave one group for all 128 tokens of the tile; the
-//             tokens' E4M3 rows are copied global -> LDS per 128-wide K chunk; epilogue SwiGLU + route
-//             weight + the per-token quantization of each 32-row block of the down input
-//   down      grid (H/256, tiles), same shape over W2 with the tile's contiguous down-input rows
+//   gate/up   grid (ceil(I/256), tiles), 8 waves: 8 groups of 32 intermediate rows (W1 + W3 interleaved
+//             per MFMA tile, as in the tiled layout), each wave one group for all 128 tokens of the tile;
+//             the tokens' E4M3 rows are copied global -> LDS per 128-wide K chunk; epilogue SwiGLU +
+//             route weight + the per-token quantization of each 32-row block of the down input
+//   down      grid (ceil(H/512), tiles), 8 waves over 64-row groups of W2 with the tile's contiguous
+//             down-input rows
 //   combine   per token: its expert rows in ascending expert ID, then the shared row; FP32 from +0,
 //             one BF16 rounding (aggregation_probe.cu:4-25). The down GEMM writes each row to the
 //             token's contiguous [k + 1][H] block in that order, so the combine streams it.
@@ -51,8 +52,28 @@ __global__ void zero_i32_kernel(int32_t* p, int n) {
   if (i < n) p[i] = 0;
 }
 
-// Routing ids outside [0, E) (the C caller's responsibility) are skipped by every plan step and by the
-// combine, so such input gives wrong rows for its token but never an access out of bounds.
+// Given routing is first copied into the workspace with each token's list made valid (the decode path's
+// rule, mxd::repair_token_routes) and the replacements counted in the layer's routing error word; the
+// plan steps below additionally skip ids outside [0, E), so no input can take an access out of bounds.
+__global__ __launch_bounds__(256) void repair_routes_kernel(const int32_t* __restrict__ ids, const float* __restrict__ w,
+                                                            int T, int k, int E, int32_t* __restrict__ out_ids,
+                                                            float* __restrict__ out_w, uint32_t* errors) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= T) return;
+  int32_t row[kMaxTopK];
+  float wr[kMaxTopK];
+  for (int i = 0; i < k; ++i) {
+    row[i] = ids[(size_t)t * k + i];
+    wr[i] = w[(size_t)t * k + i];
+  }
+  const int replaced = mxd::repair_token_routes(row, wr, k, E);
+  if (replaced) atomicAdd(errors, (uint32_t)replaced);
+  for (int i = 0; i < k; ++i) {
+    out_ids[(size_t)t * k + i] = row[i];
+    out_w[(size_t)t * k + i] = wr[i];
+  }
+}
+
 // Per-workgroup LDS histogram, then one global atomic per nonzero bin (E <= 1024).
 __global__ __launch_bounds__(256) void count_kernel(const int32_t* __restrict__ ids, int n, int E,
                                                     int32_t* __restrict__ counts) {
@@ -589,6 +610,14 @@ int mx_moe_prefill(mx_layer* layer, const uint16_t* x, int32_t T, const int32_t*
       return s;
     rid = out.indices;
     rw = out.weights;
+  } else {
+    int32_t* fixed_ids = (int32_t*)(b + ws.ids);
+    float* fixed_w = (float*)(b + ws.w);
+    hipLaunchKernelGGL(repair_routes_kernel, dim3((T + 255) / 256), dim3(256), 0, st, ids, weights, T, k, E, fixed_ids,
+                       fixed_w, v.route_errors);
+    MX_LAUNCH_CHECK("repair_routes_kernel");
+    rid = fixed_ids;
+    rw = fixed_w;
   }
   if (int s = mx_act_quant32(v.ctx, x, b + ws.xq, b + ws.xs, T, H, stream)) return s;
   PrefillPlan p{};

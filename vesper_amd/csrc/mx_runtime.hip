@@ -48,6 +48,15 @@ int scratch(mx_ctx* ctx, uint64_t bytes, void** out) {
 
 }  // namespace mxi
 
+namespace {
+
+__global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+}  // namespace
+
 using namespace mxi;
 
 extern "C" {
@@ -70,16 +79,26 @@ int mx_create(int device, uint64_t cap_bytes, mx_ctx** out) {
   MX_HIP(hipSetDevice(device));
   MX_HIP(hipFree(nullptr));  // initialise the device's primary context now
   uint32_t* tickets = nullptr;
+  float* handoff = nullptr;
   MX_HIP(hipMalloc(&tickets, MX_TICKETS * sizeof(uint32_t)));
-  if (hipMemset(tickets, 0, MX_TICKETS * sizeof(uint32_t)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
-    const hipError_t err = hipGetLastError();
+  hipError_t err = hipMalloc(&handoff, 2 * (size_t)MX_HANDOFF_BYTES);
+  if (err == hipSuccess) err = hipMemset(tickets, 0, MX_TICKETS * sizeof(uint32_t));
+  if (err == hipSuccess) {
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(2 * MX_HANDOFF_BYTES / 4 / 256), dim3(256), 0, nullptr,
+                       (uint32_t*)handoff, (int64_t)(2 * MX_HANDOFF_BYTES / 4), mxd::kHandoffEmpty);
+    err = hipGetLastError();
+  }
+  if (err == hipSuccess) err = hipDeviceSynchronize();
+  if (err != hipSuccess) {
     (void)hipFree(tickets);
-    return hip_fail(err, "mx_create: clear the arrival counters");
+    if (handoff) (void)hipFree(handoff);
+    return hip_fail(err, "mx_create: set up the arrival counters and handoff buffer");
   }
   mx_ctx* ctx = new mx_ctx();
   ctx->device = device;
   ctx->cap = cap_bytes;
   ctx->tickets = tickets;
+  ctx->handoff = handoff;
   *out = ctx;
   return MX_OK;
 }
@@ -93,6 +112,7 @@ int mx_destroy(mx_ctx* ctx) {
     for (auto& kv : ctx->pinned) (void)hipHostFree(kv.first);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->tickets) (void)hipFree(ctx->tickets);
+    if (ctx->handoff) (void)hipFree(ctx->handoff);
   }
   delete ctx;
   return status;

@@ -233,6 +233,12 @@ class MoELayer:
                 d.free()
             self.ctx.free(ws)
 
+    def route_errors(self, clear: bool = True, stream=None) -> int:
+        """Routing ids that routed decode / prefill replaced since the last clear (synchronises `stream`)."""
+        count = C.c_uint32()
+        self.lib.layer_route_errors(self.handle, C.byref(count), int(bool(clear)), _lib._stream(stream))
+        return int(count.value)
+
     # -- diagnostics ------------------------------------------------------------------------
     def buffer(self, name: str):
         p, n = C.c_void_p(), C.c_uint64()

@@ -261,12 +261,19 @@ class OffloadDecode:
     re-point the layer's table (one launch), decode, release the slots -- all asynchronous, so the next
     layer's copies overlap this layer's compute.
 
+    Routing is validated on the host when it is loaded (ids in range and distinct per token, weights finite:
+    the reference's participation refusals, src/vesper/moe.py:18-30), and step_device runs what was loaded.
+
     audit=True is the reference's gpu-sha256 admission mode for this asynchronous path: every expert's
     digest table is taken once from its pinned source bytes (hashed on the device) and kept in HBM; the
     slots a layer admits are verified in one launch on an audit stream that waits for their copies, and
-    the compute stream waits for the audit (so no expert runs unverified) while the copy stream goes on
-    with the next layer's copies; differing chunks accumulate in per-expert counters. check_audit() (after a synchronisation) refuses the steps since the last check if any
-    admitted slot differed, and drops those slots from the cache.
+    the compute stream waits for the audit while the copy stream goes on with the next layer's copies;
+    differing chunks accumulate in per-expert counters. After each layer an audit gate (mx_audit_gate)
+    overwrites the layer's output with NaN when any expert it used -- admitted now or served as a hit of
+    an earlier admission -- has a nonzero counter, so an output computed from bytes that failed their audit
+    never passes as a number, and the NaN carries through every later layer. check_audit() (after a
+    synchronisation) then refuses with ValueError, drops the failing slots from the cache and clears the
+    counters; until it is called, a failing slot stays cached and every output that used it is NaN.
     """
 
     def __init__(self, ctx: _lib.Context, config: MoEConfig, layers: int, pool_of, shared_ptrs, cache: ExpertCache,
@@ -291,6 +298,7 @@ class OffloadDecode:
                 pool, index = pool_of(layer, e)
                 cache.register(expert_key(layer, e), pool.ptr(index))
         t, k = config.max_tokens, config.top_k
+        self.routing = None
         self.ids = [ctx.empty((t, k), np.int32) for _ in range(self.layers)]
         self.wts = [ctx.empty((t, k), np.float32) for _ in range(self.layers)]
         self._owned += self.ids + self.wts
@@ -315,16 +323,74 @@ class OffloadDecode:
     def _table(self, layer: int, expert: int) -> int:
         return self.tables.ptr + (layer * self.config.experts + expert) * self.table_bytes
 
-    def load_routing(self, routing):
-        """routing[layer] = (ids [T, k] int32, weights [T, k] FP32), copied to the device (synchronously)."""
-        for layer, (ids, w) in enumerate(routing):
-            self.ctx.copy_h2d(self.ids[layer].ptr, np.ascontiguousarray(ids, np.int32))
-            self.ctx.copy_h2d(self.wts[layer].ptr, np.ascontiguousarray(w, np.float32))
+    def _checked_ids(self, ids) -> np.ndarray:
+        cfg = self.config
+        ids = np.ascontiguousarray(ids)
+        if ids.dtype.kind not in "iu" or ids.ndim != 2 or ids.shape[1] != cfg.top_k or not 1 <= len(ids) <= cfg.max_tokens:
+            raise ValueError(f"routing ids must be [T, {cfg.top_k}] integers with 1 <= T <= {cfg.max_tokens}")
+        if ids.min() < 0 or ids.max() >= cfg.experts:
+            raise ValueError("Expert ID is outside the pinned model")
+        if cfg.top_k > 1 and np.any(np.diff(np.sort(ids, axis=1), axis=1) == 0):
+            raise ValueError("Repeated expert IDs within a token are outside the unique-topk scope")
+        return ids.astype(np.int32)
 
-    def step_device(self, x_ptr: int, tokens: int, y_ptrs, routing_host):
-        """Enqueue one step on self.stream; routing_host[layer] = ids [T, k] (host, for the cache keys)."""
+    def load_routing(self, routing):
+        """routing[layer] = (ids [T, k] integers, weights [T, k] FP32): validated, kept on the host for the
+        cache keys and copied to the device (synchronously). Raises ValueError before any copy."""
+        if len(routing) != self.layers:
+            raise ValueError(f"routing must give {self.layers} layers")
+        checked = []
+        for ids, w in routing:
+            ids = self._checked_ids(ids)
+            w = np.ascontiguousarray(w, np.float32)
+            if w.shape != ids.shape or not np.isfinite(w).all():
+                raise ValueError("route weights must be finite and shaped like the ids")
+            checked.append((ids, w))
+        for layer, (ids, w) in enumerate(checked):
+            self.ctx.copy_h2d(self.ids[layer].ptr, ids)
+            self.ctx.copy_h2d(self.wts[layer].ptr, w)
+        self.routing = [ids for ids, _ in checked]
+
+    def load_routing_device(self, host_ids, device_routing, stream=None):
+        """Routing already on the device: device_routing[layer] = (ids, weights) device arrays of [T, k], copied
+        into place on `stream` without a host wait; host_ids[layer] is the same ids on the host, validated and
+        used for the cache keys. A device copy that differs from the host ids reaches the kernels' own
+        validation: check_routes() after a synchronisation refuses the steps since the last check."""
+        if len(host_ids) != self.layers or len(device_routing) != self.layers:
+            raise ValueError(f"routing must give {self.layers} layers")
+        checked = [self._checked_ids(ids) for ids in host_ids]
+        for layer, (ids_dev, w_dev) in enumerate(device_routing):
+            nbytes = checked[layer].nbytes
+            if ids_dev.nbytes != nbytes or w_dev.nbytes != nbytes:
+                raise ValueError("device routing must match the host ids' shape")
+            self.ctx.copy_d2d(self.ids[layer].ptr, ids_dev.ptr, nbytes, stream)
+            self.ctx.copy_d2d(self.wts[layer].ptr, w_dev.ptr, nbytes, stream)
+        self.routing = checked
+
+    def check_routes(self):
+        """After a synchronisation: ValueError if any layer's kernels replaced a routing id since the last check
+        (an id that the host validation did not see, e.g. a device copy that differs)."""
+        replaced = {}
+        for layer, h in enumerate(self.handles):
+            count = C.c_uint32()
+            self.lib.layer_route_errors(h, C.byref(count), 1, _lib._stream(self.stream))
+            if count.value:
+                replaced[layer] = int(count.value)
+        if replaced:
+            raise ValueError(f"routing ids outside the model or repeated within a token (per layer: {replaced})")
+
+    def step_device(self, x_ptr: int, tokens: int, y_ptrs, routing_host=None):
+        """Enqueue one step on self.stream over the routing of the last load_routing (routing_host, if given,
+        must be that routing)."""
+        if self.routing is None:
+            raise RuntimeError("load_routing() must come before a step")
+        if routing_host is not None and any(not np.array_equal(np.asarray(r)[:tokens], own[:tokens])
+                                            for r, own in zip(routing_host, self.routing)):
+            raise ValueError("step routing differs from the routing loaded on the device")
+        if not 1 <= tokens <= min(len(r) for r in self.routing):
+            raise ValueError("token count outside the loaded routing")
         for layer in range(self.layers):
-            experts = np.unique(routing_host[layer][:tokens])
+            experts = np.unique(self.routing[layer][:tokens])
             keys = [expert_key(layer, int(e)) for e in experts]
             ptrs, hits = self.cache.ensure(keys)
             if self.audit:
@@ -348,6 +414,11 @@ class OffloadDecode:
             self.lib.moe_decode_routed(self.handles[layer], C.c_void_p(int(src)), int(tokens),
                                        C.c_void_p(self.ids[layer].ptr), C.c_void_p(self.wts[layer].ptr),
                                        C.c_void_p(int(y_ptrs[layer])), _lib._stream(self.stream))
+            if self.audit:
+                used = (C.c_int32 * len(experts))(*[layer * self.config.experts + int(e) for e in experts])
+                self.lib.audit_gate(self.ctx._h(), C.c_void_p(self.mismatch.ptr), self.layers * self.config.experts,
+                                    used, len(experts), C.c_void_p(int(y_ptrs[layer])),
+                                    int(tokens) * self.config.hidden, _lib._stream(self.stream))
             self.cache.release(keys, self.stream)
 
     def check_audit(self):
@@ -381,6 +452,7 @@ class OffloadDecode:
 
 
 def decode_routed(layer, x_ptr: int, tokens: int, ids_ptr: int, weights_ptr: int, y_ptr: int, stream=None):
-    """mx_moe_decode_routed on a MoELayer (routing given on the device)."""
+    """mx_moe_decode_routed on a MoELayer (routing given on the device). Invalid ids are replaced in bounds and
+    counted: read MoELayer.route_errors() after the call to refuse its output."""
     layer.lib.moe_decode_routed(layer.handle, C.c_void_p(int(x_ptr)), int(tokens), C.c_void_p(int(ids_ptr)),
                                 C.c_void_p(int(weights_ptr)), C.c_void_p(int(y_ptr)), _lib._stream(stream))
