@@ -213,6 +213,17 @@ int mx_expert_forward_tiled(mx_ctx* ctx, const void* tiled, int32_t hidden, int3
                             const uint16_t* x_bf16, int32_t tokens, float swiglu_limit, const float* route_w,
                             uint16_t* y_bf16, const mx_expert_stages* stages, void* stream);
 
+/* mx_expert_forward_tiled without any device allocation: no counterpart in the reference. For callers that
+ * cannot allocate -- code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * Same arguments, kernels and results; the call's plan, expert table and quantized activations live in a
+ * fixed device array of MX_NOALLOC_SCRATCH_BYTES per GPU (taken by mx_create, held until the process ends)
+ * instead of the context's growable scratch. A call whose plan + tokens x (H + I) x 33/32 bytes exceed it is
+ * refused with MX_ERR_INVALID (16 tokens of a 7168 x 2048 expert need about 0.23 MiB). Every call on one GPU
+ * shares the array, so calls that overlap on one GPU race: serialise them (one stream, or events). */
+#define MX_NOALLOC_SCRATCH_BYTES (1u << 20)
+int mx_expert_forward_tiled_noalloc(mx_ctx* ctx, const void* tiled, int32_t hidden, int32_t intermediate,
+                                    const uint16_t* x_bf16, int32_t tokens, float swiglu_limit, const float* route_w,
+                                    uint16_t* y_bf16, const mx_expert_stages* stages, void* stream);
 
 /* ---- router (replaces GateProjection.project + RouterProbe, src/vesper/gate.py:133-147,
  *      src/vesper/router.py:227-264, routing_probe.cu:5-86) ---- */

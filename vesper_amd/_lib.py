@@ -107,6 +107,8 @@ SIGNATURES = {
     "mx_prefill_workspace_bytes": ([_P, _I32], _U64),
     "mx_moe_decode_routed": ([_P, _P, _I32, _P, _P, _P, _P], C.c_int),
     "mx_expert_forward_tiled": ([_P, _P, _I32, _I32, _P, _I32, _F, _P, _P, C.POINTER(MxExpertStages), _P], C.c_int),
+    "mx_expert_forward_tiled_noalloc": ([_P, _P, _I32, _I32, _P, _I32, _F, _P, _P, C.POINTER(MxExpertStages), _P],
+                                        C.c_int),
     "mx_layer_set_experts": ([_P, _I32, _P, _P, _P], C.c_int),
     "mx_layer_route_errors": ([_P, C.POINTER(C.c_uint32), _I32, _P], C.c_int),
     "mx_cache_create": ([_P, _U64, _I32, C.POINTER(_P)], C.c_int),

@@ -54,6 +54,10 @@ int use(mx_ctx* ctx);
 // Context-owned scratch of at least `bytes` (grows; never shrinks until destroy).
 int scratch(mx_ctx* ctx, uint64_t bytes, void** out);
 
+// The allocation-free tiled expert call's fixed device array (mx_moe.hip): its device address is taken once
+// per device, with the device current (mx_create), and looked up by later calls on that device.
+int noalloc_scratch_init(int device);
+int noalloc_scratch(int device, uint8_t** out);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 

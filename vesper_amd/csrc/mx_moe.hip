@@ -14,12 +14,19 @@
 // never materialises dequantized weights.
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <vector>
 
 #include "mx_device.h"
 #include "mx_internal.h"
 #include "mx_numerics.h"
 
+// Fixed device memory of the allocation-free tiled expert call (mx_expert_forward_tiled_noalloc): its plan,
+// one-entry expert table and quantized activations, MX_NOALLOC_SCRATCH_BYTES on every GPU the library runs
+// on, held until the process ends. Host code reaches it only through the device address that
+// mxi::noalloc_scratch_init takes once per device. Every call on a GPU shares it: calls that overlap on one
+// GPU race. Nothing in it needs to start at zero (each call writes what it reads).
+static __device__ __align__(256) uint8_t scratch[MX_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -1256,6 +1263,35 @@ LayerView layer_view(mx_layer* L) {
   return v;
 }
 
+namespace {
+constexpr int kNoallocDevices = 64;
+std::mutex g_noalloc_lock;
+uint8_t* g_noalloc_ptr[kNoallocDevices] = {};   // scratch's device address on each GPU (null until set up)
+}  // namespace
+
+int noalloc_scratch_init(int device) {
+  MX_REQUIRE(device >= 0 && device < kNoallocDevices, "device %d outside the %d the library supports", device,
+             kNoallocDevices);
+  std::lock_guard<std::mutex> guard(g_noalloc_lock);
+  if (g_noalloc_ptr[device]) return MX_OK;
+  // with `device` current: each GPU holds its own copy of the array at its own address; the host-side name is
+  // only a stand-in, so every later use goes through this pointer
+  void* p = nullptr;
+  MX_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(::scratch)));   // the array, not mxi::scratch
+  MX_REQUIRE(p != nullptr && ((uintptr_t)p & 255) == 0, "device scratch is not 256-byte aligned");
+  g_noalloc_ptr[device] = (uint8_t*)p;
+  return MX_OK;
+}
+
+int noalloc_scratch(int device, uint8_t** out) {
+  MX_REQUIRE(device >= 0 && device < kNoallocDevices, "device %d outside the %d the library supports", device,
+             kNoallocDevices);
+  std::lock_guard<std::mutex> guard(g_noalloc_lock);
+  if (!g_noalloc_ptr[device]) return fail(MX_ERR_STATE, "device scratch of device %d was not set up", device);
+  *out = g_noalloc_ptr[device];
+  return MX_OK;
+}
+
 }  // namespace mxi
 
 namespace {
@@ -1656,7 +1692,7 @@ static int check_tiled_call(const char* what, const void* tiled, int32_t H, int3
 }
 
 // The tiled expert call on a given scratch region of tiled_call_scratch_bytes(H, I, T) bytes, 256-byte
-// aligned.
+// aligned (the context's scratch, or the allocation-free entry point's fixed array).
 static int tiled_call_on(mx_ctx* ctx, uint8_t* b8, const void* tiled, int32_t H, int32_t I, const uint16_t* x,
                          int32_t T, float limit, const float* route_w, uint16_t* y, const mx_expert_stages* stages,
                          void* stream) {
@@ -1711,6 +1747,22 @@ int mx_expert_forward_tiled(mx_ctx* ctx, const void* tiled, int32_t H, int32_t I
   void* base = nullptr;
   if (int s = mxi::scratch(ctx, tiled_call_scratch_bytes(H, I, T), &base)) return s;
   return tiled_call_on(ctx, (uint8_t*)base, tiled, H, I, x, T, limit, route_w, y, stages, stream);
+}
+
+int mx_expert_forward_tiled_noalloc(mx_ctx* ctx, const void* tiled, int32_t H, int32_t I, const uint16_t* x,
+                                    int32_t T, float limit, const float* route_w, uint16_t* y,
+                                    const mx_expert_stages* stages, void* stream) {
+  if (int s = use(ctx)) return s;
+  if (int s = check_tiled_call("mx_expert_forward_tiled_noalloc", tiled, H, I, x, T, limit, y)) return s;
+  const uint64_t need = tiled_call_scratch_bytes(H, I, T);
+  MX_REQUIRE(need <= MX_NOALLOC_SCRATCH_BYTES,
+             "mx_expert_forward_tiled_noalloc: %d tokens of a %d x %d expert need %llu bytes of scratch, more than "
+             "the fixed %llu (use mx_expert_forward_tiled)",
+             T, H, I, (unsigned long long)need, (unsigned long long)MX_NOALLOC_SCRATCH_BYTES);
+  if (T == 0) return MX_OK;
+  uint8_t* base = nullptr;
+  if (int s = noalloc_scratch(ctx->device, &base)) return s;
+  return tiled_call_on(ctx, base, tiled, H, I, x, T, limit, route_w, y, stages, stream);
 }
 
 int mx_gemv_mxfp4(mx_ctx* ctx, const uint8_t* q, const uint8_t* sa, const uint8_t* w, const uint8_t* sw,

@@ -78,6 +78,7 @@ int mx_create(int device, uint64_t cap_bytes, mx_ctx** out) {
   MX_REQUIRE(device >= 0 && device < n, "mx_create: device %d not present (%d visible)", device, n);
   MX_HIP(hipSetDevice(device));
   MX_HIP(hipFree(nullptr));  // initialise the device's primary context now
+  if (int s = noalloc_scratch_init(device)) return s;
   uint32_t* tickets = nullptr;
   float* handoff = nullptr;
   MX_HIP(hipMalloc(&tickets, MX_TICKETS * sizeof(uint32_t)));
