@@ -52,6 +52,8 @@ int mx_create(int device, uint64_t cap_bytes, mx_ctx** out);
 int mx_destroy(mx_ctx* ctx);
 /* Name and gfx architecture of the context's device, e.g. "gfx950". */
 int mx_device_name(mx_ctx* ctx, char* name, size_t name_bytes, char* arch, size_t arch_bytes);
+/* Free and total bytes of the context's device (Device.memory, src/vesper/cuda.py:115-119). */
+int mx_device_memory(mx_ctx* ctx, uint64_t* free_bytes, uint64_t* total_bytes);
 int mx_malloc(mx_ctx* ctx, uint64_t bytes, void** dptr);       /* Device.allocate (cuda.py:121-138) */
 int mx_free(mx_ctx* ctx, void* dptr);                           /* Device.free                        */
 int mx_owned_bytes(mx_ctx* ctx, uint64_t* live, uint64_t* peak);/* Device.peak / allocations          */

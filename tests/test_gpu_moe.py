@@ -1,4 +1,4 @@
-"""GPU parity of the routed MoE layer (ConnectedMoE / mx_moe_decode) and the ordered accumulator.
+"""GPU parity of the routed MoE layer (ConnectedLayer / mx_moe_decode) and the ordered accumulator.
 
 * MoEAccumulator on the device reproduces the 38 recorded official aggregation cases
   (SHA-256 of every FP32 stage and the BF16 output).
@@ -23,7 +23,7 @@ from oracle.router import gate_logits, route
 from tests.helpers import assert_close, assert_gemv_close, max_rel_err
 from vesper_amd import _lib
 from vesper_amd.config import MoEConfig
-from vesper_amd.connected import ConnectedMoE
+from vesper_amd.connected import ConnectedLayer
 from vesper_amd.layer import ExpertBank, MoELayer
 from vesper_amd.moe import MoEAccumulator
 
@@ -63,7 +63,7 @@ def build_layer(ctx, cfg, rng, router_scale=1.0, device_fill=False):
 
 
 def check_layer_call(layer, bank, w, arrays, x, cfg):
-    out = ConnectedMoE(layer).forward(x)          # asserts fused combine == stepwise accumulation
+    out = ConnectedLayer(layer).forward(x)          # asserts fused combine == stepwise accumulation
     t = x.shape[0]
     logits = out["logits"]
     assert max_rel_err(logits, gate_logits(w, x)) < 1e-5
@@ -156,7 +156,7 @@ def test_baseline_shapes_sixteen_tokens_properties(gpu_ctx):
     layer, bank, w, _ = build_layer(gpu_ctx, cfg, rng, device_fill=True)
     try:
         x = activations(rng, 16, cfg.hidden)
-        out = ConnectedMoE(layer).forward(x)
+        out = ConnectedLayer(layer).forward(x)
         r = out["routing"]
         ref_route = route(out["logits"], cfg.top_k, cfg.route_scale, cfg.score_func)
         np.testing.assert_array_equal(r["indices"], ref_route["indices"])

@@ -1,4 +1,4 @@
-"""GPU tests of host-pinned expert streaming (ExpertCache / TieredExpertRuntime / OffloadDecode).
+"""GPU tests of host-pinned expert streaming (ExpertCache / PooledExpertRuntime / OffloadDecode).
 
 The cache moves bytes and never touches the arithmetic, so every result through it must equal the resident
 path bit for bit: the tiered single-expert call against ResidentExpert, and a chain of MoE layers whose
@@ -17,8 +17,8 @@ from vesper_amd import _lib
 from vesper_amd.config import MoEConfig
 from vesper_amd.expert import ResidentExpert
 from vesper_amd.layer import ExpertBank, MoELayer
-from vesper_amd.tiered import (CacheConfig, ExpertCache, HostExpertPool, OffloadDecode, TieredExpertRuntime,
-                               decode_routed, expert_key)
+from vesper_amd.tiered import (ExpertCache, HostExpertPool, OffloadDecode, PooledExpertRuntime, decode_routed,
+                               expert_key)
 
 pytestmark = pytest.mark.gpu
 
@@ -64,7 +64,7 @@ def test_cache_lru_order_and_slot_bytes(gpu_ctx):
         gpu_ctx.host_free_pinned(host)
 
 
-def test_tiered_runtime_matches_resident_expert(gpu_ctx):
+def test_pooled_runtime_matches_resident_expert(gpu_ctx):
     cfg = MoEConfig(hidden=512, intermediate=256, experts=4, top_k=1, swiglu_limit=10.0, shared=None)
     rng = np.random.default_rng(12)
     arrays = [mxfp4_expert(rng, cfg.hidden, cfg.intermediate) for _ in range(4)]
@@ -73,7 +73,7 @@ def test_tiered_runtime_matches_resident_expert(gpu_ctx):
     try:
         for i, arr in enumerate(arrays):
             pool.upload_arrays(i, arr, staging)
-        rt = TieredExpertRuntime(gpu_ctx, cfg, pool, {f"0:{i}": i for i in range(4)}, CacheConfig(primary_slots=2))
+        rt = PooledExpertRuntime(gpu_ctx, cfg, pool, {f"0:{i}": i for i in range(4)}, slots=2)
         x = activations(rng, 3, cfg.hidden)
         tiers = []
         try:
@@ -98,7 +98,7 @@ def test_tiered_runtime_matches_resident_expert(gpu_ctx):
 
 
 def test_gpu_sha256_admission_audit(gpu_ctx):
-    """integrity_mode "gpu-sha256": every admitted slot is hashed on the device against its source's digest
+    """audit=True (the gpu-sha256 mode): every admitted slot is hashed on the device against its source's digest
     table before the expert runs. A source byte flipped after its table was taken makes the next admission
     fail (ValueError) and the slot is dropped, never served; with the byte restored the key is admitted
     afresh and computes what the resident expert computes."""
@@ -111,10 +111,7 @@ def test_gpu_sha256_admission_audit(gpu_ctx):
         for i, arr in enumerate(arrays):
             pool.upload_arrays(i, arr, staging)
         gpu_ctx.sync()
-        with pytest.raises(ValueError):
-            CacheConfig(integrity_mode="readback")
-        rt = TieredExpertRuntime(gpu_ctx, cfg, pool, {f"0:{i}": i for i in range(3)},
-                                 CacheConfig(primary_slots=2, integrity_mode="gpu-sha256"))
+        rt = PooledExpertRuntime(gpu_ctx, cfg, pool, {f"0:{i}": i for i in range(3)}, slots=2, audit=True)
         x = activations(rng, 2, cfg.hidden)
         try:
             for key in ("0:1", "0:0", "0:2"):                   # 0:1 admitted, then evicted

@@ -60,6 +60,7 @@ SIGNATURES = {
     "mx_create": ([C.c_int, _U64, C.POINTER(_P)], C.c_int),
     "mx_destroy": ([_P], C.c_int),
     "mx_device_name": ([_P, C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t], C.c_int),
+    "mx_device_memory": ([_P, C.POINTER(_U64), C.POINTER(_U64)], C.c_int),
     "mx_malloc": ([_P, _U64, C.POINTER(_P)], C.c_int),
     "mx_free": ([_P, _P], C.c_int),
     "mx_owned_bytes": ([_P, C.POINTER(_U64), C.POINTER(_U64)], C.c_int),
@@ -261,6 +262,12 @@ class Context:
         name, arch = C.create_string_buffer(256), C.create_string_buffer(64)
         self.lib.device_name(self._h(), name, 256, arch, 64)
         return name.value.decode(), arch.value.decode()
+
+    def memory(self) -> dict:
+        """{"free", "total"} bytes of the device (Device.memory, cuda.py:115-119)."""
+        free, total = C.c_uint64(), C.c_uint64()
+        self.lib.device_memory(self._h(), C.byref(free), C.byref(total))
+        return {"free": free.value, "total": total.value}
 
     def malloc(self, nbytes: int) -> int:
         p = C.c_void_p()

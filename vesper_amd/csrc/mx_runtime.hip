@@ -128,6 +128,16 @@ int mx_device_name(mx_ctx* ctx, char* name, size_t name_bytes, char* arch, size_
   return MX_OK;
 }
 
+int mx_device_memory(mx_ctx* ctx, uint64_t* free_bytes, uint64_t* total_bytes) {
+  if (int s = use(ctx)) return s;
+  MX_REQUIRE(free_bytes != nullptr && total_bytes != nullptr, "mx_device_memory: null output");
+  size_t f = 0, t = 0;
+  MX_HIP(hipMemGetInfo(&f, &t));
+  *free_bytes = f;
+  *total_bytes = t;
+  return MX_OK;
+}
+
 int mx_malloc(mx_ctx* ctx, uint64_t bytes, void** dptr) {
   if (int s = use(ctx)) return s;
   MX_REQUIRE(dptr != nullptr, "mx_malloc: null output");

@@ -41,7 +41,7 @@ def validate_expert_arrays(arrays: dict, hidden: int, intermediate: int):
 class ExpertExecutor:
     """Native expert arithmetic and reusable workspace, independent of residency."""
 
-    def __init__(self, ordinal=0, swiglu_limit=10.0, device_cap=64 * MiB, *, hidden=7168, intermediate=2048):
+    def __init__(self, ordinal=0, swiglu_limit=10.0, device_cap=64 * MiB, *, hidden=5120, intermediate=2304):
         if not math.isfinite(swiglu_limit) or swiglu_limit < 0:
             raise ValueError("Invalid SwiGLU limit")
         if hidden <= 0 or hidden % 128 or intermediate <= 0 or intermediate % 128:
@@ -126,7 +126,7 @@ class ExpertExecutor:
 class ResidentExpert(ExpertExecutor):
     """Uploads one expert on enter; forward(x, routing_weight) (expert.py:95-114)."""
 
-    def __init__(self, arrays: dict, ordinal=0, swiglu_limit=10.0, *, hidden=7168, intermediate=2048):
+    def __init__(self, arrays: dict, ordinal=0, swiglu_limit=10.0, *, hidden=5120, intermediate=2304):
         validate_expert_arrays(arrays, hidden, intermediate)
         super().__init__(ordinal, swiglu_limit, hidden=hidden, intermediate=intermediate)
         self.arrays = arrays

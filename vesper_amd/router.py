@@ -19,12 +19,12 @@ import numpy as np
 from . import _lib
 from .layer import bf16_input
 
-ROUTER_CONFIG = {"experts": 256, "topk": 8, "score_func": "sigmoid", "route_scale": 2.5,
+ROUTER_CONFIG = {"experts": 384, "topk": 6, "score_func": "sqrtsoftplus", "route_scale": 1.5,
                  "normalization_epsilon": 1e-20}
 
 
 class RouterProbe:
-    def __init__(self, arrays=None, ordinal=0, *, experts=256, top_k=8, score_func="sigmoid", route_scale=2.5):
+    def __init__(self, arrays=None, ordinal=0, *, experts=384, top_k=6, score_func="sqrtsoftplus", route_scale=1.5):
         if score_func not in _lib.MX_SCORE:
             raise ValueError("Unknown score function")
         if not 1 <= experts <= 1024 or not 1 <= top_k <= min(32, experts) or not math.isfinite(route_scale):

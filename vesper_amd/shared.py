@@ -43,7 +43,7 @@ def validate_shared_arrays(arrays, hidden: int, intermediate: int):
 class ResidentSharedExpert(ExpertExecutor):
     """forward(x) = expert(x) with no routing weight (shared.py:169-170)."""
 
-    def __init__(self, arrays: dict, ordinal=0, swiglu_limit=10.0, *, hidden=7168, intermediate=2048):
+    def __init__(self, arrays: dict, ordinal=0, swiglu_limit=10.0, *, hidden=5120, intermediate=2304):
         w1 = arrays.get("w1_weight")
         self.fmt = "fp8" if getattr(w1, "shape", None) == (intermediate, hidden) else "mxfp4"
         if self.fmt == "fp8":
@@ -69,6 +69,11 @@ class ResidentSharedExpert(ExpertExecutor):
                     lib.fp8_tile(self.ctx._h(), C.c_void_p(self.weights[f"{p}_weight"]),
                                  C.c_void_p(self.weights[f"{p}_scale"]), rows, width, 32, C.c_void_p(blob), None)
                 self.ctx.sync()
+                # the FP8 product reads only the tiled copies: the uploaded checkpoint layout is released
+                for array in self.device_arrays.values():
+                    array.free()
+                self.device_arrays = {}
+                self.weights = dict.fromkeys(self.arrays)
             return self
         except BaseException:
             self.close()

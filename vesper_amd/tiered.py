@@ -1,12 +1,14 @@
-"""Host-pinned expert streaming (mirrors TieredCache / TieredExpertRuntime, src/vesper/cache.py:19-287 and
-src/vesper/tiered.py:130-216, made asynchronous).
+"""Expert residency: the store-backed tiers and the asynchronous streaming cache (the reference's
+TieredCache / CudaCacheBackend / TieredExpertRuntime, src/vesper/cache.py:19-287, src/vesper/tiered.py:21-216).
 
+* CacheConfig, TieredExpertRuntime(store, config): the reference's constructor and single-expert call over
+  the exclusive tiers of vesper_amd.cache (GPU slots, RAM, the on-disk store read with O_DIRECT), on the
+  HipCacheBackend (pinned staging, tiled device slots, readback or GPU SHA-256 audit).
 * ExpertCache: HBM slots over host-pinned expert bytes (mx_cache_*): LRU, misses copied with hipMemcpyAsync
   on a side stream, ordered by per-slot release events and a ready event instead of host waits.
-* HostExpertPool: tiled experts in pinned host memory (the RAM tier), filled from reference-layout arrays or
-  from device-generated synthetic experts.
-* TieredExpertRuntime: forward(key "layer:expert", x, w) on the slot the cache gives (the reference's
-  single-expert API); last_event["source_tier"] is "primary_gpu" on a hit, "host_pinned" on a miss.
+* HostExpertPool: tiled experts in pinned host memory (a RAM tier for the streaming cache), filled from
+  reference-layout arrays or from device-generated synthetic experts.
+* PooledExpertRuntime: forward(key "layer:expert", x, w) through the streaming cache over a pool.
 * OffloadDecode: several MoE layers whose routed experts live in the pool and are streamed into the cache
   per step; the shared experts stay resident.
 """
@@ -16,13 +18,19 @@ from __future__ import annotations
 import ctypes as C
 import threading
 import time
+from contextlib import ExitStack
 from dataclasses import dataclass
+from pathlib import Path
 
 import numpy as np
 
 from . import _lib
+from .cache import TieredCache
 from .config import MoEConfig
 from .layer import TENSORS, ExpertBank, bf16_input, validate_expert_arrays
+from .resources import GiB, MiB, MemoryBudget
+from .store import REFERENCE_PROFILE, ModelProfile, NativeStore, tensor_layout
+from .timing import Timings
 
 
 def expert_key(layer: int, expert: int) -> int:
@@ -125,37 +133,279 @@ class HostExpertPool:
             self.base = 0
 
 
-INTEGRITY_MODES = ("none", "gpu-sha256")
+INTEGRITY_MODES = ("readback", "gpu-sha256")
 
 
 @dataclass(frozen=True)
 class CacheConfig:
-    """Slots of the device cache (the reference's primary slots, tiered.py:21-49); RAM is the pool.
+    """The expert tiers' configuration, with the reference's fields and defaults (src/vesper/tiered.py:21-47).
 
-    integrity_mode "gpu-sha256" audits every admitted slot on the device against the SHA-256 digest table
-    of its pinned source bytes before the expert runs (the reference's gpu-sha256 mode, tiered.py:78-95,
-    cache.py:131-146); "none" admits slots unaudited (the asynchronous offload path's default). The
-    reference's host "readback" mode is not offered."""
-    primary_slots: int = 64
-    timing: bool = False
-    integrity_mode: str = "none"
+    host_cap_bytes / available_floor bound the host memory the tiers reserve; ram_cache_bytes is the RAM
+    tier; primary_slots are the compute GPU's expert slots (device allocations capped at device_cap_bytes);
+    integrity_mode "readback" (the default: each uploaded slot is read back and its SHA-256 checked on the
+    host) or "gpu-sha256" (hashed on the GPU against the verified 4 KiB digest table). The helper-GPU tier
+    (helper_device, helper_slots) needs a second device: with one GPU, set helper_device=None and
+    helper_slots=0 -- the runtime refuses a helper it cannot open."""
+    host_cap_bytes: int = 96 * GiB
+    ram_cache_bytes: int = 80 * GiB
+    available_floor: int = 32 * GiB
+    primary_device: int = 0
+    primary_slots: int = 1
+    helper_device: int | None = 1
+    helper_slots: int = 1
+    device_cap_bytes: int = 64 * MiB
+    metadata_allowance_bytes: int = MiB
+    profile: bool = False
+    integrity_mode: str = "readback"
+    max_store_experts: int = 4
 
     def __post_init__(self):
+        if type(self.max_store_experts) is not int or self.max_store_experts < 1:
+            raise ValueError("Explicit native-store limit must be one to 48 experts")
         if self.integrity_mode not in INTEGRITY_MODES:
-            raise ValueError(f"integrity_mode must be one of {INTEGRITY_MODES}")
+            raise ValueError("Unknown cache integrity mode")
+        if self.primary_slots < 1 or self.helper_slots < 0 or self.ram_cache_bytes < 0:
+            raise ValueError("Invalid expert cache capacity")
+        if self.helper_device == self.primary_device:
+            raise ValueError("The helper must be a distinct storage GPU")
+        if self.helper_device is None and self.helper_slots:
+            raise ValueError("Helper slots require a helper device")
+        if self.metadata_allowance_bytes < MiB:
+            raise ValueError("The bounded store requires at least 1 MiB metadata allowance")
+
+
+class HipCacheBackend:
+    """The compute GPU's side of the tiers (the reference's CudaCacheBackend, src/vesper/tiered.py:50-127).
+
+    Two pinned staging buffers of one store-layout expert each (store reads are copied in from the direct
+    reader's buffer), `primary_slots` device slots holding the tiled layout the expert kernels read, and one device
+    staging expert in the store layout. A write copies staging -> device staging and tiles it into the slot;
+    a read untiles the slot back and copies it to the host; the GPU audit untiles the slot and hashes it
+    against the store's digest table -- so every check sees what the slot holds."""
+
+    helper_slots = 0
+
+    def __init__(self, ctx, profile, size: int, config: CacheConfig, budget: MemoryBudget, source=None):
+        self.ctx, self.profile, self.size, self.config, self.budget = ctx, profile, size, config, budget
+        self.primary_slots = config.primary_slots
+        self.source, self.timings = source, Timings(config.profile)
+        self.tiled_bytes = int(ctx.lib.cdll.mx_tiled_expert_bytes(profile.hidden, profile.intermediate))
+        self._pinned, self._device, self.verifier = [], [], None
+
+    def __enter__(self):
+        c, ctx = self.config, self.ctx
+        self.budget.acquire(2 * self.size, category="staging")
+        try:
+            self._pinned = [ctx.host_alloc_pinned(self.size) for _ in range(2)]
+            self.staging = [np.ctypeslib.as_array((C.c_uint8 * self.size).from_address(p)) for p in self._pinned]
+            self.slots = [ctx.malloc(self.tiled_bytes) for _ in range(self.primary_slots)]
+            self.device_staging = ctx.malloc(self.size)
+            self._device = self.slots + [self.device_staging]
+            at = {}
+            for name, region in tensor_layout(self.profile).items():
+                at[name] = self.device_staging + region["offset"]
+            self.ref_ptrs = _lib.MxExpertPtrs(*[at[n] for n in TENSORS])
+            if c.integrity_mode == "gpu-sha256":
+                if self.source is None:
+                    raise ValueError("GPU integrity requires original source digest tables")
+                from .integrity import DeviceIntegrity
+                self.verifier = DeviceIntegrity(ctx, self.size, self.timings)
+            return self
+        except BaseException:
+            self.__exit__()
+            raise
+
+    def _tile(self, slot):
+        self.ctx.lib.tile_expert(self.ctx._h(), C.byref(self.ref_ptrs), self.profile.hidden, self.profile.intermediate,
+                                 C.c_void_p(self.slots[slot]), None)
+
+    def _untile(self, slot):
+        self.ctx.lib.untile_expert(self.ctx._h(), C.c_void_p(self.slots[slot]), self.profile.hidden,
+                                   self.profile.intermediate, C.byref(self.ref_ptrs), None)
+
+    def write(self, tier, slot, data):
+        with self.timings.section(f"transfer.{tier}_h2d"):
+            self.ctx.lib.memcpy_h2d(self.ctx._h(), C.c_void_p(self.device_staging), data.ctypes.data_as(C.c_void_p),
+                                    self.size, None)
+            self._tile(slot)
+            self.ctx.sync()
+
+    def read(self, tier, slot, target):
+        with self.timings.section(f"transfer.{tier}_d2h"):
+            self._untile(slot)
+            self.ctx.lib.memcpy_d2h(self.ctx._h(), target.ctypes.data_as(C.c_void_p), C.c_void_p(self.device_staging),
+                                    self.size, None)
+
+    def verify(self, tier, slot, key):
+        if key not in self.source.expected_chunks:
+            raise ValueError("Original digest table must come from a fully verified store read")
+        self._untile(slot)
+        return self.verifier.verify(self.device_staging, self.source.expected_chunks[key])
+
+    def slot_ptr(self, slot) -> int:
+        return self.slots[slot]
+
+    def __exit__(self, *_):
+        if self.verifier is not None:
+            self.verifier.close()
+            self.verifier = None
+        for p in self._device:
+            self.ctx.free(p)
+        self._device = []
+        if self._pinned:
+            for p in self._pinned:
+                self.ctx.host_free_pinned(p)
+            self._pinned = []
+            self.budget.release(2 * self.size, category="staging")
+
+
+def _stage_buffers(ctx, tokens, hidden, intermediate):
+    t, h, i = tokens, hidden, intermediate
+    return {"x": ctx.empty((t, h), np.uint16), "route": ctx.empty((t,), np.float32),
+            "q": ctx.empty((t, h), np.uint8), "s": ctx.empty((t, h // 32), np.uint8),
+            "w1": ctx.empty((t, i), np.uint16), "w3": ctx.empty((t, i), np.uint16),
+            "down_input": ctx.empty((t, i), np.uint16), "trace": ctx.empty((t, i, 5), np.float32),
+            "down_q": ctx.empty((t, i), np.uint8), "down_s": ctx.empty((t, i // 32), np.uint8),
+            "w2": ctx.empty((t, h), np.uint16)}
+
+
+def _run_tiled_expert(ctx, work, tiled_ptr, hidden, intermediate, limit, x, routing_weight):
+    """One tiled expert over the BF16 rows of x (1-D: one token, results 1-D as the reference returns them);
+    returns the reference's stage dict (src/vesper/expert.py:71-79)."""
+    one = np.asarray(x).ndim == 1
+    bits = bf16_input(x, hidden)
+    t = bits.shape[0]
+    if not 1 <= t <= work["x"].shape[0]:
+        raise ValueError(f"One expert call accepts 1 to {work['x'].shape[0]} tokens")
+    route = None
+    if routing_weight is not None:
+        route = np.broadcast_to(np.asarray(routing_weight, np.float32).reshape(-1), (t,)).copy()
+        if not np.isfinite(route).all():
+            raise ValueError("Routing weight must be finite")
+    ctx.copy_h2d(work["x"].ptr, bits)
+    if route is not None:
+        ctx.copy_h2d(work["route"].ptr, route)
+    stages = _lib.MxExpertStages(*[work[n].ptr for n in ("q", "s", "w1", "w3", "down_input", "trace", "down_q",
+                                                        "down_s")])
+    ctx.lib.expert_forward_tiled(ctx._h(), C.c_void_p(tiled_ptr), hidden, intermediate, C.c_void_p(work["x"].ptr), t,
+                                 C.c_float(limit), None if route is None else C.c_void_p(work["route"].ptr),
+                                 C.c_void_p(work["w2"].ptr), C.byref(stages), None)
+    h, i = hidden, intermediate
+    layout = {"q": ((t, h), np.uint8), "s": ((t, h // 32), np.uint8), "w1": ((t, i), np.uint16),
+              "w3": ((t, i), np.uint16), "down_input": ((t, i), np.uint16), "trace": ((t, i, 5), np.float32),
+              "down_q": ((t, i), np.uint8), "down_s": ((t, i // 32), np.uint8), "w2": ((t, h), np.uint16)}
+    out = {n: ctx.download(work[n].ptr, shape, dt) for n, (shape, dt) in layout.items()}
+    out["down_input"] = (out["down_input"].astype(np.uint32) << 16).view(np.float32)
+    return {n: v[0] for n, v in out.items()} if one else out
 
 
 class TieredExpertRuntime:
-    """Serial single-expert execution through the cache (tiered.py:130-216): forward(key, x, w)."""
+    """Single-expert execution over the tiers (the reference's TieredExpertRuntime, src/vesper/tiered.py:130-216).
 
-    def __init__(self, ctx: _lib.Context, config: MoEConfig, pool: HostExpertPool, index_of: dict,
-                 cache_config: CacheConfig = CacheConfig(), swiglu_limit: float | None = None):
+    TieredExpertRuntime(store, CacheConfig) opens the store directory as a NativeStore (or through
+    source_factory(store, budget)), the compute GPU `primary_device` and the tiers; forward(key, x, w) brings
+    expert "layer:expert" into a GPU slot -- from the store, the RAM tier or the slot itself -- and runs it
+    (mx_expert_forward_tiled), returning the reference's stage dict; last_event["source_tier"] is
+    "primary_gpu", "ram" or "store". The model's shapes come from `model` (the reference's pinned checkpoint by
+    default)."""
+
+    def __init__(self, store: Path, config: CacheConfig | None = None, *, source_factory=None,
+                 model: ModelProfile = REFERENCE_PROFILE, max_tokens: int = 16):
+        if source_factory is not None and not callable(source_factory):
+            raise ValueError("Expected an explicit expert source factory")
+        self.store_path, self.config, self.source_factory = Path(store), config or CacheConfig(), source_factory
+        self.model, self.max_tokens = model, int(max_tokens)
+        self.stack, self.cache, self.ctx = None, None, None
+
+    def __enter__(self):
+        if self.stack is not None:
+            raise RuntimeError("Tiered runtime is already open")
+        c = self.config
+        if c.helper_device is not None and c.helper_slots:
+            raise RuntimeError(f"The helper-GPU tier needs device {c.helper_device}; this build runs on one GPU "
+                               "(set helper_device=None and helper_slots=0)")
+        self.budget = MemoryBudget(c.host_cap_bytes, c.available_floor, owner="expert_tiers")
+        self.timings = Timings(c.profile)
+        self.stack = ExitStack()
+        try:
+            self.budget.acquire(c.metadata_allowance_bytes, category="metadata")
+            self.stack.callback(self.budget.release, c.metadata_allowance_bytes, category="metadata")
+            self.store = (NativeStore(self.store_path, self.budget, max_experts=c.max_store_experts, profile=self.model)
+                          if self.source_factory is None else self.source_factory(self.store_path, self.budget))
+            if self.store.budget is not self.budget:
+                raise ValueError("Expert source must use the admitted cache budget")
+            self.store.timings = self.timings
+            self.store.gpu_integrity = c.integrity_mode == "gpu-sha256"
+            self.stack.enter_context(self.store)
+            if c.metadata_allowance_bytes + self.store.size * 3 > c.host_cap_bytes:
+                raise MemoryError("Host cap cannot fit direct-I/O scratch and two pinned staging buffers")
+            self.ctx = self.stack.enter_context(_lib.Context(c.primary_device, c.device_cap_bytes))
+            self.backend = self.stack.enter_context(HipCacheBackend(self.ctx, self.model, self.store.size, c,
+                                                                    self.budget, self.store))
+            self.backend.timings = self.timings
+            self.work = _stage_buffers(self.ctx, self.max_tokens, self.model.hidden, self.model.intermediate)
+            self.stack.callback(lambda: [d.free() for d in self.work.values()])
+            self.cache = TieredCache(self.store, self.backend, self.budget, c.ram_cache_bytes, timings=self.timings,
+                                     gpu_verify=c.integrity_mode == "gpu-sha256")
+            self.stack.callback(self.cache.close)
+            self.last_event = None
+            return self
+        except BaseException:
+            self.stack.close()
+            self.stack = None
+            raise
+
+    def forward(self, key: str, x, routing_weight=None) -> dict:
+        if self.stack is None:
+            raise RuntimeError("Use the tiered runtime as a context manager")
+        started = time.perf_counter()
+        before = self.timings.snapshot()
+        with self.cache.acquire(key) as (slot, origin):
+            with self.timings.section("compute.kernels"):
+                result = _run_tiled_expert(self.ctx, self.work, self.backend.slot_ptr(slot), self.model.hidden,
+                                           self.model.intermediate, self.model.swiglu_limit, x, routing_weight)
+        self.last_event = {"key": key, "source_tier": origin, "wall_ms": (time.perf_counter() - started) * 1000}
+        if self.timings.enabled:
+            self.last_event["stage_timings"] = self.timings.since(before)
+        return result
+
+    def snapshot(self) -> dict:
+        result = self.cache.snapshot()
+        if self.timings.enabled:
+            result["stage_timings"] = self.timings.snapshot()
+        live, peak = self.ctx.owned_bytes()
+        result.update({"primary_peak_explicit_bytes": peak, "helper_peak_explicit_bytes": 0,
+                       "store_direct_read_calls": self.store.read_calls, "store_direct_read_bytes": self.store.bytes_read,
+                       "host_cap_bytes": self.config.host_cap_bytes,
+                       "host_available_floor_bytes": self.config.available_floor,
+                       "ram_capacity_bytes": self.config.ram_cache_bytes,
+                       "expected_digest_table_bytes": sum(a.nbytes for a in self.store.expected_chunks.values())})
+        return result
+
+    def __exit__(self, *_):
+        if self.stack is not None:
+            live = self.ctx.owned_bytes()[0] if self.ctx is not None else 0
+            self.stack.close()
+            self.stack = None
+            self.cleanup = {"host_buffer_reservations_bytes": self.budget.reserved,
+                            "primary_explicit_live_bytes_before_close": live}
+
+
+class PooledExpertRuntime:
+    """Single-expert execution through the asynchronous device cache over a host-pinned pool of tiled experts
+    (the pool is the RAM tier, filled from device banks or arrays): forward(key "layer:expert", x, w);
+    last_event["source_tier"] is "primary_gpu" on a hit, "host_pinned" on a miss. audit=True checks every
+    admitted slot on the GPU against the digest table of its pinned source before the expert runs (the
+    reference's gpu-sha256 mode)."""
+
+    def __init__(self, ctx: _lib.Context, config: MoEConfig, pool: HostExpertPool, index_of: dict, slots: int = 64,
+                 audit: bool = False, swiglu_limit: float | None = None):
         self.ctx, self.config, self.pool, self.index_of = ctx, config, pool, dict(index_of)
         self.limit = config.swiglu_limit if swiglu_limit is None else float(swiglu_limit)
-        self.cache = ExpertCache(ctx, pool.expert_bytes, cache_config.primary_slots)
+        self.cache = ExpertCache(ctx, pool.expert_bytes, slots)
         for key, index in self.index_of.items():
             self.cache.register(expert_key(*parse_key(key)), pool.ptr(index))
-        self.audit = cache_config.integrity_mode == "gpu-sha256"
+        self.audit = bool(audit)
         self.expected, self.slot_ptrs = {}, set()
         self.audit_stats = {"integrity_failures": 0, "gpu_audit_payload_bytes": 0, "gpu_audit_digest_d2h_bytes": 0}
         self.verifier = None
@@ -165,55 +415,25 @@ class TieredExpertRuntime:
             self.verifier = DeviceIntegrity(ctx, size, allocation_size=lambda p: size if int(p) in self.slot_ptrs
                                             else ctx.owned_size(p))
         self.lock, self.active, self.last_event = threading.Lock(), False, None
-        t, h, i = 16, config.hidden, config.intermediate
-        self.work = {"x": ctx.empty((t, h), np.uint16), "route": ctx.empty((t,), np.float32),
-                     "q": ctx.empty((t, h), np.uint8), "s": ctx.empty((t, h // 32), np.uint8),
-                     "w1": ctx.empty((t, i), np.uint16), "w3": ctx.empty((t, i), np.uint16),
-                     "down_input": ctx.empty((t, i), np.uint16), "trace": ctx.empty((t, i, 5), np.float32),
-                     "down_q": ctx.empty((t, i), np.uint8), "down_s": ctx.empty((t, i // 32), np.uint8),
-                     "w2": ctx.empty((t, h), np.uint16)}
+        self.work = _stage_buffers(ctx, 16, config.hidden, config.intermediate)
 
     def forward(self, key: str, x, routing_weight=None) -> dict:
         if key not in self.index_of:
             raise KeyError("Requested expert is absent from the pinned native store")
-        bits = bf16_input(x, self.config.hidden)
-        t = bits.shape[0]
-        if not 1 <= t <= 16:
-            raise ValueError("One expert call accepts 1 to 16 tokens")
-        route = None
-        if routing_weight is not None:
-            route = np.broadcast_to(np.asarray(routing_weight, np.float32).reshape(-1), (t,)).copy()
-            if not np.isfinite(route).all():
-                raise ValueError("Routing weight must be finite")
         with self.lock:
             if self.active:
                 raise RuntimeError("Nested requests could replace a live compute slot")
             self.active = True
             try:
                 started = time.perf_counter()
-                w = self.work
-                self.ctx.copy_h2d(w["x"].ptr, bits)
-                if route is not None:
-                    self.ctx.copy_h2d(w["route"].ptr, route)
                 k = expert_key(*parse_key(key))
                 (ptr,), (hit,) = self.cache.ensure([k])
                 self.cache.wait_ready(None)
                 if self.audit and not hit:
                     self._admit(key, k, ptr)
-                stages = _lib.MxExpertStages(*[w[n].ptr for n in ("q", "s", "w1", "w3", "down_input", "trace",
-                                                                  "down_q", "down_s")])
-                self.ctx.lib.expert_forward_tiled(self.ctx._h(), C.c_void_p(ptr), self.config.hidden,
-                                                  self.config.intermediate, C.c_void_p(w["x"].ptr), t, self.limit,
-                                                  None if route is None else C.c_void_p(w["route"].ptr),
-                                                  C.c_void_p(w["w2"].ptr), C.byref(stages), None)
+                out = _run_tiled_expert(self.ctx, self.work, ptr, self.config.hidden, self.config.intermediate,
+                                        self.limit, x, routing_weight)
                 self.cache.release([k], None)
-                h, i = self.config.hidden, self.config.intermediate
-                layout = {"q": ((t, h), np.uint8), "s": ((t, h // 32), np.uint8), "w1": ((t, i), np.uint16),
-                          "w3": ((t, i), np.uint16), "down_input": ((t, i), np.uint16),
-                          "trace": ((t, i, 5), np.float32), "down_q": ((t, i), np.uint8),
-                          "down_s": ((t, i // 32), np.uint8), "w2": ((t, h), np.uint16)}
-                out = {n: self.ctx.download(w[n].ptr, shape, dt) for n, (shape, dt) in layout.items()}
-                out["down_input"] = (out["down_input"].astype(np.uint32) << 16).view(np.float32)
                 self.last_event = {"key": key, "source_tier": "primary_gpu" if hit else "host_pinned",
                                    "wall_ms": (time.perf_counter() - started) * 1000}
                 return out
