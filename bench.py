@@ -106,32 +106,91 @@ def read_ceiling(ctx, stream, nbytes=2 << 30, reps=7):
                       f"{reps} launches"}
 
 
-def cpu_baseline(layer, bank, w, x_rows, cfg):
-    """The NumPy oracle's layer at T=1 on the host cores, single-threaded BLAS, bounded sample."""
+CPU_RUNS = 5
+CPU_SAMPLE_EXPERTS = 2
+
+
+def _median_s(fn, runs=CPU_RUNS):
+    """One untimed warm-up call, then the median of `runs` timed calls (perf_counter_ns), in seconds."""
+    fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter_ns()
+        fn()
+        times.append((time.perf_counter_ns() - t0) * 1e-9)
+    return float(np.median(times))
+
+
+def cpu_baseline(bank, w, x_rows, cfg, plans):
+    """The NumPy oracle on the host cores, bounded samples of the benchmark's own inputs (one warm-up, median
+    of 5 per leg):
+
+    * config 0: one MXFP4 expert at T = 1 in configuration 0's own formula (BF16 activations, FP32
+      accumulation, no activation quantization);
+    * config 1 at T = 1, 4, 16: the router in full, the shared expert on all T rows, and the first
+      CPU_SAMPLE_EXPERTS routed experts (ascending ID) on their own token rows; the routed time is
+      extrapolated linearly to every distinct selected expert (the per-expert cost is dominated by
+      dequantising its weights, which does not depend on its row count at these T);
+    * config 3 at T = 1, 16: all four FP8 projections in full (synthetic weights of the same shapes).
+
+    value = config 1's bytes of one bench step (T = 1, 4 and 16) / the summed CPU time of the three legs."""
     import threadpoolctl
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from oracle.moe import moe_layer
+    sys.path.insert(0, ROOT)
+    from oracle.expert import expert_forward, expert_reference_fp32
+    from oracle.moe import participation
+    from oracle.projections import fp8_projection, fp8_weights
     from oracle.router import gate_logits, route
-    x = x_rows[:1]
-    with threadpoolctl.threadpool_limits(1):
-        ids = route(gate_logits(w, x), cfg.top_k, cfg.route_scale, cfg.score_func)["indices"]
-        needed = {int(e): bank.download(int(e)) for e in np.unique(ids)}
+    from vesper_amd.fp8_workload import LAYOUT
+
+    threads = min(16, len(os.sched_getaffinity(0)))      # the GPU box's CPU share is 16 cores
+    legs, step_bytes, step_s = {}, 0, 0.0
+    with threadpoolctl.threadpool_limits(threads):
+        blas = [f"{m.get('internal_api')} {m.get('version')} x{m.get('num_threads')}"
+                for m in threadpoolctl.threadpool_info()]
         shared = bank.download(cfg.experts)
-        times = []
-        for rep in range(3):
-            t0 = time.perf_counter()
-            moe_layer(x, w, needed, shared, top_k=cfg.top_k, route_scale=cfg.route_scale,
-                      score_func=cfg.score_func, swiglu_limit=cfg.swiglu_limit)
-            times.append(time.perf_counter() - t0)
-            log(f"cpu baseline run {rep}: {times[-1]:.2f} s")
-    bytes_t1 = (len(needed) + 1) * cfg.expert_bytes + cfg.experts * cfg.hidden * 4 + cfg.hidden * 4
-    sec = float(np.median(times))
-    return {"value": bytes_t1 / sec / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"oracle (NumPy) MoE layer at T=1: router + {len(needed)} routed + shared experts + combine; "
-                      f"median of {len(times)} runs, {sec:.2f} s/layer = {sec * 1e6:.0f} us/layer",
-            "us_per_layer": sec * 1e6, "cpu": platform.processor() or platform.machine(),
-            "numpy": np.__version__, "os_cpu_count": os.cpu_count(),
-            "affinity_cores": len(os.sched_getaffinity(0))}
+        x1 = x_rows[:1]
+        sec = _median_s(lambda: expert_reference_fp32(x1, shared))
+        legs["config0_T1"] = {"us": sec * 1e6, "GB_per_s": cfg.expert_bytes / sec / 1e9,
+                              "sample": "one expert in full, BF16 activations (configuration 0's formula)"}
+        log(f"cpu config 0: {sec:.2f} s")
+        for t in TOKENS:
+            x = x_rows[:t]
+            r = route(gate_logits(w, x), cfg.top_k, cfg.route_scale, cfg.score_func)
+            selected = participation(r["indices"], cfg.experts, cfg.top_k)
+            sample = sorted(selected)[:CPU_SAMPLE_EXPERTS]
+            arrays = {e: bank.download(e) for e in sample}
+            weight = {e: np.array([r["weights"][row, list(r["indices"][row]).index(e)] for row in selected[e]],
+                                  np.float32) for e in sample}
+            router_s = _median_s(lambda: route(gate_logits(w, x), cfg.top_k, cfg.route_scale, cfg.score_func))
+            shared_s = _median_s(lambda: expert_forward(x, shared, None, cfg.swiglu_limit))
+            routed_s = _median_s(lambda: [expert_forward(x[selected[e]], arrays[e], weight[e], cfg.swiglu_limit)
+                                          for e in sample]) / len(sample)
+            total = router_s + shared_s + routed_s * len(selected)
+            nbytes = algorithmic_bytes(cfg, plans[0, t], t)
+            step_bytes += nbytes
+            step_s += total
+            legs[f"config1_T{t}"] = {"us": total * 1e6, "GB_per_s": nbytes / total / 1e9,
+                                     "router_us": router_s * 1e6, "shared_us": shared_s * 1e6,
+                                     "routed_us_per_expert": routed_s * 1e6, "distinct_experts": len(selected),
+                                     "sample": f"router + shared in full; {len(sample)} of {len(selected)} routed "
+                                               "experts timed, extrapolated linearly"}
+            log(f"cpu config 1 T={t}: {total:.2f} s (extrapolated)")
+        rng = np.random.default_rng(20261018)
+        weights = {name: fp8_weights(rng, n, k, 128) for name, (n, k) in LAYOUT.items()}
+        for t in (1, 16):
+            xs = {name: rng.standard_normal((t, k)).astype(np.float32) for name, (n, k) in LAYOUT.items()}
+            sec = _median_s(lambda: [fp8_projection(xs[name], *weights[name], 128) for name in LAYOUT])
+            nbytes = sum(n * k + ((n + 127) // 128) * (k // 128) * 4 + t * (n + k) * 2 for n, k in LAYOUT.values())
+            legs[f"config3_T{t}"] = {"us": sec * 1e6, "GB_per_s": nbytes / sec / 1e9,
+                                     "sample": "q_a, q_b, kv_a and o in full"}
+            log(f"cpu config 3 T={t}: {sec:.2f} s")
+    legs = {name: {k: (round(v, 3) if isinstance(v, float) else v) for k, v in leg.items()} for name, leg in legs.items()}
+    return {"value": round(step_bytes / step_s / 1e9, 5), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"NumPy oracle; config 1 step (T = 1, 4, 16) with {CPU_SAMPLE_EXPERTS} routed experts per T "
+                      f"timed and extrapolated ({step_s:.1f} s per step); one warm-up, median of {CPU_RUNS} per leg",
+            "legs": legs, "threads": {"blas": blas, "numpy_elementwise": 1},
+            "cpu": platform.processor() or platform.machine(), "numpy": np.__version__,
+            "os_cpu_count": os.cpu_count(), "affinity_cores": threads}
 
 
 def main():
@@ -250,7 +309,8 @@ def main():
     }
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle, bounded sample)")
-        result["cpu_baseline"] = cpu_baseline(layers[0], banks[0], routers[0], x_rows, cfg)
+        x_bf16 = (bits.astype(np.uint32) << 16).view(np.float32)
+        result["cpu_baseline"] = cpu_baseline(banks[0], routers[0], x_bf16, cfg, plans)
     for layer, bank in zip(layers, banks):
         layer.close()
         bank.free()
@@ -264,9 +324,10 @@ def main():
 def secondary(ctx):
     """The other BASELINE configurations, measured on the same GPU (each a few seconds): 2 = MoE prefill
     (T = 4096, Zipf(1.1) routing), 3 = FP8 block-128 projections at T = 1, 16, 2048, 4 = 8-layer offload
-    decode at T = 4 with 25 % of the routed experts resident; and the SHA-256 admission audit of expert
-    slots (one expert, and the 1 GiB maximum payload)."""
-    from vesper_amd import fp8_workload, integrity_workload, offload_workload, prefill_workload
+    decode at T = 4 with 25 % of the routed experts resident; the SHA-256 admission audit of expert
+    slots (one expert, and the 1 GiB maximum payload); and the promotion of single experts from the on-disk
+    store into HBM slots."""
+    from vesper_amd import fp8_workload, integrity_workload, offload_workload, prefill_workload, store_workload
     out = {}
     log("configuration 2: prefill")
     p = prefill_workload.run(4096, 5, ctx=ctx)
@@ -290,6 +351,9 @@ def secondary(ctx):
     log("cache admission audit: SHA-256 per 4 KiB chunk")
     out["integrity_sha256"] = integrity_workload.run(20, ctx=ctx)
     log(f"integrity: {out['integrity_sha256']}")
+    log("store -> HBM promotion of single experts (O_DIRECT read, pinned staging, tiled slot, audit)")
+    out["store_to_hbm"] = store_workload.run(8)
+    log(f"store: {out['store_to_hbm']}")
     return out
 
 

@@ -215,6 +215,17 @@ int mx_expert_forward_tiled(mx_ctx* ctx, const void* tiled, int32_t hidden, int3
                             const uint16_t* x_bf16, int32_t tokens, float swiglu_limit, const float* route_w,
                             uint16_t* y_bf16, const mx_expert_stages* stages, void* stream);
 
+/* The benchmark's configuration-0 expert on a tiled expert: BF16 activations, FP32 accumulation, no
+ * activation quantization and no clamp. y[T][H] (BF16, rounded once) = W2 . h with
+ * h[T][I] = silu(W1 . x) * (W3 . x) [* route_w[t]] in FP32, x BF16 [T][H]. `h` (FP32 [T][I], 16-byte aligned)
+ * and `gu` (FP32 [T][2I]: W1 . x then W3 . x) receive the intermediates when non-null. tokens <= 16,
+ * hidden <= 8192, intermediate <= 4096; uses the context scratch. The reference's expert
+ * (ExpertExecutor.execute, src/vesper/expert.py:51-79) quantizes both activations to E4M3 instead; this is
+ * the same weights under configuration 0's formula (expert_reference_fp32 of the oracle). */
+int mx_expert_forward_bf16(mx_ctx* ctx, const void* tiled, int32_t hidden, int32_t intermediate,
+                           const uint16_t* x_bf16, int32_t tokens, const float* route_w, float* h, float* gu,
+                           uint16_t* y_bf16, void* stream);
+
 /* mx_expert_forward_tiled without any device allocation: no counterpart in the reference. For callers that
  * cannot allocate -- code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
  * Same arguments, kernels and results; the call's plan, expert table and quantized activations live in a

@@ -94,13 +94,10 @@ def expert_forward(x, arrays: dict, routing_weight=None, limit: float = 10.0, fm
             "down_q": down_q, "down_s": down_s, "w2": w2}
 
 
-def expert_reference_fp32(x, arrays: dict, routing_weight=None) -> np.ndarray:
-    """Unquantized-activation FP32 reference y = W2(silu(W1 x) * W3 x) with dequantized weights.
-
-    This is BASELINE config 0's formula (no activation quantization, no clamp),
-    evaluated in float64 from FP32-dequantized MXFP4 weights. The W4A8 pipeline
-    above is compared to it only through the tolerance metrics.
-    """
+def expert_reference_stages(x, arrays: dict, routing_weight=None) -> dict:
+    """Every stage of BASELINE config 0's formula y = W2(silu(W1 x) * W3 x) in float64: g = W1 x, u = W3 x,
+    h = silu(g) u (times the route weight), y = W2 h, from the exactly dequantized MXFP4 weights and the
+    BF16-rounded activations (no activation quantization, no clamp)."""
     from .formats import unpack_fp4
     x = np.atleast_2d(bf16_round(x)).astype(np.float64)
     w1 = unpack_fp4(arrays["w1_weight"], arrays["w1_scale"]).astype(np.float64)
@@ -111,4 +108,14 @@ def expert_reference_fp32(x, arrays: dict, routing_weight=None) -> np.ndarray:
     h = g / (1.0 + np.exp(-g)) * u
     if routing_weight is not None:
         h = h * np.asarray(routing_weight, dtype=np.float64).reshape(-1, 1)
-    return h @ w2.T
+    return {"g": g, "u": u, "h": h, "y": h @ w2.T}
+
+
+def expert_reference_fp32(x, arrays: dict, routing_weight=None) -> np.ndarray:
+    """Unquantized-activation reference y = W2(silu(W1 x) * W3 x) with dequantized weights.
+
+    This is BASELINE config 0's formula (no activation quantization, no clamp),
+    evaluated in float64 from FP32-dequantized MXFP4 weights. The W4A8 pipeline
+    above is compared to it only through the tolerance metrics.
+    """
+    return expert_reference_stages(x, arrays, routing_weight)["y"]

@@ -108,6 +108,7 @@ SIGNATURES = {
     "mx_prefill_workspace_bytes": ([_P, _I32], _U64),
     "mx_moe_decode_routed": ([_P, _P, _I32, _P, _P, _P, _P], C.c_int),
     "mx_expert_forward_tiled": ([_P, _P, _I32, _I32, _P, _I32, _F, _P, _P, C.POINTER(MxExpertStages), _P], C.c_int),
+    "mx_expert_forward_bf16": ([_P, _P, _I32, _I32, _P, _I32, _P, _P, _P, _P, _P], C.c_int),
     "mx_expert_forward_tiled_noalloc": ([_P, _P, _I32, _I32, _P, _I32, _F, _P, _P, C.POINTER(MxExpertStages), _P],
                                         C.c_int),
     "mx_layer_set_experts": ([_P, _I32, _P, _P, _P], C.c_int),

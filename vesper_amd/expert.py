@@ -144,3 +144,75 @@ class ResidentExpert(ExpertExecutor):
 
     def forward(self, x, routing_weight=None) -> dict:
         return self.execute(x, self.weights, routing_weight)
+
+
+class BF16ActivationExpert:
+    """The benchmark's configuration-0 expert on the same MXFP4 weights: BF16 activations, FP32 accumulation,
+    no activation quantization and no clamp -- y = W2 (silu(W1 x) * (W3 x)) -- where the reference's expert
+    quantizes both activations to E4M3 (a separately named profile, not a replacement for ResidentExpert).
+
+    Uploads the six tensors on enter and tiles them into the device layout the decode kernels read;
+    forward(x, routing_weight=None) takes BF16 bits or FP32 values [H] or [T, H] (T <= 16) and returns
+    {"gu": FP32 [T, 2I] (W1 x then W3 x), "h": FP32 [T, I], "y": BF16 bits [T, H]} (mx_expert_forward_bf16)."""
+
+    def __init__(self, arrays: dict, ordinal=0, *, hidden=5120, intermediate=2304):
+        validate_expert_arrays(arrays, hidden, intermediate)
+        if hidden > 8192 or intermediate > 4096:
+            raise ValueError("The BF16-activation expert supports hidden <= 8192 and intermediate <= 4096")
+        self.arrays, self.ordinal = arrays, ordinal
+        self.hidden, self.intermediate = hidden, intermediate
+        self.ctx = None
+
+    def __enter__(self):
+        if self.ctx is not None:
+            raise RuntimeError("Expert is already open")
+        self.ctx = _lib.Context(self.ordinal)
+        try:
+            h, i, lib = self.hidden, self.intermediate, self.ctx.lib
+            raw = {n: self.ctx.upload(np.ascontiguousarray(self.arrays[n])) for n in TENSORS}
+            self.tiled = self.ctx.malloc(int(lib.cdll.mx_tiled_expert_bytes(h, i)))
+            ptrs = _lib.MxExpertPtrs(*[raw[n].ptr for n in TENSORS])
+            lib.tile_expert(self.ctx._h(), C.byref(ptrs), h, i, C.c_void_p(self.tiled), None)
+            self.ctx.sync()
+            for d in raw.values():
+                d.free()
+            t = 16
+            self.work = {"x": self.ctx.empty((t, h), np.uint16), "route": self.ctx.empty((t,), np.float32),
+                         "gu": self.ctx.empty((t, 2 * i), np.float32), "h": self.ctx.empty((t, i), np.float32),
+                         "y": self.ctx.empty((t, h), np.uint16)}
+            return self
+        except BaseException:
+            self.__exit__()
+            raise
+
+    def forward(self, x, routing_weight=None) -> dict:
+        if self.ctx is None:
+            raise RuntimeError("Use the expert as a context manager")
+        bits = bf16_input(np.asarray(x) if np.asarray(x).dtype == np.uint16 else np.asarray(x, np.float32),
+                          self.hidden)
+        t = bits.shape[0]
+        if not 1 <= t <= 16:
+            raise ValueError("One expert call accepts 1 to 16 tokens")
+        w = self.work
+        route = None
+        if routing_weight is not None:
+            route = np.broadcast_to(np.asarray(routing_weight, np.float32).reshape(-1), (t,)).copy()
+            if not np.isfinite(route).all():
+                raise ValueError("Routing weight must be finite")
+            self.ctx.copy_h2d(w["route"].ptr, route)
+        self.ctx.copy_h2d(w["x"].ptr, bits)
+        self.ctx.lib.expert_forward_bf16(self.ctx._h(), C.c_void_p(self.tiled), self.hidden, self.intermediate,
+                                         C.c_void_p(w["x"].ptr), t,
+                                         None if route is None else C.c_void_p(w["route"].ptr),
+                                         C.c_void_p(w["h"].ptr), C.c_void_p(w["gu"].ptr), C.c_void_p(w["y"].ptr),
+                                         None)
+        self.ctx.sync()
+        h, i = self.hidden, self.intermediate
+        return {"gu": self.ctx.download(w["gu"].ptr, (t, 2 * i), np.float32),
+                "h": self.ctx.download(w["h"].ptr, (t, i), np.float32),
+                "y": self.ctx.download(w["y"].ptr, (t, h), np.uint16)}
+
+    def __exit__(self, *_):
+        if self.ctx is not None:
+            ctx, self.ctx = self.ctx, None
+            ctx.close()

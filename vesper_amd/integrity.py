@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import ctypes as C
 import hashlib
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 
@@ -21,6 +22,10 @@ from .timing import Timings
 CHUNK_BYTES = 4096
 DIGEST_BYTES = 32
 MAX_PAYLOAD = 1 << 30
+
+# Host hashing threads: hashlib releases the GIL while it hashes a buffer of more than 2 KiB, so independent
+# large digests (the whole expert and its tensors) run on separate cores.
+HASHERS = ThreadPoolExecutor(max_workers=4, thread_name_prefix="vesper-sha256")
 
 
 def digest_shape(size):
@@ -44,6 +49,7 @@ def hash_chunks(data: np.ndarray, target: np.ndarray):
     if np.shares_memory(data, target):
         raise ValueError("Digest destination must not overwrite source bytes")
     payload = memoryview(data)
+    # one thread: per-chunk digests are too short for the hashing threads to pay (measured slower)
     table = b"".join(hashlib.sha256(payload[start:start + CHUNK_BYTES]).digest()
                      for start in range(0, data.size, CHUNK_BYTES))
     target[...] = np.frombuffer(table, np.uint8).reshape(target.shape)

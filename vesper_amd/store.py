@@ -32,7 +32,7 @@ from pathlib import Path
 import numpy as np
 
 from .disk import PAGE, DirectReader
-from .integrity import digest_shape, hash_chunks
+from .integrity import HASHERS, digest_shape, hash_chunks
 from .resources import MemoryBudget, MiB
 from .timing import Timings
 
@@ -107,6 +107,12 @@ def tensor_layout(profile: ModelProfile = REFERENCE_PROFILE) -> dict:
 
 def _hex(data) -> str:
     return hashlib.sha256(memoryview(np.ascontiguousarray(data)).cast("B")).hexdigest()
+
+
+def _hex_parallel(views) -> list:
+    """The SHA-256 of each view, on the host hashing threads: the whole-expert digest and the per-tensor
+    digests of one read run on separate cores, and the whole-expert chain bounds the wall time."""
+    return [f.result() for f in [HASHERS.submit(_hex, v) for v in views]]
 
 
 def expert_provenance(layer: int, expert: int, arrays: dict, profile: ModelProfile = REFERENCE_PROFILE,
@@ -326,31 +332,41 @@ class NativeStore:
             entry = self.entries[key]
             if data.dtype != np.uint8 or data.shape != (self.size,) or not data.flags.c_contiguous:
                 raise ValueError("Native-store payload layout differs from one expert")
-            if _hex(data) != entry["sha256"]:
+            layout = self.manifest["layout"]
+            named = entry["provenance"]["tensors"] if tensors else []
+            regions = [layout[t["name"]] for t in named]
+            views = [data] + [data[r["offset"]:r["offset"] + r["bytes"]] for r in regions]
+            digests = _hex_parallel(views) if named else [_hex(data)]
+            if digests[0] != entry["sha256"]:
                 raise ValueError("Native expert bytes differ from the store hash")
-            if tensors:
-                layout = self.manifest["layout"]
-                for tensor in entry["provenance"]["tensors"]:
-                    region = layout[tensor["name"]]
-                    if _hex(data[region["offset"]:region["offset"] + region["bytes"]]) != tensor["sha256"]:
-                        raise ValueError("Native expert tensor differs from its original source hash")
+            for tensor, digest in zip(named, digests[1:]):
+                if digest != tensor["sha256"]:
+                    raise ValueError("Native expert tensor differs from its original source hash")
 
     def _after_read(self, key: str, target: np.ndarray):
+        """Check the bytes just read against the manifest; with gpu_integrity, also build their 4 KiB digest
+        table for the GPU audit -- on a hashing thread while the manifest digests run (the table's Python loop
+        and the large GIL-free digests overlap), kept only if the bytes pass."""
         self.read_calls += 1
         self.bytes_read += self.size
-        self.validate(key, target, tensors=True)
-        if self.gpu_integrity and key not in self.expected_chunks:
-            shape = digest_shape(self.size)
-            self.budget.acquire(shape[0] * shape[1], category="integrity")
+        if not (self.gpu_integrity and key not in self.expected_chunks):
+            self.validate(key, target, tensors=True)
+            return
+        shape = digest_shape(self.size)
+        self.budget.acquire(shape[0] * shape[1], category="integrity")
+        try:
+            table = np.empty(shape, np.uint8)
+            pending = HASHERS.submit(hash_chunks, target, table)
             try:
-                table = np.empty(shape, np.uint8)
+                self.validate(key, target, tensors=True)
+            finally:
                 with self.timings.section("integrity.prepare_cpu_chunks"):
-                    hash_chunks(target, table)
-                table.setflags(write=False)
-                self.expected_chunks[key] = table
-            except BaseException:
-                self.budget.release(shape[0] * shape[1], category="integrity")
-                raise
+                    pending.result()
+            table.setflags(write=False)
+            self.expected_chunks[key] = table
+        except BaseException:
+            self.budget.release(shape[0] * shape[1], category="integrity")
+            raise
 
     def read_into(self, key: str, target: np.ndarray):
         """Direct read of `key` into the reader's buffer, copied into `target` (one expert of bytes), then

@@ -185,10 +185,11 @@ class HipCacheBackend:
 
     helper_slots = 0
 
-    def __init__(self, ctx, profile, size: int, config: CacheConfig, budget: MemoryBudget, source=None):
+    def __init__(self, ctx, profile, size: int, config: CacheConfig, budget: MemoryBudget, source=None,
+                 timings: Timings | None = None):
         self.ctx, self.profile, self.size, self.config, self.budget = ctx, profile, size, config, budget
         self.primary_slots = config.primary_slots
-        self.source, self.timings = source, Timings(config.profile)
+        self.source, self.timings = source, timings or Timings(config.profile)
         self.tiled_bytes = int(ctx.lib.cdll.mx_tiled_expert_bytes(profile.hidden, profile.intermediate))
         self._pinned, self._device, self.verifier = [], [], None
 
@@ -341,8 +342,7 @@ class TieredExpertRuntime:
                 raise MemoryError("Host cap cannot fit direct-I/O scratch and two pinned staging buffers")
             self.ctx = self.stack.enter_context(_lib.Context(c.primary_device, c.device_cap_bytes))
             self.backend = self.stack.enter_context(HipCacheBackend(self.ctx, self.model, self.store.size, c,
-                                                                    self.budget, self.store))
-            self.backend.timings = self.timings
+                                                                    self.budget, self.store, self.timings))
             self.work = _stage_buffers(self.ctx, self.max_tokens, self.model.hidden, self.model.intermediate)
             self.stack.callback(lambda: [d.free() for d in self.work.values()])
             self.cache = TieredCache(self.store, self.backend, self.budget, c.ram_cache_bytes, timings=self.timings,
