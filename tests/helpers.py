@@ -65,3 +65,27 @@ def exact_activation(rng, tokens, hidden):
     for t in range(tokens):
         x[t, np.arange(blocks) * 32 + pick[t]] = big[t]
     return x
+
+
+def write_layer(root, rng, profile, layer, stored=None, bias_shift=None):
+    """One MoE layer of `profile` as the reference's on-disk artifacts under `root`: an expert store (the
+    experts in `stored`, all by default), gate, router-bias and FP8 shared-expert fixtures. Returns
+    {"paths": (store, gate, router, shared), "experts", "gate" (BF16 bits), "biases", "shared"}."""
+    from oracle.formats import bf16_bits
+    from oracle.inputs import fp8_block32_expert_normal, mxfp4_expert, router_weight
+    from vesper_amd.fixtures import write_gate_fixture, write_router_fixture, write_shared_fixture
+    from vesper_amd.store import build_store
+
+    h, i, e = profile.hidden, profile.intermediate, profile.experts
+    stored = range(e) if stored is None else stored
+    experts = {n: mxfp4_expert(rng, h, i) for n in range(e)}
+    build_store([(layer, n, experts[n]) for n in stored], root / "store", max_experts=len(stored), profile=profile)
+    gate = bf16_bits(router_weight(rng, e, h))
+    biases = {n: (rng.standard_normal(e) * 0.05).astype(np.float32) for n in ("bias", "bias_vl")}
+    for name, shift in (bias_shift or {}).items():
+        biases[name] = biases[name] + np.asarray(shift, np.float32)
+    shared = fp8_block32_expert_normal(rng, h, i)
+    paths = (root / "store", write_gate_fixture(root / "gate", layer, gate, profile),
+             write_router_fixture(root / "router", layer, biases, profile),
+             write_shared_fixture(root / "shared", layer, shared, profile))
+    return {"paths": paths, "experts": experts, "gate": gate, "biases": biases, "shared": shared}

@@ -13,7 +13,7 @@ import pytest
 
 from oracle.formats import bf16_bits
 from oracle.inputs import fp8_block32_expert_normal, router_weight
-from vesper_amd.connected import ConnectedConfig, bf16_activation, validate_layer
+from vesper_amd.connected import ConnectedConfig, ConnectedMoE, bf16_activation, validate_layer
 from vesper_amd.fixtures import (load_gate_fixture, load_router_fixture, load_shared_fixture, shared_layout,
                                  write_gate_fixture, write_router_fixture, write_shared_fixture)
 from vesper_amd.resources import MiB
@@ -153,3 +153,12 @@ def test_connected_host_checks():
         bf16_activation(np.zeros(511, np.float32), 512)
     with pytest.raises(ValueError, match="per token"):
         bf16_activation(np.zeros(512, np.float64), 512)
+    # the provider contract a block or backbone relies on, before anything is opened
+    moe = ConnectedMoE("store", "gate.npz", "router.npz", "shared.npz", layer=2)
+    assert moe.layer == 2 and moe.stack is None and moe.config.cache.primary_device == 0
+    with pytest.raises(RuntimeError, match="context manager"):
+        moe.forward(np.zeros(5120, np.float32))
+    with pytest.raises(ValueError, match="BLAS"):
+        ConnectedMoE("store", "gate.npz", "router.npz", "shared.npz", cublas_library="libcublas.so")
+    with pytest.raises(ValueError, match="source factory"):
+        ConnectedMoE("store", "gate.npz", "router.npz", "shared.npz", source_factory=3)

@@ -18,11 +18,11 @@ import numpy as np
 import pytest
 
 from oracle.formats import bf16_bits, bf16_values
-from oracle.inputs import activations, fp8_block32_expert_normal, mxfp4_expert, router_weight
+from oracle.inputs import activations, mxfp4_expert
+from tests.helpers import write_layer
 from vesper_amd.config import MoEConfig
 from vesper_amd.connected import ConnectedConfig, ConnectedMoE
 from vesper_amd.expert import ResidentExpert
-from vesper_amd.fixtures import write_gate_fixture, write_router_fixture, write_shared_fixture
 from vesper_amd.layer import ExpertBank, MoELayer
 from vesper_amd.resources import GiB, MiB
 from vesper_amd.store import REFERENCE_PROFILE, ModelProfile, build_store
@@ -87,24 +87,6 @@ def test_tiered_runtime_over_store_matches_resident_expert(direct_io_dir, mode):
         assert runtime.snapshot()["counters"]["integrity_failures"] == 1
 
 
-def write_layer(root, rng, stored, bias_shift=None):
-    """A 16-expert layer: store (experts in `stored`), gate, router and shared fixtures; returns the paths and
-    the arrays."""
-    h, i, e = SMALL.hidden, SMALL.intermediate, SMALL.experts
-    experts = {n: mxfp4_expert(rng, h, i) for n in range(e)}
-    build_store([(LAYER, n, experts[n]) for n in stored], root / "store", max_experts=16, profile=SMALL)
-    gate = bf16_bits(router_weight(rng, e, h))
-    biases = {n: (rng.standard_normal(e) * 0.05).astype(np.float32) for n in ("bias", "bias_vl")}
-    if bias_shift is not None:
-        for name, shift in bias_shift.items():
-            biases[name] = biases[name] + shift.astype(np.float32)
-    shared = fp8_block32_expert_normal(rng, h, i)
-    paths = (root / "store", write_gate_fixture(root / "gate", LAYER, gate, SMALL),
-             write_router_fixture(root / "router", LAYER, biases, SMALL),
-             write_shared_fixture(root / "shared", LAYER, shared, SMALL))
-    return paths, experts, gate, biases
-
-
 class Resident:
     """The decode layer on the same weights, no shared expert: its output is the routed sum rounded once."""
 
@@ -132,7 +114,8 @@ class Resident:
 def check_call(out, resident, bits):
     ref_out, ref = resident.decode(bits)
     t = ref_out.shape[0]
-    np.testing.assert_array_equal(np.asarray(out["logits"]).reshape(t, -1).view(np.uint32), ref["logits"].view(np.uint32))
+    np.testing.assert_array_equal(np.asarray(out["logits"]).reshape(t, -1).view(np.uint32),
+                                  ref["logits"].view(np.uint32))
     np.testing.assert_array_equal(np.asarray(out["routing"]["indices"]).reshape(t, -1), ref["indices"])
     np.testing.assert_array_equal(np.asarray(out["routing"]["weights"]).reshape(t, -1).view(np.uint32),
                                   ref["weights"].view(np.uint32))
@@ -148,7 +131,8 @@ def check_call(out, resident, bits):
 @pytest.mark.parametrize("mode", ["readback", "gpu-sha256"])
 def test_connected_moe_over_store_matches_decode_layer(gpu_ctx, direct_io_dir, mode):
     rng = np.random.default_rng(41)
-    paths, experts, gate, biases = write_layer(direct_io_dir, rng, range(SMALL.experts))
+    layer = write_layer(direct_io_dir, rng, SMALL, LAYER)
+    paths, experts, gate, biases = layer["paths"], layer["experts"], layer["gate"], layer["biases"]
     config = ConnectedConfig(cache=cache_config(mode, 2, 2, SMALL, 16), host_cap_bytes=1024 * MiB,
                              device_free_floor=GiB)
     one = bf16_bits(activations(rng, 1, SMALL.hidden)[0])
@@ -188,7 +172,8 @@ def test_connected_moe_refuses_missing_experts_before_reading(gpu_ctx, direct_io
     rng = np.random.default_rng(43)
     # text routing never selects experts 8-15 (bias -100), image-span routing always prefers them (+100)
     high = (np.arange(SMALL.experts) >= 8).astype(np.float32) * 100
-    paths, experts, gate, biases = write_layer(direct_io_dir, rng, range(8), {"bias": -high, "bias_vl": high})
+    layer = write_layer(direct_io_dir, rng, SMALL, LAYER, range(8), {"bias": -high, "bias_vl": high})
+    paths, experts, gate, biases = layer["paths"], layer["experts"], layer["gate"], layer["biases"]
     config = ConnectedConfig(cache=cache_config("gpu-sha256", 2, 2, SMALL, 16), host_cap_bytes=1024 * MiB,
                              device_free_floor=GiB)
     x = bf16_bits(activations(rng, 1, SMALL.hidden)[0])

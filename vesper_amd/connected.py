@@ -86,6 +86,32 @@ class ConnectedConfig:
             raise ValueError("Invalid connected GPU allocation cap")
 
 
+class DeviceLedger:
+    """A component's device context in the shape of the reference's Device ledger (src/vesper/cuda.py:93-191)
+    as a transformer block reads it around a MoE call (src/vesper/block.py:43-92): `allocations` (the
+    context's live explicit bytes, as one entry), `peak`, `memory()`, `free_floor` and `allocate` / `free`."""
+
+    def __init__(self, ctx: _lib.Context, free_floor: int):
+        self.ctx, self.free_floor, self.ordinal = ctx, free_floor, ctx.ordinal
+
+    @property
+    def allocations(self) -> dict:
+        return {"explicit": self.ctx.owned_bytes()[0]}
+
+    @property
+    def peak(self) -> int:
+        return self.ctx.owned_bytes()[1]
+
+    def memory(self) -> dict:
+        return self.ctx.memory()
+
+    def allocate(self, size: int) -> int:
+        return self.ctx.malloc(size)
+
+    def free(self, pointer: int):
+        self.ctx.free(pointer)
+
+
 def bf16_activation(activation, hidden: int):
     """(FP32 values, BF16 bits) of an activation given as BF16 bits or FP32 values, refused unless every value
     is a finite BF16 (src/vesper/connected.py:46-53)."""
@@ -151,6 +177,8 @@ class ConnectedMoE:
                 raise ValueError("Connected store contains artifacts from another layer")
             self.contexts = {"gate": self.gate.ctx, "router": self.router.ctx, "shared": self.shared.ctx,
                              "accumulator": self.accumulator.ctx, "cache_primary": self.experts.ctx}
+            self.devices = {n: DeviceLedger(ctx, c.device_free_floor) for n, ctx in self.contexts.items()}
+            self.helper_device = None
             self.minimum_available = physical_memory()["available"]
             self._headroom()
             return self
@@ -164,10 +192,10 @@ class ConnectedMoE:
         available = physical_memory()["available"]
         self.minimum_available = min(self.minimum_available, available)
         self.budget.acquire(0, available)
-        total = sum(ctx.owned_bytes()[0] for ctx in self.contexts.values())
+        total = sum(sum(device.allocations.values()) for device in self.devices.values())
         if total > self.config.primary_explicit_cap_bytes:
             raise MemoryError("Combined native GPU buffers exceed the connected explicit cap")
-        if self.experts.ctx.memory()["free"] < self.config.device_free_floor:
+        if self.devices["cache_primary"].memory()["free"] < self.config.device_free_floor:
             raise MemoryError("Connected runtime refuses work below the GPU reserve")
 
     def forward(self, activation, image_span=False) -> dict:
@@ -257,7 +285,7 @@ class ConnectedMoE:
                 "combined_host_cap_bytes": self.budget.cap,
                 "minimum_observed_host_available_bytes": self.minimum_available,
                 "host_available_floor_bytes": self.budget.available_floor,
-                "component_peak_explicit_device_bytes": {n: ctx.owned_bytes()[1] for n, ctx in self.contexts.items()},
+                "component_peak_explicit_device_bytes": {n: d.peak for n, d in self.devices.items()},
                 "primary_explicit_cap_bytes": self.config.primary_explicit_cap_bytes,
                 "cache_config": asdict(self.config.cache), "device": self.gate.ctx.device_name()[1]}
 
