@@ -249,6 +249,23 @@ def test_config3_projections_within_tolerance(tokens):
             assert_close(got["output_bf16"], ref["output_bf16"], name)
 
 
+@pytest.mark.parametrize("tokens", [1, 16, 2048])
+def test_config3_stacked_q_a_kv_a(tokens):
+    """q_a and kv_a as one projection of their stacked rows (the benchmark's timed form, 2112 rows: the last
+    128-row scale block half full): sampled tokens within the bar of the oracle, for both row ranges."""
+    rng = np.random.default_rng(30 + tokens)
+    layout = {"q_kv_a": (1536 + 576, 7168)}
+    arrays = arrays_for(layout, 128, rng)
+    x = bf16_bits(rng.standard_normal((tokens, 7168)).astype(np.float32))
+    sample = np.unique(np.concatenate([[0, tokens - 1], rng.choice(tokens, min(tokens, 32), replace=False)]))
+    with NativeProjections(arrays, block=128, layout=layout) as proj:
+        got = proj.fp8("q_kv_a", x)
+    ref = fp8_projection(bf16_values(x[sample]), arrays["layers.0.attn.q_kv_a.weight"],
+                         arrays["layers.0.attn.q_kv_a.scale"], 128)
+    for rows, name in ((slice(0, 1536), "q_a rows"), (slice(1536, 2112), "kv_a rows")):
+        assert_close(got["output_bf16"][sample][:, rows], ref["output_bf16"][:, rows], f"{name} T={tokens}")
+
+
 def test_config3_T2048_sampled_tokens_within_tolerance():
     """All four configuration-3 projections at the benchmark's 2048 tokens: the whole batch runs through the
     GEMM (q_a and kv_a with K split too), and 64 sampled tokens (first and last included, spread over every

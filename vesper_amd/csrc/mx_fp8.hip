@@ -522,57 +522,61 @@ __global__ __launch_bounds__(kGemmThreads) void fp8_gemm_kernel(Fp8Args a) {
 #pragma unroll
     for (int u = 0; u < kWaveTiles; ++u) acc[t][u] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int cl) {
-    const uint8_t* st = lds + (cl % kGemmStages) * kGemmStage;
+  // One chunk's operands in registers: read from LDS one chunk ahead of their MFMAs, so the reads of chunk
+  // c + 1 are in flight while chunk c multiplies (the waves of a SIMD reach the per-chunk barrier together,
+  // so neither can cover the other's LDS latency).
+  struct Ops {
     uint4 am[kTiles][2];
+    uint4 b[kWaveTiles][2];
+    uint32_t sx[kWaveTiles];
+    uint32_t swv;
+  };
+  auto read_ops = [&](Ops& o, int cl) {
+    const uint8_t* st = lds + (cl % kGemmStages) * kGemmStage;
 #pragma unroll
     for (int t = 0; t < kTiles; ++t)
 #pragma unroll
       for (int h = 0; h < 2; ++h)
-        am[t][h] = *reinterpret_cast<const uint4*>(st + (8 * (wave & 3) + 2 * t + h) * 1024 + 16 * lane);
-    const uint32_t swv = *reinterpret_cast<const uint32_t*>(st + kGemmA + kGemmB + kGemmSA + 256 * wave +
-                                                            (kBlock == 32 ? 4 * lane : 0));
-    uint4 b[kWaveTiles][2];
-    uint32_t sx[kWaveTiles];
-    auto read_b = [&](int u) {
+        o.am[t][h] = *reinterpret_cast<const uint4*>(st + (8 * (wave & 3) + 2 * t + h) * 1024 + 16 * lane);
+#pragma unroll
+    for (int u = 0; u < kWaveTiles; ++u) {
       const int tile = u0 + u;
-      b[u][0] = *reinterpret_cast<const uint4*>(st + kGemmA + (2 * tile) * 1024 + 16 * lane);
-      b[u][1] = *reinterpret_cast<const uint4*>(st + kGemmA + (2 * tile + 1) * 1024 + 16 * lane);
-      sx[u] = *reinterpret_cast<const uint32_t*>(st + kGemmA + kGemmB + 4 * (16 * tile + n));
-    };
+      o.b[u][0] = *reinterpret_cast<const uint4*>(st + kGemmA + (2 * tile) * 1024 + 16 * lane);
+      o.b[u][1] = *reinterpret_cast<const uint4*>(st + kGemmA + (2 * tile + 1) * 1024 + 16 * lane);
+      o.sx[u] = *reinterpret_cast<const uint32_t*>(st + kGemmA + kGemmB + 4 * (16 * tile + n));
+    }
+    o.swv = *reinterpret_cast<const uint32_t*>(st + kGemmA + kGemmB + kGemmSA + 256 * wave +
+                                               (kBlock == 32 ? 4 * lane : 0));
+  };
+  auto multiply = [&](const Ops& o) {
     if constexpr (kBlock == 32) {
 #pragma unroll
-      for (int u = 0; u < kWaveTiles; ++u) read_b(u);
-#pragma unroll
       for (int u = 0; u < kWaveTiles; ++u) {
-        const int sxb = (int)((sx[u] >> (8 * q)) & 0xFF);
+        const int sxb = (int)((o.sx[u] >> (8 * q)) & 0xFF);
 #pragma unroll
         for (int t = 0; t < kTiles; ++t)
-          acc[t][u] = mfma_fp8_fp8(am[t][0], am[t][1], b[u][0], b[u][1], acc[t][u], (int)((swv >> (8 * t)) & 0xFF),
-                                   sxb);
+          acc[t][u] = mfma_fp8_fp8(o.am[t][0], o.am[t][1], o.b[u][0], o.b[u][1], acc[t][u],
+                                   (int)((o.swv >> (8 * t)) & 0xFF), sxb);
       }
     } else {
       // Per chunk the MFMA gives the block dot d (unit scales) and acc = fma(d, f32(sa * sw), acc) follows in
       // FP32: one rounding per output. MFMA k + 1 is issued before the 4 fused multiply-adds that scale MFMA k,
       // so they run while it executes; the scheduling fences keep the compiler from pairing each MFMA with its
-      // own scaling instead (which waits for every result). Token tile u + 2's operands are read from LDS
-      // while tile u multiplies.
-      const float swf = __uint_as_float(swv);
+      // own scaling instead (which waits for every result).
+      const float swf = __uint_as_float(o.swv);
       constexpr int kSteps = kTiles * kWaveTiles;
-      read_b(0);
-      read_b(1);
       v4f d[2];
-      d[0] = mfma_fp8_fp8(am[0][0], am[0][1], b[0][0], b[0][1], v4f{0.f, 0.f, 0.f, 0.f}, 127, 127);
+      d[0] = mfma_fp8_fp8(o.am[0][0], o.am[0][1], o.b[0][0], o.b[0][1], v4f{0.f, 0.f, 0.f, 0.f}, 127, 127);
 #pragma unroll
       for (int k = 0; k < kSteps; ++k) {
         const int t = k % kTiles, u = k / kTiles;
-        if (t == 1 && u + 2 < kWaveTiles) read_b(u + 2);
         if (k + 1 < kSteps) {
           const int t1 = (k + 1) % kTiles, u1 = (k + 1) / kTiles;
-          d[(k + 1) & 1] = mfma_fp8_fp8(am[t1][0], am[t1][1], b[u1][0], b[u1][1], v4f{0.f, 0.f, 0.f, 0.f}, 127, 127);
+          d[(k + 1) & 1] = mfma_fp8_fp8(o.am[t1][0], o.am[t1][1], o.b[u1][0], o.b[u1][1], v4f{0.f, 0.f, 0.f, 0.f},
+                                        127, 127);
         }
         __builtin_amdgcn_sched_barrier(0);
-        const float sc = __uint_as_float(sx[u]) * swf;
+        const float sc = __uint_as_float(o.sx[u]) * swf;
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[t][u][i] = fmaf(d[k & 1][i], sc, acc[t][u][i]);
         __builtin_amdgcn_sched_barrier(0);
@@ -580,15 +584,26 @@ __global__ __launch_bounds__(kGemmThreads) void fp8_gemm_kernel(Fp8Args a) {
     }
   };
 
-#pragma unroll
-  for (int j = 0; j < kGemmStages - 1; ++j) copy(j);
-  for (int c = 0; c < C; ++c) {
-    // chunk c's copies are done once only chunk c + 1's are outstanding; the barrier waits for everyone's
-    // (and for everyone to have finished chunk c - 1, whose stage chunk c + 2 takes)
+  // Step c: chunk c + 1's copies are done once only chunk c + 2's are outstanding, and this wave's reads of
+  // chunk c have landed; the barrier then covers every wave, so chunk c's stage can take the copies of chunk
+  // c + 3 while chunk c + 1's operands are read and chunk c multiplies.
+  auto step = [&](int c, const Ops& cur, Ops& next) {
     __builtin_amdgcn_s_waitcnt(mxd::vm_wait_imm(kGemmCopies * (kGemmStages - 2)));
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0), vmcnt and expcnt left at their maxima
     mxd::copy_barrier();
-    copy(c + kGemmStages - 1);
-    compute(c);
+    copy(c + kGemmStages);
+    read_ops(next, c + 1);
+    multiply(cur);
+  };
+#pragma unroll
+  for (int j = 0; j < kGemmStages; ++j) copy(j);
+  __builtin_amdgcn_s_waitcnt(mxd::vm_wait_imm(kGemmCopies * (kGemmStages - 1)));
+  mxd::copy_barrier();
+  Ops ops0, ops1;
+  read_ops(ops0, 0);
+  for (int c = 0; c < C; c += 2) {
+    step(c, ops0, ops1);
+    if (c + 1 < C) step(c + 1, ops1, ops0);
   }
   // every copy must land before the workgroup ends (its LDS may be handed to another workgroup)
   __builtin_amdgcn_s_waitcnt(mxd::vm_wait_imm(0));

@@ -5,7 +5,9 @@
 Builds the four configuration-3 projections (q_a 7168->1536, q_b 1536->24576, kv_a 7168->576,
 o 16384->7168; E4M3 weights with FP32 128 x 128 block scales, log-uniform in [2^-8, 2^-2]; synthetic,
 generated in HBM) and times each projection call (quantizer + product) with HIP events over `iters`
-back-to-back calls. Algorithmic work per call: weight bytes N*K + scales, x and y; FLOP 2*T*N*K.
+back-to-back calls. q_a and kv_a, which read the same input, run as one call over their stacked 2112 rows
+(FUSED_LAYOUT; `layout=LAYOUT` times them separately). Algorithmic work per call: weight bytes N*K +
+scales, x and y; FLOP 2*T*N*K.
 
 Each projection is held in as many copies as take at least ROTATE_BYTES together, and consecutive
 calls use consecutive copies, as consecutive layers of a model would: a call never finds its weights
@@ -22,17 +24,21 @@ import sys
 import numpy as np
 
 LAYOUT = {"q_a": (1536, 7168), "q_b": (24576, 1536), "kv_a": (576, 7168), "o": (7168, 16384)}
+# q_a and kv_a read the same input: as one projection of their stacked rows (q_a's rows, then kv_a's), one
+# quantization of x and one launch serve both; every output is the same dot product as in the separate calls.
+FUSED_LAYOUT = {"q_kv_a": (1536 + 576, 7168), "q_b": (24576, 1536), "o": (7168, 16384)}
 ROTATE_BYTES = 512 << 20
 
 
-def run(tokens=(1, 16, 2048), iters=20, seed=20261018, ctx=None):
+def run(tokens=(1, 16, 2048), iters=20, seed=20261018, ctx=None, layout=None):
     from . import _lib
     own = ctx is None
     ctx = ctx or _lib.Context(0)
     lib = ctx.lib
     rng = np.random.default_rng(seed)
+    layout = layout or FUSED_LAYOUT
     blobs = {}
-    for i, (name, (n, k)) in enumerate(LAYOUT.items()):
+    for i, (name, (n, k)) in enumerate(layout.items()):
         size = int(lib.cdll.mx_fp8_tiled_bytes(n, k, 128))
         w = ctx.malloc(n * k)
         ctx.fill_uniform_u8(w, n * k, seed * 31 + i, 0, 126)      # finite E4M3 codes (no 0x7F / 0xFF)
@@ -50,8 +56,8 @@ def run(tokens=(1, 16, 2048), iters=20, seed=20261018, ctx=None):
         swd.free()
         blobs[name] = copies
     tmax = max(tokens)
-    kmax = max(k for _, k in LAYOUT.values())
-    nmax = max(n for n, _ in LAYOUT.values())
+    kmax = max(k for _, k in layout.values())
+    nmax = max(n for n, _ in layout.values())
     x = rng.standard_normal((tmax, kmax)).astype(np.float32)
     b = x.view(np.uint32).astype(np.uint64)
     xd = ctx.upload(((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16))
@@ -61,7 +67,7 @@ def run(tokens=(1, 16, 2048), iters=20, seed=20261018, ctx=None):
     for t in tokens:
         per = {}
         total_us, total_bytes, total_flop = 0.0, 0, 0
-        for name, (n, k) in LAYOUT.items():
+        for name, (n, k) in layout.items():
             # the input is the first T rows of a [T, k] view of the buffer; call i uses copy i
             copies = blobs[name]
             calls = [(ctx._h(), C.c_void_p(c), n, k, 128, _lib.vp(xd), t, _lib.vp(yd), None, None, None, None)
