@@ -124,7 +124,8 @@ def run(experts: int = 8, seed: int = 20261018) -> dict:
         out = {mode: promote(directory / "store", keys, mode, REFERENCE_PROFILE)
                for mode in ("readback", "gpu-sha256")}
         out["note"] = ("one expert per request, store read -> pinned staging -> HBM slot (tiled), with the "
-                       "mode's checks; medians over the timed experts; host hashing is single-threaded")
+                       "mode's checks; medians over the timed experts; the whole-expert and per-tensor digests hash "
+                       "on up to 4 host threads beside each other, the chunk table on one of them")
         return out
     finally:
         shutil.rmtree(directory, ignore_errors=True)
