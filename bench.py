@@ -325,10 +325,17 @@ def secondary(ctx):
     """The other BASELINE configurations, measured on the same GPU (each a few seconds): 2 = MoE prefill
     (T = 4096, Zipf(1.1) routing), 3 = FP8 block-128 projections at T = 1, 16, 2048, 4 = 8-layer offload
     decode at T = 4 with 25 % of the routed experts resident; the SHA-256 admission audit of expert
-    slots (one expert, and the 1 GiB maximum payload); and the promotion of single experts from the on-disk
-    store into HBM slots."""
-    from vesper_amd import fp8_workload, integrity_workload, offload_workload, prefill_workload, store_workload
+    slots (one expert, and the 1 GiB maximum payload); the promotion of single experts from the on-disk
+    store into HBM slots; and configuration 0's expert with BF16 activations at T = 1, 4, 16."""
+    from vesper_amd import (bf16_workload, fp8_workload, integrity_workload, offload_workload, prefill_workload,
+                            store_workload)
     out = {}
+    log("configuration 0: one expert, BF16 activations")
+    c0 = bf16_workload.run((1, 4, 16), 50, ctx=ctx)
+    for v in c0["per_tokens"].values():
+        v["hbm_frac"] = round(v["GB_per_s"] / HBM_PEAK_GBS, 4)
+    out["config0_bf16_expert"] = c0
+    log(f"config 0: {c0}")
     log("configuration 2: prefill")
     p = prefill_workload.run(4096, 5, ctx=ctx)
     out["prefill_T4096"] = dict(p, mfma_peak_TFLOP_per_s=5000.0, mfma_frac=round(p["TFLOP_per_s"] / 5000.0, 4))

@@ -180,8 +180,10 @@ def test_baseline_shapes_sixteen_tokens_properties(gpu_ctx):
 def test_decode_rows_do_not_depend_on_the_batch(gpu_ctx):
     """Per token the layer's arithmetic does not depend on the batch: a token's MFMA column, its
     activation and down-input quantization blocks and its combine are its own, whichever slot position the
-    plan gives it. Every output row is bit-identical across three batchings of the same 16 tokens at the
-    BASELINE shapes (T = 16, 4 x 4 and 16 x 1; 103-odd, about 30 and 9 slots)."""
+    plan gives it. Every output row is bit-identical across four batchings of the same 16 tokens at the
+    BASELINE shapes (T = 16, 4 x 4, 8 x 2 and 16 x 1; 103-odd, about 30, about 16 and 9 slots). The one- and
+    two-token calls compute the shared expert beside the routing in other kernels, the larger ones as a plan
+    slot: the rows must still agree bit for bit."""
     cfg = MoEConfig()
     rng = np.random.default_rng(1616)
     layer, bank, w, _ = build_layer(gpu_ctx, cfg, rng, device_fill=True)
@@ -189,8 +191,10 @@ def test_decode_rows_do_not_depend_on_the_batch(gpu_ctx):
         x = activations(rng, 16, cfg.hidden)
         y16 = layer.decode(x)
         y4 = np.concatenate([layer.decode(x[i:i + 4]) for i in range(0, 16, 4)])
+        y2 = np.concatenate([layer.decode(x[i:i + 2]) for i in range(0, 16, 2)])
         y1 = np.concatenate([layer.decode(x[i:i + 1]) for i in range(16)])
         np.testing.assert_array_equal(y4, y16)
+        np.testing.assert_array_equal(y2, y16)
         np.testing.assert_array_equal(y1, y16)
         np.testing.assert_array_equal(layer.decode(x), y16)
     finally:
