@@ -216,10 +216,11 @@ int mx_expert_forward_tiled(mx_ctx* ctx, const void* tiled, int32_t hidden, int3
                             uint16_t* y_bf16, const mx_expert_stages* stages, void* stream);
 
 /* The benchmark's configuration-0 expert on a tiled expert: BF16 activations, FP32 accumulation, no
- * activation quantization and no clamp. y[T][H] (BF16, rounded once) = W2 . h with
- * h[T][I] = silu(W1 . x) * (W3 . x) [* route_w[t]] in FP32, x BF16 [T][H]. `h` (FP32 [T][I], 16-byte aligned)
- * and `gu` (FP32 [T][2I]: W1 . x then W3 . x) receive the intermediates when non-null. tokens <= 16,
- * hidden <= 8192, intermediate <= 4096; uses the context scratch. The reference's expert
+ * activation quantization and no clamp. y[T][H] (BF16, rounded once, 8-byte aligned) = W2 . h with
+ * h[T][I] = silu(W1 . x) * (W3 . x) [* route_w[t]] in FP32, x BF16 [T][H] (16-byte aligned). `h` (FP32 [T][I])
+ * and `gu` (FP32 [T][2I]: W1 . x then W3 . x) receive the intermediates when non-null; the down product
+ * takes h as two BF16 terms (hi + lo, about 16 significant bits). tokens <= 16, hidden <= 8192,
+ * intermediate <= 4096; uses the context scratch. The reference's expert
  * (ExpertExecutor.execute, src/vesper/expert.py:51-79) quantizes both activations to E4M3 instead; this is
  * the same weights under configuration 0's formula (expert_reference_fp32 of the oracle). */
 int mx_expert_forward_bf16(mx_ctx* ctx, const void* tiled, int32_t hidden, int32_t intermediate,
