@@ -645,11 +645,15 @@ int fp8_splits(int N, int K, int T) {
     if (base_wgs >= 256) return 1;
     return std::max(1, std::min({8, (K / 128) / 8, (512 + base_wgs - 1) / base_wgs}));
   }
-  // GEMV: about 512 workgroups, two per CU, every wave keeping at least one chunk. Against a 1024 target
-  // (A/B, two runs each): 8192 x 4096 block 32 (wo_a) 18.8 -> 15.9 us, 24576 x 1536 13.6 -> 11.9 us at
-  // T = 1 and 18.3 -> 15.5 us at T = 16; 7168 x 16384 29.2 against 28.5 us at T = 1, 32.7 against 33.5 at 16.
-  const int base_wgs = (N / 64) * ((T + kTok - 1) / kTok);
-  return std::max(1, std::min({16, (K / 128) / 4, (512 + base_wgs - 1) / base_wgs}));
+  // GEMV: every workgroup streams about 8 chunks of its row group -- at most kFusedChunks when the call
+  // may quantize its own activations (up to kFusedMaxTokens tokens), at least 8 otherwise -- and at most 16
+  // splits. Fewer, longer workgroups measured faster than a fixed workgroup count on MI355X (us per call,
+  // T = 1 / 16): 2112 x 7168 7 splits 11.3 / 13.1 against 14 splits (the former ~512-workgroup rule) 12.5 /
+  // 16.9; 7168 x 16384 16 splits 28.9 / 33.8 against 5 splits 30.1 / 33.3; 24576 x 1536 1 split 14.1 / 14.5
+  // against 2 splits 13.7 / 16.3, so few tokens keep 2 splits (the fused quantizer needs <= 8 chunks).
+  const int chunks = K / 128;
+  const int s = T <= kFusedMaxTokens ? (chunks + kFusedChunks - 1) / kFusedChunks : chunks / 8;
+  return std::max(1, std::min(16, s));
 }
 
 // Whether the block-128 GEMV can quantize its own activations: few tokens, and every workgroup's K range
