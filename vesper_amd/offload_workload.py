@@ -183,6 +183,12 @@ def run(steps=10, warmup=4, layers=8, tokens=4, resident_frac=0.25, seed=2026101
     overlap = min(1.0, raw)   # above 1 only by run-to-run noise (the step ran faster than copies alone)
     out = {"layers": layers, "tokens": tokens, "cache_slots": slots, "step_us": round(t_step, 1),
            "copy_us": round(t_copy, 1), "compute_us": round(t_compute, 1), "overlap": round(overlap, 4), "overlap_raw": round(raw, 4),
+           "step_over_copy": round(t_step / t_copy, 4),
+           "overlap_note": ("overlap divides by min(copy, compute); with compute at "
+                            f"{100 * t_compute / max(t_copy, 1e-9):.1f} % of the copy time, 1 % of run-to-run noise in "
+                            "the step or copy time moves it by about "
+                            f"{t_copy / max(t_compute, 1e-9):.0f} %, so it carries little information; "
+                            "step_over_copy (the step against its copies alone) is the informative figure"),
            "h2d_GB_per_s_single_copy": round(h2d_gbs, 1),
            "streamed_GB_per_s": round(st["bytes_copied"] / steps / (t_step * 1e-6) / 1e9, 1),
            "misses_per_step": st["misses"] / steps, "hits_per_step": st["hits"] / steps,
