@@ -12,11 +12,11 @@ cosine 0.9999).
 import numpy as np
 import pytest
 
-from oracle.expert import expert_forward, swiglu
+from oracle.expert import expert_forward, expert_reference_stages, swiglu
 from oracle.formats import bf16_bits, mxfp4_gemv_spec, quantize_activation
-from oracle.inputs import activations, mxfp4_expert
+from oracle.inputs import SEEDS, activations, mxfp4_expert
 from tests.helpers import assert_close, assert_gemv_close, exact_activation
-from vesper_amd.expert import ExpertExecutor, ResidentExpert
+from vesper_amd.expert import BF16ActivationExpert, ExpertExecutor, ResidentExpert
 from vesper_amd.shared import ResidentSharedExpert
 
 pytestmark = pytest.mark.gpu
@@ -92,3 +92,20 @@ def test_shared_expert_is_unweighted_and_executor_validates_before_device():
     with ExpertExecutor(hidden=256, intermediate=128) as ex:
         with pytest.raises(ValueError):
             ex.execute(x, {"w1_weight": 0})
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_canonical_seeds(seed):
+    """The reference's canonical seed set (src/vesper/expert_reference.py:110): the W4A8 expert stage by stage
+    and the BF16-activation expert (configuration 0's formula) on the same weights, two tokens each."""
+    rng = np.random.default_rng(seed)
+    hidden, intermediate = 1024, 512
+    arrays = mxfp4_expert(rng, hidden, intermediate)
+    x = activations(rng, 2, hidden)
+    route = np.array([1.0, 0.5], np.float32)
+    with ResidentExpert(arrays, swiglu_limit=10.0, hidden=hidden, intermediate=intermediate) as expert:
+        got = expert.forward(x, route)
+    check_stages(got, x, arrays, route, 10.0)
+    with BF16ActivationExpert(arrays, hidden=hidden, intermediate=intermediate) as expert:
+        out = expert.forward(x, route)
+    assert_close(out["y"], expert_reference_stages(x, arrays, route)["y"], f"configuration 0, seed {seed}")

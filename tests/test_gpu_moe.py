@@ -105,7 +105,7 @@ def check_layer_call(layer, bank, w, arrays, x, cfg):
     return out
 
 
-@pytest.mark.parametrize("tokens", [1, 3, 16])
+@pytest.mark.parametrize("tokens", [1, 2, 3, 16])
 @pytest.mark.parametrize("limit", [0.0, 10.0])
 def test_small_layer_matches_oracle(gpu_ctx, tokens, limit):
     cfg = MoEConfig(hidden=512, intermediate=256, experts=32, top_k=4, swiglu_limit=limit, shared="mxfp4")
