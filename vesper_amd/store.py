@@ -210,7 +210,7 @@ def read_bounded_npz(path: Path, members: dict, what: str) -> dict:
 def load_expert_fixture(path: Path, profile: ModelProfile = REFERENCE_PROFILE):
     """(arrays, manifest) of a fixture; every member's header is bounded before NumPy allocates."""
     path = Path(path)
-    manifest = json.loads((path.parent / "manifest.json").read_text(encoding="utf-8"))
+    manifest = read_manifest(path)
     validate_expert_provenance(manifest, profile)
     layout = profile.expert_layout()
     arrays = read_bounded_npz(path, {name: (shape, np.uint8) for name, shape in layout.items()}, "Expert")
