@@ -11,7 +11,8 @@ src/vesper/connected.py:56-213).
   the same weights, for one token and for five; the output is that sum plus the FP8 shared expert's BF16
   rows, rounded once; a second call served from other tiers returns the same bits; the image-span bias
   selects differently and matches the layer built on that bias; experts missing from the store are refused
-  before any store read, and the next call succeeds.
+  before any store read, and the next call succeeds; a store read failing in the middle of a call fails
+  that call only.
 """
 
 import numpy as np
@@ -25,7 +26,7 @@ from vesper_amd.connected import ConnectedConfig, ConnectedMoE
 from vesper_amd.expert import ResidentExpert
 from vesper_amd.layer import ExpertBank, MoELayer
 from vesper_amd.resources import GiB, MiB
-from vesper_amd.store import REFERENCE_PROFILE, ModelProfile, build_store
+from vesper_amd.store import REFERENCE_PROFILE, ModelProfile, NativeStore, build_store
 from vesper_amd.tiered import CacheConfig, TieredExpertRuntime
 
 pytestmark = pytest.mark.gpu
@@ -194,5 +195,46 @@ def test_connected_moe_refuses_missing_experts_before_reading(gpu_ctx, direct_io
         with pytest.raises(ValueError, match="selected layer"):
             with ConnectedMoE(*paths, config, layer=0, model=SMALL):
                 pass
+    finally:
+        text.close()
+
+
+class FailingStore(NativeStore):
+    """A store whose n-th expert read fails once with OSError (an injected device-read fault)."""
+
+    def __init__(self, *args, fail_at=3, **kwargs):
+        super().__init__(*args, **kwargs)
+        self.fail_at, self.reads = fail_at, 0
+
+    def read_into(self, key, target):
+        self.reads += 1
+        if self.reads == self.fail_at:
+            raise OSError("injected read failure")
+        return super().read_into(key, target)
+
+
+def test_connected_moe_injected_read_failure_then_fresh_call(gpu_ctx, direct_io_dir):
+    """The reference's injected-expert-failure case (tests/test_connected.py:35-70 of the reference): a read
+    failing in the middle of a call fails that call with the experts completed so far recorded and publishes
+    nothing; the next call starts from a zeroed accumulator and matches the resident layer."""
+    rng = np.random.default_rng(47)
+    layer = write_layer(direct_io_dir, rng, SMALL, LAYER)
+    paths, experts, gate, biases = layer["paths"], layer["experts"], layer["gate"], layer["biases"]
+    config = ConnectedConfig(cache=cache_config("gpu-sha256", 2, 2, SMALL, 16), host_cap_bytes=1024 * MiB,
+                             device_free_floor=GiB)
+    x = bf16_bits(activations(rng, 1, SMALL.hidden)[0])
+    text = Resident(gpu_ctx, experts, gate, biases["bias"])
+
+    def factory(path, budget):
+        return FailingStore(path, budget, max_experts=16, profile=SMALL, fail_at=3)
+    try:
+        with ConnectedMoE(*paths, config, layer=LAYER, model=SMALL, source_factory=factory) as moe:
+            with pytest.raises(OSError, match="injected"):
+                moe.forward(x)
+            attempt = moe.last_attempt
+            assert attempt["status"] == "failed" and len(attempt["completed_expert_ids"]) == 2
+            check_call(moe.forward(x), text, x)
+            assert moe.snapshot()["calls"] == {"calls_started": 2, "calls_completed": 1, "calls_failed": 1}
+        assert moe.cleanup["parent_reservation_bytes"] == 0 and moe.cleanup["cache_reservation_bytes"] == 0
     finally:
         text.close()
