@@ -14,7 +14,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from oracle.expert import expert_forward, expert_reference_fp32, swiglu
+from oracle.expert import expert_forward, expert_reference_fp32, expert_reference_stages, swiglu
 from oracle.formats import bf16_bits, bf16_values
 from oracle.inputs import activations, aggregation_cases, mxfp4_expert, router_weight
 from oracle.moe import combine, moe_layer, participation
@@ -128,3 +128,42 @@ def test_layer_routes_weights_before_w2_and_combines_in_id_order():
     unweighted = expert_forward(x[0], bank[e0], None, 0.0)["w2"]
     post = bf16_bits(bf16_values(unweighted) * weights[0, 0])
     assert np.count_nonzero(post != out["experts"][e0]["w2"][0]) > 0
+
+
+def _brute_dequant(packed, scales):
+    """E2M1 byte pairs (low nibble = even K) times 2^(E8M0 - 127) per 32 K, written out per element."""
+    magnitude = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
+    rows, half = packed.shape
+    out = np.zeros((rows, 2 * half))
+    for r in range(rows):
+        for b in range(half):
+            for j, code in enumerate((int(packed[r, b]) & 0xF, int(packed[r, b]) >> 4)):
+                k = 2 * b + j
+                value = magnitude[code & 7] * (-1.0 if code & 8 else 1.0)
+                out[r, k] = value * 2.0 ** (int(scales[r, k // 32]) - 127)
+    return out
+
+
+def test_configuration0_formula_against_brute_force():
+    """expert_reference_stages (BASELINE configuration 0's formula) against an element-by-element
+    restatement on a tiny expert: W1 and W3 kept apart, W2 applied to h (not to g or u), K and rows not
+    transposed, the route weight on h."""
+    rng = np.random.default_rng(11)
+    hidden, inter = 64, 32
+    arrays = mxfp4_expert(rng, hidden, inter, scale_lo=124, scale_hi=129)
+    x = activations(rng, 2, hidden)
+    route = np.array([0.5, 2.0], np.float32)
+    ref = expert_reference_stages(x, arrays, route)
+    xv = bf16_values(bf16_bits(x)).astype(np.float64)
+    w1 = _brute_dequant(arrays["w1_weight"], arrays["w1_scale"])
+    w3 = _brute_dequant(arrays["w3_weight"], arrays["w3_scale"])
+    w2 = _brute_dequant(arrays["w2_weight"], arrays["w2_scale"])
+    for t in range(2):
+        g = [sum(w1[i, k] * xv[t, k] for k in range(hidden)) for i in range(inter)]
+        u = [sum(w3[i, k] * xv[t, k] for k in range(hidden)) for i in range(inter)]
+        h = [g[i] / (1.0 + np.exp(-g[i])) * u[i] * float(route[t]) for i in range(inter)]
+        y = [sum(w2[o, i] * h[i] for i in range(inter)) for o in range(hidden)]
+        np.testing.assert_allclose(ref["g"][t], g, rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(ref["u"][t], u, rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(ref["h"][t], h, rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(ref["y"][t], y, rtol=1e-10, atol=1e-12)
