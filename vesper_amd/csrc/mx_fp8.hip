@@ -25,6 +25,7 @@
 namespace {
 
 using mxd::ldg128;
+using mxd::ldg128_nt;
 using mxd::ldg32;
 using mxd::ldgf;
 using mxd::mfma_fp8_fp8;
@@ -158,8 +159,10 @@ struct Fp8Args {
 // the B operand and the activation scale from there. Saves the quantizer launch for decode-size calls;
 // at 16 tokens the repeated quantization in every workgroup costs more than the launch (measured).
 constexpr int kFusedMaxTokens = 4;
-constexpr int kFusedChunks = 8;
+constexpr int kFusedChunks = 16;
 constexpr int kFusedRow = 144;
+// the 16 lane groups of 16 threads quantize kFusedMaxTokens blocks each: every (token, chunk) block
+static_assert(16 * kFusedMaxTokens >= kFusedMaxTokens * kFusedChunks, "fused quantization leaves blocks out");
 
 template <int kBlock>
 struct Fp8Chunk {
@@ -175,10 +178,12 @@ template <int kBlock, bool kFused>
 __device__ __forceinline__ void fp8_load(Fp8Chunk<kBlock>& r, const Fp8Args& a, const uint8_t* wlane,
                                          const uint8_t* slane, const float* swrow, const uint8_t* xrow,
                                          const uint8_t* xsrow, int c, int q) {
+  // weights: non-temporal loads (each byte is read once per call); 48.8 against 53.0 us for the
+  // configuration-3 projections at T = 1 with plain loads (MI355X)
 #pragma unroll
   for (int t = 0; t < kTiles; ++t) {
-    r.a[t][0] = ldg128(wlane + (size_t)c * 8192 + t * 2048);
-    r.a[t][1] = ldg128(wlane + (size_t)c * 8192 + t * 2048 + 1024);
+    r.a[t][0] = ldg128_nt(wlane + (size_t)c * 8192 + t * 2048);
+    r.a[t][1] = ldg128_nt(wlane + (size_t)c * 8192 + t * 2048 + 1024);
   }
   r.c = c;
   if constexpr (kFused) {
@@ -202,10 +207,10 @@ template <int kBlock, bool kFused>
 __device__ __forceinline__ void fp8_mma(Fp8Chunk<kBlock> r, v4f (&acc)[kTiles], int q, uint32_t keep,
                                         const uint8_t* qrow, const float* qs, int cb) {
   if constexpr (kFused) {
-    const uint8_t* row = qrow + (size_t)(r.c - cb) * kTok * kFusedRow;
+    const uint8_t* row = qrow + (size_t)(r.c - cb) * kFusedMaxTokens * kFusedRow;
     r.b0 = *reinterpret_cast<const uint4*>(row + 16 * q);
     r.b1 = *reinterpret_cast<const uint4*>(row + 64 + 16 * q);
-    r.sx = __float_as_uint(qs[(r.c - cb) * kTok]);
+    r.sx = __float_as_uint(qs[(r.c - cb) * kFusedMaxTokens]);
   }
   const uint4 b0 = make_uint4(r.b0.x & keep, r.b0.y & keep, r.b0.z & keep, r.b0.w & keep);
   const uint4 b1 = make_uint4(r.b1.x & keep, r.b1.y & keep, r.b1.z & keep, r.b1.w & keep);
@@ -271,8 +276,8 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
   const int cn = cb + (cw * (wave + 1)) / 4 - c0;
   // fused: this workgroup's quantized activations, [chunk][token] rows (tokens past T read token ntok - 1's
   // row: finite scale, codes masked at the MFMA)
-  __shared__ __attribute__((aligned(16))) uint8_t qx[kFused ? kFusedChunks * kTok * kFusedRow : 16];
-  __shared__ float qsc[kFused ? kFusedChunks * kTok : 1];
+  __shared__ __attribute__((aligned(16))) uint8_t qx[kFused ? kFusedChunks * kFusedMaxTokens * kFusedRow : 16];
+  __shared__ float qsc[kFused ? kFusedChunks * kFusedMaxTokens : 1];
   const int ntok = min(kTok, a.T - (int)blockIdx.y * kTok);
   const int nq = min(n, ntok - 1);
   const int sub = tid & 15, grp = tid >> 4;
@@ -315,7 +320,7 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
         uint2 codes;
         codes.x = mxd::e4m3x4(v[0] / sc, v[1] / sc, v[2] / sc, v[3] / sc);
         codes.y = mxd::e4m3x4(v[4] / sc, v[5] / sc, v[6] / sc, v[7] / sc);
-        const int slot = (bi % cw) * kTok + bi / cw;
+        const int slot = (bi % cw) * kFusedMaxTokens + bi / cw;
         *reinterpret_cast<uint2*>(qx + slot * kFusedRow + 8 * sub) = codes;
         if (sub == 0) qsc[slot] = sc;
       }
@@ -646,12 +651,13 @@ int fp8_splits(int N, int K, int T) {
     if (base_wgs >= 128) return 1;
     return std::max(1, std::min({8, (K / 128) / 8, (512 + base_wgs - 1) / base_wgs}));
   }
-  // GEMV: every workgroup streams about 8 chunks of its row group -- at most kFusedChunks when the call
-  // may quantize its own activations (up to kFusedMaxTokens tokens), at least 8 otherwise -- and at most 16
-  // splits. Fewer, longer workgroups measured faster than a fixed workgroup count on MI355X (us per call,
-  // T = 1 / 16): 2112 x 7168 7 splits 11.3 / 13.1 against 14 splits (the former ~512-workgroup rule) 12.5 /
-  // 16.9; 7168 x 16384 16 splits 28.9 / 33.8 against 5 splits 30.1 / 33.3; 24576 x 1536 1 split 14.1 / 14.5
-  // against 2 splits 13.7 / 16.3, so few tokens keep 2 splits (the fused quantizer needs <= 8 chunks).
+  // GEMV: up to kFusedMaxTokens tokens (the call may quantize its own activations) every workgroup takes
+  // up to kFusedChunks = 16 chunks of its row group, else about 8; at most 16 splits. Fewer, longer
+  // workgroups measured faster than a fixed workgroup count on MI355X (us per call, T = 1 / 16): 2112 x 7168
+  // 7 splits 11.3 / 13.1 against 14 splits (the former ~512-workgroup rule) 12.5 / 16.9; 7168 x 16384 16
+  // splits 28.9 / 33.8 against 5 splits 30.1 / 33.3. At T = 1 with non-temporal weight loads: 24576 x 1536
+  // unsplit 10.3 us against 12.5 us with 2 splits (no split-K handoff); 2112 x 7168 4 splits 10.4 us, 7168 x
+  // 16384 8 splits 26.6 us, both as with 7 and 16.
   const int chunks = K / 128;
   const int s = T <= kFusedMaxTokens ? (chunks + kFusedChunks - 1) / kFusedChunks : chunks / 8;
   return std::max(1, std::min(16, s));
