@@ -136,9 +136,19 @@ def test_exact_through_the_split_k_gemm(block):
 @pytest.mark.parametrize("block", [32, 128])
 @pytest.mark.parametrize("tokens,rows,width", [(33, 64, 128), (129, 64, 256), (33, 192, 384), (257, 128, 128)])
 def test_exact_gemm_edges(block, tokens, rows, width):
-    """The GEMM's 3-stage LDS ring at its edges: one K chunk (the copies issued ahead repeat it), a single
-    64-row group in a 256-row workgroup, token counts just past the GEMV's limit and a partial last tile."""
+    """The GEMM's 3-stage LDS ring at its edges: one K chunk (nothing copied ahead), a single 64-row group
+    in a 256-row workgroup, token counts just past the GEMV's limit and a partial last tile."""
     w, sw, x = exact_case(block, tokens, rows, width, 8, 16, 1000 * block + tokens + rows + width)
+    check_exact(block, w, sw, x)
+
+
+@pytest.mark.parametrize("block", [32, 128])
+@pytest.mark.parametrize("tokens,rows,width,wmax,xmax", [(512, 320, 640, 8, 16), (600, 64, 128, 8, 16),
+                                                         (777, 192, 2048, 1, 2)])
+def test_exact_long_batches(block, tokens, rows, width, wmax, xmax):
+    """Several 128-token tiles: a partial last row tile, one K chunk with a single 64-row group and a
+    partial last token tile, and K = 2048 split in two."""
+    w, sw, x = exact_case(block, tokens, rows, width, wmax, xmax, 3000 * block + tokens + rows + width)
     check_exact(block, w, sw, x)
 
 

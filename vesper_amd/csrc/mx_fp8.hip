@@ -451,27 +451,33 @@ __global__ void fp8_splitk_reduce_kernel(const float* __restrict__ partial, int 
 
 // ---- GEMM for many tokens ------------------------------------------------------------------------
 //
-// grid (ceil(N / 256), ceil(T / 128), K splits), 512 threads = 8 waves. Wave w owns the 64-row group
-// 4 * blockIdx.x + (w % 4) and the token half w / 4 (64 tokens = 4 MFMA column tiles), accumulating
-// 4 row tiles x 4 token tiles of 16 x 16. Every operand of a 128-wide K chunk reaches LDS by direct
-// global->LDS copies (no registers) into a 3-stage ring: the 4 row groups' weight chunks (32 KB, copied
-// 1 KB per wave instruction in the tiled blob's MFMA operand order, so both token halves read the
-// weights from LDS), the 128 tokens' activation codes (16 KB, block 2u + h holding at lane (q, n) the
-// bytes 64h + 16q.. of token 16u + n: the MFMA B operand of token tile u), the tokens' activation
-// scales and the row groups' weight scales. Each wave issues the same 8 copies per chunk, so a step
-// waits until only the next chunk's 8 are outstanding, meets the others at a bare barrier, starts the
-// copies of the chunk two ahead and multiplies. The loop has no compiler-visible global loads, so the
-// compiler adds no vmcnt waits that would drain the ring.
+// grid (ceil(N / 256), ceil(T / 128), K splits), 768 threads = 12 waves. Waves 0-7 multiply: wave w owns
+// the 64-row group 4 * blockIdx.x + (w % 4) and the token half w / 4 (64 tokens), 4 row tiles x 4 token
+// tiles of 16 x 16. Waves 8-11 only copy operands global -> LDS (direct copies, no registers) into a
+// 3-stage ring, two chunks ahead. Measured on MI355X: a CU moves at most 64 bytes per clock from L2 into
+// LDS, and while a chunk is still on its way from HBM (the first workgroup of an XCD to ask for it, and
+// every workgroup asking at the same time) a wave issuing copies stalls for most of their latency. When
+// the multiplying waves issue the copies themselves, each 128-wide chunk takes about 2,700 clocks: the
+// stalled copies hold up the MFMAs behind them. In waves of their own the stalls hold up no MFMA, since
+// each SIMD issues from whichever of its waves is ready; the copy waves then set the pace (about 1,900
+// clocks per chunk for the o projection at T = 2048, 1,000 when every chunk is already in L2) against
+// about 1,450 for the multiplying waves. Stage layout: the 4 row groups' weight chunks
+// (32 KB, piece 8 g + 2 t + h in the tiled blob's MFMA operand order), the 128 tokens' activation codes
+// (16 KB, block 2 u + h holding at lane (q, n) bytes 64 h + 16 q .. of token 16 u + n: the B operand of
+// token tile u), their scales (512 B) and the 4 row groups' weight-scale words (1 KB, 256 B each). Step
+// c: the multiplying waves read chunk c from its stage and multiply; the copy waves issue chunk c + 2 into
+// the stage chunk c - 1 left and wait for chunk c + 1; one barrier ends the step. The loops have no
+// compiler-visible global loads (the copies are inline assembly), so the compiler adds no vmcnt waits.
 constexpr int kGemmTok = 128;                 // tokens per workgroup
-constexpr int kGemmThreads = 512;
-constexpr int kWaveTiles = 4;                 // token tiles per wave
-constexpr int kGemmStages = 3;
-constexpr int kGemmCopies = 8;                // copies per wave and chunk: 4 weight, 2 activation, 2 scale
-constexpr int kGemmA = 32768;                 // stage layout: weights,
-constexpr int kGemmB = 16384;                 //   activation codes,
-constexpr int kGemmSA = 512;                  //   activation scales (4 bytes per token),
-constexpr int kGemmSW = 2048;                 //   weight scales (256 bytes per wave)
+constexpr int kWaveTiles = 4;                 // token tiles per multiplying wave
+constexpr int kGemmThreads = 768;
+constexpr int kGemmA = 32768;
+constexpr int kGemmB = 16384;
+constexpr int kGemmSA = 512;
+constexpr int kGemmSW = 1024;
 constexpr int kGemmStage = kGemmA + kGemmB + kGemmSA + kGemmSW;
+constexpr int kGemmStages = 3;
+constexpr int kGemmCopies = 14;   // per copy wave and chunk: 8 weight, 4 activation, 1 + 1 scale
 static_assert(kGemmStages * kGemmStage <= 160 * 1024, "GEMM LDS ring");
 
 template <int kBlock>
@@ -480,138 +486,125 @@ __global__ __launch_bounds__(kGemmThreads) void fp8_gemm_kernel(Fp8Args a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q = lane >> 4, n = lane & 15;
-  // split K (grid z): this workgroup's chunks [c0, c0 + C)
   const int chunks = a.K / 128, per = (chunks + gridDim.z - 1) / gridDim.z;
   const int c0 = blockIdx.z * per;
   const int C = min(per, chunks - c0);
   const int groups = a.N / 64;
-  const int g_raw = blockIdx.x * 4 + (wave & 3);
+  const int bx = blockIdx.x;
+  const int m0 = blockIdx.y * kGemmTok;
+  const Fp8Blob off = fp8_blob(a.N, a.K, kBlock);
+  const uint32_t lds0 = mxd::lds_addr(lds);
+
+  if (wave >= 8) {
+    // copy wave p: row group p's 8 weight pieces and scale word(s), activation tiles 2p and 2p + 1 (both
+    // blocks of each), the scales of tokens 32p .. 32p + 31. Rows past N and tokens past T repeat valid ones.
+    const int p = wave - 8;
+    const int gp = min(bx * 4 + p, groups - 1);
+    const uint8_t* wsrc = a.blob + (size_t)gp * chunks * 8192 + 16 * lane;
+    const uint8_t* bsrc0 = a.xq + (size_t)min(m0 + 32 * p + n, a.T - 1) * a.K + 16 * q;
+    const uint8_t* bsrc1 = a.xq + (size_t)min(m0 + 32 * p + 16 + n, a.T - 1) * a.K + 16 * q;
+    const int stok = min(m0 + 32 * p + (lane & 31), a.T - 1);
+    const uint8_t* sasrc = kBlock == 32 ? (const uint8_t*)a.xs + (size_t)stok * (a.K / 32)
+                                        : (const uint8_t*)a.xs + (size_t)stok * chunks * 4;
+    const uint8_t* swsrc = kBlock == 32 ? a.blob + off.scales + (size_t)gp * chunks * 256 + 4 * lane
+                                        : a.blob + off.scales + ((size_t)((64 * gp) / 128) * chunks) * 4;
+    auto copy = [&](int cl) {
+      const int c = c0 + cl;
+      const uint32_t st = lds0 + (uint32_t)(cl % kGemmStages) * kGemmStage;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        mxd::global_to_lds16(wsrc + (size_t)c * 8192 + i * 1024, __builtin_amdgcn_readfirstlane(st + (8 * p + i) * 1024));
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        mxd::global_to_lds16(bsrc0 + (size_t)c * 128 + 64 * h,
+                             __builtin_amdgcn_readfirstlane(st + kGemmA + (4 * p + h) * 1024));
+        mxd::global_to_lds16(bsrc1 + (size_t)c * 128 + 64 * h,
+                             __builtin_amdgcn_readfirstlane(st + kGemmA + (4 * p + 2 + h) * 1024));
+      }
+      const uint32_t sa_lds = __builtin_amdgcn_readfirstlane(st + kGemmA + kGemmB + 128 * p);
+      if (lane < 32) mxd::global_to_lds4(sasrc + (size_t)c * 4, sa_lds);
+      const uint32_t sw_lds = __builtin_amdgcn_readfirstlane(st + kGemmA + kGemmB + kGemmSA + 256 * p);
+      if (kBlock == 32 || lane == 0) mxd::global_to_lds4(swsrc + (size_t)c * (kBlock == 32 ? 256 : 4), sw_lds);
+    };
+    copy(0);
+    if (C > 1) {
+      copy(1);
+      __builtin_amdgcn_s_waitcnt(mxd::vm_wait_imm(kGemmCopies));
+    } else {
+      __builtin_amdgcn_s_waitcnt(mxd::vm_wait_imm(0));
+    }
+    mxd::copy_barrier();
+    for (int c = 0; c < C; ++c) {
+      if (c + 2 < C) {
+        copy(c + 2);
+        __builtin_amdgcn_s_waitcnt(mxd::vm_wait_imm(kGemmCopies));   // chunk c + 1 has landed
+      } else {
+        __builtin_amdgcn_s_waitcnt(mxd::vm_wait_imm(0));
+      }
+      mxd::copy_barrier();
+    }
+    return;
+  }
+
+  const int g_raw = bx * 4 + (wave & 3);
   const bool has_rows = g_raw < groups;
   const int g = has_rows ? g_raw : groups - 1;
   const int u0 = (wave >> 2) * kWaveTiles;
-  const int m0 = blockIdx.y * kGemmTok;
-  const Fp8Blob off = fp8_blob(a.N, a.K, kBlock);
-
-  // this wave's copies: weight pieces 4 wave .. 4 wave + 3 (row group wave / 2, pieces 4 (wave % 2) ..),
-  // activation blocks 2 wave, 2 wave + 1 (token tile wave), the scales of tokens 16 wave .. 16 wave + 15,
-  // and its own row group's weight scales. Rows past N and tokens past T repeat valid ones.
-  const int ga = min(blockIdx.x * 4 + (wave >> 1), groups - 1);
-  const uint8_t* wsrc = a.blob + (size_t)ga * chunks * 8192 + (size_t)(4 * (wave & 1)) * 1024 + 16 * lane;
-  const int btok = min(m0 + 16 * wave + n, a.T - 1);
-  const uint8_t* bsrc = a.xq + (size_t)btok * a.K + 16 * q;
-  const int stok = min(m0 + 16 * wave + (lane & 15), a.T - 1);
-  const uint8_t* sasrc = kBlock == 32 ? (const uint8_t*)a.xs + (size_t)stok * (a.K / 32)
-                                      : (const uint8_t*)a.xs + (size_t)stok * chunks * 4;
-  const uint8_t* swsrc = kBlock == 32 ? a.blob + off.scales + (size_t)g * chunks * 256 + 4 * lane
-                                      : a.blob + off.scales + ((size_t)((64 * g) / 128) * chunks) * 4;
-  const uint32_t lds0 = mxd::lds_addr(lds);
-  auto copy = [&](int cl) {
-    const int c = c0 + min(cl, C - 1);   // past the end: repeats of the last chunk, so the count stays fixed
-    const uint32_t st = lds0 + (uint32_t)(cl % kGemmStages) * kGemmStage;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      mxd::global_to_lds16(wsrc + (size_t)c * 8192 + i * 1024, __builtin_amdgcn_readfirstlane(st + (4 * wave + i) * 1024));
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      mxd::global_to_lds16(bsrc + (size_t)c * 128 + 64 * h,
-                           __builtin_amdgcn_readfirstlane(st + kGemmA + (2 * wave + h) * 1024));
-    const uint32_t sa_lds = __builtin_amdgcn_readfirstlane(st + kGemmA + kGemmB + 64 * wave);
-    if (lane < 16) mxd::global_to_lds4(sasrc + (size_t)c * 4, sa_lds);
-    const uint32_t sw_lds = __builtin_amdgcn_readfirstlane(st + kGemmA + kGemmB + kGemmSA + 256 * wave);
-    if (kBlock == 32 || lane == 0) mxd::global_to_lds4(swsrc + (size_t)c * (kBlock == 32 ? 256 : 4), sw_lds);
-  };
-
   v4f acc[kTiles][kWaveTiles];
 #pragma unroll
   for (int t = 0; t < kTiles; ++t)
 #pragma unroll
     for (int u = 0; u < kWaveTiles; ++u) acc[t][u] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  // One chunk's operands in registers: read from LDS one chunk ahead of their MFMAs, so the reads of chunk
-  // c + 1 are in flight while chunk c multiplies (the waves of a SIMD reach the per-chunk barrier together,
-  // so neither can cover the other's LDS latency).
-  struct Ops {
-    uint4 am[kTiles][2];
-    uint4 b[kWaveTiles][2];
-    uint32_t sx[kWaveTiles];
-    uint32_t swv;
-  };
-  auto read_ops = [&](Ops& o, int cl) {
-    const uint8_t* st = lds + (cl % kGemmStages) * kGemmStage;
+  mxd::copy_barrier();
+  for (int c = 0; c < C; ++c) {
+    const uint8_t* st = lds + (c % kGemmStages) * kGemmStage;
+    uint4 am[kTiles][2], b[kWaveTiles][2];
+    float sx[kWaveTiles];
 #pragma unroll
     for (int t = 0; t < kTiles; ++t)
 #pragma unroll
       for (int h = 0; h < 2; ++h)
-        o.am[t][h] = *reinterpret_cast<const uint4*>(st + (8 * (wave & 3) + 2 * t + h) * 1024 + 16 * lane);
+        am[t][h] = *reinterpret_cast<const uint4*>(st + (8 * (wave & 3) + 2 * t + h) * 1024 + 16 * lane);
 #pragma unroll
     for (int u = 0; u < kWaveTiles; ++u) {
       const int tile = u0 + u;
-      o.b[u][0] = *reinterpret_cast<const uint4*>(st + kGemmA + (2 * tile) * 1024 + 16 * lane);
-      o.b[u][1] = *reinterpret_cast<const uint4*>(st + kGemmA + (2 * tile + 1) * 1024 + 16 * lane);
-      o.sx[u] = *reinterpret_cast<const uint32_t*>(st + kGemmA + kGemmB + 4 * (16 * tile + n));
+      b[u][0] = *reinterpret_cast<const uint4*>(st + kGemmA + (2 * tile) * 1024 + 16 * lane);
+      b[u][1] = *reinterpret_cast<const uint4*>(st + kGemmA + (2 * tile + 1) * 1024 + 16 * lane);
+      sx[u] = *reinterpret_cast<const float*>(st + kGemmA + kGemmB + 4 * (16 * tile + n));
     }
-    o.swv = *reinterpret_cast<const uint32_t*>(st + kGemmA + kGemmB + kGemmSA + 256 * wave +
-                                               (kBlock == 32 ? 4 * lane : 0));
-  };
-  auto multiply = [&](const Ops& o) {
+    const uint32_t swv = *reinterpret_cast<const uint32_t*>(st + kGemmA + kGemmB + kGemmSA + 256 * (wave & 3) +
+                                                            (kBlock == 32 ? 4 * lane : 0));
     if constexpr (kBlock == 32) {
 #pragma unroll
       for (int u = 0; u < kWaveTiles; ++u) {
-        const int sxb = (int)((o.sx[u] >> (8 * q)) & 0xFF);
+        const int sxb = (int)((__float_as_uint(sx[u]) >> (8 * q)) & 0xFF);
 #pragma unroll
         for (int t = 0; t < kTiles; ++t)
-          acc[t][u] = mfma_fp8_fp8(o.am[t][0], o.am[t][1], o.b[u][0], o.b[u][1], acc[t][u],
-                                   (int)((o.swv >> (8 * t)) & 0xFF), sxb);
+          acc[t][u] = mfma_fp8_fp8(am[t][0], am[t][1], b[u][0], b[u][1], acc[t][u], (int)((swv >> (8 * t)) & 0xFF),
+                                   sxb);
       }
     } else {
-      // Per chunk the MFMA gives the block dot d (unit scales) and acc = fma(d, f32(sa * sw), acc) follows in
-      // FP32: one rounding per output. MFMA k + 1 is issued before the 4 fused multiply-adds that scale MFMA k,
-      // so they run while it executes; the scheduling fences keep the compiler from pairing each MFMA with its
-      // own scaling instead (which waits for every result).
-      const float swf = __uint_as_float(o.swv);
+      const float swf = __uint_as_float(swv);
       constexpr int kSteps = kTiles * kWaveTiles;
       v4f d[2];
-      d[0] = mfma_fp8_fp8(o.am[0][0], o.am[0][1], o.b[0][0], o.b[0][1], v4f{0.f, 0.f, 0.f, 0.f}, 127, 127);
+      d[0] = mfma_fp8_fp8(am[0][0], am[0][1], b[0][0], b[0][1], v4f{0.f, 0.f, 0.f, 0.f}, 127, 127);
 #pragma unroll
       for (int k = 0; k < kSteps; ++k) {
         const int t = k % kTiles, u = k / kTiles;
         if (k + 1 < kSteps) {
           const int t1 = (k + 1) % kTiles, u1 = (k + 1) / kTiles;
-          d[(k + 1) & 1] = mfma_fp8_fp8(o.am[t1][0], o.am[t1][1], o.b[u1][0], o.b[u1][1], v4f{0.f, 0.f, 0.f, 0.f},
-                                        127, 127);
+          d[(k + 1) & 1] = mfma_fp8_fp8(am[t1][0], am[t1][1], b[u1][0], b[u1][1], v4f{0.f, 0.f, 0.f, 0.f}, 127, 127);
         }
         __builtin_amdgcn_sched_barrier(0);
-        const float sc = __uint_as_float(o.sx[u]) * swf;
+        const float sc = sx[u] * swf;
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[t][u][i] = fmaf(d[k & 1][i], sc, acc[t][u][i]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-  };
-
-  // Step c: chunk c + 1's copies are done once only chunk c + 2's are outstanding, and this wave's reads of
-  // chunk c have landed; the barrier then covers every wave, so chunk c's stage can take the copies of chunk
-  // c + 3 while chunk c + 1's operands are read and chunk c multiplies.
-  auto step = [&](int c, const Ops& cur, Ops& next) {
-    __builtin_amdgcn_s_waitcnt(mxd::vm_wait_imm(kGemmCopies * (kGemmStages - 2)));
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0), vmcnt and expcnt left at their maxima
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's reads of chunk c are done
     mxd::copy_barrier();
-    copy(c + kGemmStages);
-    read_ops(next, c + 1);
-    multiply(cur);
-  };
-#pragma unroll
-  for (int j = 0; j < kGemmStages; ++j) copy(j);
-  __builtin_amdgcn_s_waitcnt(mxd::vm_wait_imm(kGemmCopies * (kGemmStages - 1)));
-  mxd::copy_barrier();
-  Ops ops0, ops1;
-  read_ops(ops0, 0);
-  for (int c = 0; c < C; c += 2) {
-    step(c, ops0, ops1);
-    if (c + 1 < C) step(c + 1, ops1, ops0);
   }
-  // every copy must land before the workgroup ends (its LDS may be handed to another workgroup)
-  __builtin_amdgcn_s_waitcnt(mxd::vm_wait_imm(0));
   if (!has_rows) return;
 #pragma unroll
   for (int u = 0; u < kWaveTiles; ++u) {
@@ -724,7 +717,6 @@ int launch_fp8_product(const uint8_t* blob, int N, int K, int block, const uint8
     const dim3 grid((N / 64 + 3) / 4, (T + kGemmTok - 1) / kGemmTok, splits);
     if (block == 32) hipLaunchKernelGGL(fp8_gemm_kernel<32>, grid, dim3(kGemmThreads), 0, st, a);
     else hipLaunchKernelGGL(fp8_gemm_kernel<128>, grid, dim3(kGemmThreads), 0, st, a);
-    MX_LAUNCH_CHECK("fp8_gemm_kernel");
     if (splits > 1) {
       const int64_t count = (int64_t)T * N;
       hipLaunchKernelGGL(fp8_splitk_reduce_kernel, dim3((unsigned)((count / 4 + 255) / 256)), dim3(256), 0, st,
