@@ -7,11 +7,12 @@
 //   plan      count pairs per expert, expert-major row offsets (shared expert last) and 128-row tiles;
 //             a stable per-expert scatter gives each expert's rows in ascending token order
 //             (participation, src/vesper/moe.py:18-30) and each (token, rank) pair its row
-//   gate/up   grid (ceil(I/256), tiles), 8 waves: 8 groups of 32 intermediate rows (W1 + W3 interleaved
-//             per MFMA tile, as in the tiled layout), each wave one group for all 128 tokens of the tile;
-//             the tokens' E4M3 rows are copied global -> LDS per 128-wide K chunk; epilogue SwiGLU +
-//             route weight + the per-token quantization of each 32-row block of the down input
-//   down      grid (ceil(H/512), tiles), 8 waves over 64-row groups of W2 with the tile's contiguous
+//   gate/up   grid (ceil(I/256), tiles), 8 multiplying waves: 8 groups of 32 intermediate rows (W1 + W3
+//             interleaved per MFMA tile, as in the tiled layout), each wave one group for all 128 tokens of
+//             the tile; 4 copy waves bring each 128-wide K chunk of the weights and of the tokens' E4M3
+//             rows global -> LDS; epilogue SwiGLU + route weight + the per-token quantization of each
+//             32-row block of the down input
+//   down      grid (ceil(H/512), tiles), the same over 64-row groups of W2 with the tile's contiguous
 //             down-input rows
 //   combine   per token: its expert rows in ascending expert ID, then the shared row; FP32 from +0,
 //             one BF16 rounding (aggregation_probe.cu:4-25). The down GEMM writes each row to the
@@ -204,67 +205,58 @@ using mxd::global_to_lds4;
 using mxd::lds_addr;
 using mxd::vm_wait_imm;
 
-// Two 16-token tiles' MFMA B operands (per tile two 16-byte reads 1 KB apart, the tiles' blocks being
-// consecutive) and their scale bytes (saddr: this lane's byte of tile u's scale words, +64 for u + 1),
-// read from LDS and waited for. Inline assembly: for compiler-visible
-// LDS reads the compiler cannot tell which global->LDS copies they depend on and waits for all of them
-// (vmcnt(0)), draining the copies in flight for later chunks; the caller's explicit vmcnt wait before the
-// barrier orders these reads after the copies they read.
-__device__ __forceinline__ void lds_read_b2(uint32_t addr, uint32_t saddr, uint4 (&b)[4], uint32_t (&sw)[2]) {
-  mxd::u32x4_t x0, x1, x2, x3;
-  uint32_t s0, s1;
+// One 16-token tile's MFMA B operand (two 16-byte reads 1 KB apart) and its scale byte (saddr: this lane's
+// byte of the tile's scale words), read from LDS and waited for. Inline assembly: for compiler-visible LDS
+// reads the compiler cannot tell which global->LDS copies they depend on and waits for all of them.
+__device__ __forceinline__ void lds_read_b1(uint32_t addr, uint32_t saddr, uint4 (&b)[2], uint32_t& sw) {
+  mxd::u32x4_t x0, x1;
+  uint32_t s0;
   asm volatile(
-      "ds_read_b128 %0, %6\n\t"
-      "ds_read_b128 %1, %6 offset:1024\n\t"
-      "ds_read_b128 %2, %6 offset:2048\n\t"
-      "ds_read_b128 %3, %6 offset:3072\n\t"
-      "ds_read_u8 %4, %7\n\t"
-      "ds_read_u8 %5, %7 offset:64\n\t"
+      "ds_read_b128 %0, %3\n\t"
+      "ds_read_b128 %1, %3 offset:1024\n\t"
+      "ds_read_u8 %2, %4\n\t"
       "s_waitcnt lgkmcnt(0)"
-      : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3), "=&v"(s0), "=&v"(s1)
+      : "=&v"(x0), "=&v"(x1), "=&v"(s0)
       : "v"(addr), "v"(saddr));
   b[0] = uint4{x0.x, x0.y, x0.z, x0.w};
   b[1] = uint4{x1.x, x1.y, x1.z, x1.w};
-  b[2] = uint4{x2.x, x2.y, x2.z, x2.w};
-  b[3] = uint4{x3.x, x3.y, x3.z, x3.w};
-  sw[0] = s0;
-  sw[1] = s1;
+  sw = s0;
 }
 
-constexpr int kGThreads = 512;   // 8 waves (two per SIMD), one 64-row group of the weights each
-constexpr int kStages = 5;       // activation chunks in LDS: chunk c + 4 is copied in while chunk c multiplies
-constexpr int kADepth = 3;       // weight chunks per wave in registers: chunk c + 3 loads after chunk c
-constexpr int kBCopies = 3;      // per wave and chunk: 2 activation blocks + 1 block of scale words
-constexpr int kALoads = 5;       // per wave and chunk: 4 weight tiles + 1 scale word
-// a stage: 16 activation blocks of 1 KB, then 512 scale words (wave w writes words 64w.., rows 64w +
-// lane; only the first 128 are read)
-constexpr int kStageSB = 16384, kStageBytes = 18432;
+constexpr int kGThreads = 768;   // 8 multiplying waves (two per SIMD, one 64-row group each) + 4 copy waves
+constexpr int kStages = 3;       // operand chunks in LDS: chunk c + 2 is copied in while chunk c multiplies
+constexpr int kCopies = 15;      // per copy wave and chunk: 8 weight pieces, 2 weight-scale, 4 activation,
+                                 // 1 activation-scale copies
+// a stage: the 8 groups' weight tiles (group w, tile t at 1 KB x (4 w + t)), their scale words (256 B per
+// group), the 16 activation blocks of 1 KB, then the 128 rows' activation scale words
+constexpr int kStageA = 0, kStageAS = 32768, kStageB = 34816, kStageBS = 51200, kStageBytes = 51712;
 // epilogue tiles in the same LDS: gate and up [128][kEpiRowG] BF16, or the down output [128][kEpiRowD]
 constexpr int kEpiRowG = 256 + 8, kEpiRowD = 512 + 8;
-constexpr int kLdsBytes = 2 * kTileRows * kEpiRowG * 2;
-static_assert(kStages * kStageBytes <= kLdsBytes && kTileRows * kEpiRowD * 2 <= kLdsBytes, "LDS layout");
+constexpr int kLdsBytes = kStages * kStageBytes;
+static_assert(kLdsBytes <= 160 * 1024 && 2 * kTileRows * kEpiRowG * 2 <= kLdsBytes && kTileRows * kEpiRowD * 2 <= kLdsBytes,
+              "LDS layout");
 
 // Grouped GEMM over one 128-row tile of one slot. kGateUp: A = W1/W3 tiles (a group = 32 intermediate
 // rows of W1 and 32 of W3 as the tiled layout interleaves them, 64 MFMA rows), B = the tile's gathered
 // token rows of xq; else A = W2 tiles (a group = 64 hidden rows), B = the tile's rows of dq. Grid x covers
 // the groups eight per workgroup (ceil(I / 256) gate/up, ceil(H / 512) down), grid y the tiles.
 //
-// Each wave keeps its 64 x 128 output block in 128 accumulator registers and fits in 256 registers, so
-// two waves share a SIMD and one's waits are covered by the other's MFMAs. The weights stream into a
-// register ring kADepth chunks deep. The activations go global -> LDS without registers (global_load_lds,
-// 16 bytes a lane) as 16 blocks of 1 KB per chunk, block 2u + h holding at lane (q, n) the bytes 64h +
-// 16q.. of row 16u + n, which is exactly the MFMA B operand of lane (q, n) for token tile u, so every LDS
-// read is one linear 1 KB wave access. A step: wait for chunk c's activation copies (this wave's) and a
-// barrier (everyone's copies, and everyone done with the stage chunk c + 4 overwrites), start chunk
-// c + 4's copies, multiply chunk c, load chunk c + 3's weights into the register slot chunk c used. Every
-// step issues the same loads (past the end, repeats of chunk C - 1), so the count of operations issued
-// after chunk c's copies is never below kBCopies (kStages - 2) + kALoads kADepth (the first step's).
+// Waves 0-7 multiply: each keeps its 64 x 128 output block in 128 accumulator registers. Waves 8-11 only
+// copy every operand of a 128-wide K chunk global -> LDS without registers (global_load_lds, 16 bytes a
+// lane) into a 3-stage ring: the weight tiles as stored in the tiled layout (1 KB of MFMA operand per
+// lane-ordered piece), their scale words, and the activations as 16 blocks of 1 KB, block 2u + h holding
+// at lane (q, n) the bytes 64h + 16q.. of row 16u + n, which is exactly the MFMA B operand of lane (q, n)
+// for token tile u, so every LDS read is one linear 1 KB wave access. A wave that issues copies stalls
+// while its copies are on their way from HBM; in waves of their own those stalls hold up no MFMA, since
+// each SIMD issues from whichever of its waves is ready. A step: the multiplying waves read chunk c from
+// its stage and multiply; the copy waves issue chunk c + 2 into the stage chunk c - 1 left and wait for
+// chunk c + 1; one barrier ends the step.
 //
 // Epilogue: the accumulators go to LDS as BF16 [token][column] and every thread then finishes whole
 // 32-column blocks of one token: gate/up SwiGLU + route weight + the block's E4M3 quantization (32 code
 // bytes and one scale byte), or 16-byte row segments of the down output.
 template <bool kGateUp>
-__global__ __launch_bounds__(kGThreads, 2) void grouped_kernel(GemmArgs a) {
+__global__ __launch_bounds__(kGThreads) void grouped_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsBytes];
   const int ti = blockIdx.y;
   if (ti >= *a.plan.n_tiles) return;
@@ -275,95 +267,110 @@ __global__ __launch_bounds__(kGThreads, 2) void grouped_kernel(GemmArgs a) {
   const int q = lane >> 4, n = lane & 15;
   const int K = kGateUp ? a.H : a.I;
   const int C = K / 128;
-  // a wave past the last group (I / 32 or H / 64 groups) still copies its share of the activations and
-  // loads repeats of the last group's weights, but computes and stores nothing
+  // a multiplying wave past the last group (I / 32 or H / 64 groups) computes and stores nothing
   const int groups = kGateUp ? a.I / 32 : a.H / 64;
   const int g = blockIdx.x * 8 + wave;
-  const bool active = g < groups;
-  const int gl = min(g, groups - 1);
+  const bool active = wave < 8 && g < groups;
   const uint8_t* blob = a.tiles[slot];
   const TiledOffsets off = tiled_offsets(a.H, a.I);
-  const uint8_t* wl = blob + (kGateUp ? 0 : off.dn_w) + (size_t)gl * C * 4096 + 16 * lane;
-  const uint8_t* sl = blob + (kGateUp ? off.gu_s : off.dn_s) + (size_t)gl * C * 256 + 4 * lane;
   const int live_tiles = min(8, (rows + 15) / 16);
-
-  // this wave's activation blocks 2 wave + h (token tile u = wave) and scale words of rows 64 wave + lane;
-  // rows past the tile repeat its last row. The offsets fit 32 bits (the host bounds the buffers).
-  const uint8_t* bbase = kGateUp ? a.xq : a.dq;
-  const uint8_t* sbbase = kGateUp ? a.xs : a.ds;
-  const int br = row0 + min(16 * wave + n, rows - 1);
-  const uint32_t boff = (kGateUp ? (uint32_t)a.plan.sorted_tok[br] * (uint32_t)a.H : (uint32_t)br * (uint32_t)a.I) + 16 * q;
-  const int sr = row0 + min(64 * wave + lane, rows - 1);
-  const uint32_t soff = kGateUp ? (uint32_t)a.plan.sorted_tok[sr] * (uint32_t)(a.H / 32) : (uint32_t)sr * (uint32_t)(a.I / 32);
   const uint32_t lds0 = lds_addr(lds);
-  auto copy_b = [&](int c) {
-    const uint32_t st = __builtin_amdgcn_readfirstlane(lds0 + (c % kStages) * kStageBytes + 2048 * wave);
-    global_to_lds16(bbase + (size_t)c * 128 + boff, st);
-    global_to_lds16(bbase + (size_t)c * 128 + boff + 64, st + 1024);
-    global_to_lds4(sbbase + (size_t)c * 4 + soff, st - 2048 * wave + kStageSB + 256 * wave);
-  };
-  auto load_a = [&](int c, uint4 (&am)[4], uint32_t& sw) {
-#pragma unroll
-    for (int t = 0; t < 4; ++t) am[t] = ldg128(wl + (size_t)c * 4096 + t * 1024);
-    sw = ldg32(sl + (size_t)c * 256);
-  };
   v4f acc[4][8];
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
     for (int u = 0; u < 8; ++u) acc[t][u] = v4f{0.f, 0.f, 0.f, 0.f};
-  const uint32_t lb = lds0 + 16 * lane;
-  const uint32_t lsb = lds0 + kStageSB + 4 * n + q;   // byte q (K block q) of token n's scale word
-  auto compute = [&](int c, const uint4 (&am)[4], uint32_t sw) {
-    const uint32_t so = (c % kStages) * kStageBytes;
-#pragma unroll
-    for (int u = 0; u < 8; u += 2) {
-      if (u >= live_tiles) break;   // wave-uniform
-      uint4 b[4];
-      uint32_t sx[2];
-      lds_read_b2(lb + so + 2 * u * 1024, lsb + so + 64 * u, b, sx);
-      acc[0][u] = mxd::mfma_fp4_fp8_sel<0>(am[0], b[0], b[1], acc[0][u], sw, (int)sx[0]);
-      acc[1][u] = mxd::mfma_fp4_fp8_sel<1>(am[1], b[0], b[1], acc[1][u], sw, (int)sx[0]);
-      acc[2][u] = mxd::mfma_fp4_fp8_sel<2>(am[2], b[0], b[1], acc[2][u], sw, (int)sx[0]);
-      acc[3][u] = mxd::mfma_fp4_fp8_sel<3>(am[3], b[0], b[1], acc[3][u], sw, (int)sx[0]);
-      if (u + 1 < live_tiles) {
-        acc[0][u + 1] = mxd::mfma_fp4_fp8_sel<0>(am[0], b[2], b[3], acc[0][u + 1], sw, (int)sx[1]);
-        acc[1][u + 1] = mxd::mfma_fp4_fp8_sel<1>(am[1], b[2], b[3], acc[1][u + 1], sw, (int)sx[1]);
-        acc[2][u + 1] = mxd::mfma_fp4_fp8_sel<2>(am[2], b[2], b[3], acc[2][u + 1], sw, (int)sx[1]);
-        acc[3][u + 1] = mxd::mfma_fp4_fp8_sel<3>(am[3], b[2], b[3], acc[3][u + 1], sw, (int)sx[1]);
-      }
-      // pins these tiles' MFMAs before the next tiles' reads: the compiler would otherwise sink every MFMA
-      // past the last read and keep all eight tiles' operands live at once
-      asm volatile("" : "+v"(acc[0][u]), "+v"(acc[1][u]), "+v"(acc[2][u]), "+v"(acc[3][u]), "+v"(acc[0][u + 1]),
-                   "+v"(acc[1][u + 1]), "+v"(acc[2][u + 1]), "+v"(acc[3][u + 1]));
-    }
-  };
 
-  uint4 a_ring[kADepth][4];
-  uint32_t sw_ring[kADepth];
+  if (wave >= 8) {
+    // copy wave p: groups 2p and 2p + 1 (weight tiles and scale words), activation tiles 2p and 2p + 1
+    // (both blocks of each) and the scale words of rows 32p .. 32p + 31. Rows past the tile repeat its last
+    // row; groups past the last repeat it. The activation offsets fit 32 bits (the host bounds the buffers).
+    const int pw = wave - 8;
+    const uint8_t* wsrc[2];
+    const uint8_t* ssrc[2];
 #pragma unroll
-  for (int j = 0; j < kStages - 1; ++j) copy_b(min(j, C - 1));
+    for (int i = 0; i < 2; ++i) {
+      const int gi = min((int)blockIdx.x * 8 + 2 * pw + i, groups - 1);
+      wsrc[i] = blob + (kGateUp ? 0 : off.dn_w) + (size_t)gi * C * 4096 + 16 * lane;
+      ssrc[i] = blob + (kGateUp ? off.gu_s : off.dn_s) + (size_t)gi * C * 256 + 4 * lane;
+    }
+    const uint8_t* bbase = kGateUp ? a.xq : a.dq;
+    const uint8_t* sbbase = kGateUp ? a.xs : a.ds;
+    uint32_t boff[2];
 #pragma unroll
-  for (int j = 0; j < kADepth; ++j) load_a(min(j, C - 1), a_ring[j], sw_ring[j]);
-  auto step = [&](int c, int j) {
-    // chunk c's copies are done once at most this many later operations are outstanding (first step:
-    // the copies of chunks 1 .. kStages - 2 and the weight loads of chunks 0 .. kADepth - 1)
-    __builtin_amdgcn_s_waitcnt(vm_wait_imm(kBCopies * (kStages - 2) + kALoads * kADepth) & ~(15 << 8));  // + lgkmcnt(0)
+    for (int i = 0; i < 2; ++i) {
+      const int br = row0 + min(16 * (2 * pw + i) + n, rows - 1);
+      boff[i] = (kGateUp ? (uint32_t)a.plan.sorted_tok[br] * (uint32_t)a.H : (uint32_t)br * (uint32_t)a.I) + 16 * q;
+    }
+    const int sr = row0 + min(32 * pw + (lane & 31), rows - 1);
+    const uint32_t soff = kGateUp ? (uint32_t)a.plan.sorted_tok[sr] * (uint32_t)(a.H / 32) : (uint32_t)sr * (uint32_t)(a.I / 32);
+    auto copy = [&](int c) {
+      const uint32_t st = lds0 + (uint32_t)(c % kStages) * kStageBytes;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        global_to_lds16(wsrc[i >> 2] + (size_t)c * 4096 + (i & 3) * 1024,
+                        __builtin_amdgcn_readfirstlane(st + kStageA + (8 * pw + i) * 1024));
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        global_to_lds4(ssrc[i] + (size_t)c * 256, __builtin_amdgcn_readfirstlane(st + kStageAS + 256 * (2 * pw + i)));
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          global_to_lds16(bbase + (size_t)c * 128 + boff[i] + 64 * h,
+                          __builtin_amdgcn_readfirstlane(st + kStageB + (4 * pw + 2 * i + h) * 1024));
+      if (lane < 32) global_to_lds4(sbbase + (size_t)c * 4 + soff, __builtin_amdgcn_readfirstlane(st + kStageBS + 128 * pw));
+    };
+    copy(0);
+    if (C > 1) {
+      copy(1);
+      __builtin_amdgcn_s_waitcnt(vm_wait_imm(kCopies));
+    } else {
+      __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));
+    }
     copy_barrier();
-    copy_b(min(c + kStages - 1, C - 1));
-    if (active) compute(c, a_ring[j], sw_ring[j]);
-    load_a(min(c + kADepth, C - 1), a_ring[j], sw_ring[j]);
-  };
-  int base = 0;
-  for (; base + kADepth <= C; base += kADepth) {
+    for (int c = 0; c < C; ++c) {
+      if (c + 2 < C) {
+        copy(c + 2);
+        __builtin_amdgcn_s_waitcnt(vm_wait_imm(kCopies));   // chunk c + 1 has landed
+      } else {
+        __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));
+      }
+      copy_barrier();
+    }
+  } else {
+    const uint32_t la = lds0 + kStageA + 1024 * 4 * wave + 16 * lane;
+    const uint32_t las = lds0 + kStageAS + 256 * wave + 4 * lane;
+    const uint32_t lb = lds0 + kStageB + 16 * lane;
+    const uint32_t lsb = lds0 + kStageBS + 4 * n + q;   // byte q (K block q) of token n's scale word
+    copy_barrier();
+    for (int c = 0; c < C; ++c) {
+      const uint32_t so = (c % kStages) * kStageBytes;
+      if (active) {
+        uint4 am[4];
 #pragma unroll
-    for (int j = 0; j < kADepth; ++j) step(base + j, j);
+        for (int t = 0; t < 4; ++t)
+          am[t] = *reinterpret_cast<const uint4*>(lds + (la - lds0) + so + 1024 * t);
+        const uint32_t sw = *reinterpret_cast<const uint32_t*>(lds + (las - lds0) + so);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (u >= live_tiles) break;   // wave-uniform
+          uint4 b[2];
+          uint32_t sx;
+          lds_read_b1(lb + so + 2 * u * 1024, lsb + so + 64 * u, b, sx);
+          acc[0][u] = mxd::mfma_fp4_fp8_sel<0>(am[0], b[0], b[1], acc[0][u], sw, (int)sx);
+          acc[1][u] = mxd::mfma_fp4_fp8_sel<1>(am[1], b[0], b[1], acc[1][u], sw, (int)sx);
+          acc[2][u] = mxd::mfma_fp4_fp8_sel<2>(am[2], b[0], b[1], acc[2][u], sw, (int)sx);
+          acc[3][u] = mxd::mfma_fp4_fp8_sel<3>(am[3], b[0], b[1], acc[3][u], sw, (int)sx);
+          // pins this tile's MFMAs before the next tile's reads: the compiler would otherwise sink every MFMA
+          // past the last read and keep all eight tiles' operands live at once
+          asm volatile("" : "+v"(acc[0][u]), "+v"(acc[1][u]), "+v"(acc[2][u]), "+v"(acc[3][u]));
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's reads of chunk c are done
+      copy_barrier();
+    }
   }
-#pragma unroll
-  for (int j = 0; j < kADepth - 1; ++j)
-    if (base + j < C) step(base + j, j);
-  // every copy must land before the LDS is reused below (and before it can be handed to another workgroup)
-  __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));
   __syncthreads();
 
   if constexpr (kGateUp) {
@@ -453,11 +460,11 @@ __global__ __launch_bounds__(kGThreads, 2) void grouped_kernel(GemmArgs a) {
     // thread tid copies segment tid % 64 of rows tid / 64 + 8 i (i < 16); their destinations are loaded
     // together first
     const int cols = min(512, a.H - 512 * (int)blockIdx.x);
-    const int seg = tid & 63, tok0 = tid >> 6;
+    const int seg = tid & 63, tok0 = tid >> 6;   // the multiplying waves' 512 threads
     int dest[kTileRows / 8];
 #pragma unroll
     for (int i = 0; i < kTileRows / 8; ++i) dest[i] = a.plan.row_dest[row0 + min(tok0 + 8 * i, rows - 1)];
-    if (8 * seg < cols) {
+    if (tid < 512 && 8 * seg < cols) {
 #pragma unroll
       for (int i = 0; i < kTileRows / 8; ++i) {
         const int tok = tok0 + 8 * i;
