@@ -5,7 +5,8 @@
 * The product: exact on designed inputs whose every partial sum is representable (both profiles), so
   the operand layouts and scale placement are pinned bit for bit; random inputs within the GEMV bar;
   configuration-3 shapes at T = 1, 16, 300 and 2048 (the GEMM and split-K branches the benchmark times,
-  sampled tokens) and the reference shapes within the north-star tolerance.
+  sampled tokens; at 2048 also on exact inputs, bit for bit) and the reference shapes within the
+  north-star tolerance.
 """
 
 import ctypes as C
@@ -105,7 +106,8 @@ def exact_case(block, tokens, rows, width, wmax, xmax, seed):
     """Small-integer codes, power-of-two scales: every partial sum is exact, so any order gives the
     same FP32 result and the trace must equal the oracle bit for bit."""
     rng = np.random.default_rng(seed)
-    w = encode_e4m3(rng.integers(-wmax, wmax + 1, (rows, width)).astype(np.float32))
+    codes = encode_e4m3(np.arange(-wmax, wmax + 1, dtype=np.float32))      # the integers' E4M3 codes
+    w = codes[rng.integers(-wmax, wmax + 1, (rows, width)) + wmax]
     if block == 32:
         sw = rng.integers(125, 130, (rows // 32, width // 32), dtype=np.uint8)
         x = rng.integers(-xmax, xmax + 1, (tokens, width)).astype(np.float32)
@@ -295,6 +297,24 @@ def test_config3_T2048_sampled_tokens_within_tolerance():
             np.testing.assert_array_equal(got["scale_f32"][sample].view(np.uint32), ref["scale"].view(np.uint32))
             assert_close(got["output_bf16"][sample], ref["output_bf16"], f"{name} T={tokens}")
             assert_gemv_close(got["output_bf16"][sample], ref["output_bf16"], f"{name} T={tokens}", min_equal=0.90)
+
+
+def test_config3_T2048_exact_sampled_tokens():
+    """The four configuration-3 shapes at 2048 tokens on exact inputs (small integer codes, power-of-two
+    scales, |sums| below 2^16 units of the smallest scale, so every partial sum is representable): the GEMM's
+    tiling, copy pipeline and K splits at the benchmark's shapes are pinned bit for bit on 64 sampled tokens,
+    tile edges included."""
+    tokens = 2048
+    rng = np.random.default_rng(20262049)
+    sample = np.unique(np.concatenate([[0, 127, 128, tokens - 1], rng.choice(tokens, 60, replace=False)]))
+    for i, (name, (rows, width)) in enumerate(CONFIG3_LAYOUT.items()):
+        w, sw, x = exact_case(128, tokens, rows, width, 1, 2, 777 + i)
+        bits = bf16_bits(x)
+        got = run_projection(128, w, sw, bits)
+        ref = fp8_projection(bf16_values(bits[sample]), w, sw, 128)
+        np.testing.assert_array_equal(got["output_fp32"][sample].view(np.uint32), ref["output_fp32"].view(np.uint32),
+                                      err_msg=name)
+        np.testing.assert_array_equal(got["output_bf16"][sample], ref["output_bf16"], err_msg=name)
 
 
 def test_reference_shapes_block32_and_refusals():
