@@ -418,7 +418,7 @@ int mx_moe_prefill(mx_layer* layer, const uint16_t* x_bf16, int32_t tokens, cons
 #define MX_BUF_WEIGHTS 4     /* float [T][k]          */
 #define MX_BUF_XQ 5          /* uint8 [T][H]          */
 #define MX_BUF_XS 6          /* uint8 [T][H/32]       */
-#define MX_BUF_PLAN 7        /* int32 plan (see DESIGN) */
+#define MX_BUF_PLAN 7        /* int32 plan: struct Plan of csrc/mx_moe.hip (slot experts, rows, tokens) */
 #define MX_BUF_W1 8          /* uint16 [rows][I]      */
 #define MX_BUF_W3 9          /* uint16 [rows][I]      */
 #define MX_BUF_DOWN_INPUT 10 /* uint16 [rows][I]      */
