@@ -3,9 +3,10 @@
 * MoEAccumulator on the device reproduces the 38 recorded official aggregation cases
   (SHA-256 of every FP32 stage and the BF16 output).
 * The decode layer: routing (indices, weights, scores) bit-exact against the oracle on the
-  kernel's own logits; every expert's epilogue and quantizers bit-exact on the kernel's own
-  GEMV outputs; the combine bit-exact on the kernel's own expert outputs; the layer output
-  within tolerance of the oracle's.
+  kernel's own logits; every expert's W1/W3 outputs and down-input codes bit-exact against the
+  oracle (the gate/up GEMVs reproduce fp4_gemv_spec's per-block rounding and order); the epilogue
+  and quantizers bit-exact on the kernel's own GEMV outputs; the combine bit-exact on the kernel's
+  own expert outputs; W2 within the GEMV bar; the layer output within tolerance of the oracle's.
 """
 
 import hashlib
@@ -100,7 +101,12 @@ def check_layer_call(layer, bank, w, arrays, x, cfg):
     ref = moe_layer(x, w, needed, shared, top_k=cfg.top_k, route_scale=cfg.route_scale,
                     score_func=cfg.score_func, swiglu_limit=cfg.swiglu_limit, logits=logits)
     for e, st in out["experts"].items():
-        assert_gemv_close(st["w1"], ref["experts"][e]["w1"], f"expert {e} w1")
+        # the gate/up GEMVs follow fp4_gemv_spec's order and rounding: W1, W3 and the down input's codes exactly
+        for name in ("w1", "w3", "down_q", "down_s"):
+            np.testing.assert_array_equal(st[name], ref["experts"][e][name], err_msg=f"expert {e} {name}")
+        # W2 sums in a K-split order (it feeds only the ordered combine): on a few hundred outputs a few percent
+        # of BF16 results land one ulp apart
+        assert_gemv_close(st["w2"], ref["experts"][e]["w2"], f"expert {e} w2", min_equal=0.95)
     assert_close(out["output_bf16"], ref["output_bf16"], "layer output")
     return out
 

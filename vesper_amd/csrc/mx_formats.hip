@@ -136,6 +136,26 @@ __global__ __launch_bounds__(256) void e4m3_pack_check_kernel(uint32_t* counts) 
   counts[tid] = bad;
 }
 
+namespace mxi {
+
+int act_quant32_scaled(mx_ctx* ctx, const uint16_t* x, uint8_t* q, uint8_t* scales, uint16_t* scaled, int64_t rows,
+                       int64_t width, hipStream_t stream) {
+  if (int st = use(ctx)) return st;
+  MX_REQUIRE(rows >= 0 && width > 0 && width % 32 == 0, "act_quant32_scaled: width must be a positive multiple of 32");
+  if (!rows) return MX_OK;
+  MX_REQUIRE(x && q && scales && scaled && ((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 7) == 0 &&
+                 ((uintptr_t)scaled & 15) == 0,
+             "act_quant32_scaled: x and scaled 16-byte, q 8-byte aligned pointers required");
+  const int64_t groups = rows * (width / 32) * 4;
+  const int64_t want = (groups + 255) / 256;
+  hipLaunchKernelGGL(act_quant32_v8_kernel, dim3((unsigned)(want < 65536 ? want : 65536)), dim3(256), 0, stream, x, q,
+                     scales, groups, scaled);
+  MX_LAUNCH_CHECK("act_quant32_v8_kernel");
+  return MX_OK;
+}
+
+}  // namespace mxi
+
 extern "C" {
 
 int mx_check_e4m3_pack(mx_ctx* ctx, uint64_t* mismatches) {

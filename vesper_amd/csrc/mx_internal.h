@@ -61,6 +61,12 @@ int noalloc_scratch(int device, uint8_t** out);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// mx_act_quant32 that also writes each code times its block scale as BF16 (exact: at most 4 significant bits)
+// into `scaled` [rows][width], the activation operand of the exact gate/up GEMVs. x 16-byte and q 8-byte
+// aligned (mx_formats.hip).
+int act_quant32_scaled(mx_ctx* ctx, const uint16_t* x, uint8_t* q, uint8_t* scales, uint16_t* scaled, int64_t rows,
+                       int64_t width, hipStream_t stream);
+
 // What other translation units need of a decode layer (defined with the layer in mx_moe.hip).
 struct LayerView {
   mx_ctx* ctx;

@@ -38,9 +38,6 @@ using mxd::v4f;
 using mxd::v8i;
 
 constexpr int kMaxTokens = 16;   // MFMA N: tokens per expert per decode call
-// The gate/up products run over K as 4 x kGateUpSegs fixed segments (see stream_range): the early shared-expert
-// path computes them one segment per wave and must reproduce the in-kernel order.
-constexpr int kGateUpSegs = 4;
 constexpr int kMaxTopK = 32;
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxSlots = kMaxTokens * kMaxTopK + 1;
@@ -537,69 +534,11 @@ __global__ void single_plan_kernel(Plan* plan, int T, const float* __restrict__ 
   }
 }
 
-// The shared expert's gate/up epilogue from its early segment sums (see shared_gateup_segments): per row and
-// token the 4 * kGateUpSegs segment sums are added in the gate/up kernel's order (each wave's segments in
-// order, then the waves in order), and the SwiGLU epilogue and the per-32 quantization of the down input
-// follow with gateup_tile_epilogue's and gateup_quantize_block's arithmetic, into the shared slot's rows
-// T * k + token.
-struct SharedEpilogue {
-  const float* seg_part;   // [4 * kGateUpSegs][T][2I], or null: no early shared work in this call
-  int I, k;
-  float limit;
-  uint8_t* dq;
-  uint8_t* ds;
-  uint16_t* w1;            // diagnostics (nullable)
-  uint16_t* w3;
-  uint16_t* din;
-  float* trace;
-};
-
-// Workgroup j: intermediate rows [32 j, 32 j + 32) for every token, 32 threads per token.
-__device__ void shared_epilogue(const SharedEpilogue& e, int T, int j) {
-  const int tok = threadIdx.x >> 5, l32 = threadIdx.x & 31;
-  if (tok >= T) return;
-  const int I = e.I, i = 32 * j + l32;
-  const size_t stride = (size_t)T * 2 * I;
-  const float* p = e.seg_part + (size_t)tok * 2 * I + i;
-  float sum[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {   // h = 0: W1 row, 1: W3 row
-    float total = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      float wave_sum = p[(size_t)(kGateUpSegs * w) * stride + h * I];
-#pragma unroll
-      for (int s = 1; s < kGateUpSegs; ++s) wave_sum = wave_sum + p[(size_t)(kGateUpSegs * w + s) * stride + h * I];
-      total = w == 0 ? wave_sum : total + wave_sum;
-    }
-    sum[h] = total;
-  }
-  const uint32_t b1 = mx::bf16_bits(sum[0]), b3 = mx::bf16_bits(sum[1]);
-  const size_t row = (size_t)T * e.k + tok, o2 = row * I + i;
-  const float din = mxd::swiglu_element(b1, b3, e.limit, false, 1.0f, e.trace ? e.trace + o2 * 5 : nullptr);
-  if (e.w1) e.w1[o2] = (uint16_t)b1;
-  if (e.w3) e.w3[o2] = (uint16_t)b3;
-  if (e.din) e.din[o2] = (uint16_t)mx::bf16_bits(din);
-  float amax = fabsf(din);
-#pragma unroll
-  for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
-  amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
-  const uint32_t code = mx::act_scale_code(amax);
-  const float inv = 1.0f / mx::e8m0_value(code);   // exact: a power of two
-  e.dq[o2] = (uint8_t)mx::act_quant_pow2(din, inv);
-  if (l32 == 0) e.ds[row * (I / 32) + j] = (uint8_t)code;
-}
-
-// Workgroup 0 ranks the tokens, one wave per token: wave t ranks token t, the results are staged in LDS and
-// written out, then the same workgroup builds the plan from the staged IDs. Workgroups 1.. (early shared
-// expert only) run the shared expert's gate/up epilogue meanwhile.
+// One workgroup ranks the tokens, one wave per token: wave t ranks token t, the results are staged in LDS and
+// written out, then the same workgroup builds the plan from the staged IDs.
 __global__ __launch_bounds__(kRouteThreads) void route_plan_kernel(const float* selection, const float* scores, int T,
                                                                    int E, int k, float route_scale, TopkOut o,
-                                                                   Plan* plan, int has_shared, SharedEpilogue ep) {
-  if (blockIdx.x > 0) {
-    shared_epilogue(ep, T, blockIdx.x - 1);
-    return;
-  }
+                                                                   Plan* plan, int has_shared) {
   __shared__ int32_t s_idx[kMaxTokens * kMaxTopK];
   __shared__ float s_w[kMaxTokens * kMaxTopK];
   const TopkOut staged{s_idx, s_w, o.raw, o.den, o.tied};
@@ -674,19 +613,16 @@ struct ExpertArgs {
   float limit;
   const uint8_t* xq;             // [T][H]
   const uint8_t* xs;             // [T][H/32]
+  const uint16_t* xd;            // [T][H] BF16: each E4M3 code of xq times its block scale (exact)
   uint8_t* dq;                   // [rows][I]
   uint8_t* ds;                   // [rows][I/32]
   uint16_t* out;                 // [rows][H]
+  int tokens;                    // the call's token count: bounds every slot's (sizes the gate/up LDS ring)
   // diagnostics (nullable)
   uint16_t* w1;
   uint16_t* w3;
   uint16_t* din;
   float* trace;
-  // early shared expert: its gate/up ran beside the routing, so the gate/up launch skips the shared slot and
-  // instead runs the shared slot's down rows (a 1-D grid: routed gate/up workgroups, then H/64 of those), and
-  // the down launch skips the shared slot
-  int early;
-  int routed_slots;   // gate/up workgroups are (row group, slot) for slots below this
 };
 
 // Operand layout of V_MFMA_SCALE_F32_16X16X128_F8F6F4 (measured on gfx950 with one-hot probe kernels):
@@ -770,20 +706,6 @@ struct ActOperand {
   }
 };
 
-// The same operand staged in LDS from chunk c0 on: codes [chunk - c0][128], scale words [chunk - c0].
-struct ActLds {
-  const uint8_t* xrow;
-  const uint32_t* xsrow;
-  int c0;
-  bool live;
-  __device__ __forceinline__ void load(int c, int q, uint4& b0, uint4& b1, uint32_t& sx) const {
-    const uint8_t* chunk = xrow + (size_t)(c - c0) * 128;
-    b0 = *reinterpret_cast<const uint4*>(chunk + 16 * q);
-    b1 = *reinterpret_cast<const uint4*>(chunk + 64 + 16 * q);
-    sx = xsrow[c - c0];
-  }
-};
-
 template <class W>
 struct ChunkRegs {
   typename W::Regs w;
@@ -808,85 +730,261 @@ __device__ __forceinline__ void mma_chunk(const ChunkRegs<W>& r, v4f (&acc)[kTil
   for (int t = 0; t < kTiles; ++t) acc[t] = mfma_fp4xfp8(r.w.wa[t], b0, b1, acc[t], W::scale(r.w, t, q), sx);
 }
 
-// The K chunks [c0, c0 + n) of one wave, as kSegs consecutive segments: segment k ends (exclusively) at the
-// wave-relative chunk ends[k], with ends[kSegs - 1] = n. Each segment is accumulated from zero, one MFMA per
-// chunk in order, and the segment sums are added in order: acc = ((S0 + S1) + S2) + ... Fixing the segments
-// of the whole K range fixes every output's rounding, so work split differently over waves and workgroups
-// (each computing some segments) reproduces the same bits when its segment sums are added in this order.
-template <int P, int kSegs, class W, class X>
-__device__ __forceinline__ void stream_range(const W& ws, const X& x, int c0, int n, const int (&ends)[kSegs], int q,
-                                             v4f (&acc)[kTiles]) {
-  if constexpr (kSegs == 1) {   // one segment: the chain accumulates in place
+// The K chunks [c0, c0 + n) of one wave, accumulated in place from zero, one MFMA per chunk in order. Loads
+// run P chunks ahead; ring slots past the end repeat the last chunk (a cache hit) and are masked to zero.
+template <int P, class W, class X>
+__device__ __forceinline__ void stream_range(const W& ws, const X& x, int c0, int n, int q, v4f (&acc)[kTiles]) {
 #pragma unroll
-    for (int t = 0; t < kTiles; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
-    if (n == 0) return;
-    const uint32_t live = x.live ? 0xFFFFFFFFu : 0u;
-    ChunkRegs<W> buf[P];
-#pragma unroll
-    for (int j = 0; j < P; ++j) load_chunk(buf[j], ws, x, c0 + min(j, n - 1), q);
-    int i = 0;
-    for (; i + P < n; i += P) {
-#pragma unroll
-      for (int j = 0; j < P; ++j) {
-        mma_chunk(buf[j], acc, q, live);
-        load_chunk(buf[j], ws, x, c0 + min(i + j + P, n - 1), q);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < P; ++j) mma_chunk(buf[j], acc, q, i + j < n ? live : 0u);
-    return;
-  }
-  v4f seg[kTiles];
-#pragma unroll
-  for (int t = 0; t < kTiles; ++t) seg[t] = acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
-  int k = 0;
-  bool first = true;
-  auto fold = [&]() {   // close segment k (an empty one adds zeros)
-#pragma unroll
-    for (int t = 0; t < kTiles; ++t) {
-      acc[t] = first ? seg[t] : acc[t] + seg[t];
-      seg[t] = v4f{0.f, 0.f, 0.f, 0.f};
-    }
-    first = false;
-    ++k;
-  };
-  while (k < kSegs && ends[k] == 0) fold();
+  for (int t = 0; t < kTiles; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
   if (n == 0) return;
   const uint32_t live = x.live ? 0xFFFFFFFFu : 0u;
   ChunkRegs<W> buf[P];
 #pragma unroll
   for (int j = 0; j < P; ++j) load_chunk(buf[j], ws, x, c0 + min(j, n - 1), q);
-  // Steady state: consume P chunks and refill them P ahead. The only branches are the uniform segment
-  // closes, which touch no memory, so the waitcnt pass keeps the refills in flight. Slots past the end
-  // repeat the last chunk (a cache hit) and are masked to zero.
   int i = 0;
   for (; i + P < n; i += P) {
 #pragma unroll
     for (int j = 0; j < P; ++j) {
-      mma_chunk(buf[j], seg, q, live);
+      mma_chunk(buf[j], acc, q, live);
       load_chunk(buf[j], ws, x, c0 + min(i + j + P, n - 1), q);
-      while (k < kSegs && ends[k] == i + j + 1) fold();
     }
   }
 #pragma unroll
-  for (int j = 0; j < P; ++j) {
-    mma_chunk(buf[j], seg, q, i + j < n ? live : 0u);
-    while (k < kSegs && ends[k] == i + j + 1) fold();
+  for (int j = 0; j < P; ++j) mma_chunk(buf[j], acc, q, i + j < n ? live : 0u);
+}
+
+// Wave `wave` of 4 streams its contiguous quarter of the K chunks.
+template <int P, class W, class X>
+__device__ __forceinline__ void stream_ksplit(const W& ws, const X& x, int chunks, int wave, int q,
+                                              v4f (&acc)[kTiles]) {
+  const int c0 = (chunks * wave) / 4, c1 = (chunks * (wave + 1)) / 4;
+  stream_range<P>(ws, x, c0, c1 - c0, q, acc);
+}
+
+// ---- Exact in-order core of the gate/up GEMVs ---------------------------------------------------
+//
+// fp4_gemv_spec (formats.py:97-118) rounds each 32-wide block dot to FP32 once, scales it by both E8M0
+// codes, and adds the blocks to an FP32 sum in ascending block order. Here one wave owns one 16-row tile
+// over the whole K range, so each (row, token) sum is a single chain in one lane, and every block is one
+// V_MFMA_F32_16X16X32_BF16 whose operands carry the scales: the E2M1 weights times 2^(code - 127) (at most
+// two significant bits: exact in BF16, converted by V_CVT_SCALEF32_PK_BF16_FP4) and the E4M3 activations
+// times their block scale (four significant bits: exact in BF16, written by the quantizer). Measured on
+// MI355X against the exact dot on 1.5 M random blocks (realistic, all-codes and sparse operands): with a zero
+// accumulator the instruction returns the exact sum of its 32 products rounded once to FP32 in every case,
+// so D = RN(dot) * sa * sw, the spec's block term; its accumulator input is not rounded that way, so the chain
+// adds D in VALU: acc = acc + D, blocks 4c, 4c + 1, 4c + 2, 4c + 3 of chunk c in order.
+//
+// Operand map (gfx950): A lane l = row l % 16, K 8 (l / 16) + 0..7; B lane l = token column l % 16, same K;
+// D lane l register i = row 4 (l / 16) + i, column l % 16. A lane (m, q) of the tiled layout holds the whole
+// 32-value block 4c + q of row m as four words; two permlane32 and two permlane16 swaps transpose the
+// 4 x 4 (lane group, word) matrix so that lane group g holds word g of every block, and MFMA b of the chunk
+// takes register b: K = 32 (4c + b) + 8 g + 0..7 at lane group g.
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+
+// 8 E2M1 values (one word, low nibble first) times 2^(code - 127), as 8 BF16 MFMA operand values (exact; the
+// conversion's scale operand carries the E8M0 code in its exponent field).
+__device__ __forceinline__ v8bf fp4_word_scaled(uint32_t word, uint32_t code) {
+  const float scale = __uint_as_float(code << 23);
+  const v2bf p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 0);
+  const v2bf p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 1);
+  const v2bf p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 2);
+  const v2bf p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 3);
+  return v8bf{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+
+__device__ __forceinline__ uint32_t ldg_u8(const uint8_t* p) {
+  return *(const __attribute__((address_space(1))) uint8_t*)(p);
+}
+
+// The core's loop runs its own memory pipeline. Each wave streams its tile's weights into a register ring;
+// the operands all four waves share -- the chunk's 256 bytes of scale words and the slot's activations -- are
+// copied once per workgroup into an LDS ring (direct global -> LDS copies) and read from there. Loads, copies
+// and LDS reads are issued from inline assembly with counted waits: with compiler-issued loads, register
+// allocation around the ring made the compiler's in-order vmcnt waits cover loads issued a chunk earlier (a
+// memory round trip per chunk), and nine loads per wave and chunk (codes and activations read by every
+// wave) filled the address unit's queues. The compiler does not track these loads: every register
+// destination passes through a tied wait before it is read, and the loop drains them before its registers
+// are released.
+using mxd::u32x4_t;
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Loads and copies address memory as a wave-uniform base (SGPRs, advanced per chunk by scalar arithmetic) plus
+// a constant per-lane 32-bit offset, so the per-chunk address arithmetic runs on the scalar unit.
+__device__ __forceinline__ u32x4_t asm_ldg128_nt(const uint8_t* base, uint32_t off) {
+  u32x4_t v;
+  asm volatile("global_load_dwordx4 %0, %1, %2 nt" : "=v"(v) : "v"(off), "s"(base));
+  return v;
+}
+__device__ __forceinline__ u32x4_t asm_ldg128(const uint8_t* base, uint32_t off) {
+  u32x4_t v;
+  asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(v) : "v"(off), "s"(base));
+  return v;
+}
+// Direct global -> LDS copies of 4 (16) bytes per lane at base + off: lane l's bytes land at lds + 4 l (16 l).
+__device__ __forceinline__ void asm_copy4(const uint8_t* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" : : "v"(off), "s"(base), "s"(lds) : "m0");
+}
+__device__ __forceinline__ void asm_copy16(const uint8_t* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base), "s"(lds) : "m0");
+}
+
+// Readable memory for the core's loads past the last chunk (each lane reads 16 bytes at 16 x lane): small
+// enough to stay cached, read with plain loads.
+__device__ __align__(256) uint8_t exact_dummy_page[1024];
+
+// Exact-core LDS ring: kXStages stages, each the scale words (256 B) and the slot's token rows of one chunk's
+// scaled activations (256 B each, in groups of 4: xstage_bytes(T) with the call's token count T bounding every
+// slot's). The ring lives in the launch's dynamic LDS.
+constexpr int kXStages = 6;
+constexpr int kXStageScale = 0, kXStageAct = 256;
+__host__ __device__ constexpr int xstage_bytes(int T) { return 256 + 1024 * ((T + 3) / 4); }
+
+// Chunk c's shared operands into stage st: wave 0 copies the scale words, wave w the token rows 4w .. 4w + 3
+// (one copy instruction each) when the slot has such tokens. Past the last chunk the same copies read the dummy
+// page (the stage is never read again), so a wave issues the same number of loads every iteration.
+struct SharedCopies {
+  const uint8_t* scale;   // row group's scale words (chunk c at + 256 c); lane offset 4 lane
+  const uint8_t* act;     // the scaled activations (chunk c at + 256 c); lane offset act_off
+  const uint8_t* dummy;   // exact_dummy_page; lane offsets 4 lane / 16 lane
+  uint32_t act_off;       // this lane's token row (2 H bytes each) + 16 (lane & 15)
+  uint32_t lane;
+  uint32_t lds;           // the ring's LDS byte address
+  int stage_bytes;
+  bool copies_scale, copies_act;
+  int wave;
+  __device__ __forceinline__ void issue(int c, int n, int st) const {
+    const uint32_t base = lds + st * stage_bytes;
+    const bool real = c < n;
+    if (copies_scale) asm_copy4(real ? scale + (size_t)c * 256 : dummy, 4 * lane, base + kXStageScale);
+    if (copies_act)
+      asm_copy16(real ? act + (size_t)c * 256 : dummy, real ? act_off : 16 * lane, base + kXStageAct + 1024 * wave);
+  }
+};
+
+__device__ __forceinline__ uint32_t fp4_scale_float_bits(uint32_t code) { return code << 23; }
+
+// 8 E2M1 values (one word, low nibble first) times the scale whose FP32 bits are `scale_bits`, as 8 BF16 MFMA
+// operand values (exact).
+__device__ __forceinline__ v8bf fp4_word_bits(uint32_t word, uint32_t scale_bits) {
+  const float scale = __uint_as_float(scale_bits);
+  const v2bf p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 0);
+  const v2bf p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 1);
+  const v2bf p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 2);
+  const v2bf p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 3);
+  return v8bf{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+
+// 4 x 4 transpose across lane groups: afterwards lane group g register r holds what lane group r register g held
+// (two permlane32 swaps exchange the upper half of v0 / v1 with the lower half of v2 / v3, two permlane16 swaps
+// the odd 16-lane rows of v0 / v2 with the even rows of v1 / v3).
+__device__ __forceinline__ void transpose_groups(uint32_t (&v)[4]) {
+  auto a = __builtin_amdgcn_permlane32_swap(v[0], v[2], false, false);
+  auto b = __builtin_amdgcn_permlane32_swap(v[1], v[3], false, false);
+  auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+  auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+  v[0] = c[0];
+  v[1] = c[1];
+  v[2] = d[0];
+  v[3] = d[1];
+}
+
+// Stage st's operands of this lane, read and waited for: the activations of blocks 0..3 at K 8 g (token column
+// n, or the slot's first token for idle columns) and the E8M0 codes of row m, blocks 0..3 (byte t of scale
+// word m + 16 b).
+__device__ __forceinline__ void lds_read_stage(uint32_t xaddr, uint32_t caddr, u32x4_t (&xb)[4], uint32_t (&code)[4]) {
+  asm volatile(
+      "ds_read_b128 %0, %8\n\t"
+      "ds_read_b128 %1, %8 offset:64\n\t"
+      "ds_read_b128 %2, %8 offset:128\n\t"
+      "ds_read_b128 %3, %8 offset:192\n\t"
+      "ds_read_u8 %4, %9\n\t"
+      "ds_read_u8 %5, %9 offset:64\n\t"
+      "ds_read_u8 %6, %9 offset:128\n\t"
+      "ds_read_u8 %7, %9 offset:192\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(xb[0]), "=&v"(xb[1]), "=&v"(xb[2]), "=&v"(xb[3]), "=&v"(code[0]), "=&v"(code[1]), "=&v"(code[2]),
+        "=&v"(code[3])
+      : "v"(xaddr), "v"(caddr));
+}
+
+// Multiply chunk c (this lane's 16 weight bytes wa, LDS stage operands) into the chains.
+__device__ __forceinline__ void exact_chunk(const u32x4_t& wa, const u32x4_t (&xb)[4], const uint32_t (&code)[4],
+                                            v4f& acc) {
+  uint32_t wv[4] = {wa.x, wa.y, wa.z, wa.w};
+  transpose_groups(wv);   // lane group g now holds word g of every block: K 32 (4c + b) + 8 g + 0..7 in wv[b]
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const v8bf av = fp4_word_bits(wv[b], fp4_scale_float_bits(code[b]));
+    const v4f d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(v8bf, xb[b]),
+                                                          v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = acc[i] + d[i];
   }
 }
 
-// Segment s of a K range of `chunks` chunks cut into `total` segments: chunks [seg_begin(s), seg_begin(s + 1)).
-__device__ __forceinline__ int seg_begin(int chunks, int s, int total) { return (chunks * s) / total; }
+// The whole K range (n chunks) of tile `wave` of a row group. Per iteration k a wave waits until its own copies
+// of chunk k have landed, a barrier makes every wave's copies visible, and the wave reads chunk k's stage and
+// multiplies chunk k; it then issues its copies for chunk k + kXStages - 1 (into the stage of chunk k - 1, which
+// every wave read before this iteration's barrier) and its weights for chunk k + kW. Past the end the weights
+// load from the dummy page and the copies read it, so every iteration issues the same `loads` instructions per
+// wave: when a wave waits for its copies of chunk k, at most 1 + (kXStages - 2) x loads loads issued after them
+// may still be in flight (its weights of chunk k were issued kW - kXStages + 1 iterations before those copies),
+// and a wave without copies waits for its weights of chunk k (kW - 1 later loads in flight).
+constexpr int kWRing = 6;
+static_assert(kWRing % kXStages == 0 && kWRing >= kXStages, "stage and weight slot indices are static per pass");
 
-// Wave `wave` of 4 streams its quarter of the K chunks as kSegs of the 4 * kSegs segments of the range.
-template <int P, int kSegs, class W, class X>
-__device__ __forceinline__ void stream_ksplit(const W& ws, const X& x, int chunks, int wave, int q,
-                                              v4f (&acc)[kTiles]) {
-  const int c0 = seg_begin(chunks, kSegs * wave, 4 * kSegs);
-  int ends[kSegs];
+template <int kAfter>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(kAfter <= 63, "vmcnt holds at most 63 outstanding loads");
+  __builtin_amdgcn_s_waitcnt(mxd::vm_wait_imm(kAfter));
+}
+
+__device__ __forceinline__ void stream_exact(const uint8_t* wbase, uint32_t woff, const SharedCopies& sc,
+                                             uint32_t xaddr, uint32_t caddr, int n, v4f& acc) {
+  constexpr int kW = kWRing, kX = kXStages;
+  const int sb = sc.stage_bytes;
+  acc = v4f{0.f, 0.f, 0.f, 0.f};
+  u32x4_t wr[kW];
+  const int copies = (int)sc.copies_scale + (int)sc.copies_act;   // per iteration, uniform per wave
+  auto load_w = [&](u32x4_t& r, int c) {
+    if (c < n) r = asm_ldg128_nt(wbase + (size_t)c * 4096, woff);
+    else r = asm_ldg128(sc.dummy, 16 * sc.lane);
+  };
+  // the loads of iterations -kW .. -1 in the steady state's order: iteration k issues C(k + kX - 1) (when that
+  // chunk index is not negative), then W(k + kW)
 #pragma unroll
-  for (int k = 0; k < kSegs; ++k) ends[k] = seg_begin(chunks, kSegs * wave + k + 1, 4 * kSegs) - c0;
-  stream_range<P, kSegs>(ws, x, c0, ends[kSegs - 1], ends, q, acc);
+  for (int vk = -kW; vk < 0; ++vk) {
+    if (vk + kX - 1 >= 0) sc.issue(vk + kX - 1, n, (vk + kX - 1) % kX);
+    load_w(wr[vk + kW], vk + kW);
+  }
+  for (int i = 0; i < n; i += kW) {
+#pragma unroll
+    for (int j = 0; j < kW; ++j) {
+      const int k = i + j;
+      // the wait and the tie run for every slot, past the end too: a slot's registers are only released (and
+      // reusable by the compiler) once the load that writes them has landed
+      if (copies == 2) vm_wait<1 + (kX - 2) * 3>();
+      else if (copies == 1) vm_wait<1 + (kX - 2) * 2>();
+      else vm_wait<kW - 1>();
+      asm volatile("" : "+v"(wr[j]));   // the weights of chunk k landed with the wait above
+      if (k < n) {
+        mxd::copy_barrier();   // every wave's copies of chunk k have landed
+        u32x4_t xb[4];
+        uint32_t code[4];
+        lds_read_stage(xaddr + (j % kX) * sb, caddr + (j % kX) * sb, xb, code);
+        exact_chunk(wr[j], xb, code, acc);
+      }
+      sc.issue(k + kX - 1, n, (j + kX - 1) % kX);
+      load_w(wr[j], k + kW);
+    }
+  }
+  // drain: no load may still be writing a ring register, and no copy the LDS, once the loop is left
+  vm_wait<0>();
+#pragma unroll
+  for (int j = 0; j < kW; ++j) asm volatile("" : "+v"(wr[j]));
+  mxd::copy_barrier();
 }
 
 // ----------------------------------------------------------------------------------------------
@@ -904,116 +1002,10 @@ struct RouterArgs {
   float* selection;
   uint8_t* xq;
   uint8_t* xs;
-  // Early shared expert (up to kEarlyTokens tokens): workgroups E.. of the launch compute the shared expert's
-  // gate/up segment sums (shared_gateup_segments) while the others route.
-  const uint8_t* shared_blob;   // the tiled shared expert, or null for no early work
-  float* seg_part;              // [4 * kGateUpSegs][T][2I] FP32 segment sums: W1 rows, then W3 rows
-  int I;
+  uint16_t* xd;   // each code times its block scale, BF16 (the exact gate/up GEMVs' activation operand)
 };
 
-// The shared expert does not depend on the routing, so for few tokens its work runs beside the routing
-// instead of after it (the gate/up and down launches then carry only routed slots). Its gate/up products are
-// split into the 4 * kGateUpSegs segments of K that the gate/up kernel accumulates separately: workgroup
-// (g, quarter) of the router launch stages the quarter's activations in LDS, quantized exactly as the router
-// quantizes x, and wave w streams row group g's tiles over segment 4 quarter + w, writing that segment's sum
-// per row and token. shared_epilogue_kernel-side code adds the segments in the kernel's order.
-constexpr int kEarlyTokens = 4;          // the buffers' token bound
-constexpr int kEarlyUseTokens = 2;       // mx_moe_decode uses the early path up to this many tokens
-constexpr int kEarlyQuarterChunks = 16;   // H <= 8192: a quarter of K is at most 16 chunks of 128
-constexpr int kEarlySegChunks = 4;        // and a segment at most 4
-
-__device__ void shared_gateup_segments(const RouterArgs& a, int idx) {
-  __shared__ __attribute__((aligned(16))) uint8_t s_xq[kEarlyTokens][kEarlyQuarterChunks * 128];
-  __shared__ uint32_t s_xs[kEarlyTokens][kEarlyQuarterChunks];
-  const int H = a.H, I = a.I, T = a.T, groups = I / 32;
-  const int g = idx % groups, quarter = idx / groups;
-  const int C = H / 128, nseg = 4 * kGateUpSegs;
-  const int q_lo = seg_begin(C, kGateUpSegs * quarter, nseg), q_hi = seg_begin(C, kGateUpSegs * (quarter + 1), nseg);
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // this wave's segment (at most kEarlySegChunks chunks): its weight tiles are loaded first, so they are in
-  // flight while the activations are read and quantized
-  const int s = kGateUpSegs * quarter + wave;
-  const int c0 = seg_begin(C, s, nseg), cn = seg_begin(C, s + 1, nseg) - c0;
-  TiledW ws;
-  ws.w = a.shared_blob + (size_t)g * C * 4096 + 16 * lane;
-  ws.s = a.shared_blob + tiled_offsets(H, I).gu_s + (size_t)g * C * 256 + 4 * lane;
-  TiledW::Regs wr[kEarlySegChunks];
-#pragma unroll
-  for (int j = 0; j < kEarlySegChunks; ++j)
-    if (j < cn) ws.load(wr[j], c0 + j, 0);
-  // per-32 quantization of the quarter's blocks for every token with the router's arithmetic: 8 values per
-  // thread (4 threads per block), every load issued before the first is used
-  {
-    const int per_tok = (q_hi - q_lo) * 16, units = T * per_tok;   // 16-byte units of 8 BF16 values
-    uint4 raw[kEarlyTokens];
-#pragma unroll
-    for (int j = 0; j < kEarlyTokens; ++j) {
-      const int u = tid + 256 * j, tok = u / per_tok, w = u - tok * per_tok;
-      raw[j] = u < units ? *reinterpret_cast<const uint4*>(a.x + (size_t)tok * H + (size_t)q_lo * 128 + 8 * w)
-                         : make_uint4(0u, 0u, 0u, 0u);
-    }
-#pragma unroll
-    for (int j = 0; j < kEarlyTokens; ++j) {
-      const int u = tid + 256 * j, tok = u / per_tok, w = u - tok * per_tok;
-      if (256 * j >= units) break;   // uniform: no unit of this round exists
-      const uint32_t words[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
-      float v[8];
-      float amax = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        v[e] = mx::bf16_value((words[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
-        amax = fmaxf(amax, fabsf(v[e]));
-      }
-      amax = fmaxf(amax, __shfl_xor(amax, 1, 4));
-      amax = fmaxf(amax, __shfl_xor(amax, 2, 4));
-      amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
-      const uint32_t code = mx::act_scale_code(amax);
-      const float inv = 1.0f / mx::e8m0_value(code);
-      uint32_t packed[2] = {0u, 0u};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) packed[e >> 2] |= mx::act_quant_pow2(v[e], inv) << (8 * (e & 3));
-      if (u < units) {
-        *reinterpret_cast<uint2*>(&s_xq[tok][8 * w]) = make_uint2(packed[0], packed[1]);
-        if ((w & 3) == 0) reinterpret_cast<uint8_t*>(&s_xs[tok][w >> 4])[(w >> 2) & 3] = (uint8_t)code;
-      }
-    }
-  }
-  __syncthreads();
-  const int n = lane & 15, q = lane >> 4;
-  ActLds x;
-  x.live = n < T;
-  x.xrow = &s_xq[x.live ? n : 0][0];
-  x.xsrow = &s_xs[x.live ? n : 0][0];
-  x.c0 = q_lo;
-  // the segment's chain, as stream_range accumulates it: from zero, chunk by chunk
-  v4f acc[kTiles];
-#pragma unroll
-  for (int t = 0; t < kTiles; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
-  const uint32_t live = x.live ? 0xFFFFFFFFu : 0u;
-#pragma unroll
-  for (int j = 0; j < kEarlySegChunks; ++j)
-    if (j < cn) {
-      ChunkRegs<TiledW> r;
-      r.w = wr[j];
-      x.load(c0 + j, q, r.b0, r.b1, r.sx);
-      mma_chunk(r, acc, q, live);
-    }
-  if (!x.live) return;
-#pragma unroll
-  for (int t = 0; t < kTiles; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 4 * q + i, row = 32 * g + 8 * t + (r & 7);
-      a.seg_part[((size_t)s * T + n) * (2 * I) + (r < 8 ? row : I + row)] = acc[t][i];
-    }
-}
-
 __global__ __launch_bounds__(256) void router_kernel(RouterArgs a) {
-  if ((int)blockIdx.x >= a.E) {   // early shared-expert workgroups
-    shared_gateup_segments(a, blockIdx.x - a.E);
-    return;
-  }
   const int e = blockIdx.x;
   const int t0 = blockIdx.y * kMaxTokens;
   const int nt = min(kMaxTokens, a.T - t0);
@@ -1074,7 +1066,9 @@ __global__ __launch_bounds__(256) void router_kernel(RouterArgs a) {
       for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
       amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
       const uint32_t code = mx::act_scale_code(amax);
-      a.xq[(size_t)b * 32 + l32] = (uint8_t)mx::act_quant_pow2(v, 1.0f / mx::e8m0_value(code));
+      const uint32_t qc = mx::act_quant_pow2(v, 1.0f / mx::e8m0_value(code));
+      a.xq[(size_t)b * 32 + l32] = (uint8_t)qc;
+      a.xd[(size_t)b * 32 + l32] = (uint16_t)mx::bf16_bits(mx::e4m3_value(qc) * mx::e8m0_value(code));
       if (l32 == 0) a.xs[b] = (uint8_t)code;
     }
   }
@@ -1103,15 +1097,16 @@ __device__ __forceinline__ v4f reduce_tiles(const v4f (&acc)[kTiles], int wave, 
   return out;
 }
 
-// SwiGLU epilogue of gate/up tile t of row group g once its 4 partial tiles are summed: in `mine`, lanes
-// with q < 2 hold W1 rows 4q + i of the tile (D[4q + i][n]) and lane + 32 the matching W3 rows. Writes
-// the down input of token column n to s_din[n][8t + 4q + i] (and the diagnostic copies when requested).
+// SwiGLU epilogue of gate/up tile t of row group g: in `mine` (the in-order chains), lane (n, q) holds token
+// column n; lanes with q < 2 hold W1 rows 4q + i of the tile (D[4q + i][n]) and lane + 32 the matching W3
+// rows. Writes the down input of token n to s_din[n][8t + 4q + i] (and the diagnostic copies when requested).
 __device__ __forceinline__ void gateup_tile_epilogue(const ExpertArgs& a, int s, int g, int t, const v4f& mine,
-                                                     int q, int n, int ntok, float (*s_din)[32]) {
+                                                     int lane, int ntok, float (*s_din)[32]) {
   const Plan* __restrict__ plan = a.plan;
   float upv[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) upv[i] = __shfl_xor(mine[i], 32, 64);
+  const int q = lane >> 4, n = lane & 15;
   if (q < 2 && n < ntok) {
     const int row0 = plan->slot_row0[s];
     const bool weighted = plan->slot_weighted[s] != 0;
@@ -1152,64 +1147,44 @@ __device__ __forceinline__ void gateup_quantize_block(const ExpertArgs& a, int s
   if (j2 == 0) a.ds[r * (I / 32) + g] = (uint8_t)code;
 }
 
-// grid (I/32, slots), 256 threads. The workgroup computes intermediate rows [32g, 32g + 32) of W1 and
-// W3 for the slot's tokens: tile t holds W1 rows 32g + 8t + (0..7) as MFMA rows 0-7 and the same W3
-// rows as MFMA rows 8-15. After the cross-wave sum, wave t owns tile t, applies the SwiGLU epilogue,
-// and the workgroup quantizes its 32-row block of the down input per token (one E8M0 block).
-template <bool kTiled>
-__device__ void down_rows(const ExpertArgs& a, int s, int b, float (*red)[kTiles][64][4]);
-
-template <bool kTiled>
-__global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
+// grid (I/32, slots), 256 threads, tiled experts. The workgroup computes intermediate rows [32g, 32g + 32) of
+// W1 and W3 for the slot's tokens: tile t holds W1 rows 32g + 8t + (0..7) as MFMA rows 0-7 and the same W3
+// rows as MFMA rows 8-15. Wave t streams tile t over all of K (the exact in-order core), applies the SwiGLU
+// epilogue, and the workgroup quantizes its 32-row block of the down input per token (one E8M0 block).
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void gateup_kernel(ExpertArgs a) {
   const Plan* __restrict__ plan = a.plan;
-  __shared__ float red[4][kTiles][64][4];
-  int s = blockIdx.y, g = blockIdx.x;
-  if (a.early) {
-    const int groups = a.I / 32, bid = blockIdx.x;
-    if (bid >= groups * a.routed_slots) {   // the shared slot's down rows
-      down_rows<kTiled>(a, plan->n_routed, bid - groups * a.routed_slots, red);
-      return;
-    }
-    g = bid % groups;
-    s = bid / groups;
-    if (s >= plan->n_routed) return;
-  }
+  const int s = blockIdx.y, g = blockIdx.x;
   if (s >= plan->n_slots) return;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int m = lane & 15, q = lane >> 4, n = lane & 15;
+  const int q = lane >> 4, m = lane & 15, n = lane & 15;
   const int ntok = plan->slot_ntok[s];
   const int H = a.H, I = a.I;
-  ActOperand x;
-  x.live = n < ntok;
-  const int tok = x.live ? plan->slot_tok[s][n] : 0;
-  x.xrow = a.xq + (size_t)tok * H;
-  x.xsrow = a.xs + (size_t)tok * (H / 32);
-  v4f acc[kTiles];
-  if constexpr (kTiled) {
-    const uint8_t* blob = a.tiles[plan->slot_expert[s]];
-    const size_t chunks = H / 128;
-    TiledW ws;
-    ws.w = blob + (size_t)g * chunks * 4096 + 16 * lane;
-    ws.s = blob + tiled_offsets(H, I).gu_s + (size_t)g * chunks * 256 + 4 * lane;
-    stream_ksplit<3, kGateUpSegs>(ws, x, H / 128, wave, q, acc);
-  } else {
-    const mx_expert_ptrs& p = a.single;
-    const bool up = m >= 8;
-    const uint8_t* wbase = (const uint8_t*)(up ? p.w3_weight : p.w1_weight);
-    const uint8_t* sbase = (const uint8_t*)(up ? p.w3_scale : p.w1_scale);
-    RowMajorW ws;
-#pragma unroll
-    for (int t = 0; t < kTiles; ++t) {
-      const int row = g * 32 + t * 8 + (m & 7);
-      ws.wrow[t] = wbase + (size_t)row * (H / 2);
-      ws.srow[t] = sbase + (size_t)row * (H / 32);
-    }
-    stream_ksplit<3, kGateUpSegs>(ws, x, H / 128, wave, q, acc);
-  }
+  const size_t chunks = H / 128;
+  const uint8_t* blob = a.tiles[plan->slot_expert[s]];
+  extern __shared__ __attribute__((aligned(16))) uint8_t ring[];   // kXStages x xstage_bytes(a.tokens)
+  const uint32_t ring0 = mxd::lds_addr(ring);
+  SharedCopies sc;
+  sc.scale = blob + tiled_offsets(H, I).gu_s + (size_t)g * chunks * 256;
+  const int copy_tok = 4 * wave + (lane >> 4);   // the token row this lane copies
+  sc.act = reinterpret_cast<const uint8_t*>(a.xd);
+  sc.act_off = (uint32_t)plan->slot_tok[s][copy_tok < ntok ? copy_tok : 0] * (uint32_t)(2 * H) + 16 * (lane & 15);
+  sc.dummy = exact_dummy_page;
+  sc.lane = lane;
+  sc.lds = ring0;
+  sc.stage_bytes = xstage_bytes(a.tokens);
+  sc.copies_scale = wave == 0;
+  sc.copies_act = 4 * wave < ntok;
+  sc.wave = wave;
+  // this lane's LDS operands: token column n's row (the slot's first token for idle columns) at K 8 q, and the
+  // scale byte of tile `wave` for row m (word m + 16 b holds block b)
+  const uint32_t xaddr = ring0 + kXStageAct + 256 * (n < ntok ? n : 0) + 16 * q;
+  const uint32_t caddr = ring0 + kXStageScale + 4 * m + wave;
+  const uint8_t* wbase = blob + (size_t)g * chunks * 4096 + (size_t)wave * 1024;
+  v4f acc;
+  stream_exact(wbase, 16 * lane, sc, xaddr, caddr, (int)chunks, acc);
   __shared__ float s_din[kMaxTokens][32];
-  const v4f mine = reduce_tiles(acc, wave, lane, red);
-  gateup_tile_epilogue(a, s, g, wave, mine, q, n, ntok, s_din);
+  gateup_tile_epilogue(a, s, g, wave, acc, lane, ntok, s_din);
   __syncthreads();
   gateup_quantize_block(a, s, g, tid >> 4, tid & 15, ntok, s_din);
 }
@@ -1238,7 +1213,7 @@ __device__ void down_rows(const ExpertArgs& a, int s, int b, float (*red)[kTiles
     TiledW ws;
     ws.w = blob + off.dn_w + (size_t)b * chunks * 4096 + 16 * lane;
     ws.s = blob + off.dn_s + (size_t)b * chunks * 256 + 4 * lane;
-    stream_ksplit<4, 1>(ws, x, I / 128, wave, q, acc);
+    stream_ksplit<4>(ws, x, I / 128, wave, q, acc);
   } else {
     RowMajorW ws;
 #pragma unroll
@@ -1246,7 +1221,7 @@ __device__ void down_rows(const ExpertArgs& a, int s, int b, float (*red)[kTiles
       ws.wrow[t] = (const uint8_t*)a.single.w2_weight + (size_t)(hb + 16 * t + m) * (I / 2);
       ws.srow[t] = (const uint8_t*)a.single.w2_scale + (size_t)(hb + 16 * t + m) * (I / 32);
     }
-    stream_ksplit<4, 1>(ws, x, I / 128, wave, q, acc);
+    stream_ksplit<4>(ws, x, I / 128, wave, q, acc);
   }
   const v4f mine = reduce_tiles(acc, wave, lane, red);
   if (n < ntok) {
@@ -1257,13 +1232,12 @@ __device__ void down_rows(const ExpertArgs& a, int s, int b, float (*red)[kTiles
   }
 }
 
-// grid (H/64, slots), 256 threads; with a.early the shared slot is left out (its rows ran in the gate/up
-// launch).
+// grid (H/64, slots), 256 threads.
 template <bool kTiled>
 __global__ __launch_bounds__(256) void down_kernel(ExpertArgs a) {
   const Plan* __restrict__ plan = a.plan;
   const int s = blockIdx.y;
-  if (s >= plan->n_slots || (a.early && s == plan->n_routed)) return;
+  if (s >= plan->n_slots) return;
   __shared__ float red[4][kTiles][64][4];
   down_rows<kTiled>(a, s, blockIdx.x, red);
 }
@@ -1432,19 +1406,17 @@ struct mx_layer {
         *den = nullptr, *trace = nullptr;
   int32_t *indices = nullptr, *tied = nullptr;
   uint8_t *xq = nullptr, *xs = nullptr, *dq = nullptr, *ds = nullptr;
+  uint16_t* xd = nullptr;             // [T][H] BF16: x's codes times their block scales
   uint16_t *w1 = nullptr, *w3 = nullptr, *din = nullptr, *eout = nullptr;
   Plan* plan = nullptr;
   float* silu = nullptr;   // [mxd::kSiluEntries] SiLU table (prefill epilogue)
   uint32_t* route_errors = nullptr;   // routing ids replaced by routed decode / prefill since the last clear
-  const void* shared_blob = nullptr;  // the shared expert's tiled blob (device address), or null
-  float* seg_part = nullptr;          // early shared expert: [4 * kGateUpSegs][kEarlyTokens][2I] segment sums
   int max_rows = 0;
   // the most recent decode call (mx_layer_time_stage repeats its stages)
   const uint16_t* last_x = nullptr;
   uint16_t* last_y = nullptr;
   int last_T = 0;
   bool last_diag = false;
-  bool last_early = false;   // the shared expert ran beside the routing (mx_moe_decode, few tokens)
   std::vector<std::pair<void*, uint64_t>> allocs;
   // profiling: events bracket each kernel of a call; a ring of kProfRing calls is recorded without
   // host synchronisation and folded into the totals when full or when the profile is read.
@@ -1584,35 +1556,15 @@ int launch_stage(mx_layer* L, int stage, hipStream_t st) {
     r.selection = L->selection;
     r.xq = L->xq;
     r.xs = L->xs;
-    int early_wgs = 0;
-    if (L->last_early) {
-      r.shared_blob = (const uint8_t*)L->shared_blob;
-      r.seg_part = L->seg_part;
-      r.I = c.intermediate;
-      early_wgs = 4 * (c.intermediate / 32);
-    }
-    hipLaunchKernelGGL(router_kernel, dim3(c.experts + early_wgs, 1), dim3(256), 0, st, r);
+    r.xd = L->xd;
+    hipLaunchKernelGGL(router_kernel, dim3(c.experts, 1), dim3(256), 0, st, r);
     MX_LAUNCH_CHECK("router_kernel");
     return MX_OK;
   }
   if (stage == MX_STAGE_ROUTE_PLAN) {
-    SharedEpilogue ep{};
-    int blocks = 1, threads = 64 * T;
-    if (L->last_early) {
-      ep = SharedEpilogue{L->seg_part, c.intermediate, c.top_k, c.swiglu_limit, L->dq, L->ds, nullptr, nullptr,
-                          nullptr, nullptr};
-      if (L->last_diag) {
-        ep.w1 = L->w1;
-        ep.w3 = L->w3;
-        ep.din = L->din;
-        ep.trace = L->trace;
-      }
-      blocks += c.intermediate / 32;
-      threads = std::max(threads, 32 * kEarlyTokens);
-    }
-    hipLaunchKernelGGL(route_plan_kernel, dim3(blocks), dim3(threads), 0, st, (const float*)L->selection,
+    hipLaunchKernelGGL(route_plan_kernel, dim3(1), dim3(64 * T), 0, st, (const float*)L->selection,
                        (const float*)L->scores, T, c.experts, c.top_k, c.route_scale,
-                       TopkOut{L->indices, L->weights, L->raw, L->den, L->tied}, L->plan, L->has_shared, ep);
+                       TopkOut{L->indices, L->weights, L->raw, L->den, L->tied}, L->plan, L->has_shared);
     MX_LAUNCH_CHECK("route_plan_kernel");
     return MX_OK;
   }
@@ -1631,6 +1583,7 @@ int launch_stage(mx_layer* L, int stage, hipStream_t st) {
   a.limit = c.swiglu_limit;
   a.xq = L->xq;
   a.xs = L->xs;
+  a.xd = L->xd;
   a.dq = L->dq;
   a.ds = L->ds;
   a.out = L->eout;
@@ -1643,17 +1596,13 @@ int launch_stage(mx_layer* L, int stage, hipStream_t st) {
   // grid rows beyond the plan's slot count exit at once
   const int routed = std::min(c.experts, T * c.top_k);
   const int slots = routed + L->has_shared;
-  a.early = L->last_early;
-  a.routed_slots = routed;
   if (stage == MX_STAGE_GATEUP) {
-    if (L->last_early)   // routed (row group, slot) workgroups, then the shared slot's down rows
-      hipLaunchKernelGGL(gateup_kernel<true>, dim3((c.intermediate / 32) * routed + c.hidden / 64), dim3(256), 0, st,
-                         a);
-    else
-      hipLaunchKernelGGL(gateup_kernel<true>, dim3(c.intermediate / 32, slots), dim3(256), 0, st, a);
+    a.tokens = T;
+    hipLaunchKernelGGL(gateup_kernel, dim3(c.intermediate / 32, slots), dim3(256), kXStages * xstage_bytes(T), st,
+                       a);
     MX_LAUNCH_CHECK("gateup_kernel");
   } else {
-    hipLaunchKernelGGL(down_kernel<true>, dim3(c.hidden / 64, L->last_early ? routed : slots), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(down_kernel<true>, dim3(c.hidden / 64, slots), dim3(256), 0, st, a);
     MX_LAUNCH_CHECK("down_kernel");
   }
   return MX_OK;
@@ -1701,6 +1650,7 @@ int mx_layer_create(mx_ctx* ctx, const mx_moe_config* cfg, const float* router_w
   if ((s = layer_alloc_t(L, (uint64_t)T, &L->tied))) return fail_out(s);
   if ((s = layer_alloc_t(L, (uint64_t)T * H, &L->xq))) return fail_out(s);
   if ((s = layer_alloc_t(L, (uint64_t)T * H / 32 + 16, &L->xs))) return fail_out(s);
+  if ((s = layer_alloc_t(L, (uint64_t)T * H, &L->xd))) return fail_out(s);
   if ((s = layer_alloc_t(L, 1, &L->plan))) return fail_out(s);
   const uint64_t R = (uint64_t)L->max_rows;
   if ((s = layer_alloc_t(L, R * I, &L->w1))) return fail_out(s);
@@ -1712,10 +1662,6 @@ int mx_layer_create(mx_ctx* ctx, const mx_moe_config* cfg, const float* router_w
   if ((s = layer_alloc_t(L, R * H, &L->eout))) return fail_out(s);
   if ((s = layer_alloc_t(L, (uint64_t)mxd::kSiluEntries, &L->silu))) return fail_out(s);
   if ((s = layer_alloc_t(L, 64, &L->route_errors))) return fail_out(s);
-  if (shared) {
-    L->shared_blob = shared;
-    if ((s = layer_alloc_t(L, (uint64_t)4 * kGateUpSegs * kEarlyTokens * 2 * I, &L->seg_part))) return fail_out(s);
-  }
   hipLaunchKernelGGL(silu_table_kernel, dim3((mxd::kSiluEntries + 255) / 256), dim3(256), 0, nullptr, L->silu,
                      cfg->swiglu_limit);
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return fail_out(hip_fail(e, "mx_layer_create: SiLU table"));
@@ -1823,9 +1769,6 @@ int mx_moe_decode(mx_layer* L, const uint16_t* x, int32_t T, uint16_t* y, int32_
   L->last_y = y;
   L->last_T = T;
   L->last_diag = diagnostics != 0;
-  // early shared expert: measured on MI355X at the BASELINE shapes, 56.7 -> 55.4 us per layer at T = 1; at
-  // T = 4 its activation staging lengthens the routing launch by more than the gate/up launch saves
-  L->last_early = L->has_shared && T <= kEarlyUseTokens;
   // event i + 1 closes profiled stage i: router (GEMV + top-k/plan), gate/up, down, combine
   static const int kEventAfter[5] = {-1, 1, 2, 3, 4};
   for (int stage = 0; stage < 5; ++stage) {
@@ -1846,7 +1789,7 @@ int mx_moe_decode_routed(mx_layer* L, const uint16_t* x, int32_t T, const int32_
   MX_REQUIRE(x && y && ids && weights && aligned(x, 16) && aligned(y, 16),
              "x, y (16-byte aligned), ids and weights must be device pointers");
   hipStream_t st = as_stream(stream);
-  if (int s = mx_act_quant32(L->ctx, x, L->xq, L->xs, T, c.hidden, stream)) return s;
+  if (int s = act_quant32_scaled(L->ctx, x, L->xq, L->xs, L->xd, T, c.hidden, st)) return s;
   hipLaunchKernelGGL(routed_plan_kernel, dim3(1), dim3(64 * T), 0, st, ids, weights, T, c.top_k, c.experts, L->indices,
                      L->weights, L->plan, L->has_shared, L->route_errors);
   MX_LAUNCH_CHECK("routed_plan_kernel");
@@ -1854,7 +1797,6 @@ int mx_moe_decode_routed(mx_layer* L, const uint16_t* x, int32_t T, const int32_
   L->last_y = y;
   L->last_T = T;
   L->last_diag = false;
-  L->last_early = false;
   for (int stage = MX_STAGE_GATEUP; stage <= MX_STAGE_COMBINE; ++stage)
     if (int s = launch_stage(L, stage, st)) return s;
   return MX_OK;
@@ -1923,66 +1865,12 @@ int mx_layer_time_stage(mx_layer* L, int32_t stage, int32_t iters, float* us_per
 // ------------------------------------------------------------------------------------------------
 // Single expert, T tokens (ExpertExecutor.execute / ResidentSharedExpert.forward)
 
-int mx_expert_forward(mx_ctx* ctx, const mx_expert_ptrs* w, int32_t format, int32_t H, int32_t I,
-                      const uint16_t* x, int32_t T, float limit, const float* route_w, uint16_t* y,
-                      const mx_expert_stages* stages, void* stream) {
-  if (int s = use(ctx)) return s;
-  MX_REQUIRE(w != nullptr, "mx_expert_forward: null expert pointers");
-  MX_REQUIRE(format == MX_FMT_MXFP4, "mx_expert_forward: only the MXFP4 format runs on this path");
-  MX_REQUIRE(H > 0 && H % 128 == 0 && I > 0 && I % 128 == 0, "expert shapes must be positive multiples of 128");
-  MX_REQUIRE(T >= 0 && T <= kMaxTokens, "token count %d outside [0, %d]", T, kMaxTokens);
-  MX_REQUIRE(std::isfinite(limit) && limit >= 0.f, "Invalid SwiGLU limit");
-  if (int s = check_expert_ptrs(*w, "mx_expert_forward")) return s;
-  if (T == 0) return MX_OK;
-  MX_REQUIRE(x && y && aligned(x, 16) && aligned(y, 16), "x and y must be 16-byte aligned device pointers");
-  hipStream_t st = as_stream(stream);
-  // scratch: plan | xq | xs | dq | ds (stage buffers replace them when supplied)
-  const uint64_t plan_b = (sizeof(Plan) + 255) & ~255ull;
-  const uint64_t xq_b = ((uint64_t)T * H + 255) & ~255ull, xs_b = ((uint64_t)T * H / 32 + 255) & ~255ull;
-  const uint64_t dq_b = ((uint64_t)T * I + 255) & ~255ull, ds_b = ((uint64_t)T * I / 32 + 255) & ~255ull;
-  void* base = nullptr;
-  if (int s = mxi::scratch(ctx, plan_b + xq_b + xs_b + dq_b + ds_b, &base)) return s;
-  uint8_t* b8 = (uint8_t*)base;
-  Plan* plan = (Plan*)b8;
-  uint8_t* xq = (stages && stages->q) ? stages->q : b8 + plan_b;
-  uint8_t* xs = (stages && stages->s) ? stages->s : b8 + plan_b + xq_b;
-  uint8_t* dq = (stages && stages->down_q) ? stages->down_q : b8 + plan_b + xq_b + xs_b;
-  uint8_t* ds = (stages && stages->down_s) ? stages->down_s : b8 + plan_b + xq_b + xs_b + dq_b;
-  MX_REQUIRE(aligned(xq, 16) && aligned(dq, 16) && aligned(xs, 4) && aligned(ds, 4),
-             "stage buffers q/down_q must be 16-byte and s/down_s 4-byte aligned");
-  hipLaunchKernelGGL(single_plan_kernel, dim3(1), dim3(64), 0, st, plan, T, route_w);
-  MX_LAUNCH_CHECK("single_plan_kernel");
-  if (int s = mx_act_quant32(ctx, x, xq, xs, T, H, stream)) return s;
-  ExpertArgs a{};
-  a.single = *w;
-  a.plan = plan;
-  a.H = H;
-  a.I = I;
-  a.limit = limit;
-  a.xq = xq;
-  a.xs = xs;
-  a.dq = dq;
-  a.ds = ds;
-  a.out = y;
-  if (stages) {
-    a.w1 = stages->w1;
-    a.w3 = stages->w3;
-    a.din = stages->down_input;
-    a.trace = stages->trace;
-  }
-  hipLaunchKernelGGL(gateup_kernel<false>, dim3(I / 32, 1), dim3(256), 0, st, a);
-  MX_LAUNCH_CHECK("gateup_kernel");
-  hipLaunchKernelGGL(down_kernel<false>, dim3(H / 64, 1), dim3(256), 0, st, a);
-  MX_LAUNCH_CHECK("down_kernel");
-  return MX_OK;
-}
-
-// Bytes of device scratch one tiled expert call needs: plan | one-entry expert table | xq | xs | dq | ds.
+// Bytes of device scratch one tiled expert call needs: plan | one-entry expert table | xq | xs | dq | ds | xd.
 static uint64_t tiled_call_scratch_bytes(int32_t H, int32_t I, int32_t T) {
   const uint64_t plan_b = (sizeof(Plan) + 255) & ~255ull, table_b = 256;
   const uint64_t xq_b = ((uint64_t)T * H + 255) & ~255ull, xs_b = ((uint64_t)T * H / 32 + 255) & ~255ull;
   const uint64_t dq_b = ((uint64_t)T * I + 255) & ~255ull, ds_b = ((uint64_t)T * I / 32 + 255) & ~255ull;
-  return plan_b + table_b + xq_b + xs_b + dq_b + ds_b;
+  return plan_b + table_b + xq_b + xs_b + dq_b + ds_b + 2 * xq_b;
 }
 
 static int check_tiled_call(const char* what, const void* tiled, int32_t H, int32_t I, const uint16_t* x, int32_t T,
@@ -2003,10 +1891,11 @@ static int tiled_call_on(mx_ctx* ctx, uint8_t* b8, const void* tiled, int32_t H,
   hipStream_t st = as_stream(stream);
   const uint64_t plan_b = (sizeof(Plan) + 255) & ~255ull, table_b = 256;
   const uint64_t xq_b = ((uint64_t)T * H + 255) & ~255ull, xs_b = ((uint64_t)T * H / 32 + 255) & ~255ull;
-  const uint64_t dq_b = ((uint64_t)T * I + 255) & ~255ull;
+  const uint64_t dq_b = ((uint64_t)T * I + 255) & ~255ull, ds_b = ((uint64_t)T * I / 32 + 255) & ~255ull;
   Plan* plan = (Plan*)b8;
   const uint8_t** table = (const uint8_t**)(b8 + plan_b);
   uint8_t* cur = b8 + plan_b + table_b;
+  uint16_t* xd = (uint16_t*)(cur + xq_b + xs_b + dq_b + ds_b);
   uint8_t* xq = (stages && stages->q) ? stages->q : cur;
   uint8_t* xs = (stages && stages->s) ? stages->s : cur + xq_b;
   uint8_t* dq = (stages && stages->down_q) ? stages->down_q : cur + xq_b + xs_b;
@@ -2017,9 +1906,10 @@ static int tiled_call_on(mx_ctx* ctx, uint8_t* b8, const void* tiled, int32_t H,
   MX_LAUNCH_CHECK("set_expert_kernel");
   hipLaunchKernelGGL(single_plan_kernel, dim3(1), dim3(64), 0, st, plan, T, route_w);
   MX_LAUNCH_CHECK("single_plan_kernel");
-  if (int s = mx_act_quant32(ctx, x, xq, xs, T, H, stream)) return s;
+  if (int s = act_quant32_scaled(ctx, x, xq, xs, xd, T, H, st)) return s;
   ExpertArgs a{};
   a.tiles = table;
+  a.xd = xd;
   a.plan = plan;
   a.H = H;
   a.I = I;
@@ -2035,11 +1925,34 @@ static int tiled_call_on(mx_ctx* ctx, uint8_t* b8, const void* tiled, int32_t H,
     a.din = stages->down_input;
     a.trace = stages->trace;
   }
-  hipLaunchKernelGGL(gateup_kernel<true>, dim3(I / 32, 1), dim3(256), 0, st, a);
+  a.tokens = T;
+  hipLaunchKernelGGL(gateup_kernel, dim3(I / 32, 1), dim3(256), kXStages * xstage_bytes(T), st, a);
   MX_LAUNCH_CHECK("gateup_kernel");
   hipLaunchKernelGGL(down_kernel<true>, dim3(H / 64, 1), dim3(256), 0, st, a);
   MX_LAUNCH_CHECK("down_kernel");
   return MX_OK;
+}
+
+int mx_expert_forward(mx_ctx* ctx, const mx_expert_ptrs* w, int32_t format, int32_t H, int32_t I,
+                      const uint16_t* x, int32_t T, float limit, const float* route_w, uint16_t* y,
+                      const mx_expert_stages* stages, void* stream) {
+  if (int s = use(ctx)) return s;
+  MX_REQUIRE(w != nullptr, "mx_expert_forward: null expert pointers");
+  MX_REQUIRE(format == MX_FMT_MXFP4, "mx_expert_forward: only the MXFP4 format runs on this path");
+  MX_REQUIRE(H > 0 && H % 128 == 0 && I > 0 && I % 128 == 0, "expert shapes must be positive multiples of 128");
+  MX_REQUIRE(T >= 0 && T <= kMaxTokens, "token count %d outside [0, %d]", T, kMaxTokens);
+  MX_REQUIRE(std::isfinite(limit) && limit >= 0.f, "Invalid SwiGLU limit");
+  if (int s = check_expert_ptrs(*w, "mx_expert_forward")) return s;
+  if (T == 0) return MX_OK;
+  MX_REQUIRE(x && y && aligned(x, 16) && aligned(y, 16), "x and y must be 16-byte aligned device pointers");
+  // the reference layout is tiled into scratch (one pass over the expert's bytes) and the tiled call runs on it
+  const uint64_t blob_b = (tiled_offsets(H, I).total + 255) & ~255ull;
+  void* base = nullptr;
+  if (int s = mxi::scratch(ctx, blob_b + tiled_call_scratch_bytes(H, I, T), &base)) return s;
+  uint8_t* b8 = (uint8_t*)base;
+  hipLaunchKernelGGL(tile_expert_kernel, dim3(2048), dim3(256), 0, as_stream(stream), *w, b8, H, I, 1);
+  MX_LAUNCH_CHECK("tile_expert_kernel");
+  return tiled_call_on(ctx, b8 + blob_b, b8, H, I, x, T, limit, route_w, y, stages, stream);
 }
 
 int mx_expert_forward_tiled(mx_ctx* ctx, const void* tiled, int32_t H, int32_t I, const uint16_t* x, int32_t T,
