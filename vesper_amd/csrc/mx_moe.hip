@@ -834,32 +834,46 @@ __device__ __forceinline__ void asm_copy16(const uint8_t* base, uint32_t off, ui
 // enough to stay cached, read with plain loads.
 __device__ __align__(256) uint8_t exact_dummy_page[1024];
 
-// Exact-core LDS ring: kXStages stages, each the scale words (256 B) and the slot's token rows of one chunk's
-// scaled activations (256 B each, in groups of 4: xstage_bytes(T) with the call's token count T bounding every
-// slot's). The ring lives in the launch's dynamic LDS.
-constexpr int kXStages = 6;
-constexpr int kXStageScale = 0, kXStageAct = 256;
-__host__ __device__ constexpr int xstage_bytes(int T) { return 256 + 1024 * ((T + 3) / 4); }
+// Exact-core LDS ring: kXStages stages of kStageChunks chunks each: the chunks' scale words (256 B each, 1 KB)
+// and, per token of the slot, the chunks' scaled activations (256 B each, 1 KB per token); xstage_bytes(T)
+// with the call's token count T bounding every slot's. The ring lives in the launch's dynamic LDS.
+constexpr int kStageChunks = 4;
+constexpr int kXStages = 2;
+constexpr int kXStageScale = 0, kXStageAct = 1024;
+__host__ __device__ constexpr int xstage_bytes(int T) { return 1024 + 1024 * T; }
 
-// Chunk c's shared operands into stage st: wave 0 copies the scale words, wave w the token rows 4w .. 4w + 3
-// (one copy instruction each) when the slot has such tokens. Past the last chunk the same copies read the dummy
-// page (the stage is never read again), so a wave issues the same number of loads every iteration.
+// Stage g's shared operands (chunks 4g .. 4g + 3) into ring slot st, one 1 KB copy instruction each: the scale
+// words, and one per token (token j by wave j % 4, the scale words by wave ntok % 4). In a last stage holding
+// fewer than 4 chunks the lanes past the row's end copy its first bytes instead (those LDS bytes are never
+// read), and past the last stage the copies read the dummy page, so a wave issues the same number of copies for
+// every stage.
 struct SharedCopies {
-  const uint8_t* scale;   // row group's scale words (chunk c at + 256 c); lane offset 4 lane
-  const uint8_t* act;     // the scaled activations (chunk c at + 256 c); lane offset act_off
-  const uint8_t* dummy;   // exact_dummy_page; lane offsets 4 lane / 16 lane
-  uint32_t act_off;       // this lane's token row (2 H bytes each) + 16 (lane & 15)
+  const uint8_t* scale;   // row group's scale words (chunk c at + 256 c)
+  const uint8_t* act;     // the scaled activations (token t's row at + 2 H t)
+  const uint8_t* dummy;   // exact_dummy_page
+  uint32_t act_row[kMaxTokens / 4];   // byte offsets of this wave's tokens' rows
+  int act_tok[kMaxTokens / 4];        // and their token indices within the slot
+  int n_act;                          // how many tokens this wave copies
+  int n;                              // chunks of the row
   uint32_t lane;
   uint32_t lds;           // the ring's LDS byte address
   int stage_bytes;
-  bool copies_scale, copies_act;
-  int wave;
-  __device__ __forceinline__ void issue(int c, int n, int st) const {
+  bool copies_scale;
+  __device__ __forceinline__ int copies() const { return n_act + (copies_scale ? 1 : 0); }
+  __device__ __forceinline__ void issue(int g, int st) const {
     const uint32_t base = lds + st * stage_bytes;
-    const bool real = c < n;
-    if (copies_scale) asm_copy4(real ? scale + (size_t)c * 256 : dummy, 4 * lane, base + kXStageScale);
-    if (copies_act)
-      asm_copy16(real ? act + (size_t)c * 256 : dummy, real ? act_off : 16 * lane, base + kXStageAct + 1024 * wave);
+    if (kStageChunks * g < n) {
+      const uint32_t k = (int)lane < 16 * (n - kStageChunks * g) ? (uint32_t)g * 1024 + 16 * lane : 0;
+      if (copies_scale) asm_copy16(scale, k, base + kXStageScale);
+#pragma unroll
+      for (int i = 0; i < kMaxTokens / 4; ++i)
+        if (i < n_act) asm_copy16(act, act_row[i] + k, base + kXStageAct + 1024 * act_tok[i]);
+    } else {
+      if (copies_scale) asm_copy16(dummy, 16 * lane, base + kXStageScale);
+#pragma unroll
+      for (int i = 0; i < kMaxTokens / 4; ++i)
+        if (i < n_act) asm_copy16(dummy, 16 * lane, base + kXStageAct + 1024 * act_tok[i]);
+    }
   }
 };
 
@@ -924,16 +938,16 @@ __device__ __forceinline__ void exact_chunk(const u32x4_t& wa, const u32x4_t (&x
   }
 }
 
-// The whole K range (n chunks) of tile `wave` of a row group. Per iteration k a wave waits until its own copies
-// of chunk k have landed, a barrier makes every wave's copies visible, and the wave reads chunk k's stage and
-// multiplies chunk k; it then issues its copies for chunk k + kXStages - 1 (into the stage of chunk k - 1, which
-// every wave read before this iteration's barrier) and its weights for chunk k + kW. Past the end the weights
-// load from the dummy page and the copies read it, so every iteration issues the same `loads` instructions per
-// wave: when a wave waits for its copies of chunk k, at most 1 + (kXStages - 2) x loads loads issued after them
-// may still be in flight (its weights of chunk k were issued kW - kXStages + 1 iterations before those copies),
-// and a wave without copies waits for its weights of chunk k (kW - 1 later loads in flight).
-constexpr int kWRing = 6;
-static_assert(kWRing % kXStages == 0 && kWRing >= kXStages, "stage and weight slot indices are static per pass");
+// The whole K range (n chunks) of tile `wave` of a row group, stage by stage. At the
+// start of stage g a wave waits until its own copies of stage g have landed, a barrier makes every wave's copies
+// visible, and the wave issues its copies of stage g + kXStages - 1 (into the ring slot of stage g - 1, which
+// every wave finished reading before this barrier); then for each chunk c of the stage it reads the chunk's
+// operands from LDS, multiplies chunk c and issues its weights for chunk c + kW. kW = kXStages x kStageChunks,
+// so the weights of a stage's chunks are issued before that stage's copies, and past the end weights load from
+// the dummy page and copies read it: every stage issues the same loads per wave, and when a wave waits for its
+// copies of stage g, the loads issued after them -- the weights of stage g - kXStages + 1's chunks and, per
+// later stage, copies + kStageChunks weights -- may still be in flight.
+constexpr int kWRing = kXStages * kStageChunks;
 
 template <int kAfter>
 __device__ __forceinline__ void vm_wait() {
@@ -941,43 +955,61 @@ __device__ __forceinline__ void vm_wait() {
   __builtin_amdgcn_s_waitcnt(mxd::vm_wait_imm(kAfter));
 }
 
+// wait for this wave's copies of a stage, with `copies` copy instructions per stage (0 .. 5)
+template <int kCopies>
+__device__ __forceinline__ void wait_stage() {
+  vm_wait<kStageChunks + (kXStages - 2) * (kCopies + kStageChunks)>();
+}
+
 __device__ __forceinline__ void stream_exact(const uint8_t* wbase, uint32_t woff, const SharedCopies& sc,
                                              uint32_t xaddr, uint32_t caddr, int n, v4f& acc) {
-  constexpr int kW = kWRing, kX = kXStages;
-  const int sb = sc.stage_bytes;
+  constexpr int kW = kWRing, kX = kXStages, kC = kStageChunks;
+  const int sb = sc.stage_bytes, n_stages = (n + kC - 1) / kC, copies = sc.copies();
   acc = v4f{0.f, 0.f, 0.f, 0.f};
   u32x4_t wr[kW];
-  const int copies = (int)sc.copies_scale + (int)sc.copies_act;   // per iteration, uniform per wave
   auto load_w = [&](u32x4_t& r, int c) {
     if (c < n) r = asm_ldg128_nt(wbase + (size_t)c * 4096, woff);
     else r = asm_ldg128(sc.dummy, 16 * sc.lane);
   };
-  // the loads of iterations -kW .. -1 in the steady state's order: iteration k issues C(k + kX - 1) (when that
-  // chunk index is not negative), then W(k + kW)
+  // the loads of stages -kX .. -1 in the steady state's order: stage g issues C(g + kX - 1) (when that stage
+  // index is not negative), then the weights of chunks kC g + kW .. kC g + kW + kC - 1
 #pragma unroll
-  for (int vk = -kW; vk < 0; ++vk) {
-    if (vk + kX - 1 >= 0) sc.issue(vk + kX - 1, n, (vk + kX - 1) % kX);
-    load_w(wr[vk + kW], vk + kW);
+  for (int vg = -kX; vg < 0; ++vg) {
+    if (vg + kX - 1 >= 0) sc.issue(vg + kX - 1, (vg + kX - 1) % kX);
+#pragma unroll
+    for (int u = 0; u < kC; ++u) load_w(wr[kC * (vg + kX) + u], kC * vg + kW + u);
   }
-  for (int i = 0; i < n; i += kW) {
+  for (int g0 = 0; g0 < n_stages; g0 += kX) {
 #pragma unroll
-    for (int j = 0; j < kW; ++j) {
-      const int k = i + j;
-      // the wait and the tie run for every slot, past the end too: a slot's registers are only released (and
+    for (int gs = 0; gs < kX; ++gs) {
+      const int g = g0 + gs;
+      // the waits and ties run for every slot, past the end too: a slot's registers are only released (and
       // reusable by the compiler) once the load that writes them has landed
-      if (copies == 2) vm_wait<1 + (kX - 2) * 3>();
-      else if (copies == 1) vm_wait<1 + (kX - 2) * 2>();
-      else vm_wait<kW - 1>();
-      asm volatile("" : "+v"(wr[j]));   // the weights of chunk k landed with the wait above
-      if (k < n) {
-        mxd::copy_barrier();   // every wave's copies of chunk k have landed
-        u32x4_t xb[4];
-        uint32_t code[4];
-        lds_read_stage(xaddr + (j % kX) * sb, caddr + (j % kX) * sb, xb, code);
-        exact_chunk(wr[j], xb, code, acc);
+      switch (copies) {
+        case 0: wait_stage<0>(); break;
+        case 1: wait_stage<1>(); break;
+        case 2: wait_stage<2>(); break;
+        case 3: wait_stage<3>(); break;
+        case 4: wait_stage<4>(); break;
+        default: wait_stage<5>(); break;
       }
-      sc.issue(k + kX - 1, n, (j + kX - 1) % kX);
-      load_w(wr[j], k + kW);
+#pragma unroll
+      for (int u = 0; u < kC; ++u) asm volatile("" : "+v"(wr[kC * gs + u]));   // landed with the wait above
+      // every wave's copies of stage g have landed, and every wave has finished reading stage g - 1, whose slot
+      // this stage's copies overwrite (past the last stage only that one is still read)
+      if (g <= n_stages) mxd::copy_barrier();
+      sc.issue(g + kX - 1, (gs + kX - 1) % kX);
+#pragma unroll
+      for (int u = 0; u < kC; ++u) {
+        const int c = kC * g + u;
+        if (c < n) {
+          u32x4_t xb[4];
+          uint32_t code[4];
+          lds_read_stage(xaddr + gs * sb + 256 * u, caddr + gs * sb + 256 * u, xb, code);
+          exact_chunk(wr[kC * gs + u], xb, code, acc);
+        }
+        load_w(wr[kC * gs + u], c + kW);
+      }
     }
   }
   // drain: no load may still be writing a ring register, and no copy the LDS, once the loop is left
@@ -1166,19 +1198,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void g
   const uint32_t ring0 = mxd::lds_addr(ring);
   SharedCopies sc;
   sc.scale = blob + tiled_offsets(H, I).gu_s + (size_t)g * chunks * 256;
-  const int copy_tok = 4 * wave + (lane >> 4);   // the token row this lane copies
   sc.act = reinterpret_cast<const uint8_t*>(a.xd);
-  sc.act_off = (uint32_t)plan->slot_tok[s][copy_tok < ntok ? copy_tok : 0] * (uint32_t)(2 * H) + 16 * (lane & 15);
+  sc.n_act = 0;
+#pragma unroll
+  for (int i = 0; i < kMaxTokens / 4; ++i) {   // tokens wave, wave + 4, ... of the slot
+    const int j = wave + 4 * i;
+    sc.act_tok[i] = j;
+    sc.act_row[i] = (uint32_t)plan->slot_tok[s][j < ntok ? j : 0] * (uint32_t)(2 * H);
+    if (j < ntok) sc.n_act = i + 1;
+  }
   sc.dummy = exact_dummy_page;
+  sc.n = (int)chunks;
   sc.lane = lane;
   sc.lds = ring0;
   sc.stage_bytes = xstage_bytes(a.tokens);
-  sc.copies_scale = wave == 0;
-  sc.copies_act = 4 * wave < ntok;
-  sc.wave = wave;
+  sc.copies_scale = wave == (ntok & 3);
   // this lane's LDS operands: token column n's row (the slot's first token for idle columns) at K 8 q, and the
   // scale byte of tile `wave` for row m (word m + 16 b holds block b)
-  const uint32_t xaddr = ring0 + kXStageAct + 256 * (n < ntok ? n : 0) + 16 * q;
+  const uint32_t xaddr = ring0 + kXStageAct + 1024 * (n < ntok ? n : 0) + 16 * q;
   const uint32_t caddr = ring0 + kXStageScale + 4 * m + wave;
   const uint8_t* wbase = blob + (size_t)g * chunks * 4096 + (size_t)wave * 1024;
   v4f acc;
