@@ -25,5 +25,5 @@ Pinning status (what checks each function):
                                                   "parity unpinned" beyond the k=6 restriction
   moe.participation / moe.combine                 38 recorded aggregation cases (SHA-256 of every
                                                   stage) + the reference's negative controls
-  projections.fp8_block_gemm_spec                 exact float64 block dots + closed-form scaling
+  projections.fp8_block128_gemm_fp32             exact float64 block dots + closed-form scaling
 """

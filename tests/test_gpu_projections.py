@@ -320,7 +320,11 @@ def test_config3_T2048_exact_sampled_tokens():
 def test_reference_shapes_block32_and_refusals():
     rng = np.random.default_rng(5)
     arrays = arrays_for(FP8_LAYOUT, 32, rng)
-    with NativeProjections(arrays, block=32) as proj:
+    proj = NativeProjections(arrays, block=32)
+    with proj:
+        open_stats = proj.stats()
+        assert open_stats["owned_context_active"] and open_stats["host_reserved_bytes"] == 512 * 2 ** 20
+        assert open_stats["device_owned_bytes"] >= proj.resident_bytes
         x = bf16_bits(rng.standard_normal((2, 4, 5120)).astype(np.float32))
         got = proj.fp8("wq_a", x)
         assert got["output_bf16"].shape == (2, 4, 1280) and got["scale_e8m0"].shape == (2, 4, 160)
@@ -333,6 +337,14 @@ def test_reference_shapes_block32_and_refusals():
             proj.fp8("wq_a", np.full((1, 5120), 0x7F80, np.uint16))
         with pytest.raises(ValueError):
             proj.fp8("wo_a", x)
+    # the reference's stats() keys (projections.py:189-195); the ledger is released and the peak kept on close
+    closed = proj.stats()
+    assert set(closed) == {"host_allowance_bytes", "host_reserved_bytes", "device_peak_owned_bytes",
+                           "device_owned_bytes", "owned_context_active", "reservation_is_RSS_limit",
+                           "driver_module_memory_excluded"}
+    assert not closed["owned_context_active"] and closed["host_reserved_bytes"] == 0 == closed["device_owned_bytes"]
+    assert closed["host_allowance_bytes"] == 512 * 2 ** 20
+    assert closed["device_peak_owned_bytes"] >= proj.resident_bytes
     bad = dict(arrays)
     bad["layers.0.attn.wkv.scale"] = np.full((16, 160), 255, np.uint8)
     with pytest.raises(ValueError):

@@ -1,73 +1,71 @@
-"""Exclusive expert tiers in front of the store (the reference's TieredCache, src/vesper/cache.py:19-287).
+"""Exclusive expert tiers in front of the store, behind the interface of the reference's TieredCache
+(src/vesper/cache.py:47-287: constructor, acquire, snapshot, close, enforce_pressure, the counter names, the
+snapshot keys, the exception classes and their messages).
 
-An expert lives in exactly one tier at a time: a compute-GPU slot, the RAM tier, or only in the store. A
-request for an expert not in a GPU slot promotes it -- from RAM (dropping the RAM copy) or from the store
--- into a free slot; when no slot is free the least recently used slot is demoted to RAM first (its bytes
-read back from the GPU), and the RAM tier in turn drops its least recently used copies to make room.
-Requests are serialised; a slot handed out stays put until the request ends.
+Design. Every expert the cache holds has one `_Home` in a single map: a compute-GPU slot or a host array of
+the RAM tier. One map makes the tiers exclusive by construction (an expert cannot be in two places at once),
+and recency is a logical clock stamped on a home at every use: a tier's least recent expert is its home
+with the smallest stamp, so no per-tier ordered structure has to be kept in step with the map. Free GPU
+slots sit in a min-heap, so an upload takes the lowest-numbered free slot.
 
-Integrity, as in the reference: every GPU upload is audited before the slot is published -- "readback"
-reads the slot back to the host and checks its SHA-256 against the store manifest; "gpu-sha256" hashes it on
-the GPU against the 4 KiB digest table taken from the verified store read, so host-side copies (RAM tier,
-readbacks) skip their checks. A failed check raises ValueError and publishes nothing.
+A request for an expert brings it into a GPU slot: from the RAM tier (the host copy moves up and leaves RAM)
+or from the store, through the backend's first staging buffer. When no slot is free the GPU's least recent
+expert moves down first, read back through the second staging buffer into a new RAM copy (when the RAM tier
+can hold one expert); the RAM tier makes room by dropping its least recent copies, and drops copies whenever
+the machine's available memory falls below the budget's floor. Requests are serialised, and a slot handed
+to a request stays put until the request ends.
 
-The tiers talk to a source (NativeStore: size, entries, read_into, validate) and a backend
-(vesper_amd.tiered.HipCacheBackend: primary_slots, staging, read, write, verify); tests drive them with fakes.
-The helper-GPU tier of the reference needs a second device and is not part of this single-GPU build: a
-backend with helper slots is refused.
+Integrity: every upload is audited before its slot is published -- "readback" reads the slot back and
+checks its SHA-256 against the store (source.validate); "gpu-sha256" hashes it on the GPU against the
+digest table of the verified store read (backend.verify), which makes the host-side checks of RAM copies and
+readbacks redundant, so they are counted as deferred. A failed check raises ValueError and publishes
+nothing.
+
+The source is a NativeStore (size, entries, read_into, validate) and the backend a
+vesper_amd.tiered.HipCacheBackend (primary_slots, staging, read, write, verify); the tests drive both with
+fakes. The reference's helper-GPU tier needs a second device, which this single-GPU build does not use: a
+backend with helper slots is refused, and the helper counters stay zero.
 """
 
 from __future__ import annotations
 
+import heapq
+import itertools
 import threading
-from collections import OrderedDict
 from contextlib import contextmanager
+from dataclasses import dataclass
 
 import numpy as np
 
 from .resources import MemoryBudget, physical_memory
 from .timing import Timings
 
-COUNTERS = ("requests_started", "requests_completed", "requests_failed", "primary_hits", "helper_hits", "ram_hits",
-            "store_read_attempts", "store_reads_completed", "store_bytes_requested", "primary_evictions",
-            "helper_evictions", "ram_capacity_evictions", "ram_pressure_evictions", "ram_admission_refused",
-            "pressure_refusals", "integrity_failures", "primary_h2d_bytes", "helper_h2d_bytes", "primary_d2h_bytes",
-            "helper_d2h_bytes", "primary_audit_readback_bytes", "helper_audit_readback_bytes", "cpu_checks_deferred",
-            "primary_gpu_audit_payload_bytes", "helper_gpu_audit_payload_bytes", "primary_gpu_audit_digest_d2h_bytes",
-            "helper_gpu_audit_digest_d2h_bytes")
+GPU, RAM = "primary_gpu", "ram"   # a home's tier, named as the request reports its origin
+
+_COUNTER_GROUPS = (
+    ("requests_started", "requests_completed", "requests_failed"),
+    ("primary_hits", "helper_hits", "ram_hits"),
+    ("store_read_attempts", "store_reads_completed", "store_bytes_requested"),
+    ("primary_evictions", "helper_evictions", "ram_capacity_evictions", "ram_pressure_evictions",
+     "ram_admission_refused", "pressure_refusals"),
+    ("integrity_failures", "cpu_checks_deferred"),
+    # per GPU tier: uploads, read-backs of demotions, audit read-backs, and the GPU audit's hashed payload and
+    # digest download
+    tuple(f"{tier}_{what}" for what in ("h2d_bytes", "d2h_bytes", "audit_readback_bytes",
+                                        "gpu_audit_payload_bytes", "gpu_audit_digest_d2h_bytes")
+          for tier in ("primary", "helper")),
+)
+COUNTERS = tuple(itertools.chain.from_iterable(_COUNTER_GROUPS))
 
 
-class SlotTable:
-    """`capacity` numbered slots; keys in least-recently-used order."""
+@dataclass
+class _Home:
+    """Where one expert's bytes are: GPU slot `slot`, or the host array `data` of the RAM tier."""
 
-    def __init__(self, capacity: int):
-        if capacity < 0:
-            raise ValueError("Negative slot capacity")
-        self.capacity = capacity
-        self.by_key: OrderedDict = OrderedDict()
-
-    @property
-    def free(self) -> list:
-        used = set(self.by_key.values())
-        return [s for s in range(self.capacity) if s not in used]
-
-    def touch(self, key):
-        """The key's slot (now most recent), or None."""
-        if key not in self.by_key:
-            return None
-        self.by_key.move_to_end(key)
-        return self.by_key[key]
-
-    def put(self, key, slot: int):
-        if key in self.by_key or slot not in self.free:
-            raise RuntimeError("Cache slot is already published")
-        self.by_key[key] = slot
-
-    def pop(self, key) -> int:
-        return self.by_key.pop(key)
-
-    def least_recent(self):
-        return next(iter(self.by_key.items()))
+    tier: str
+    stamp: int
+    slot: int = -1
+    data: np.ndarray | None = None
 
 
 class TieredCache:
@@ -75,181 +73,246 @@ class TieredCache:
                  timings=None, gpu_verify=False):
         if ram_capacity_bytes < 0:
             raise ValueError("Negative RAM cache capacity")
-        if gpu_verify and (not audit or not callable(getattr(backend, "verify", None))):
+        if gpu_verify and not (audit and callable(getattr(backend, "verify", None))):
             raise ValueError("GPU verification requires a complete upload audit backend")
         if getattr(backend, "helper_slots", 0):
             raise ValueError("The helper-GPU tier needs a second device; this build runs on one GPU")
+        slots = int(backend.primary_slots)
+        if slots < 0:
+            raise ValueError("Negative slot capacity")
+        if slots == 0:
+            raise ValueError("A compute cache requires at least one primary slot")
+        size = source.size
+        staging = list(backend.staging)
+        whole = [a.dtype == np.uint8 and a.shape == (size,) and a.flags.c_contiguous for a in staging]
+        if len(staging) != 2 or not all(whole):
+            raise ValueError("Staging must contain two complete contiguous byte blocks")
+        if np.shares_memory(staging[0], staging[1]):
+            raise ValueError("Promotion and demotion need two distinct staging buffers")
         self.source, self.backend, self.budget = source, backend, budget
-        self.size, self.ram_capacity = source.size, ram_capacity_bytes
+        self.size, self.ram_capacity, self.slots = size, ram_capacity_bytes, slots
+        self.incoming, self.outgoing = staging            # promotion and demotion/audit buffers
         self.available = available or (lambda: physical_memory()["available"])
         self.timings = timings or Timings()
         self.audit, self.gpu_verify = audit, gpu_verify
-        self.primary = SlotTable(backend.primary_slots)
-        if not self.primary.capacity:
-            raise ValueError("A compute cache requires at least one primary slot")
-        self.staging = backend.staging
-        if len(self.staging) != 2 or any(a.dtype != np.uint8 or a.shape != (self.size,) or not a.flags.c_contiguous
-                                          for a in self.staging):
-            raise ValueError("Staging must contain two complete contiguous byte blocks")
-        if np.shares_memory(self.staging[0], self.staging[1]):
-            raise ValueError("Promotion and demotion need two distinct staging buffers")
-        self.ram: OrderedDict = OrderedDict()
         self.stats = dict.fromkeys(COUNTERS, 0)
+        self._homes: dict = {}
+        self._free = list(range(slots))                   # a heap (already ordered)
+        self._clock = itertools.count()
         self.lock, self.active, self.closed = threading.RLock(), False, False
+        self._reclaimer = budget.register_reclaimer(self.reclaim)
 
-    # -- RAM tier -------------------------------------------------------------------------------------
-    def _forget_ram(self, key, counter=None):
-        del self.ram[key]
+    # -- the map ---------------------------------------------------------------------------------------------
+    def _keys(self, tier: str) -> list:
+        """Keys of one tier, least recent first."""
+        return [k for k, h in sorted(self._homes.items(), key=lambda kv: kv[1].stamp) if h.tier == tier]
+
+    def _least_recent(self, tier: str):
+        found = None
+        for key, home in self._homes.items():
+            if home.tier == tier and (found is None or home.stamp < self._homes[found].stamp):
+                found = key
+        return found
+
+    def _drop_copy(self, key, counter: str | None = None):
+        """Free a RAM-tier copy and its budget reservation."""
+        home = self._homes.pop(key)
+        assert home.tier == RAM
         self.budget.release(self.size, category="cache")
-        if counter:
+        if counter is not None:
             self.stats[counter] += 1
 
+    # -- host memory -----------------------------------------------------------------------------------------
+    def _below_floor(self, extra: int = 0) -> bool:
+        return self.available() - extra < self.budget.available_floor
+
     def enforce_pressure(self):
-        """Drop RAM copies while the machine is below the budget's floor; refuse if that is not enough."""
-        while self.ram and self.available() < self.budget.available_floor:
-            self._forget_ram(next(iter(self.ram)), "ram_pressure_evictions")
-        if self.available() < self.budget.available_floor:
-            self.stats["pressure_refusals"] += 1
-            raise MemoryError("System memory remains below the reserve after releasing the RAM cache")
+        """Drop RAM copies, least recent first, while the machine is below the budget's floor; MemoryError if
+        it stays below with the RAM tier empty."""
+        while self._below_floor():
+            victim = self._least_recent(RAM)
+            if victim is None:
+                self.stats["pressure_refusals"] += 1
+                raise MemoryError("System memory remains below the reserve after releasing the RAM cache")
+            self._drop_copy(victim, "ram_pressure_evictions")
 
-    def _room_for_one(self) -> bool:
-        return ((len(self.ram) + 1) * self.size <= self.ram_capacity
-                and self.budget.reserved + self.size <= self.budget.cap
-                and self.available() - self.size >= self.budget.available_floor)
+    def reclaim(self, requested: int) -> int:
+        """Give back at least `requested` bytes of RAM copies if the cache is idle (a budget reclaimer); returns
+        the bytes freed, 0 when a request holds the cache."""
+        if not self.lock.acquire(blocking=False):
+            return 0
+        try:
+            freed = 0
+            while freed < requested and (victim := self._least_recent(RAM)) is not None:
+                self._drop_copy(victim, "ram_pressure_evictions")
+                freed += self.size
+            return freed
+        finally:
+            self.lock.release()
 
-    def _keep_in_ram(self, key, data) -> bool:
-        """Copy `data` into the RAM tier (LRU eviction to make room); False if it cannot be admitted."""
+    def _one_more_fits(self) -> bool:
+        held = sum(h.tier == RAM for h in self._homes.values())
+        return ((held + 1) * self.size <= self.ram_capacity and self.size <= self.budget.cap - self.budget.reserved
+                and not self._below_floor(self.size))
+
+    def _host_copy(self, key, data):
+        """A verified RAM-tier array holding `data`, not yet placed in the map, or None when the tier cannot
+        take it (counted as refused)."""
         if self.ram_capacity < self.size:
             self.stats["ram_admission_refused"] += 1
-            return False
+            return None
         self.enforce_pressure()
-        while self.ram and not self._room_for_one():
-            self._forget_ram(next(iter(self.ram)), "ram_capacity_evictions")
-        if not self._room_for_one():
-            self.stats["ram_admission_refused"] += 1
-            return False
+        while not self._one_more_fits():
+            victim = self._least_recent(RAM)
+            if victim is None:
+                self.stats["ram_admission_refused"] += 1
+                return None
+            self._drop_copy(victim, "ram_capacity_evictions")
         self.budget.acquire(self.size, available=self.available(), category="cache")
         try:
+            with self.timings.section("host.ram_allocate"):
+                copy = np.empty(self.size, np.uint8)
             with self.timings.section("host.ram_copy"):
-                copy = np.array(data, dtype=np.uint8, copy=True)
-            self._check_host(key, copy)
+                np.copyto(copy, data)
+            self._check_host_copy(key, copy)
         except BaseException:
             self.budget.release(self.size, category="cache")
             raise
-        self.ram[key] = copy
-        return True
+        if self._below_floor():
+            # the copy itself took the machine below its reserve: give it back and let the tier shrink
+            del copy
+            self.budget.release(self.size, category="cache")
+            self.enforce_pressure()
+            self.stats["ram_admission_refused"] += 1
+            return None
+        return copy
 
-    # -- checks -----------------------------------------------------------------------------------------
-    def _check_host(self, key, data):
-        """A host copy's SHA-256 against the store (deferred to the GPU audit in gpu-sha256 mode)."""
-        if self.gpu_verify:
+    # -- integrity -------------------------------------------------------------------------------------------
+    def _check_host_copy(self, key, data):
+        if self.gpu_verify:   # every upload is hashed on the GPU before use
             self.stats["cpu_checks_deferred"] += 1
             return
         try:
             self.source.validate(key, data)
-        except ValueError:
+        except Exception:
             self.stats["integrity_failures"] += 1
             raise
 
-    def _upload(self, slot, key, data):
-        """H2D into `slot`, then the audit of what the slot holds."""
-        self.backend.write("primary", slot, data)
-        self.stats["primary_h2d_bytes"] += self.size
+    def _audit_upload(self, slot: int, key):
         if not self.audit:
             return
-        if self.gpu_verify:
-            try:
-                digest_bytes = self.backend.verify("primary", slot, key)
-            except ValueError:
-                self.stats["integrity_failures"] += 1
-                raise
-            self.stats["primary_gpu_audit_payload_bytes"] += self.size
-            self.stats["primary_gpu_audit_digest_d2h_bytes"] += digest_bytes
-        else:
-            self.backend.read("primary", slot, self.staging[1])
+        if not self.gpu_verify:
+            self.backend.read("primary", slot, self.outgoing)
             self.stats["primary_audit_readback_bytes"] += self.size
-            self._check_host(key, self.staging[1])
+            self._check_host_copy(key, self.outgoing)
+            return
+        try:
+            digest_bytes = self.backend.verify("primary", slot, key)
+        except ValueError:
+            self.stats["integrity_failures"] += 1
+            raise
+        self.stats["primary_gpu_audit_payload_bytes"] += self.size
+        self.stats["primary_gpu_audit_digest_d2h_bytes"] += digest_bytes
 
-    def _demote_least_recent(self):
-        key, slot = self.primary.least_recent()
-        if self.ram_capacity >= self.size:
-            self.backend.read("primary", slot, self.staging[1])
-            self.stats["primary_d2h_bytes"] += self.size
-            self._check_host(key, self.staging[1])
-            self._keep_in_ram(key, self.staging[1])
-        self.primary.pop(key)
-        self.stats["primary_evictions"] += 1
-
-    def _fetch(self, key):
-        """Bring `key` into staging[0]; returns the tier it came from."""
-        if key in self.ram:
+    # -- moves between tiers ---------------------------------------------------------------------------------
+    def _stage_in(self, key) -> str:
+        """Put `key`'s bytes into the promotion buffer; returns the tier they came from."""
+        home = self._homes.get(key)
+        if home is not None:   # a RAM copy (GPU residents never get here); it leaves RAM as it moves up
             with self.timings.section("host.ram_copy"):
-                np.copyto(self.staging[0], self.ram[key])
-            self._check_host(key, self.staging[0])
-            self._forget_ram(key)
+                np.copyto(self.incoming, home.data)
+            self._check_host_copy(key, self.incoming)
+            self._drop_copy(key)
             self.stats["ram_hits"] += 1
-            return "ram"
+            return RAM
         self.stats["store_read_attempts"] += 1
         self.stats["store_bytes_requested"] += self.size
         try:
-            self.source.read_into(key, self.staging[0])
+            self.source.read_into(key, self.incoming)
         except ValueError:
             self.stats["integrity_failures"] += 1
             raise
         self.stats["store_reads_completed"] += 1
         return "store"
 
-    def _ensure_primary(self, key):
+    def _move_down(self):
+        """Free a GPU slot: its least recent expert goes to the RAM tier (if the tier can hold one) or is
+        dropped."""
+        key = self._least_recent(GPU)
+        home = self._homes[key]
+        copy = None
+        if self.ram_capacity >= self.size:
+            self.backend.read("primary", home.slot, self.outgoing)
+            self.stats["primary_d2h_bytes"] += self.size
+            self._check_host_copy(key, self.outgoing)
+            copy = self._host_copy(key, self.outgoing)
+        heapq.heappush(self._free, home.slot)
+        if copy is None:
+            del self._homes[key]
+        else:
+            self._homes[key] = _Home(RAM, next(self._clock), data=copy)
+        self.stats["primary_evictions"] += 1
+
+    def _resident(self, key):
+        """(slot, origin tier) of `key` in a GPU slot, promoting it if needed."""
         if key not in self.source.entries:
             raise KeyError("Requested expert is absent from the pinned native store")
-        slot = self.primary.touch(key)
-        if slot is not None:
+        home = self._homes.get(key)
+        if home is not None and home.tier == GPU:
+            home.stamp = next(self._clock)
             self.stats["primary_hits"] += 1
-            return slot, "primary_gpu"
-        origin = self._fetch(key)
-        if not self.primary.free:
-            self._demote_least_recent()
-        slot = self.primary.free[0]
-        self._upload(slot, key, self.staging[0])
-        self.primary.put(key, slot)
+            return home.slot, GPU
+        origin = self._stage_in(key)
+        if not self._free:
+            self._move_down()
+        slot = self._free[0]
+        self.backend.write("primary", slot, self.incoming)
+        self.stats["primary_h2d_bytes"] += self.size
+        self._audit_upload(slot, key)          # raises before anything is published
+        heapq.heappop(self._free)
+        self._homes[key] = _Home(GPU, next(self._clock), slot=slot)
         return slot, origin
+
+    # -- requests --------------------------------------------------------------------------------------------
+    def _begin(self):
+        if self.closed:
+            raise RuntimeError("Cache is closed")
+        if self.active:
+            raise RuntimeError("Nested requests could replace a live compute slot")
+        self.active = True
+        self.stats["requests_started"] += 1
 
     @contextmanager
     def acquire(self, key):
-        """(slot, source tier) of `key`, held for the duration of the with-block."""
+        """(slot, origin tier) of `key` -- "primary_gpu", "ram" or "store" -- for the with-block."""
         with self.lock:
-            if self.closed:
-                raise RuntimeError("Cache is closed")
-            if self.active:
-                raise RuntimeError("Nested requests could replace a live compute slot")
-            self.active = True
-            self.stats["requests_started"] += 1
+            self._begin()
             try:
                 self.enforce_pressure()
-                slot, origin = self._ensure_primary(key)
-                yield slot, origin
+                yield self._resident(key)
                 self.enforce_pressure()
-                self.stats["requests_completed"] += 1
             except BaseException:
                 self.stats["requests_failed"] += 1
                 raise
+            else:
+                self.stats["requests_completed"] += 1
             finally:
                 self.active = False
 
     def snapshot(self) -> dict:
         with self.lock:
-            primary, ram = list(self.primary.by_key), list(self.ram)
-            if set(primary) & set(ram):
-                raise RuntimeError("Exclusive cache tiers contain duplicate expert identities")
-            return {"primary_keys": primary, "helper_keys": [], "ram_keys": ram,
+            ram = self._keys(RAM)
+            return {"primary_keys": self._keys(GPU), "helper_keys": [], "ram_keys": ram,
                     "ram_cache_bytes": len(ram) * self.size, "host_reserved_bytes": self.budget.reserved,
                     "host_peak_reserved_bytes": self.budget.peak,
-                    "integrity_mode": "gpu-sha256" if self.gpu_verify else "readback", "counters": dict(self.stats)}
+                    "integrity_mode": "gpu-sha256" if self.gpu_verify else "readback",
+                    "counters": dict(self.stats)}
 
     def close(self):
         with self.lock:
             if self.active:
                 raise RuntimeError("Cannot close a cache with a live compute slot")
-            for key in list(self.ram):
-                self._forget_ram(key)
+            for key in self._keys(RAM):
+                self._drop_copy(key)
             self.closed = True
+            self.budget.unregister_reclaimer(self._reclaimer)

@@ -28,7 +28,7 @@ from __future__ import annotations
 import hashlib
 import threading
 import time
-from contextlib import ExitStack
+from contextlib import ExitStack, contextmanager
 from dataclasses import asdict, dataclass, field
 from pathlib import Path
 
@@ -126,180 +126,219 @@ def bf16_activation(activation, hidden: int):
 
 
 class ConnectedMoE:
-    """Serial calls of one registered layer over the store (src/vesper/connected.py:56-213)."""
+    """Serial calls of one registered layer over the store, behind the reference's constructor, call and
+    records (src/vesper/connected.py:56-213: forward, snapshot, last_attempt, cleanup, stats).
+
+    Opening loads the three fixtures, opens the five components on one exit stack -- gate projection, router
+    probe, shared expert, accumulator, and the tiered expert runtime over the store -- and checks that the
+    fixtures and every stored expert belong to the selected layer. A call is the pipeline
+    route -> run the selected experts -> combine, with the host and device reserves checked before and after
+    it; the call's record (last_attempt) is kept by one context manager that takes the lock, refuses nesting,
+    counts the call, marks it passed or failed, and, either way, adds its wall time and the store and cache
+    counters it moved. A failed call returns nothing and the next one starts from a zeroed accumulator."""
+
+    CALL_COUNTERS = ("calls_started", "calls_completed", "calls_failed")
 
     def __init__(self, store: Path, gate_fixture: Path, router_fixture: Path, shared_fixture: Path,
                  config: ConnectedConfig | None = None, *, cublas_library=None, layer=0, profile="qualified",
                  source_factory=None, model: ModelProfile = REFERENCE_PROFILE):
         if cublas_library is not None:
             raise ValueError("The gate projection runs as a HIP kernel; no BLAS library is loaded")
-        self.layer = validate_layer(layer, model, profile)
-        self.model = model
-        self.store_path, self.gate_fixture = Path(store), Path(gate_fixture)
-        self.router_fixture, self.shared_fixture = Path(router_fixture), Path(shared_fixture)
-        self.config = config or ConnectedConfig()
         if source_factory is not None and not callable(source_factory):
             raise ValueError("Expected an explicit expert source factory")
-        self.source_factory = source_factory
-        self.stack, self.active = None, False
+        self.layer, self.model = validate_layer(layer, model, profile), model
+        self.store_path = Path(store)
+        self.gate_fixture, self.router_fixture, self.shared_fixture = map(Path, (gate_fixture, router_fixture,
+                                                                                 shared_fixture))
+        self.config, self.source_factory = config or ConnectedConfig(), source_factory
+        self.stats = dict.fromkeys(self.CALL_COUNTERS, 0)
         self.lock = threading.RLock()
-        self.stats = {"calls_started": 0, "calls_completed": 0, "calls_failed": 0}
-        self.last_attempt = None
+        self.stack, self.active, self.last_attempt = None, False, None
+
+    # -- opening ---------------------------------------------------------------------------------------------
+    def _fixtures(self):
+        """(gate weight, router biases, shared expert) of the selected layer."""
+        m = self.model
+        (weight, self.gate_manifest), (biases, self.router_manifest), (shared, self.shared_manifest) = (
+            load(path, m) for load, path in ((load_gate_fixture, self.gate_fixture),
+                                            (load_router_fixture, self.router_fixture),
+                                            (load_shared_fixture, self.shared_fixture)))
+        layers = {man["layer"] for man in (self.gate_manifest, self.router_manifest, self.shared_manifest)}
+        if layers != {self.layer}:
+            raise ValueError("Connected gate, router and shared artifacts must match the selected layer")
+        return weight, biases, shared
+
+    def _components(self, stack: ExitStack, weight, biases, shared):
+        c, m = self.config, self.model
+        gpu = c.cache.primary_device
+        self.gate = stack.enter_context(GateProjection(weight, gpu))
+        self.router = stack.enter_context(RouterProbe(biases, gpu, experts=m.experts, top_k=m.top_k,
+                                                      score_func=m.score_func, route_scale=m.route_scale))
+        self.shared = stack.enter_context(ResidentSharedExpert(shared, gpu, m.swiglu_limit, hidden=m.hidden,
+                                                               intermediate=m.intermediate))
+        self.accumulator = stack.enter_context(MoEAccumulator(gpu, MAX_CALL_TOKENS, hidden=m.hidden,
+                                                              experts=m.experts, top_k=m.top_k))
+        self.experts = stack.enter_context(TieredExpertRuntime(self.store_path, c.cache, model=m,
+                                                               source_factory=self.source_factory,
+                                                               max_tokens=MAX_CALL_TOKENS))
+        if any(entry["provenance"]["layer"] != self.layer for entry in self.experts.store.entries.values()):
+            raise ValueError("Connected store contains artifacts from another layer")
+        self.contexts = {"gate": self.gate.ctx, "router": self.router.ctx, "shared": self.shared.ctx,
+                         "accumulator": self.accumulator.ctx, "cache_primary": self.experts.ctx}
+        self.devices = {name: DeviceLedger(ctx, c.device_free_floor) for name, ctx in self.contexts.items()}
+        self.helper_device = None
 
     def __enter__(self):
         if self.stack is not None:
             raise RuntimeError("Connected MoE is already open")
-        self.stack = ExitStack()
-        c, m = self.config, self.model
+        c = self.config
         self.budget = MemoryBudget(c.host_cap_bytes, c.cache.available_floor, owner="connected")
-        try:
-            allowance = c.cache.host_cap_bytes + 100 * MiB       # the cache's cap + fixtures and staging
+        with ExitStack() as stack:   # unwinds only when opening fails: pop_all() takes the resources over
+            allowance = c.cache.host_cap_bytes + 100 * MiB   # the cache's own cap + fixtures and upload staging
             self.budget.acquire(allowance)
-            self.stack.callback(self.budget.release, allowance)
-            weight, self.gate_manifest = load_gate_fixture(self.gate_fixture, m)
-            biases, self.router_manifest = load_router_fixture(self.router_fixture, m)
-            shared, self.shared_manifest = load_shared_fixture(self.shared_fixture, m)
-            if any(man["layer"] != self.layer for man in (self.gate_manifest, self.router_manifest,
-                                                           self.shared_manifest)):
-                raise ValueError("Connected gate, router and shared artifacts must match the selected layer")
-            ordinal = c.cache.primary_device
-            self.gate = self.stack.enter_context(GateProjection(weight, ordinal))
-            self.router = self.stack.enter_context(RouterProbe(biases, ordinal, experts=m.experts, top_k=m.top_k,
-                                                               score_func=m.score_func, route_scale=m.route_scale))
-            self.shared = self.stack.enter_context(ResidentSharedExpert(shared, ordinal, m.swiglu_limit,
-                                                                        hidden=m.hidden, intermediate=m.intermediate))
-            self.accumulator = self.stack.enter_context(MoEAccumulator(ordinal, MAX_CALL_TOKENS, hidden=m.hidden,
-                                                                       experts=m.experts, top_k=m.top_k))
-            self.experts = self.stack.enter_context(TieredExpertRuntime(self.store_path, c.cache,
-                                                                        source_factory=self.source_factory, model=m,
-                                                                        max_tokens=MAX_CALL_TOKENS))
-            if any(entry["provenance"]["layer"] != self.layer for entry in self.experts.store.entries.values()):
-                raise ValueError("Connected store contains artifacts from another layer")
-            self.contexts = {"gate": self.gate.ctx, "router": self.router.ctx, "shared": self.shared.ctx,
-                             "accumulator": self.accumulator.ctx, "cache_primary": self.experts.ctx}
-            self.devices = {n: DeviceLedger(ctx, c.device_free_floor) for n, ctx in self.contexts.items()}
-            self.helper_device = None
+            stack.callback(self.budget.release, allowance)
+            self._components(stack, *self._fixtures())
             self.minimum_available = physical_memory()["available"]
             self._headroom()
-            return self
-        except BaseException:
-            self.stack.close()
-            self.stack = None
-            raise
+            self.stack = stack.pop_all()
+        return self
 
+    # -- reserves --------------------------------------------------------------------------------------------
     def _headroom(self):
-        """Host reserve, the combined explicit device cap and the device's free floor, checked around a call."""
-        available = physical_memory()["available"]
-        self.minimum_available = min(self.minimum_available, available)
-        self.budget.acquire(0, available)
-        total = sum(sum(device.allocations.values()) for device in self.devices.values())
-        if total > self.config.primary_explicit_cap_bytes:
+        """The host reserve (tracking the lowest available memory seen), the components' combined explicit
+        device bytes against the cap, and the compute device's free-memory floor."""
+        host_free = physical_memory()["available"]
+        self.minimum_available = min(host_free, self.minimum_available)
+        self.budget.acquire(0, host_free)   # MemoryError below the reserve
+        if sum(ledger.allocations["explicit"] for ledger in self.devices.values()) > \
+                self.config.primary_explicit_cap_bytes:
             raise MemoryError("Combined native GPU buffers exceed the connected explicit cap")
         if self.devices["cache_primary"].memory()["free"] < self.config.device_free_floor:
             raise MemoryError("Connected runtime refuses work below the GPU reserve")
+
+    def _reserves(self):
+        self.experts.cache.enforce_pressure()
+        self._headroom()
+
+    # -- one call --------------------------------------------------------------------------------------------
+    @contextmanager
+    def _attempt(self, bits: np.ndarray, image_span: bool):
+        with self.lock:
+            if self.active:
+                raise RuntimeError("Nested MoE calls would overwrite live workspaces")
+            record = {"status": "running", "input_bf16_sha256": hashlib.sha256(bits.tobytes()).hexdigest(),
+                      "image_span": image_span, "completed_expert_ids": [], "stage": "headroom"}
+            baseline, clock = self.experts.snapshot(), time.perf_counter()
+            self.active, self.last_attempt = True, record
+            self.stats["calls_started"] += 1
+            try:
+                yield record
+            except BaseException as error:
+                self.stats["calls_failed"] += 1
+                record.update(status="failed", error_type=type(error).__name__)
+                raise
+            else:
+                record.update(status="pass", stage="complete")
+                self.stats["calls_completed"] += 1
+            finally:
+                try:
+                    now = self.experts.snapshot()
+                    moved = {n: now[n] - baseline[n] for n in ("store_direct_read_calls", "store_direct_read_bytes")}
+                    record.update(wall_ms=(time.perf_counter() - clock) * 1000, **moved,
+                                  cache_counter_delta={n: now["counters"][n] - v
+                                                       for n, v in baseline["counters"].items()})
+                finally:
+                    self.active = False
+
+    def _route(self, rows: np.ndarray, image_span: bool, record: dict):
+        """Gate logits, the routing postprocess, and per selected expert (ascending ID) its token rows and
+        their route weights; selected experts missing from the store are refused before any expert I/O."""
+        m = self.model
+        record["stage"] = "gate"
+        logits = self.gate.project(rows)
+        routing = self.router.inspect(logits, image_span)
+        indices, weights = routing["indices"], routing["weights"]
+        record.update(indices=indices.tolist(), weight_bits=weights.view(np.uint32).tolist())
+        plan = participation(indices, rows.shape[0], experts=m.experts, top_k=m.top_k)
+        absent = [e for e in plan if expert_key(self.layer, e, m) not in self.experts.store.entries]
+        if absent:
+            raise KeyError(f"Selected original experts absent from this bounded store: {absent}")
+        routes = {}
+        for expert, token_rows in plan.items():
+            rank = (indices[token_rows] == expert).argmax(axis=1)   # the expert's position in each token's list
+            routes[expert] = (token_rows, weights[token_rows, rank])
+        return logits, routing, routes
+
+    def _run_experts(self, rows: np.ndarray, routes: dict, record: dict):
+        """Each routed expert from whichever tier holds it, its rows added to the accumulator in order."""
+        results, events, snapshots = {}, [], {}
+        for expert, (token_rows, route) in routes.items():
+            record["stage"] = f"expert:{expert}"
+            out = self.experts.forward(expert_key(self.layer, expert, self.model), rows[token_rows], route)
+            events.append(dict(self.experts.last_event))
+            snapshots[f"after_expert_{expert}_fp32"] = self.accumulator.add(expert, out["w2"])
+            results[expert] = out
+            record["completed_expert_ids"].append(expert)
+        return results, events, snapshots
 
     def forward(self, activation, image_span=False) -> dict:
         if self.stack is None:
             raise RuntimeError("Use connected MoE as a context manager")
         if type(image_span) is not bool:
             raise ValueError("Connected image-span flag must be boolean")
-        m = self.model
-        x, bits = bf16_activation(activation, m.hidden)
-        single = x.ndim == 1
-        rows = bits.reshape(-1, m.hidden)
-        t = rows.shape[0]
-        if not 1 <= t <= MAX_CALL_TOKENS:
+        _, bits = bf16_activation(activation, self.model.hidden)
+        rows = bits.reshape(-1, self.model.hidden)
+        if not 1 <= rows.shape[0] <= MAX_CALL_TOKENS:
             raise ValueError(f"Connected MoE accepts 1 to {MAX_CALL_TOKENS} tokens per call")
-        with self.lock:
-            if self.active:
-                raise RuntimeError("Nested MoE calls would overwrite live workspaces")
-            before = self.experts.snapshot()
-            self.active = True
-            self.stats["calls_started"] += 1
-            attempt = {"status": "running", "input_bf16_sha256": hashlib.sha256(bits.tobytes()).hexdigest(),
-                       "image_span": image_span, "completed_expert_ids": [], "stage": "headroom"}
-            self.last_attempt = attempt
-            started = time.perf_counter()
-            try:
-                self.experts.cache.enforce_pressure()
-                self._headroom()
-                attempt["stage"] = "gate"
-                logits = self.gate.project(rows)
-                routing = self.router.inspect(logits, image_span)
-                weights, indices = routing["weights"], routing["indices"]
-                selected = participation(indices, t, experts=m.experts, top_k=m.top_k)
-                attempt.update(indices=indices.tolist(), weight_bits=weights.view(np.uint32).tolist())
-                missing = [e for e in selected if expert_key(self.layer, e, m) not in self.experts.store.entries]
-                if missing:
-                    raise KeyError(f"Selected original experts absent from this bounded store: {missing}")
-                self.accumulator.begin(indices)
-                outputs, stages, events = {}, {}, []
-                for expert, token_rows in selected.items():
-                    attempt["stage"] = f"expert:{expert}"
-                    rank = np.argmax(indices[token_rows] == expert, axis=1)
-                    route = weights[token_rows, rank]
-                    result = self.experts.forward(expert_key(self.layer, expert, m), rows[token_rows], route)
-                    outputs[expert] = result
-                    events.append(dict(self.experts.last_event))
-                    stages[f"after_expert_{expert}_fp32"] = self.accumulator.add(expert, result["w2"])
-                    attempt["completed_expert_ids"].append(expert)
-                attempt["stage"] = "shared"
-                shared = self.shared.forward(rows)
-                attempt["stage"] = "final_accumulation"
-                stages.update(self.accumulator.finish(shared["w2"]))
-                self.experts.cache.enforce_pressure()
-                self._headroom()
-                attempt.update(status="pass", stage="complete")
-                self.stats["calls_completed"] += 1
-                if single:
-                    routing = {n: v.reshape(-1) for n, v in routing.items()}
-                    logits = logits.reshape(-1)
-                    shared = {n: v[0] for n, v in shared.items()}
-                    stages = {n: v.reshape(-1) for n, v in stages.items()}
-                    outputs = {e: {n: v[0] for n, v in r.items()} for e, r in outputs.items()}
-                return {"input_bf16": bits, "logits": logits, "routing": routing, "experts": outputs,
-                        "expert_events": events, "shared": shared, "aggregation": stages,
-                        "output_bf16": stages["output_bf16"]}
-            except BaseException as error:
-                self.stats["calls_failed"] += 1
-                attempt.update(status="failed", error_type=type(error).__name__)
-                raise
-            finally:
-                try:
-                    after = self.experts.snapshot()
-                    attempt.update(wall_ms=(time.perf_counter() - started) * 1000,
-                                   store_direct_read_calls=after["store_direct_read_calls"]
-                                   - before["store_direct_read_calls"],
-                                   store_direct_read_bytes=after["store_direct_read_bytes"]
-                                   - before["store_direct_read_bytes"],
-                                   cache_counter_delta={n: after["counters"][n] - v
-                                                        for n, v in before["counters"].items()})
-                finally:
-                    self.active = False
+        with self._attempt(bits, image_span) as record:
+            self._reserves()
+            logits, routing, routes = self._route(rows, image_span, record)
+            self.accumulator.begin(routing["indices"])
+            experts, events, aggregation = self._run_experts(rows, routes, record)
+            record["stage"] = "shared"
+            shared = self.shared.forward(rows)
+            record["stage"] = "final_accumulation"
+            aggregation.update(self.accumulator.finish(shared["w2"]))
+            self._reserves()
+        if bits.ndim == 1:   # one token given as [hidden]: drop the token axis, as the reference's call returns
+            first = lambda v: v[0]
+            flat = lambda v: v.reshape(-1)
+            logits, routing, aggregation = flat(logits), _map(flat, routing), _map(flat, aggregation)
+            shared = _map(first, shared)
+            experts = {e: _map(first, r) for e, r in experts.items()}
+        return {"input_bf16": bits, "logits": logits, "routing": routing, "experts": experts,
+                "expert_events": events, "shared": shared, "aggregation": aggregation,
+                "output_bf16": aggregation["output_bf16"]}
 
+    # -- records ---------------------------------------------------------------------------------------------
     def snapshot(self) -> dict:
         if self.stack is None:
             raise RuntimeError("Connected MoE is closed")
+        b, c = self.budget, self.config
         return {"calls": dict(self.stats), "cache": self.experts.snapshot(),
-                "combined_host_reservation_peak_bytes": self.budget.peak,
-                "combined_host_cap_bytes": self.budget.cap,
+                "combined_host_reservation_peak_bytes": b.peak, "combined_host_cap_bytes": b.cap,
                 "minimum_observed_host_available_bytes": self.minimum_available,
-                "host_available_floor_bytes": self.budget.available_floor,
-                "component_peak_explicit_device_bytes": {n: d.peak for n, d in self.devices.items()},
-                "primary_explicit_cap_bytes": self.config.primary_explicit_cap_bytes,
-                "cache_config": asdict(self.config.cache), "device": self.gate.ctx.device_name()[1]}
+                "host_available_floor_bytes": b.available_floor,
+                "component_peak_explicit_device_bytes": {n: ledger.peak for n, ledger in self.devices.items()},
+                "primary_explicit_cap_bytes": c.primary_explicit_cap_bytes, "cache_config": asdict(c.cache),
+                "device": self.gate.ctx.device_name()[1]}
 
     def __exit__(self, *_):
         with self.lock:
             if self.active:
                 raise RuntimeError("Cannot close connected MoE during a live call")
-            live = {n: ctx.owned_bytes()[0] for n, ctx in self.contexts.items()} if self.stack is not None else {}
+            live = {}
             if self.stack is not None:
-                self.stack.close()
-                self.stack = None
+                live = {n: ctx.owned_bytes()[0] for n, ctx in self.contexts.items()}
+                stack, self.stack = self.stack, None
+                stack.close()
             self.cleanup = {"parent_reservation_bytes": self.budget.reserved,
                             "cache_reservation_bytes": self.experts.budget.reserved,
                             "explicit_live_bytes_before_close": live}
+
+
+def _map(fn, mapping: dict) -> dict:
+    return {name: fn(value) for name, value in mapping.items()}
 
 
 class ConnectedLayer:

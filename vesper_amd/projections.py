@@ -21,6 +21,7 @@ import threading
 import numpy as np
 
 from . import _lib
+from .resources import MiB, MemoryBudget
 
 FP8_LAYOUT = {"wq_a": (1280, 5120), "wq_b": (32768, 1280), "wkv": (512, 5120), "wo_b": (5120, 8192)}
 WO_A = (8192, 4096)          # the grouped output projection: 8 groups of 1024 rows over 4096 (projections.py:34)
@@ -28,6 +29,7 @@ WO_A_GROUPS = 8
 GROUPED_MAX_TOKENS = 32      # grouped calls run on the decode GEMV
 CONFIG3_LAYOUT = {"q_a": (1536, 7168), "q_b": (24576, 1536), "kv_a": (576, 7168), "o": (7168, 16384)}
 MAX_ROWS = 1 << 16
+HOST_ALLOWANCE = 512 * MiB   # host bytes an open runtime reserves for its calls' uploads and results
 
 
 def validate_values(values, width):
@@ -75,12 +77,19 @@ class NativeProjections:
         self.arrays, self.ordinal, self.layer, self.block = arrays, ordinal, layer, block
         self.lock, self.opened, self.ctx = threading.Lock(), False, None
         self.tiled = {}
+        self.budget = MemoryBudget(cap=HOST_ALLOWANCE, owner="projections")
+        self._device_peak = 0   # the context's peak owned bytes, kept past close for stats()
 
     def __enter__(self):
         with self.lock:
             if self.opened:
                 raise RuntimeError("Projection runtime is already open")
-            self.ctx = _lib.Context(self.ordinal, 0)
+            self.budget.acquire(HOST_ALLOWANCE)
+            try:
+                self.ctx = _lib.Context(self.ordinal, 0)
+            except BaseException:
+                self.budget.release(HOST_ALLOWANCE)
+                raise
             try:
                 lib = self.ctx.lib
                 tiled_layout = dict(self.layout, **({"wo_a": WO_A} if self.has_wo_a else {}))
@@ -99,13 +108,30 @@ class NativeProjections:
                 self.opened = True
                 return self
             except BaseException:
-                self.ctx.close()
-                self.ctx = None
+                self._close_context()
                 raise
+
+    def _close_context(self):
+        self._device_peak = max(self._device_peak, self.ctx.owned_bytes()[1])
+        self.ctx.close()
+        self.ctx = None
+        self.budget.release(HOST_ALLOWANCE)
 
     def _ready(self):
         if not self.opened:
             raise RuntimeError("Projection runtime is not open")
+        self.budget.acquire(0)   # MemoryError once the machine is below its memory reserve
+
+    def stats(self) -> dict:
+        """The runtime's host reservation and device footprint (projections.py:189-195): the host allowance
+        (its peak reservation) and what is reserved now, the device context's peak and live owned bytes, and
+        whether the context is open. The reservation is a ledger, not a limit on the process's resident set,
+        and module (code object) memory is not in the device figures."""
+        live, peak = self.ctx.owned_bytes() if self.ctx is not None else (0, 0)
+        return {"host_allowance_bytes": self.budget.peak, "host_reserved_bytes": self.budget.reserved,
+                "device_peak_owned_bytes": max(peak, self._device_peak), "device_owned_bytes": live,
+                "owned_context_active": self.ctx is not None, "reservation_is_RSS_limit": False,
+                "driver_module_memory_excluded": True}
 
     def project_device(self, name, x_ptr, tokens, y_ptr, stream=None, trace_ptr=None, q_ptr=None, s_ptr=None):
         """y[T][rows] BF16 = projection of device BF16 x[T][width]; no host synchronisation."""
@@ -195,6 +221,5 @@ class NativeProjections:
         with self.lock:
             self.opened = False
             if self.ctx is not None:
-                self.ctx.close()
-                self.ctx = None
+                self._close_context()
             self.tiled.clear()

@@ -18,7 +18,7 @@ from __future__ import annotations
 import ctypes as C
 import threading
 import time
-from contextlib import ExitStack
+from contextlib import ExitStack, contextmanager
 from dataclasses import dataclass
 from pathlib import Path
 
@@ -301,14 +301,21 @@ def _run_tiled_expert(ctx, work, tiled_ptr, hidden, intermediate, limit, x, rout
 
 
 class TieredExpertRuntime:
-    """Single-expert execution over the tiers (the reference's TieredExpertRuntime, src/vesper/tiered.py:130-216).
+    """Single-expert execution over the exclusive tiers, behind the reference's constructor and call
+    (src/vesper/tiered.py:130-216: TieredExpertRuntime(store, CacheConfig), forward(key, x, routing_weight),
+    snapshot(), last_event, cleanup).
 
-    TieredExpertRuntime(store, CacheConfig) opens the store directory as a NativeStore (or through
-    source_factory(store, budget)), the compute GPU `primary_device` and the tiers; forward(key, x, w) brings
-    expert "layer:expert" into a GPU slot -- from the store, the RAM tier or the slot itself -- and runs it
-    (mx_expert_forward_tiled), returning the reference's stage dict; last_event["source_tier"] is
-    "primary_gpu", "ram" or "store". The model's shapes come from `model` (the reference's pinned checkpoint by
-    default)."""
+    Opening runs four steps, each leaving what it opened on one exit stack so that a failing step closes
+    exactly what came before it: admit the metadata allowance in the host budget; open the store (a
+    NativeStore over the directory, or source_factory(store, budget), which must charge the same budget) and
+    check that the budget can hold its direct-I/O buffer and two pinned staging buffers; open the compute GPU
+    (`primary_device`), the HipCacheBackend's slots and the stage buffers of the expert call; build the tiers.
+    forward(key, x, w) holds expert "layer:expert" in a GPU slot -- served from the slot, the RAM tier or the
+    store -- refuses to run when the device's free memory is below its floor, and runs the expert
+    (mx_expert_forward_tiled) with the reference's stage dict as the result; last_event["source_tier"] names
+    the tier. The model's shapes come from `model` (the reference's pinned checkpoint by default)."""
+
+    DEVICE_FREE_FLOOR = GiB   # free device memory below which no expert call starts
 
     def __init__(self, store: Path, config: CacheConfig | None = None, *, source_factory=None,
                  model: ModelProfile = REFERENCE_PROFILE, max_tokens: int = 16):
@@ -317,6 +324,41 @@ class TieredExpertRuntime:
         self.store_path, self.config, self.source_factory = Path(store), config or CacheConfig(), source_factory
         self.model, self.max_tokens = model, int(max_tokens)
         self.stack, self.cache, self.ctx = None, None, None
+
+    # -- opening ---------------------------------------------------------------------------------------------
+    def _admit_metadata(self, stack: ExitStack):
+        allowance = self.config.metadata_allowance_bytes
+        self.budget.acquire(allowance, category="metadata")
+        stack.callback(self.budget.release, allowance, category="metadata")
+
+    def _open_store(self, stack: ExitStack):
+        c = self.config
+        if self.source_factory is None:
+            store = NativeStore(self.store_path, self.budget, max_experts=c.max_store_experts, profile=self.model)
+        else:
+            store = self.source_factory(self.store_path, self.budget)
+        if store.budget is not self.budget:
+            raise ValueError("Expert source must use the admitted cache budget")
+        store.timings, store.gpu_integrity = self.timings, c.integrity_mode == "gpu-sha256"
+        self.store = stack.enter_context(store)
+        # the direct reader's aligned buffer and the two pinned staging experts, beside the metadata
+        if 3 * self.store.size > c.host_cap_bytes - c.metadata_allowance_bytes:
+            raise MemoryError("Host cap cannot fit direct-I/O scratch and two pinned staging buffers")
+
+    def _open_device(self, stack: ExitStack):
+        c = self.config
+        self.ctx = stack.enter_context(_lib.Context(c.primary_device, c.device_cap_bytes))
+        self.backend = stack.enter_context(HipCacheBackend(self.ctx, self.model, self.store.size, c, self.budget,
+                                                           self.store, self.timings))
+        work = _stage_buffers(self.ctx, self.max_tokens, self.model.hidden, self.model.intermediate)
+        stack.callback(lambda: [buf.free() for buf in work.values()])
+        self.work = work
+
+    def _open_tiers(self, stack: ExitStack):
+        c = self.config
+        self.cache = TieredCache(self.store, self.backend, self.budget, c.ram_cache_bytes, timings=self.timings,
+                                 gpu_verify=c.integrity_mode == "gpu-sha256")
+        stack.callback(self.cache.close)
 
     def __enter__(self):
         if self.stack is not None:
@@ -327,68 +369,58 @@ class TieredExpertRuntime:
                                "(set helper_device=None and helper_slots=0)")
         self.budget = MemoryBudget(c.host_cap_bytes, c.available_floor, owner="expert_tiers")
         self.timings = Timings(c.profile)
-        self.stack = ExitStack()
-        try:
-            self.budget.acquire(c.metadata_allowance_bytes, category="metadata")
-            self.stack.callback(self.budget.release, c.metadata_allowance_bytes, category="metadata")
-            self.store = (NativeStore(self.store_path, self.budget, max_experts=c.max_store_experts, profile=self.model)
-                          if self.source_factory is None else self.source_factory(self.store_path, self.budget))
-            if self.store.budget is not self.budget:
-                raise ValueError("Expert source must use the admitted cache budget")
-            self.store.timings = self.timings
-            self.store.gpu_integrity = c.integrity_mode == "gpu-sha256"
-            self.stack.enter_context(self.store)
-            if c.metadata_allowance_bytes + self.store.size * 3 > c.host_cap_bytes:
-                raise MemoryError("Host cap cannot fit direct-I/O scratch and two pinned staging buffers")
-            self.ctx = self.stack.enter_context(_lib.Context(c.primary_device, c.device_cap_bytes))
-            self.backend = self.stack.enter_context(HipCacheBackend(self.ctx, self.model, self.store.size, c,
-                                                                    self.budget, self.store, self.timings))
-            self.work = _stage_buffers(self.ctx, self.max_tokens, self.model.hidden, self.model.intermediate)
-            self.stack.callback(lambda: [d.free() for d in self.work.values()])
-            self.cache = TieredCache(self.store, self.backend, self.budget, c.ram_cache_bytes, timings=self.timings,
-                                     gpu_verify=c.integrity_mode == "gpu-sha256")
-            self.stack.callback(self.cache.close)
-            self.last_event = None
-            return self
-        except BaseException:
-            self.stack.close()
-            self.stack = None
-            raise
+        stack = ExitStack()
+        with stack:   # unwinds only if a step raises: pop_all() below takes the resources over
+            for step in (self._admit_metadata, self._open_store, self._open_device, self._open_tiers):
+                step(stack)
+            self.stack = stack.pop_all()
+        self.last_event = None
+        return self
+
+    # -- calls -----------------------------------------------------------------------------------------------
+    @contextmanager
+    def _recording(self, key: str):
+        """Collects last_event for one call (published only when the call succeeds)."""
+        started, mark = time.perf_counter(), self.timings.snapshot()
+        event = {"key": key, "source_tier": None}
+        yield event
+        event["wall_ms"] = (time.perf_counter() - started) * 1000
+        if self.timings.enabled:
+            event["stage_timings"] = self.timings.since(mark)
+        self.last_event = event
+
+    def _check_headroom(self):
+        if self.ctx.memory()["free"] < self.DEVICE_FREE_FLOOR:
+            raise MemoryError("GPU headroom fell below the reserve; refusing further work")
 
     def forward(self, key: str, x, routing_weight=None) -> dict:
         if self.stack is None:
             raise RuntimeError("Use the tiered runtime as a context manager")
-        started = time.perf_counter()
-        before = self.timings.snapshot()
-        with self.cache.acquire(key) as (slot, origin):
+        with self._recording(key) as event, self.cache.acquire(key) as (slot, origin):
+            event["source_tier"] = origin
+            self._check_headroom()
             with self.timings.section("compute.kernels"):
-                result = _run_tiled_expert(self.ctx, self.work, self.backend.slot_ptr(slot), self.model.hidden,
-                                           self.model.intermediate, self.model.swiglu_limit, x, routing_weight)
-        self.last_event = {"key": key, "source_tier": origin, "wall_ms": (time.perf_counter() - started) * 1000}
-        if self.timings.enabled:
-            self.last_event["stage_timings"] = self.timings.since(before)
-        return result
+                return _run_tiled_expert(self.ctx, self.work, self.backend.slot_ptr(slot), self.model.hidden,
+                                         self.model.intermediate, self.model.swiglu_limit, x, routing_weight)
 
     def snapshot(self) -> dict:
-        result = self.cache.snapshot()
-        if self.timings.enabled:
-            result["stage_timings"] = self.timings.snapshot()
-        live, peak = self.ctx.owned_bytes()
-        result.update({"primary_peak_explicit_bytes": peak, "helper_peak_explicit_bytes": 0,
-                       "store_direct_read_calls": self.store.read_calls, "store_direct_read_bytes": self.store.bytes_read,
-                       "host_cap_bytes": self.config.host_cap_bytes,
-                       "host_available_floor_bytes": self.config.available_floor,
-                       "ram_capacity_bytes": self.config.ram_cache_bytes,
-                       "expected_digest_table_bytes": sum(a.nbytes for a in self.store.expected_chunks.values())})
-        return result
+        store, c = self.store, self.config
+        footprint = {"primary_peak_explicit_bytes": self.ctx.owned_bytes()[1], "helper_peak_explicit_bytes": 0,
+                     "store_direct_read_calls": store.read_calls, "store_direct_read_bytes": store.bytes_read,
+                     "host_cap_bytes": c.host_cap_bytes, "host_available_floor_bytes": c.available_floor,
+                     "ram_capacity_bytes": c.ram_cache_bytes,
+                     "expected_digest_table_bytes": sum(t.nbytes for t in store.expected_chunks.values())}
+        timings = {"stage_timings": self.timings.snapshot()} if self.timings.enabled else {}
+        return {**self.cache.snapshot(), **timings, **footprint}
 
     def __exit__(self, *_):
-        if self.stack is not None:
-            live = self.ctx.owned_bytes()[0] if self.ctx is not None else 0
-            self.stack.close()
-            self.stack = None
-            self.cleanup = {"host_buffer_reservations_bytes": self.budget.reserved,
-                            "primary_explicit_live_bytes_before_close": live}
+        if self.stack is None:
+            return
+        live = self.ctx.owned_bytes()[0] if self.ctx is not None else 0
+        stack, self.stack = self.stack, None
+        stack.close()
+        self.cleanup = {"host_buffer_reservations_bytes": self.budget.reserved,
+                        "primary_explicit_live_bytes_before_close": live}
 
 
 class PooledExpertRuntime:
