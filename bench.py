@@ -108,6 +108,8 @@ def read_ceiling(ctx, stream, nbytes=2 << 30, reps=7):
 
 CPU_RUNS = 5
 CPU_SAMPLE_EXPERTS = 2
+CPU_FP8_SAMPLE_ROWS = 64
+CPU_PREFILL_SAMPLE_ROWS = (32, 64)
 
 
 def _median_s(fn, runs=CPU_RUNS):
@@ -121,6 +123,37 @@ def _median_s(fn, runs=CPU_RUNS):
     return float(np.median(times))
 
 
+def cpu_prefill_leg(bank, cfg, tokens=4096, seed=20261018):
+    """Configuration 2 (prefill, T = 4096, the prefill workload's own seeded Zipf routing) on the NumPy oracle,
+    as a declared subset: the busiest expert through expert_forward on its first 32 and first 64 rows gives a
+    per-expert cost (dequantising the weights, independent of the rows) and a per-row cost; the linear model
+    is summed over every expert with rows and the shared expert's T rows. The combine's per-token sums are
+    not included (a few milliseconds)."""
+    from oracle.expert import expert_forward
+    from oracle.formats import bf16_round
+    from vesper_amd.prefill_workload import seeded_inputs
+    _, x, ids, wts = seeded_inputs(tokens, seed, cfg)
+    counts = np.bincount(ids.ravel(), minlength=cfg.experts)
+    busiest = int(np.argmax(counts))
+    rows = np.flatnonzero((ids == busiest).any(axis=1))
+    route = wts[rows, (ids[rows] == busiest).argmax(axis=1)]
+    xr = bf16_round(x[rows[:max(CPU_PREFILL_SAMPLE_ROWS)]])
+    arrays = bank.download(busiest)
+    lo, hi = CPU_PREFILL_SAMPLE_ROWS
+    t_lo = _median_s(lambda: expert_forward(xr[:lo], arrays, route[:lo], cfg.swiglu_limit), 1)
+    t_hi = _median_s(lambda: expert_forward(xr[:hi], arrays, route[:hi], cfg.swiglu_limit), 1)
+    per_row = max(t_hi - t_lo, 0.0) / (hi - lo)
+    fixed = t_lo - lo * per_row
+    slots = [int(c) for c in counts if c] + [tokens]
+    total = sum(fixed + per_row * r for r in slots)
+    flop = 2 * sum(slots) * 3 * cfg.intermediate * cfg.hidden
+    return {"us": total * 1e6, "TFLOP_per_s": flop / total / 1e12, "us_per_expert_fixed": fixed * 1e6,
+            "us_per_row": per_row * 1e6, "expert_slots": len(slots), "rows": sum(slots),
+            "sample": f"declared subset: the busiest expert ({counts[busiest]} rows) on its first {lo} and {hi} "
+                      "rows in full (one warm-up, one timed call each), a linear per-expert + per-row model summed "
+                      "over the routing's experts and the shared expert"}
+
+
 def cpu_baseline(bank, w, x_rows, cfg, plans):
     """The NumPy oracle on the host cores, bounded samples of the benchmark's own inputs (one warm-up, median
     of 5 per leg):
@@ -131,7 +164,9 @@ def cpu_baseline(bank, w, x_rows, cfg, plans):
       CPU_SAMPLE_EXPERTS routed experts (ascending ID) on their own token rows; the routed time is
       extrapolated linearly to every distinct selected expert (the per-expert cost is dominated by
       dequantising its weights, which does not depend on its row count at these T);
-    * config 3 at T = 1, 16: all four FP8 projections in full (synthetic weights of the same shapes).
+    * config 2 at T = 4096 (declared subset, cpu_prefill_leg): one expert at 32 and 64 rows, extrapolated;
+    * config 3 at T = 1, 16: all four FP8 projections in full (synthetic weights of the same shapes), and
+      T = 2048 as a declared subset (T = 64 in full, extrapolated linearly in rows).
 
     value = config 1's bytes of one bench step (T = 1, 4 and 16) / the summed CPU time of the three legs."""
     import threadpoolctl
@@ -175,15 +210,33 @@ def cpu_baseline(bank, w, x_rows, cfg, plans):
                                      "sample": f"router + shared in full; {len(sample)} of {len(selected)} routed "
                                                "experts timed, extrapolated linearly"}
             log(f"cpu config 1 T={t}: {total:.2f} s (extrapolated)")
+        legs["config2_T4096"] = cpu_prefill_leg(bank, cfg)
+        log(f"cpu config 2 T=4096: {legs['config2_T4096']['us'] * 1e-6:.2f} s (extrapolated)")
         rng = np.random.default_rng(20261018)
         weights = {name: fp8_weights(rng, n, k, 128) for name, (n, k) in LAYOUT.items()}
-        for t in (1, 16):
+        c3 = {}
+        for t in (1, 16, CPU_FP8_SAMPLE_ROWS):
             xs = {name: rng.standard_normal((t, k)).astype(np.float32) for name, (n, k) in LAYOUT.items()}
-            sec = _median_s(lambda: [fp8_projection(xs[name], *weights[name], 128) for name in LAYOUT])
-            nbytes = sum(n * k + ((n + 127) // 128) * (k // 128) * 4 + t * (n + k) * 2 for n, k in LAYOUT.values())
-            legs[f"config3_T{t}"] = {"us": sec * 1e6, "GB_per_s": nbytes / sec / 1e9,
+            runs = CPU_RUNS if t <= 16 else 1
+            c3[t] = _median_s(lambda: [fp8_projection(xs[name], *weights[name], 128) for name in LAYOUT], runs)
+            log(f"cpu config 3 T={t}: {c3[t]:.2f} s")
+
+        def fp8_bytes(t):
+            return sum(n * k + ((n + 127) // 128) * (k // 128) * 4 + t * (n + k) * 2 for n, k in LAYOUT.values())
+        for t in (1, 16):
+            legs[f"config3_T{t}"] = {"us": c3[t] * 1e6, "GB_per_s": fp8_bytes(t) / c3[t] / 1e9,
                                      "sample": "q_a, q_b, kv_a and o in full"}
-            log(f"cpu config 3 T={t}: {sec:.2f} s")
+        # T = 2048: token rows are independent, so the T = 16 and T = 128 times give a per-call and a per-row
+        # cost, extrapolated linearly
+        s0 = CPU_FP8_SAMPLE_ROWS
+        per_row = (c3[s0] - c3[16]) / (s0 - 16)
+        sec = c3[16] + per_row * (2048 - 16)
+        flop = 2 * 2048 * sum(n * k for n, k in LAYOUT.values())
+        legs["config3_T2048"] = {"us": sec * 1e6, "GB_per_s": fp8_bytes(2048) / sec / 1e9,
+                                 "TFLOP_per_s": flop / sec / 1e12, "us_per_row": per_row * 1e6,
+                                 "sample": f"declared subset: all four projections at T = 16 and T = {s0} in full (one warm-up, "
+                                           f"one timed call at T = {s0}), extrapolated linearly in rows to T = 2048"}
+        log(f"cpu config 3 T=2048: {sec:.2f} s (extrapolated)")
     legs = {name: {k: (round(v, 3) if isinstance(v, float) else v) for k, v in leg.items()} for name, leg in legs.items()}
     return {"value": round(step_bytes / step_s / 1e9, 5), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"NumPy oracle; config 1 step (T = 1, 4, 16) with {CPU_SAMPLE_EXPERTS} routed experts per T "

@@ -6,7 +6,8 @@
 experts (8 x 256 / 4 = 512 slots of 23.4 MB); every routed expert's tiled bytes sit in host pinned memory
 and misses stream over PCIe with hipMemcpyAsync on the cache's side stream, overlapped with compute. The
 expert selection is a seeded trace: each token picks 8 distinct experts at step 0, and at every later step
-keeps 5 of its previous 8 (60 %) and draws 3 new ones. Route weights are uniform positive, normalized,
+keeps each of its previous 8 with probability 0.6 (independently) and replaces the others with experts it did
+not use at the previous step. Route weights are uniform positive, normalized,
 times 2.5. Shared experts stay resident. The experts' E8M0 codes are drawn from [118, 120] rather than
 configuration 0's [118, 126], which would scale each layer's output up about a million-fold and overflow a
 chain of 8 layers (the timing does not depend on the values).
@@ -37,8 +38,11 @@ import sys
 import numpy as np
 
 
-def trace(rng, steps, layers, tokens, experts, top_k, keep=5, route_scale=2.5):
-    """routing[step][layer] = (ids [T, k] int32, weights [T, k] FP32)."""
+def trace(rng, steps, layers, tokens, experts, top_k, repeat=0.6, route_scale=2.5):
+    """routing[step][layer] = (ids [T, k] int32, weights [T, k] FP32). After the first step each of a
+    token's k previous experts is kept independently with probability `repeat`, and the dropped ones are
+    replaced by experts the token did not use at the previous step, so a slot repeats with probability
+    exactly `repeat`."""
     out = []
     prev = [[None] * tokens for _ in range(layers)]
     for _ in range(steps):
@@ -46,12 +50,13 @@ def trace(rng, steps, layers, tokens, experts, top_k, keep=5, route_scale=2.5):
         for layer in range(layers):
             ids = np.empty((tokens, top_k), np.int32)
             for t in range(tokens):
-                if prev[layer][t] is None:
+                last = prev[layer][t]
+                if last is None:
                     ids[t] = rng.choice(experts, top_k, replace=False)
                 else:
-                    kept = rng.choice(prev[layer][t], keep, replace=False)
-                    rest = np.setdiff1d(np.arange(experts), kept)
-                    ids[t] = np.concatenate([kept, rng.choice(rest, top_k - keep, replace=False)])
+                    kept = last[rng.random(top_k) < repeat]
+                    fresh = rng.choice(np.setdiff1d(np.arange(experts), last), top_k - kept.size, replace=False)
+                    ids[t] = np.concatenate([kept, fresh])
                 prev[layer][t] = ids[t].copy()
             raw = rng.uniform(0.05, 1.0, (tokens, top_k)).astype(np.float32)
             step.append((ids, (raw / raw.sum(1, keepdims=True) * np.float32(route_scale)).astype(np.float32)))

@@ -18,20 +18,42 @@ import sys
 import numpy as np
 
 
+HBM_PEAK = 8.0e12        # B/s
+FP8_MFMA_PEAK = 5.0e15   # FLOP/s, dense
+
+
+def seeded_inputs(tokens, seed, cfg):
+    """(router weight [E, H], x [T, H] FP32, ids [T, k], weights [T, k]) of the workload's seeded stream (the
+    experts themselves are generated in HBM from the same seed)."""
+    from .workloads import zipf_routing
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((cfg.experts, cfg.hidden)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((tokens, cfg.hidden)).astype(np.float32)
+    ids, wts = zipf_routing(rng, tokens, cfg.experts, cfg.top_k)
+    return w, x, ids, wts
+
+
+def per_expert_roofline(ids, tokens, cfg, has_shared=True):
+    """Sum over the experts with rows (the shared expert with all T) of max(weight bytes / HBM peak,
+    2 rows 3 I H / dense FP8 MFMA peak), in microseconds: each expert's weights stream once while its rows'
+    products run at the MFMA peak, experts back to back."""
+    counts = np.bincount(np.asarray(ids).ravel(), minlength=cfg.experts)
+    rows = [int(c) for c in counts if c] + ([tokens] if has_shared else [])
+    return sum(max(cfg.expert_bytes / HBM_PEAK, 2.0 * r * 3 * cfg.intermediate * cfg.hidden / FP8_MFMA_PEAK)
+               for r in rows) * 1e6
+
+
 def run(tokens=4096, iters=5, seed=20261018, ctx=None):
     from . import _lib
     from .config import BASELINE as cfg
     from .layer import ExpertBank, MoELayer, bf16_input
-    from .workloads import zipf_routing
     own = ctx is None
     ctx = ctx or _lib.Context(0)
-    rng = np.random.default_rng(seed)
     bank = ExpertBank(ctx, cfg, cfg.experts + 1)
     bank.fill_synthetic(seed)
-    w = (rng.standard_normal((cfg.experts, cfg.hidden)) * 0.02).astype(np.float32)
+    w, xv, ids, wts = seeded_inputs(tokens, seed, cfg)
     layer = MoELayer(ctx, cfg, w, bank)
-    x = ctx.upload(bf16_input(rng.standard_normal((tokens, cfg.hidden)).astype(np.float32), cfg.hidden))
-    ids, wts = zipf_routing(rng, tokens, cfg.experts, cfg.top_k)
+    x = ctx.upload(bf16_input(xv, cfg.hidden))
     idd, wd = ctx.upload(ids), ctx.upload(wts)
     y = ctx.empty((tokens, cfg.hidden), np.uint16)
     nbytes = layer.workspace_bytes(tokens)
@@ -52,6 +74,9 @@ def run(tokens=4096, iters=5, seed=20261018, ctx=None):
            "experts_used": used, "weight_bytes": used * cfg.expert_bytes,
            "weight_GB_per_s": round(used * cfg.expert_bytes / us / 1e3, 1),
            "max_tokens_per_expert": int(counts.max()), "median_tokens_per_expert": float(np.median(counts))}
+    roof = per_expert_roofline(ids, tokens, cfg)
+    out.update(roofline_us=round(roof, 1), roofline_frac=round(roof / us, 4),
+               roofline_rule="sum over experts of max(weight bytes / 8 TB/s, 6 rows I H / 5 PFLOP/s)")
     ctx.free(ws)
     for d in (x, idd, wd, y):
         d.free()
