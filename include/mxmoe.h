@@ -407,6 +407,14 @@ int mx_cache_set_timing(mx_cache* cache, int32_t enable);
  * mx_prefill_workspace_bytes(layer, T) bytes, 256-byte aligned (no allocation inside the call).
  * H % 256 == 0. Replaces the reference's per-token ConnectedMoE.forward loop (connected.py:125-186). */
 uint64_t mx_prefill_workspace_bytes(mx_layer* layer, int32_t tokens);
+/* Byte offsets, inside a prefill workspace of `tokens` rows, of the intermediate stages a finished
+ * mx_moe_prefill call leaves there: offsets[0] the down-input E4M3 codes [rows][I] (uint8), [1] their
+ * E8M0 scales [rows][I/32], [2] the row of each routed pair (token t, rank j) [T][k] (int32), [3] the
+ * first row of each expert [E + 1] (int32; the shared expert's rows, one per token in order, start at
+ * entry E). The reference returns these stages from its per-token call (ConnectedMoE.forward's expert
+ * dicts, connected.py:154-160); here they are read from the batched call's workspace. */
+#define MX_PREFILL_STAGES 4
+int mx_prefill_stage_offsets(mx_layer* layer, int32_t tokens, uint64_t* offsets);
 int mx_moe_prefill(mx_layer* layer, const uint16_t* x_bf16, int32_t tokens, const int32_t* ids, const float* weights,
                    uint16_t* y_bf16, void* workspace, uint64_t workspace_bytes, void* stream);
 

@@ -1,15 +1,21 @@
-"""GPU parity of the MoE prefill (mx_moe_prefill: token-sorted grouped GEMMs on scaled MXFP4 MFMA).
+"""GPU parity of the MoE prefill (mx_moe_prefill: token-sorted grouped GEMMs).
 
-Per token the prefill is the decode layer's arithmetic (the oracle's per-token layer): compared within the
-north-star tolerance on Zipf-skewed routing (experts with several 128-row tiles, experts with none, ragged
-tails), through the layer's own router (identical logits to mx_gate_project), and at the BASELINE shapes
-on a sample of tokens. The routed rows' plan is checked bit-exactly through the combine: a wrong row,
-order or token would move whole outputs, far outside the tolerance.
+Per token the prefill is the decode layer's arithmetic (the oracle's per-token layer). The gate/up GEMM
+follows the block spec bit for bit (every 32-block dot rounded once, blocks added in ascending order), so
+every routed pair's and the shared expert's down-input codes and scales -- which W1 and W3 determine
+through the SwiGLU and the per-32 quantizer -- must equal the oracle's (mx_prefill_stage_offsets reads them
+from the workspace); the layer output is compared within the north-star tolerance (the down GEMM sums K in
+its own order). Cases: Zipf-skewed routing (experts with several 128-row tiles, experts with none, ragged
+tails), narrow shapes, the layer's own router, the BASELINE and reference-model shapes on sampled tokens,
+and the three configurations a one-off randomized sweep found outside the bar while gate/up summed four
+blocks per rounding. The routed rows' plan is checked through the combine: a wrong row, order or token
+would move whole outputs, far outside the tolerance.
 """
 
 import numpy as np
 import pytest
 
+from oracle.expert import expert_forward
 from oracle.inputs import activations, mxfp4_expert, router_weight
 from vesper_amd.workloads import zipf_routing
 from oracle.moe import moe_layer, moe_layer_routed
@@ -31,6 +37,23 @@ def small_layer(ctx, rng, cfg):
     return MoELayer(ctx, cfg, w, bank), bank, w, arrays
 
 
+def check_down_codes(stages, ids, ref_experts, tokens=None, shared=None, what=""):
+    """The prefill's down-input codes and scales of every routed pair (and of the shared expert's rows, when
+    `shared` is the oracle's stage dict for it) equal the oracle's. ref_experts: the oracle's per-expert
+    stage dicts over `tokens` (all tokens if None), rows in ascending token order."""
+    tokens = np.arange(ids.shape[0]) if tokens is None else np.asarray(tokens)
+    for e, out in ref_experts.items():
+        toks = tokens[(ids[tokens] == e).any(axis=1)]
+        ranks = (ids[toks] == e).argmax(axis=1)
+        rows = stages["pair_row"][toks, ranks]
+        np.testing.assert_array_equal(stages["down_q"][rows], out["down_q"], err_msg=f"{what} expert {e} codes")
+        np.testing.assert_array_equal(stages["down_s"][rows], out["down_s"], err_msg=f"{what} expert {e} scales")
+    if shared is not None:
+        rows = stages["row0"][-1] + tokens
+        np.testing.assert_array_equal(stages["down_q"][rows], shared["down_q"], err_msg=f"{what} shared codes")
+        np.testing.assert_array_equal(stages["down_s"][rows], shared["down_s"], err_msg=f"{what} shared scales")
+
+
 @pytest.mark.parametrize("tokens,shared", [(300, True), (129, False), (7, True)])
 def test_prefill_zipf_routing_matches_oracle(gpu_ctx, tokens, shared):
     cfg = MoEConfig(hidden=512, intermediate=256, experts=32, top_k=4, swiglu_limit=10.0,
@@ -46,10 +69,12 @@ def test_prefill_zipf_routing_matches_oracle(gpu_ctx, tokens, shared):
         counts = np.bincount(ids.ravel(), minlength=cfg.experts)
         if tokens == 300:
             assert counts.max() > 128 and (counts == 0).any()      # multi-tile experts and idle ones
-        got = layer.prefill(x, ids, wts)
+        got, stages = layer.prefill(x, ids, wts, stages=True)
         ref = moe_layer_routed(x, ids, wts, {e: arrays[e] for e in range(cfg.experts)},
                                arrays[cfg.experts] if shared else None, num_experts=cfg.experts,
                                swiglu_limit=cfg.swiglu_limit)
+        sh = expert_forward(x, arrays[cfg.experts], None, cfg.swiglu_limit) if shared else None
+        check_down_codes(stages, ids, ref["experts"], shared=sh, what="prefill")
         assert_close(got, ref["output_bf16"], "prefill")
         for t in range(tokens):                                     # every token, not just the aggregate
             assert max_rel_err(got[t], ref["output_bf16"][t]) <= 2e-2, t
@@ -67,9 +92,11 @@ def test_prefill_narrow_shapes_take_the_smaller_tiles(gpu_ctx):
     try:
         x = activations(rng, 200, cfg.hidden)
         ids, wts = zipf_routing(rng, 200, cfg.experts, cfg.top_k)
-        got = layer.prefill(x, ids, wts)
+        got, stages = layer.prefill(x, ids, wts, stages=True)
         ref = moe_layer_routed(x, ids, wts, {e: arrays[e] for e in range(cfg.experts)}, arrays[cfg.experts],
                                num_experts=cfg.experts, swiglu_limit=cfg.swiglu_limit)
+        check_down_codes(stages, ids, ref["experts"], shared=expert_forward(x, arrays[cfg.experts], None,
+                                                                           cfg.swiglu_limit), what="narrow")
         assert_close(got, ref["output_bf16"], "prefill narrow")
         for t in range(200):
             assert max_rel_err(got[t], ref["output_bf16"][t]) <= 2e-2, t
@@ -125,12 +152,15 @@ def test_prefill_baseline_shapes_sampled_tokens(gpu_ctx):
         T = 4096
         x = activations(rng, T, cfg.hidden)
         ids, wts = zipf_routing(rng, T, cfg.experts, cfg.top_k)
-        got = layer.prefill(x, ids, wts)
+        got, stages = layer.prefill(x, ids, wts, stages=True)
         sample = np.array([0, 1234, 2048, 3001, T - 1])
         needed = sorted({int(e) for e in ids[sample].ravel()})
         experts = {e: bank.download(e) for e in needed}
-        ref = moe_layer_routed(x, ids, wts, experts, bank.download(cfg.experts), num_experts=cfg.experts,
+        shared = bank.download(cfg.experts)
+        ref = moe_layer_routed(x, ids, wts, experts, shared, num_experts=cfg.experts,
                                swiglu_limit=cfg.swiglu_limit, tokens=sample)
+        check_down_codes(stages, ids, ref["experts"], tokens=sample,
+                         shared=expert_forward(x[sample], shared, None, cfg.swiglu_limit), what="T=4096")
         assert_close(got[sample], ref["output_bf16"], "prefill T=4096 sample")
     finally:
         layer.close()
@@ -176,6 +206,48 @@ def test_prefill_refuses_bad_routing(gpu_ctx):
             layer.prefill(x, np.array([[0, 16]] * 4, np.int32), np.ones((4, 2), np.float32))
         with pytest.raises(ValueError):
             layer.prefill(x, np.array([[0, 1]] * 4, np.int32), None)
+    finally:
+        layer.close()
+        bank.free()
+
+
+def sweep_case(ctx, seed):
+    """Configuration `seed` of the one-off randomized prefill sweep (rng = default_rng(5000 + seed)): the
+    layer, T, x and a Zipf routing over a random subset of the experts, drawn in the sweep's order."""
+    rng = np.random.default_rng(5000 + seed)
+    experts = int(rng.choice([8, 16, 32, 64]))
+    top_k = min(int(rng.choice([1, 2, 4, 8])), experts)
+    cfg = MoEConfig(hidden=int(rng.choice([256, 512, 1024])), intermediate=int(rng.choice([128, 256, 512])),
+                    experts=experts, top_k=top_k, swiglu_limit=float(rng.choice([0.0, 10.0])),
+                    shared="mxfp4" if rng.integers(2) else None, max_tokens=16)
+    layer, bank, w, arrays = small_layer(ctx, rng, cfg)
+    T = int(rng.choice([1, 2, 5, 17, 64, 127, 128, 129, 255, 300, 513]))
+    x = activations(rng, T, cfg.hidden)
+    used_n = int(rng.integers(max(top_k, 1), experts + 1))
+    used = np.sort(rng.choice(experts, used_n, replace=False)).astype(np.int32)
+    ids, wts = zipf_routing(rng, T, used_n, top_k)
+    return cfg, layer, bank, arrays, x, used[ids], wts
+
+
+@pytest.mark.parametrize("seed,tokens", [(131, 127), (133, 128), (396, 513)])
+def test_prefill_sweep_misses_are_bit_exact_in_gate_up(gpu_ctx, seed, tokens):
+    """The sweep's three misses (max relative error 1.36e-2, 1.08e-2, 1.08e-2 while gate/up summed four
+    blocks per rounding; sigmoid scores, no shared expert): one BF16 ulp of a W1 output moved one E4M3 code
+    of the down input. With the in-order block sums the codes equal the oracle's and the output meets the
+    bar, every token included."""
+    cfg, layer, bank, arrays, x, ids, wts = sweep_case(gpu_ctx, seed)
+    try:
+        assert x.shape[0] == tokens
+        print(f"prefill sweep seed {seed}: T={tokens} {cfg}", flush=True)
+        got, stages = layer.prefill(x, ids, wts, stages=True)
+        ref = moe_layer_routed(x, ids, wts, {e: arrays[e] for e in range(cfg.experts)},
+                               arrays[cfg.experts] if cfg.shared else None, num_experts=cfg.experts,
+                               swiglu_limit=cfg.swiglu_limit)
+        sh = expert_forward(x, arrays[cfg.experts], None, cfg.swiglu_limit) if cfg.shared else None
+        check_down_codes(stages, ids, ref["experts"], shared=sh, what=f"seed {seed}")
+        assert_close(got, ref["output_bf16"], f"seed {seed}")
+        for t in range(tokens):
+            assert max_rel_err(got[t], ref["output_bf16"][t]) <= 2e-2, t
     finally:
         layer.close()
         bank.free()

@@ -106,6 +106,7 @@ SIGNATURES = {
     "mx_layer_profile": ([_P, _I32, C.POINTER(_F), C.POINTER(_I32)], C.c_int),
     "mx_layer_time_stage": ([_P, _I32, _I32, C.POINTER(_F), _P], C.c_int),
     "mx_prefill_workspace_bytes": ([_P, _I32], _U64),
+    "mx_prefill_stage_offsets": ([_P, _I32, _P], C.c_int),
     "mx_moe_decode_routed": ([_P, _P, _I32, _P, _P, _P, _P], C.c_int),
     "mx_expert_forward_tiled": ([_P, _P, _I32, _I32, _P, _I32, _F, _P, _P, C.POINTER(MxExpertStages), _P], C.c_int),
     "mx_expert_forward_bf16": ([_P, _P, _I32, _I32, _P, _I32, _P, _P, _P, _P, _P], C.c_int),

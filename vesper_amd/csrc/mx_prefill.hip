@@ -236,10 +236,8 @@ constexpr int kLdsBytes = kStages * kStageBytes;
 static_assert(kLdsBytes <= 160 * 1024 && 2 * kTileRows * kEpiRowG * 2 <= kLdsBytes && kTileRows * kEpiRowD * 2 <= kLdsBytes,
               "LDS layout");
 
-// Grouped GEMM over one 128-row tile of one slot. kGateUp: A = W1/W3 tiles (a group = 32 intermediate
-// rows of W1 and 32 of W3 as the tiled layout interleaves them, 64 MFMA rows), B = the tile's gathered
-// token rows of xq; else A = W2 tiles (a group = 64 hidden rows), B = the tile's rows of dq. Grid x covers
-// the groups eight per workgroup (ceil(I / 256) gate/up, ceil(H / 512) down), grid y the tiles.
+// The down GEMM over one 128-row tile of one slot: A = W2 tiles (a group = 64 hidden rows), B = the tile's
+// rows of dq. Grid x covers the groups eight per workgroup (ceil(H / 512)), grid y the tiles.
 //
 // Waves 0-7 multiply: each keeps its 64 x 128 output block in 128 accumulator registers. Waves 8-11 only
 // copy every operand of a 128-wide K chunk global -> LDS without registers (global_load_lds, 16 bytes a
@@ -252,11 +250,9 @@ static_assert(kLdsBytes <= 160 * 1024 && 2 * kTileRows * kEpiRowG * 2 <= kLdsByt
 // its stage and multiply; the copy waves issue chunk c + 2 into the stage chunk c - 1 left and wait for
 // chunk c + 1; one barrier ends the step.
 //
-// Epilogue: the accumulators go to LDS as BF16 [token][column] and every thread then finishes whole
-// 32-column blocks of one token: gate/up SwiGLU + route weight + the block's E4M3 quantization (32 code
-// bytes and one scale byte), or 16-byte row segments of the down output.
-template <bool kGateUp>
-__global__ __launch_bounds__(kGThreads) void grouped_kernel(GemmArgs a) {
+// Epilogue: the accumulators go to LDS as BF16 [token][column] and every thread then copies 16-byte row
+// segments of the down output to the token-major output rows (plan.row_dest).
+__global__ __launch_bounds__(kGThreads) void grouped_down_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsBytes];
   const int ti = blockIdx.y;
   if (ti >= *a.plan.n_tiles) return;
@@ -265,10 +261,10 @@ __global__ __launch_bounds__(kGThreads) void grouped_kernel(GemmArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q = lane >> 4, n = lane & 15;
-  const int K = kGateUp ? a.H : a.I;
+  const int K = a.I;
   const int C = K / 128;
-  // a multiplying wave past the last group (I / 32 or H / 64 groups) computes and stores nothing
-  const int groups = kGateUp ? a.I / 32 : a.H / 64;
+  // a multiplying wave past the last group (H / 64 groups) computes and stores nothing
+  const int groups = a.H / 64;
   const int g = blockIdx.x * 8 + wave;
   const bool active = wave < 8 && g < groups;
   const uint8_t* blob = a.tiles[slot];
@@ -291,19 +287,19 @@ __global__ __launch_bounds__(kGThreads) void grouped_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int gi = min((int)blockIdx.x * 8 + 2 * pw + i, groups - 1);
-      wsrc[i] = blob + (kGateUp ? 0 : off.dn_w) + (size_t)gi * C * 4096 + 16 * lane;
-      ssrc[i] = blob + (kGateUp ? off.gu_s : off.dn_s) + (size_t)gi * C * 256 + 4 * lane;
+      wsrc[i] = blob + off.dn_w + (size_t)gi * C * 4096 + 16 * lane;
+      ssrc[i] = blob + off.dn_s + (size_t)gi * C * 256 + 4 * lane;
     }
-    const uint8_t* bbase = kGateUp ? a.xq : a.dq;
-    const uint8_t* sbbase = kGateUp ? a.xs : a.ds;
+    const uint8_t* bbase = a.dq;
+    const uint8_t* sbbase = a.ds;
     uint32_t boff[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int br = row0 + min(16 * (2 * pw + i) + n, rows - 1);
-      boff[i] = (kGateUp ? (uint32_t)a.plan.sorted_tok[br] * (uint32_t)a.H : (uint32_t)br * (uint32_t)a.I) + 16 * q;
+      boff[i] = (uint32_t)br * (uint32_t)a.I + 16 * q;
     }
     const int sr = row0 + min(32 * pw + (lane & 31), rows - 1);
-    const uint32_t soff = kGateUp ? (uint32_t)a.plan.sorted_tok[sr] * (uint32_t)(a.H / 32) : (uint32_t)sr * (uint32_t)(a.I / 32);
+    const uint32_t soff = (uint32_t)sr * (uint32_t)(a.I / 32);
     auto copy = [&](int c) {
       const uint32_t st = lds0 + (uint32_t)(c % kStages) * kStageBytes;
 #pragma unroll
@@ -373,106 +369,313 @@ __global__ __launch_bounds__(kGThreads) void grouped_kernel(GemmArgs a) {
   }
   __syncthreads();
 
-  if constexpr (kGateUp) {
-    // D[4q + i][n] of tile t: lanes q < 2 hold W1 rows 32g + 8t + 4q + i, lanes q >= 2 the same W3 rows
-    uint16_t* eg = reinterpret_cast<uint16_t*>(lds);
-    if (active) {
-      uint16_t* dst = eg + (q >> 1) * (kTileRows * kEpiRowG) + n * kEpiRowG + 32 * wave + 4 * (q & 1);
+  // D[4q + i][n] of tile t: W2 rows 64g + 16t + 4q + i
+  uint16_t* eo = reinterpret_cast<uint16_t*>(lds);
+  if (active) {
+    uint16_t* dst = eo + n * kEpiRowD + 64 * wave + 4 * q;
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        uint2 packed;
+        packed.x = mx::bf16_bits(acc[t][u][0]) | (mx::bf16_bits(acc[t][u][1]) << 16);
+        packed.y = mx::bf16_bits(acc[t][u][2]) | (mx::bf16_bits(acc[t][u][3]) << 16);
+        *reinterpret_cast<uint2*>(dst + 16 * u * kEpiRowD + 16 * t) = packed;
+      }
+  }
+  __syncthreads();
+  // thread tid copies segment tid % 64 of rows tid / 64 + 8 i (i < 16); their destinations are loaded
+  // together first
+  const int cols = min(512, a.H - 512 * (int)blockIdx.x);
+  const int seg = tid & 63, tok0 = tid >> 6;   // the multiplying waves' 512 threads
+  int dest[kTileRows / 8];
+#pragma unroll
+  for (int i = 0; i < kTileRows / 8; ++i) dest[i] = a.plan.row_dest[row0 + min(tok0 + 8 * i, rows - 1)];
+  if (tid < 512 && 8 * seg < cols) {
+#pragma unroll
+    for (int i = 0; i < kTileRows / 8; ++i) {
+      const int tok = tok0 + 8 * i;
+      if (tok < rows)
+        *reinterpret_cast<uint4*>(a.out + (size_t)dest[i] * a.H + 512 * blockIdx.x + 8 * seg) =
+            *reinterpret_cast<const uint4*>(eo + tok * kEpiRowD + 8 * seg);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Exact gate/up: W1 and W3 of the tile's tokens as the block spec defines them (E4M3 x MXFP4 per 32-block,
+// src/vesper/formats.py:97-118 and src/vesper/kernels/format_probe.cu:90-118): every block dot is the exact
+// 32-product sum of the scaled values rounded once to FP32, and the blocks are added to the FP32 result one
+// at a time in ascending K order. The scaled FP4 x FP8 MFMA does not round its block sums exactly on gfx950
+// (its adder drops low product bits), so each block runs on V_MFMA_F32_16X16X32_BF16 with a zero
+// accumulator -- which returns the exact 32-product dot rounded once -- over operands converted exactly:
+// weights by V_CVT_SCALEF32_PK_BF16_FP4 with the block's E8M0 scale as the scale operand (an E2M1 value
+// times a power of two has at most two significant bits), activations by V_CVT_SCALEF32_PK_BF16_FP8 with the
+// token's block scale (four significant bits). The in-order chain acc = acc + d runs on the VALU: with a
+// non-zero accumulator the MFMA does not round acc + dot as IEEE addition does.
+//
+// grid (ceil(I / 256), tiles), 512 threads: 8 waves, wave w one group of 32 intermediate rows (4 MFMA
+// tiles, W1 rows 8t + 0..7 and the same W3 rows in tile t) for all 128 rows of the tile, 128 accumulator
+// registers. Every wave also copies its share of chunk c + 2's operands global -> LDS (global_load_lds,
+// kXCopies instructions: its group's four weight pieces and scale words, its token tile's two activation
+// blocks and the 16 rows' activation scale words) into the same 3-stage ring and layout as the down
+// kernel's; a step waits for this wave's copies of chunk c + 1, meets the barrier, issues chunk c + 2 and
+// multiplies chunk c. Operands come from LDS with the bf16 MFMA's lane map (A lane (m, q) = row m, K 8q..8q+7
+// of a block: word q of lane (m, b)'s 16 bytes; B lane (n, q) = token n, the same K: 8 bytes of the
+// activation block), read by inline assembly and waited for explicitly (the compiler cannot see that the
+// copies write LDS).
+constexpr int kXThreads = 512;
+constexpr int kXCopies = 8;
+
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+// 8 E2M1 values (one 32-bit word) times 2^(code - 127), exact in BF16
+__device__ __forceinline__ v8bf fp4_word_scaled(uint32_t word, uint32_t code) {
+  const float scale = __uint_as_float(code << 23);
+  const v2bf p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 0);
+  const v2bf p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 1);
+  const v2bf p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 2);
+  const v2bf p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 3);
+  return v8bf{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+
+// 8 E4M3 values (two 32-bit words, K order) times 2^(code - 127), exact in BF16
+__device__ __forceinline__ v8bf fp8_pair_scaled(uint32_t lo, uint32_t hi, uint32_t code) {
+  const float scale = __uint_as_float(code << 23);
+  const v2bf p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, scale, false);
+  const v2bf p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, scale, true);
+  const v2bf p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, scale, false);
+  const v2bf p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, scale, true);
+  return v8bf{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+
+// this lane's weight words of a chunk (word [t][b]: tile t, block b) and its rows' scale words per block
+__device__ __forceinline__ void lds_read_weights(uint32_t a_addr, uint32_t s_addr, uint32_t (&w)[4][4],
+                                                 uint32_t (&sw)[4]) {
+  asm volatile(
+      "ds_read_b32 %0, %20\n\t"
+      "ds_read_b32 %1, %20 offset:256\n\t"
+      "ds_read_b32 %2, %20 offset:512\n\t"
+      "ds_read_b32 %3, %20 offset:768\n\t"
+      "ds_read_b32 %4, %20 offset:1024\n\t"
+      "ds_read_b32 %5, %20 offset:1280\n\t"
+      "ds_read_b32 %6, %20 offset:1536\n\t"
+      "ds_read_b32 %7, %20 offset:1792\n\t"
+      "ds_read_b32 %8, %20 offset:2048\n\t"
+      "ds_read_b32 %9, %20 offset:2304\n\t"
+      "ds_read_b32 %10, %20 offset:2560\n\t"
+      "ds_read_b32 %11, %20 offset:2816\n\t"
+      "ds_read_b32 %12, %20 offset:3072\n\t"
+      "ds_read_b32 %13, %20 offset:3328\n\t"
+      "ds_read_b32 %14, %20 offset:3584\n\t"
+      "ds_read_b32 %15, %20 offset:3840\n\t"
+      "ds_read_b32 %16, %21\n\t"
+      "ds_read_b32 %17, %21 offset:64\n\t"
+      "ds_read_b32 %18, %21 offset:128\n\t"
+      "ds_read_b32 %19, %21 offset:192\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(w[0][0]), "=&v"(w[0][1]), "=&v"(w[0][2]), "=&v"(w[0][3]), "=&v"(w[1][0]), "=&v"(w[1][1]),
+        "=&v"(w[1][2]), "=&v"(w[1][3]), "=&v"(w[2][0]), "=&v"(w[2][1]), "=&v"(w[2][2]), "=&v"(w[2][3]),
+        "=&v"(w[3][0]), "=&v"(w[3][1]), "=&v"(w[3][2]), "=&v"(w[3][3]), "=&v"(sw[0]), "=&v"(sw[1]),
+        "=&v"(sw[2]), "=&v"(sw[3])
+      : "v"(a_addr), "v"(s_addr));
+}
+
+// the activation piece (8 bytes) of token tile u at LDS address addr + 2048 u, for u < 8, and the tiles'
+// scale words at saddr + 64 u
+__device__ __forceinline__ void lds_read_acts(uint32_t addr, uint32_t saddr, uint2 (&x)[8], uint32_t (&xs)[8]) {
+  typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+  u32x2_t r[8];
+  asm volatile(
+      "ds_read_b64 %0, %16\n\t"
+      "ds_read_b64 %1, %16 offset:2048\n\t"
+      "ds_read_b64 %2, %16 offset:4096\n\t"
+      "ds_read_b64 %3, %16 offset:6144\n\t"
+      "ds_read_b64 %4, %16 offset:8192\n\t"
+      "ds_read_b64 %5, %16 offset:10240\n\t"
+      "ds_read_b64 %6, %16 offset:12288\n\t"
+      "ds_read_b64 %7, %16 offset:14336\n\t"
+      "ds_read_b32 %8, %17\n\t"
+      "ds_read_b32 %9, %17 offset:64\n\t"
+      "ds_read_b32 %10, %17 offset:128\n\t"
+      "ds_read_b32 %11, %17 offset:192\n\t"
+      "ds_read_b32 %12, %17 offset:256\n\t"
+      "ds_read_b32 %13, %17 offset:320\n\t"
+      "ds_read_b32 %14, %17 offset:384\n\t"
+      "ds_read_b32 %15, %17 offset:448\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7]),
+        "=&v"(xs[0]), "=&v"(xs[1]), "=&v"(xs[2]), "=&v"(xs[3]), "=&v"(xs[4]), "=&v"(xs[5]), "=&v"(xs[6]),
+        "=&v"(xs[7])
+      : "v"(addr), "v"(saddr));
+#pragma unroll
+  for (int u = 0; u < 8; ++u) x[u] = uint2{r[u].x, r[u].y};
+}
+
+__global__ __launch_bounds__(kXThreads) void gateup_exact_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsBytes];
+  const int ti = blockIdx.y;
+  if (ti >= *a.plan.n_tiles) return;
+  const int32_t* info = a.plan.tile_info + (size_t)ti * 4;
+  const int slot = info[0], row0 = info[1], rows = info[2];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q = lane >> 4, n = lane & 15, m = lane & 15;
+  const int H = a.H, C = H / 128;
+  // a wave past the last group (I / 32 groups) copies the last group's weights and computes nothing
+  const int groups = a.I / 32;
+  const int g = blockIdx.x * 8 + wave;
+  const bool active = g < groups;
+  const uint8_t* blob = a.tiles[slot];
+  const TiledOffsets off = tiled_offsets(H, a.I);
+  const int live_tiles = min(8, (rows + 15) / 16);
+  const uint32_t lds0 = lds_addr(lds);
+
+  // this wave's copies: group gc's weight pieces and scale words, token tile u = wave's two activation blocks
+  // (rows past the tile repeat its last row) and rows 16 wave .. + 15's activation scale words
+  const int gc = min(g, groups - 1);
+  const uint8_t* wsrc = blob + (size_t)gc * C * 4096 + 16 * lane;
+  const uint8_t* ssrc = blob + off.gu_s + (size_t)gc * C * 256 + 4 * lane;
+  const uint32_t boff = (uint32_t)a.plan.sorted_tok[row0 + min(16 * wave + n, rows - 1)] * (uint32_t)H + 16 * q;
+  const uint32_t soff = (uint32_t)a.plan.sorted_tok[row0 + min(16 * wave + (lane & 15), rows - 1)] * (uint32_t)(H / 32);
+  // the offsets are loaded before the first copy is issued: a wait for them afterwards would also wait for
+  // the copies (the vector memory counter retires in order)
+  asm volatile("" : : "v"(boff), "v"(soff));
+  auto copy = [&](int c) {
+    const uint32_t st = lds0 + (uint32_t)(c % kStages) * kStageBytes;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      global_to_lds16(wsrc + (size_t)c * 4096 + t * 1024, __builtin_amdgcn_readfirstlane(st + kStageA + (4 * wave + t) * 1024));
+    global_to_lds4(ssrc + (size_t)c * 256, __builtin_amdgcn_readfirstlane(st + kStageAS + 256 * wave));
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      global_to_lds16(a.xq + (size_t)c * 128 + boff + 64 * h,
+                      __builtin_amdgcn_readfirstlane(st + kStageB + (2 * wave + h) * 1024));
+    if (lane < 16) global_to_lds4(a.xs + (size_t)c * 4 + soff, __builtin_amdgcn_readfirstlane(st + kStageBS + 64 * wave));
+  };
+
+  // LDS operand addresses of this lane (chunk stage offset added per step): weight word q of lane (m, b) of
+  // tile t at kStageA + (4 wave + t) KB + 16 (16 b + m) + 4 q; its scale byte t of word 16 b + m; activation
+  // block b of token tile u: bytes 32 b + 8 q .. of row 16 u + n sit in block 2u + (b >> 1) at lane slot
+  // 16 (2 (b & 1) + (q >> 1)) + n, byte 8 (q & 1); the row's scale byte b in word 16 u + n
+  const uint32_t la = lds0 + kStageA + 4096 * wave + 16 * m + 4 * q;
+  const uint32_t las = lds0 + kStageAS + 256 * wave + 4 * m;
+  const uint32_t lb = lds0 + kStageB + 16 * (16 * (q >> 1) + n) + 8 * (q & 1);
+  const uint32_t lbs = lds0 + kStageBS + 4 * n;
+
+  v4f acc[4][8];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc[t][u] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  copy(0);
+  if (C > 1) copy(1);
+  for (int c = 0; c < C; ++c) {
+    // chunk c has landed once at most chunk c + 1's copies are still in flight
+    if (c + 1 < C) __builtin_amdgcn_s_waitcnt(vm_wait_imm(kXCopies));
+    else __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));
+    copy_barrier();   // every wave's copies of chunk c are visible; chunk c - 1's stage is free
+    if (c + 2 < C) copy(c + 2);
+    if (!active) continue;
+    const uint32_t so = (uint32_t)(c % kStages) * kStageBytes;
+    uint32_t w[4][4], sw[4];
+    lds_read_weights(la + so, las + so, w, sw);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      v8bf av[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) av[t] = fp4_word_scaled(w[t][b], (sw[b] >> (8 * t)) & 0xFF);
+      uint2 x[8];
+      uint32_t xs[8];
+      lds_read_acts(lb + so + 1024 * (b >> 1) + 512 * (b & 1), lbs + so, x, xs);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (u >= live_tiles) break;   // wave-uniform
+        mxd::u32x4_t xw = __builtin_bit_cast(mxd::u32x4_t, fp8_pair_scaled(x[u].x, x[u].y, (xs[u] >> (8 * b)) & 0xFF));
+        // ordered after the previous token tile's pin below: this tile's MFMAs cannot be hoisted above the
+        // previous tile's additions, so at most one tile's four results are live at a time
+        asm volatile("" : "+v"(xw));
+        const v8bf xv = __builtin_bit_cast(v8bf, xw);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          uint2 packed;
-          packed.x = mx::bf16_bits(acc[t][u][0]) | (mx::bf16_bits(acc[t][u][1]) << 16);
-          packed.y = mx::bf16_bits(acc[t][u][2]) | (mx::bf16_bits(acc[t][u][3]) << 16);
-          *reinterpret_cast<uint2*>(dst + 16 * u * kEpiRowG + 8 * t) = packed;
+          const v4f d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[t], xv, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[t][u][i] = acc[t][u][i] + d[i];
         }
-    }
-    __syncthreads();
-    const bool weighted = slot < a.E;
-    // the clamp limit, or +inf when unclamped (no comparison then holds, as with no clamp)
-    const float lim = a.limit > 0.f ? a.limit : __builtin_inff();
-    for (int p = tid; p < kTileRows * 8; p += kGThreads) {
-      const int tok = p >> 3, blk = p & 7, gg = blockIdx.x * 8 + blk;
-      if (tok >= rows || gg >= groups) continue;
-      const int row = row0 + tok;
-      const float rw = a.plan.sorted_w[row];
-      const uint4* gsrc = reinterpret_cast<const uint4*>(eg + tok * kEpiRowG + 32 * blk);
-      const uint4* usrc = reinterpret_cast<const uint4*>(eg + kTileRows * kEpiRowG + tok * kEpiRowG + 32 * blk);
-      // mxd::swiglu_table per element, written as three passes so that the 32 table loads are in flight
-      // together: clamp and table index, loads, then the products
-      uint32_t idx[32];
-      float up[32];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint4 gv = gsrc[j], uv = usrc[j];
-        const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const uint32_t gb = (gw[k >> 1] >> (16 * (k & 1))) & 0xFFFFu, ub = (uw[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
-          float upf = mx::bf16_value(ub);
-          upf = upf > lim ? lim : upf;
-          upf = upf < -lim ? -lim : upf;
-          idx[8 * j + k] = mx::bf16_value(gb) > lim ? mxd::kSiluLimit : gb;
-          up[8 * j + k] = upf;
-        }
-      }
-      float din[32];
-#pragma unroll
-      for (int k = 0; k < 32; ++k) din[k] = mxd::ldgf(a.silu + idx[k]);
-      float amax = 0.f;
-#pragma unroll
-      for (int k = 0; k < 32; ++k) {
-        const float product = din[k] * up[k];
-        din[k] = mxd::bf16_round_sel(weighted ? rw * product : product);
-        amax = fmaxf(amax, fabsf(din[k]));
-      }
-      amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
-      const uint32_t code = mx::act_scale_code(amax);
-      // x / 2^e as x * 2^-e: both are exact or one rounding of the same exact value (code is in
-      // [105, 246] for amax in [1e-4, FLT_MAX], so 2^-e is a normal float)
-      const float inv = mx::u2f((254u - code) << 23);
-      uint32_t words[8];
-#pragma unroll
-      for (int w = 0; w < 8; ++w)
-        words[w] = mxd::e4m3x4(din[4 * w] * inv, din[4 * w + 1] * inv, din[4 * w + 2] * inv, din[4 * w + 3] * inv);
-      uint4* dst = reinterpret_cast<uint4*>(a.dq + (size_t)row * a.I + 32 * gg);
-      dst[0] = uint4{words[0], words[1], words[2], words[3]};
-      dst[1] = uint4{words[4], words[5], words[6], words[7]};
-      a.ds[(size_t)row * (a.I / 32) + gg] = (uint8_t)code;
-    }
-  } else {
-    // D[4q + i][n] of tile t: W2 rows 64g + 16t + 4q + i
-    uint16_t* eo = reinterpret_cast<uint16_t*>(lds);
-    if (active) {
-      uint16_t* dst = eo + n * kEpiRowD + 64 * wave + 4 * q;
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          uint2 packed;
-          packed.x = mx::bf16_bits(acc[t][u][0]) | (mx::bf16_bits(acc[t][u][1]) << 16);
-          packed.y = mx::bf16_bits(acc[t][u][2]) | (mx::bf16_bits(acc[t][u][3]) << 16);
-          *reinterpret_cast<uint2*>(dst + 16 * u * kEpiRowD + 16 * t) = packed;
-        }
-    }
-    __syncthreads();
-    // thread tid copies segment tid % 64 of rows tid / 64 + 8 i (i < 16); their destinations are loaded
-    // together first
-    const int cols = min(512, a.H - 512 * (int)blockIdx.x);
-    const int seg = tid & 63, tok0 = tid >> 6;   // the multiplying waves' 512 threads
-    int dest[kTileRows / 8];
-#pragma unroll
-    for (int i = 0; i < kTileRows / 8; ++i) dest[i] = a.plan.row_dest[row0 + min(tok0 + 8 * i, rows - 1)];
-    if (tid < 512 && 8 * seg < cols) {
-#pragma unroll
-      for (int i = 0; i < kTileRows / 8; ++i) {
-        const int tok = tok0 + 8 * i;
-        if (tok < rows)
-          *reinterpret_cast<uint4*>(a.out + (size_t)dest[i] * a.H + 512 * blockIdx.x + 8 * seg) =
-              *reinterpret_cast<const uint4*>(eo + tok * kEpiRowD + 8 * seg);
+        asm volatile("" : "+v"(acc[0][u]), "+v"(acc[1][u]), "+v"(acc[2][u]), "+v"(acc[3][u]));
       }
     }
+  }
+  __syncthreads();   // the last chunk's LDS reads are done before the epilogue reuses the LDS
+
+  // D[4q + i][n] of tile t: lanes q < 2 hold W1 rows 32g + 8t + 4q + i, lanes q >= 2 the same W3 rows
+  uint16_t* eg = reinterpret_cast<uint16_t*>(lds);
+  if (active) {
+    uint16_t* dst = eg + (q >> 1) * (kTileRows * kEpiRowG) + n * kEpiRowG + 32 * wave + 4 * (q & 1);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        uint2 packed;
+        packed.x = mx::bf16_bits(acc[t][u][0]) | (mx::bf16_bits(acc[t][u][1]) << 16);
+        packed.y = mx::bf16_bits(acc[t][u][2]) | (mx::bf16_bits(acc[t][u][3]) << 16);
+        *reinterpret_cast<uint2*>(dst + 16 * u * kEpiRowG + 8 * t) = packed;
+      }
+  }
+  __syncthreads();
+  const bool weighted = slot < a.E;
+  // the clamp limit, or +inf when unclamped (no comparison then holds, as with no clamp)
+  const float lim = a.limit > 0.f ? a.limit : __builtin_inff();
+  for (int p = tid; p < kTileRows * 8; p += kXThreads) {
+    const int tok = p >> 3, blk = p & 7, gg = blockIdx.x * 8 + blk;
+    if (tok >= rows || gg >= groups) continue;
+    const int row = row0 + tok;
+    const float rw = a.plan.sorted_w[row];
+    const uint4* gsrc = reinterpret_cast<const uint4*>(eg + tok * kEpiRowG + 32 * blk);
+    const uint4* usrc = reinterpret_cast<const uint4*>(eg + kTileRows * kEpiRowG + tok * kEpiRowG + 32 * blk);
+    // mxd::swiglu_table per element, written as three passes so that the 32 table loads are in flight
+    // together: clamp and table index, loads, then the products
+    uint32_t idx[32];
+    float up[32];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint4 gv = gsrc[j], uv = usrc[j];
+      const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t gb = (gw[k >> 1] >> (16 * (k & 1))) & 0xFFFFu, ub = (uw[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
+        float upf = mx::bf16_value(ub);
+        upf = upf > lim ? lim : upf;
+        upf = upf < -lim ? -lim : upf;
+        idx[8 * j + k] = mx::bf16_value(gb) > lim ? mxd::kSiluLimit : gb;
+        up[8 * j + k] = upf;
+      }
+    }
+    float din[32];
+#pragma unroll
+    for (int k = 0; k < 32; ++k) din[k] = mxd::ldgf(a.silu + idx[k]);
+    float amax = 0.f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+      const float product = din[k] * up[k];
+      din[k] = mxd::bf16_round_sel(weighted ? rw * product : product);
+      amax = fmaxf(amax, fabsf(din[k]));
+    }
+    amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
+    const uint32_t code = mx::act_scale_code(amax);
+    // x / 2^e as x * 2^-e: both are exact or one rounding of the same exact value (code is in
+    // [105, 246] for amax in [1e-4, FLT_MAX], so 2^-e is a normal float)
+    const float inv = mx::u2f((254u - code) << 23);
+    uint32_t words[8];
+#pragma unroll
+    for (int w = 0; w < 8; ++w)
+      words[w] = mxd::e4m3x4(din[4 * w] * inv, din[4 * w + 1] * inv, din[4 * w + 2] * inv, din[4 * w + 3] * inv);
+    uint4* dst = reinterpret_cast<uint4*>(a.dq + (size_t)row * a.I + 32 * gg);
+    dst[0] = uint4{words[0], words[1], words[2], words[3]};
+    dst[1] = uint4{words[4], words[5], words[6], words[7]};
+    a.ds[(size_t)row * (a.I / 32) + gg] = (uint8_t)code;
   }
 }
 
@@ -582,6 +785,17 @@ uint64_t mx_prefill_workspace_bytes(mx_layer* layer, int32_t T) {
   return workspace_layout(v.cfg, T, v.has_shared).total;
 }
 
+int mx_prefill_stage_offsets(mx_layer* layer, int32_t T, uint64_t* offsets) {
+  const LayerView v = layer_view(layer);
+  MX_REQUIRE(v.ctx != nullptr, "layer is closed");
+  MX_REQUIRE(T > 0 && T <= (1 << 20), "token count %d outside [1, 2^20]", T);
+  MX_REQUIRE(offsets != nullptr, "mx_prefill_stage_offsets: null output");
+  const Workspace ws = workspace_layout(v.cfg, T, v.has_shared);
+  const uint64_t at[MX_PREFILL_STAGES] = {ws.dq, ws.ds, ws.pair_row, ws.row0};
+  for (int i = 0; i < MX_PREFILL_STAGES; ++i) offsets[i] = at[i];
+  return MX_OK;
+}
+
 int mx_moe_prefill(mx_layer* layer, const uint16_t* x, int32_t T, const int32_t* ids, const float* weights,
                    uint16_t* y, void* workspace, uint64_t workspace_bytes, void* stream) {
   const LayerView v = layer_view(layer);
@@ -660,10 +874,10 @@ int mx_moe_prefill(mx_layer* layer, const uint16_t* x, int32_t T, const int32_t*
   a.dq = b + ws.dq;
   a.ds = b + ws.ds;
   a.out = (uint16_t*)(b + ws.eout);
-  hipLaunchKernelGGL(grouped_kernel<true>, dim3((I + 255) / 256, ws.max_tiles), dim3(kGThreads), 0, st, a);
-  MX_LAUNCH_CHECK("grouped_kernel<gate/up>");
-  hipLaunchKernelGGL(grouped_kernel<false>, dim3((H + 511) / 512, ws.max_tiles), dim3(kGThreads), 0, st, a);
-  MX_LAUNCH_CHECK("grouped_kernel<down>");
+  hipLaunchKernelGGL(gateup_exact_kernel, dim3((I + 255) / 256, ws.max_tiles), dim3(kXThreads), 0, st, a);
+  MX_LAUNCH_CHECK("gateup_exact_kernel");
+  hipLaunchKernelGGL(grouped_down_kernel, dim3((H + 511) / 512, ws.max_tiles), dim3(kGThreads), 0, st, a);
+  MX_LAUNCH_CHECK("grouped_down_kernel");
   const int64_t items = (int64_t)T * (H / 8);
   hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)std::min<int64_t>(2048, (items + 255) / 256)), dim3(256), 0,
                      st, rid, (const uint16_t*)a.out, T, H, k, E, v.has_shared, y);

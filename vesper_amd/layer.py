@@ -203,9 +203,10 @@ class MoELayer:
                              C.c_void_p(int(y_ptr)), C.c_void_p(int(workspace)), int(workspace_bytes),
                              _lib._stream(stream))
 
-    def prefill(self, x, ids=None, weights=None) -> np.ndarray:
+    def prefill(self, x, ids=None, weights=None, stages: bool = False):
         """Host convenience: BF16 bits or FP32 [T, H] in (and optional int32 ids / FP32 weights [T, k]),
-        BF16 bits [T, H] out."""
+        BF16 bits [T, H] out. With stages=True also the call's intermediate stages (mx_prefill_stage_offsets):
+        (y, {"down_q" [rows, I], "down_s" [rows, I/32], "pair_row" [T, k], "row0" [E + 1]})."""
         bits = bf16_input(x, self.config.hidden)
         t = bits.shape[0]
         k = self.config.top_k
@@ -227,7 +228,18 @@ class MoELayer:
         dev = [self.ctx.upload(ids), self.ctx.upload(weights)] if ids is not None else [None, None]
         try:
             self.prefill_device(xd.ptr, t, yd.ptr, ws, nbytes, dev[0], dev[1])
-            return yd.download()
+            y = yd.download()
+            if not stages:
+                return y
+            cfg = self.config
+            at = (C.c_uint64 * 4)()
+            self.lib.prefill_stage_offsets(self.handle, t, at)
+            rows = t * cfg.top_k + (t if cfg.shared else 0)
+            i = cfg.intermediate
+            return y, {"down_q": self.ctx.download(ws + at[0], (rows, i), np.uint8),
+                       "down_s": self.ctx.download(ws + at[1], (rows, i // 32), np.uint8),
+                       "pair_row": self.ctx.download(ws + at[2], (t, cfg.top_k), np.int32),
+                       "row0": self.ctx.download(ws + at[3], (cfg.experts + 1,), np.int32)}
         finally:
             for d in [xd, yd] + [d for d in dev if d is not None]:
                 d.free()
