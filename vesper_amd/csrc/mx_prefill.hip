@@ -194,6 +194,7 @@ struct GemmArgs {
   const float* silu;             // [mxd::kSiluEntries] the layer's SiLU table
   const uint8_t* xq;             // [T][H] E4M3 codes of the tokens
   const uint8_t* xs;             // [T][H / 32] E8M0
+  const uint16_t* xd;            // [T][H] each code times its block scale, BF16 (exact)
   uint8_t* dq;                   // [rows][I] down-input codes
   uint8_t* ds;                   // [rows][I / 32]
   uint16_t* out;                 // [T][k + 1][H] expert outputs (BF16), token-major (plan.row_dest)
@@ -410,43 +411,50 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(GemmArgs a) {
 // (its adder drops low product bits), so each block runs on V_MFMA_F32_16X16X32_BF16 with a zero
 // accumulator -- which returns the exact 32-product dot rounded once -- over operands converted exactly:
 // weights by V_CVT_SCALEF32_PK_BF16_FP4 with the block's E8M0 scale as the scale operand (an E2M1 value
-// times a power of two has at most two significant bits), activations by V_CVT_SCALEF32_PK_BF16_FP8 with the
-// token's block scale (four significant bits). The in-order chain acc = acc + d runs on the VALU: with a
-// non-zero accumulator the MFMA does not round acc + dot as IEEE addition does.
+// times a power of two has at most two significant bits), activations as the quantizer's BF16 copy of each
+// code times its block scale (four significant bits). The in-order chain acc = acc + d runs on the VALU:
+// with a non-zero accumulator the MFMA does not round acc + dot as IEEE addition does.
 //
 // grid (ceil(I / 256), tiles), 512 threads: 8 waves, wave w one group of 32 intermediate rows (4 MFMA
 // tiles, W1 rows 8t + 0..7 and the same W3 rows in tile t) for all 128 rows of the tile, 128 accumulator
-// registers. Every wave also copies its share of chunk c + 2's operands global -> LDS (global_load_lds,
-// kXCopies instructions: its group's four weight pieces and scale words, its token tile's two activation
-// blocks and the 16 rows' activation scale words) into the same 3-stage ring and layout as the down
-// kernel's; a step waits for this wave's copies of chunk c + 1, meets the barrier, issues chunk c + 2 and
-// multiplies chunk c. Operands come from LDS with the bf16 MFMA's lane map (A lane (m, q) = row m, K 8q..8q+7
-// of a block: word q of lane (m, b)'s 16 bytes; B lane (n, q) = token n, the same K: 8 bytes of the
-// activation block), read by inline assembly and waited for explicitly (the compiler cannot see that the
-// copies write LDS).
+// registers. Every wave copies its share of chunk c + 1's operands global -> LDS (global_load_lds, kXCopies
+// instructions: its group's four weight pieces and scale words, and token tile w's four BF16 activation
+// blocks) into a 2-stage ring; a step waits for this wave's copies of chunk c, meets the barrier, issues
+// chunk c + 1 and multiplies chunk c. (Half-chunk steps through a 4-stage ring, which copy three steps
+// ahead, and FP8 activations through a 3-stage ring, converted per wave, both measured slower: per-step
+// costs -- the barrier, the first LDS reads, the last additions -- and the conversions outweigh the deeper
+// prefetch.) Operands come from LDS with the bf16 MFMA's lane map (A lane
+// (m, q) = row m, K 8q..8q+7 of a block: word q of lane (m, b)'s 16 bytes in the tiled layout; B lane
+// (n, q) = token n, the same K: the copy puts them at lane slot 16 q + n of the (token tile, block) KB),
+// read by inline assembly and waited for explicitly (the compiler cannot see that the copies write LDS).
 constexpr int kXThreads = 512;
-constexpr int kXCopies = 8;
+constexpr int kXCopies = 9;
+constexpr int kXStages = 2;
+// a stage: the 8 groups' weight tiles (group w, tile t at 1 KB x (4 w + t)), their scale words (256 B per
+// group), then the activations: token tile u, block b at 1 KB x (4 u + b)
+constexpr int kXStageA = 0, kXStageAS = 32768, kXStageB = 34816, kXStageBytes = 67584;
+static_assert(kXStages * kXStageBytes <= 160 * 1024 && 2 * kTileRows * kEpiRowG * 2 <= kXStages * kXStageBytes,
+              "exact gate/up LDS layout");
 
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
-// 8 E2M1 values (one 32-bit word) times 2^(code - 127), exact in BF16
-__device__ __forceinline__ v8bf fp4_word_scaled(uint32_t word, uint32_t code) {
-  const float scale = __uint_as_float(code << 23);
+// byte `kByte` of `word` shifted to an FP32 exponent field: the E8M0 code as the power of two it encodes
+// (one SDWA instruction)
+template <int kByte>
+__device__ __forceinline__ float e8m0_scale(uint32_t word, uint32_t twenty_three) {
+  uint32_t r;
+  asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_%3"
+      : "=v"(r) : "v"(twenty_three), "v"(word), "n"(kByte));
+  return __uint_as_float(r);
+}
+
+// 8 E2M1 values (one 32-bit word) times the power of two `scale`, exact in BF16
+__device__ __forceinline__ v8bf fp4_word_scaled(uint32_t word, float scale) {
   const v2bf p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 0);
   const v2bf p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 1);
   const v2bf p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 2);
   const v2bf p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 3);
-  return v8bf{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
-}
-
-// 8 E4M3 values (two 32-bit words, K order) times 2^(code - 127), exact in BF16
-__device__ __forceinline__ v8bf fp8_pair_scaled(uint32_t lo, uint32_t hi, uint32_t code) {
-  const float scale = __uint_as_float(code << 23);
-  const v2bf p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, scale, false);
-  const v2bf p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, scale, true);
-  const v2bf p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, scale, false);
-  const v2bf p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, scale, true);
   return v8bf{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
 }
 
@@ -482,39 +490,91 @@ __device__ __forceinline__ void lds_read_weights(uint32_t a_addr, uint32_t s_add
       : "v"(a_addr), "v"(s_addr));
 }
 
-// the activation piece (8 bytes) of token tile u at LDS address addr + 2048 u, for u < 8, and the tiles'
-// scale words at saddr + 64 u
-__device__ __forceinline__ void lds_read_acts(uint32_t addr, uint32_t saddr, uint2 (&x)[8], uint32_t (&xs)[8]) {
-  typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
-  u32x2_t r[8];
+// four token tiles' activation operands of one block: 16 bytes at addr + 4 KB j, j < 4
+__device__ __forceinline__ void lds_read_acts4(uint32_t addr, mxd::u32x4_t (&x)[4]) {
   asm volatile(
-      "ds_read_b64 %0, %16\n\t"
-      "ds_read_b64 %1, %16 offset:2048\n\t"
-      "ds_read_b64 %2, %16 offset:4096\n\t"
-      "ds_read_b64 %3, %16 offset:6144\n\t"
-      "ds_read_b64 %4, %16 offset:8192\n\t"
-      "ds_read_b64 %5, %16 offset:10240\n\t"
-      "ds_read_b64 %6, %16 offset:12288\n\t"
-      "ds_read_b64 %7, %16 offset:14336\n\t"
-      "ds_read_b32 %8, %17\n\t"
-      "ds_read_b32 %9, %17 offset:64\n\t"
-      "ds_read_b32 %10, %17 offset:128\n\t"
-      "ds_read_b32 %11, %17 offset:192\n\t"
-      "ds_read_b32 %12, %17 offset:256\n\t"
-      "ds_read_b32 %13, %17 offset:320\n\t"
-      "ds_read_b32 %14, %17 offset:384\n\t"
-      "ds_read_b32 %15, %17 offset:448\n\t"
+      "ds_read_b128 %0, %4\n\t"
+      "ds_read_b128 %1, %4 offset:4096\n\t"
+      "ds_read_b128 %2, %4 offset:8192\n\t"
+      "ds_read_b128 %3, %4 offset:12288\n\t"
       "s_waitcnt lgkmcnt(0)"
-      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7]),
-        "=&v"(xs[0]), "=&v"(xs[1]), "=&v"(xs[2]), "=&v"(xs[3]), "=&v"(xs[4]), "=&v"(xs[5]), "=&v"(xs[6]),
-        "=&v"(xs[7])
-      : "v"(addr), "v"(saddr));
+      : "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3])
+      : "v"(addr));
+}
+
+// One wave's copies and LDS operand addresses (see gateup_exact_kernel).
+struct ExactStream {
+  const uint8_t* wsrc;    // group's weight pieces, + 16 lane
+  const uint8_t* ssrc;    // group's scale words, + 4 lane
+  const uint8_t* xbase;   // the BF16 activations
+  uint32_t boff;          // this lane's activation row and K offset
+  uint32_t lds0, la, las, lb;
+  int wave, C;
+  bool active;
+  __device__ __forceinline__ void copy(int c) const {
+    const uint32_t st = lds0 + (uint32_t)(c % kXStages) * kXStageBytes;
 #pragma unroll
-  for (int u = 0; u < 8; ++u) x[u] = uint2{r[u].x, r[u].y};
+    for (int t = 0; t < 4; ++t)
+      global_to_lds16(wsrc + (size_t)c * 4096 + t * 1024, __builtin_amdgcn_readfirstlane(st + kXStageA + (4 * wave + t) * 1024));
+    global_to_lds4(ssrc + (size_t)c * 256, __builtin_amdgcn_readfirstlane(st + kXStageAS + 256 * wave));
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      global_to_lds16(xbase + (size_t)c * 256 + boff + 64 * b,
+                      __builtin_amdgcn_readfirstlane(st + kXStageB + (4 * wave + b) * 1024));
+  }
+};
+
+// The K loop for a tile with L live 16-row token tiles (L is a template argument so that the token-tile loop
+// has no per-tile branches).
+template <int L>
+__device__ __forceinline__ void exact_stream(const ExactStream& s, v4f (&acc)[4][8]) {
+  const uint32_t k23 = 23;
+  s.copy(0);
+  for (int c = 0; c < s.C; ++c) {
+    __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));   // this wave's copies of chunk c have landed
+    copy_barrier();   // every wave's copies of chunk c are visible; chunk c - 1's stage is free
+    if (c + 1 < s.C) s.copy(c + 1);
+    if (!s.active) continue;
+    const uint32_t so = (uint32_t)(c % kXStages) * kXStageBytes;
+    uint32_t w[4][4], sw[4];
+    lds_read_weights(s.la + so, s.las + so, w, sw);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const float ws[4] = {e8m0_scale<0>(sw[b], k23), e8m0_scale<1>(sw[b], k23), e8m0_scale<2>(sw[b], k23),
+                           e8m0_scale<3>(sw[b], k23)};
+      v8bf av[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) av[t] = fp4_word_scaled(w[t][b], ws[t]);
+      // token tile u's four MFMAs are issued before tile u - 1's additions, so every addition reads a result
+      // finished while other work issued; the empty statements fix that order (the compiler keeps them in
+      // sequence) and keep at most two tiles' results live
+      v4f d[2][4];   // results of token tiles u (d[u & 1]) and u - 1
+      mxd::u32x4_t x[4];
+#pragma unroll
+      for (int u = 0; u <= L; ++u) {
+        if (u < L) {
+          if ((u & 3) == 0) lds_read_acts4(s.lb + so + (4 * u + b) * 1024, x);
+          mxd::u32x4_t xw = x[u & 3];
+          asm volatile("" : "+v"(xw));
+          const v8bf xv = __builtin_bit_cast(v8bf, xw);
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            d[u & 1][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[t], xv, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        }
+        if (u >= 1) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[t][u - 1][i] = acc[t][u - 1][i] + d[(u - 1) & 1][t][i];
+          asm volatile("" : "+v"(acc[0][u - 1]), "+v"(acc[1][u - 1]), "+v"(acc[2][u - 1]), "+v"(acc[3][u - 1]));
+        }
+      }
+    }
+  }
 }
 
 __global__ __launch_bounds__(kXThreads) void gateup_exact_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kXStages * kXStageBytes];
   const int ti = blockIdx.y;
   if (ti >= *a.plan.n_tiles) return;
   const int32_t* info = a.plan.tile_info + (size_t)ti * 4;
@@ -522,91 +582,54 @@ __global__ __launch_bounds__(kXThreads) void gateup_exact_kernel(GemmArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q = lane >> 4, n = lane & 15, m = lane & 15;
-  const int H = a.H, C = H / 128;
+  const int H = a.H;
   // a wave past the last group (I / 32 groups) copies the last group's weights and computes nothing
   const int groups = a.I / 32;
   const int g = blockIdx.x * 8 + wave;
   const bool active = g < groups;
   const uint8_t* blob = a.tiles[slot];
   const TiledOffsets off = tiled_offsets(H, a.I);
-  const int live_tiles = min(8, (rows + 15) / 16);
+  const int live_tiles = __builtin_amdgcn_readfirstlane(min(8, (rows + 15) / 16));
   const uint32_t lds0 = lds_addr(lds);
 
-  // this wave's copies: group gc's weight pieces and scale words, token tile u = wave's two activation blocks
-  // (rows past the tile repeat its last row) and rows 16 wave .. + 15's activation scale words
+  // this wave's copies: group gc's weight pieces and scale words, and token tile u = wave's four activation
+  // blocks (rows past the tile repeat its last row); lane (n, q) of block b's copy takes 16 bytes at
+  // K 32 b + 8 q of row 16 wave + n, so that it lands at lane slot 16 q + n. LDS operand addresses of this
+  // lane (stage offset added per step): weight word q of lane (m, b) of tile t at kXStageA + (4 wave + t) KB
+  // + 16 (16 b + m) + 4 q; its scale byte t of word 16 b + m; activation block b of token tile u at
+  // kXStageB + (4 u + b) KB + 16 lane
+  ExactStream s;
   const int gc = min(g, groups - 1);
-  const uint8_t* wsrc = blob + (size_t)gc * C * 4096 + 16 * lane;
-  const uint8_t* ssrc = blob + off.gu_s + (size_t)gc * C * 256 + 4 * lane;
-  const uint32_t boff = (uint32_t)a.plan.sorted_tok[row0 + min(16 * wave + n, rows - 1)] * (uint32_t)H + 16 * q;
-  const uint32_t soff = (uint32_t)a.plan.sorted_tok[row0 + min(16 * wave + (lane & 15), rows - 1)] * (uint32_t)(H / 32);
-  // the offsets are loaded before the first copy is issued: a wait for them afterwards would also wait for
-  // the copies (the vector memory counter retires in order)
-  asm volatile("" : : "v"(boff), "v"(soff));
-  auto copy = [&](int c) {
-    const uint32_t st = lds0 + (uint32_t)(c % kStages) * kStageBytes;
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-      global_to_lds16(wsrc + (size_t)c * 4096 + t * 1024, __builtin_amdgcn_readfirstlane(st + kStageA + (4 * wave + t) * 1024));
-    global_to_lds4(ssrc + (size_t)c * 256, __builtin_amdgcn_readfirstlane(st + kStageAS + 256 * wave));
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      global_to_lds16(a.xq + (size_t)c * 128 + boff + 64 * h,
-                      __builtin_amdgcn_readfirstlane(st + kStageB + (2 * wave + h) * 1024));
-    if (lane < 16) global_to_lds4(a.xs + (size_t)c * 4 + soff, __builtin_amdgcn_readfirstlane(st + kStageBS + 64 * wave));
-  };
-
-  // LDS operand addresses of this lane (chunk stage offset added per step): weight word q of lane (m, b) of
-  // tile t at kStageA + (4 wave + t) KB + 16 (16 b + m) + 4 q; its scale byte t of word 16 b + m; activation
-  // block b of token tile u: bytes 32 b + 8 q .. of row 16 u + n sit in block 2u + (b >> 1) at lane slot
-  // 16 (2 (b & 1) + (q >> 1)) + n, byte 8 (q & 1); the row's scale byte b in word 16 u + n
-  const uint32_t la = lds0 + kStageA + 4096 * wave + 16 * m + 4 * q;
-  const uint32_t las = lds0 + kStageAS + 256 * wave + 4 * m;
-  const uint32_t lb = lds0 + kStageB + 16 * (16 * (q >> 1) + n) + 8 * (q & 1);
-  const uint32_t lbs = lds0 + kStageBS + 4 * n;
+  const int C = H / 128;
+  s.C = C;
+  s.wsrc = blob + (size_t)gc * C * 4096 + 16 * lane;
+  s.ssrc = blob + off.gu_s + (size_t)gc * C * 256 + 4 * lane;
+  s.xbase = reinterpret_cast<const uint8_t*>(a.xd);
+  s.boff = (uint32_t)a.plan.sorted_tok[row0 + min(16 * wave + n, rows - 1)] * (uint32_t)(2 * H) + 16 * q;
+  // the offset is loaded before the first copy is issued: a wait for it afterwards would also wait for the
+  // copies (the vector memory counter retires in order)
+  asm volatile("" : : "v"(s.boff));
+  s.lds0 = lds0;
+  s.la = lds0 + kXStageA + 4096 * wave + 16 * m + 4 * q;
+  s.las = lds0 + kXStageAS + 256 * wave + 4 * m;
+  s.lb = lds0 + kXStageB + 16 * lane;
+  s.wave = wave;
+  s.active = active;
 
   v4f acc[4][8];
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
     for (int u = 0; u < 8; ++u) acc[t][u] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  copy(0);
-  if (C > 1) copy(1);
-  for (int c = 0; c < C; ++c) {
-    // chunk c has landed once at most chunk c + 1's copies are still in flight
-    if (c + 1 < C) __builtin_amdgcn_s_waitcnt(vm_wait_imm(kXCopies));
-    else __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));
-    copy_barrier();   // every wave's copies of chunk c are visible; chunk c - 1's stage is free
-    if (c + 2 < C) copy(c + 2);
-    if (!active) continue;
-    const uint32_t so = (uint32_t)(c % kStages) * kStageBytes;
-    uint32_t w[4][4], sw[4];
-    lds_read_weights(la + so, las + so, w, sw);
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      v8bf av[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) av[t] = fp4_word_scaled(w[t][b], (sw[b] >> (8 * t)) & 0xFF);
-      uint2 x[8];
-      uint32_t xs[8];
-      lds_read_acts(lb + so + 1024 * (b >> 1) + 512 * (b & 1), lbs + so, x, xs);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        if (u >= live_tiles) break;   // wave-uniform
-        mxd::u32x4_t xw = __builtin_bit_cast(mxd::u32x4_t, fp8_pair_scaled(x[u].x, x[u].y, (xs[u] >> (8 * b)) & 0xFF));
-        // ordered after the previous token tile's pin below: this tile's MFMAs cannot be hoisted above the
-        // previous tile's additions, so at most one tile's four results are live at a time
-        asm volatile("" : "+v"(xw));
-        const v8bf xv = __builtin_bit_cast(v8bf, xw);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const v4f d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[t], xv, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[t][u][i] = acc[t][u][i] + d[i];
-        }
-        asm volatile("" : "+v"(acc[0][u]), "+v"(acc[1][u]), "+v"(acc[2][u]), "+v"(acc[3][u]));
-      }
-    }
+  switch (live_tiles) {
+    case 1: exact_stream<1>(s, acc); break;
+    case 2: exact_stream<2>(s, acc); break;
+    case 3: exact_stream<3>(s, acc); break;
+    case 4: exact_stream<4>(s, acc); break;
+    case 5: exact_stream<5>(s, acc); break;
+    case 6: exact_stream<6>(s, acc); break;
+    case 7: exact_stream<7>(s, acc); break;
+    default: exact_stream<8>(s, acc); break;
   }
   __syncthreads();   // the last chunk's LDS reads are done before the epilogue reuses the LDS
 
@@ -734,7 +757,7 @@ uint64_t r256(uint64_t b) { return (b + 255) & ~255ull; }
 
 // Workspace layout (each piece 256-byte aligned).
 struct Workspace {
-  uint64_t logits, scores, selection, ids, w, xq, xs, counts, row0, tile_info, n_tiles, sorted_tok, sorted_w,
+  uint64_t logits, scores, selection, ids, w, xq, xs, xd, counts, row0, tile_info, n_tiles, sorted_tok, sorted_w,
       pair_row, row_dest, dq, ds, eout, total;
   int max_tiles, rows;
 };
@@ -758,6 +781,7 @@ Workspace workspace_layout(const mx_moe_config& c, int T, int has_shared) {
   w.w = take(pairs * 4);
   w.xq = take((uint64_t)T * H);
   w.xs = take((uint64_t)T * H / 32);
+  w.xd = take((uint64_t)T * H * 2);
   w.counts = take((E + 1) * 4);
   w.row0 = take((E + 1) * 4);
   w.tile_info = take((uint64_t)w.max_tiles * 16);
@@ -840,7 +864,7 @@ int mx_moe_prefill(mx_layer* layer, const uint16_t* x, int32_t T, const int32_t*
     rid = fixed_ids;
     rw = fixed_w;
   }
-  if (int s = mx_act_quant32(v.ctx, x, b + ws.xq, b + ws.xs, T, H, stream)) return s;
+  if (int s = mxi::act_quant32_scaled(v.ctx, x, b + ws.xq, b + ws.xs, (uint16_t*)(b + ws.xd), T, H, st)) return s;
   PrefillPlan p{};
   p.counts = (int32_t*)(b + ws.counts);
   p.row0 = (int32_t*)(b + ws.row0);
@@ -871,6 +895,7 @@ int mx_moe_prefill(mx_layer* layer, const uint16_t* x, int32_t T, const int32_t*
   a.silu = v.silu;
   a.xq = b + ws.xq;
   a.xs = b + ws.xs;
+  a.xd = (const uint16_t*)(b + ws.xd);
   a.dq = b + ws.dq;
   a.ds = b + ws.ds;
   a.out = (uint16_t*)(b + ws.eout);
