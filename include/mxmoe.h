@@ -411,9 +411,11 @@ uint64_t mx_prefill_workspace_bytes(mx_layer* layer, int32_t tokens);
  * mx_moe_prefill call leaves there: offsets[0] the down-input E4M3 codes [rows][I] (uint8), [1] their
  * E8M0 scales [rows][I/32], [2] the row of each routed pair (token t, rank j) [T][k] (int32), [3] the
  * first row of each expert [E + 1] (int32; the shared expert's rows, one per token in order, start at
- * entry E). The reference returns these stages from its per-token call (ConnectedMoE.forward's expert
- * dicts, connected.py:154-160); here they are read from the batched call's workspace. */
-#define MX_PREFILL_STAGES 4
+ * entry E), [4] the expert outputs [T][k + 1][H] (BF16; token t's j-th routed expert in ascending ID at
+ * place j, the shared expert at place k). The reference returns these stages from its per-token call
+ * (ConnectedMoE.forward's expert dicts, connected.py:154-160); here they are read from the batched call's
+ * workspace. */
+#define MX_PREFILL_STAGES 5
 int mx_prefill_stage_offsets(mx_layer* layer, int32_t tokens, uint64_t* offsets);
 int mx_moe_prefill(mx_layer* layer, const uint16_t* x_bf16, int32_t tokens, const int32_t* ids, const float* weights,
                    uint16_t* y_bf16, void* workspace, uint64_t workspace_bytes, void* stream);

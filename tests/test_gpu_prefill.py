@@ -19,10 +19,11 @@ from oracle.expert import expert_forward
 from oracle.inputs import activations, mxfp4_expert, router_weight
 from vesper_amd.workloads import zipf_routing
 from oracle.moe import moe_layer, moe_layer_routed
-from tests.helpers import assert_close, max_rel_err
+from tests.helpers import assert_close, assert_gemv_close, max_rel_err
 from vesper_amd import _lib
 from vesper_amd.config import MoEConfig
-from vesper_amd.layer import ExpertBank, MoELayer
+from vesper_amd.layer import ExpertBank, MoELayer, bf16_input
+from vesper_amd.tiered import decode_routed
 
 pytestmark = pytest.mark.gpu
 
@@ -249,5 +250,55 @@ def test_prefill_sweep_misses_are_bit_exact_in_gate_up(gpu_ctx, seed, tokens):
         for t in range(tokens):
             assert max_rel_err(got[t], ref["output_bf16"][t]) <= 2e-2, t
     finally:
+        layer.close()
+        bank.free()
+
+
+def test_prefill_T4096_in_full_against_routed_decode_and_tile_edges(gpu_ctx):
+    """BASELINE configuration 2 in full (T = 4096, Zipf(1.1) routing): every one of the 4096 prefill outputs
+    against mx_moe_decode_routed on the same ids and weights (256 calls of 16 tokens) within the north-star
+    bar -- per token, not only in aggregate; and the busiest expert (28 tiles of 128 rows): the first and
+    last row of every tile through the oracle's expert -- down-input codes and scales bit-exact (they come
+    from the exact gate/up), the expert's W2 output rows GEMV-close (the down GEMM sums K in its own order)."""
+    cfg = MoEConfig()
+    rng = np.random.default_rng(20261018)
+    bank = ExpertBank(gpu_ctx, cfg, cfg.experts + 1)
+    bank.fill_synthetic(seed=5)
+    w = router_weight(rng, cfg.experts, cfg.hidden)
+    layer = MoELayer(gpu_ctx, cfg, w, bank)
+    T, k, h = 4096, cfg.top_k, cfg.hidden
+    bufs = []
+    try:
+        x = activations(rng, T, h)
+        ids, wts = zipf_routing(rng, T, cfg.experts, k)
+        got, stages = layer.prefill(x, ids, wts, stages=True)
+        xd, idd, wd = gpu_ctx.upload(bf16_input(x, h)), gpu_ctx.upload(ids), gpu_ctx.upload(wts)
+        yd = gpu_ctx.empty((T, h), np.uint16)
+        bufs = [xd, idd, wd, yd]
+        for t0 in range(0, T, 16):
+            decode_routed(layer, xd.ptr + 2 * h * t0, 16, idd.ptr + 4 * k * t0, wd.ptr + 4 * k * t0,
+                          yd.ptr + 2 * h * t0)
+        dec = yd.download()
+        assert_close(got, dec, "prefill vs routed decode, all 4096 tokens")
+        worst = max(max_rel_err(got[t], dec[t]) for t in range(T))
+        assert worst <= 2e-2, worst
+
+        counts = np.bincount(ids.ravel(), minlength=cfg.experts)
+        e = int(np.argmax(counts))
+        toks = np.flatnonzero((ids == e).any(axis=1))             # the expert's rows, ascending token
+        tiles = (len(toks) + 127) // 128
+        assert tiles == 28
+        edges = sorted({i for tl in range(tiles) for i in (128 * tl, min(128 * tl + 127, len(toks) - 1))})
+        sample = toks[edges]
+        rank = (ids[sample] == e).argmax(axis=1)
+        ref = expert_forward(x[sample], bank.download(e), wts[sample, rank], cfg.swiglu_limit)
+        rows = stages["pair_row"][sample, rank]
+        np.testing.assert_array_equal(stages["down_q"][rows], ref["down_q"], err_msg="busiest expert codes")
+        np.testing.assert_array_equal(stages["down_s"][rows], ref["down_s"], err_msg="busiest expert scales")
+        place = (np.sort(ids[sample], axis=1) == e).argmax(axis=1)  # the expert's place among the token's
+        assert_gemv_close(stages["expert_out"][sample, place], ref["w2"], "busiest expert W2 rows")
+    finally:
+        for d in bufs:
+            d.free()
         layer.close()
         bank.free()

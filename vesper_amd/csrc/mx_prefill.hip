@@ -815,7 +815,7 @@ int mx_prefill_stage_offsets(mx_layer* layer, int32_t T, uint64_t* offsets) {
   MX_REQUIRE(T > 0 && T <= (1 << 20), "token count %d outside [1, 2^20]", T);
   MX_REQUIRE(offsets != nullptr, "mx_prefill_stage_offsets: null output");
   const Workspace ws = workspace_layout(v.cfg, T, v.has_shared);
-  const uint64_t at[MX_PREFILL_STAGES] = {ws.dq, ws.ds, ws.pair_row, ws.row0};
+  const uint64_t at[MX_PREFILL_STAGES] = {ws.dq, ws.ds, ws.pair_row, ws.row0, ws.eout};
   for (int i = 0; i < MX_PREFILL_STAGES; ++i) offsets[i] = at[i];
   return MX_OK;
 }

@@ -206,7 +206,8 @@ class MoELayer:
     def prefill(self, x, ids=None, weights=None, stages: bool = False):
         """Host convenience: BF16 bits or FP32 [T, H] in (and optional int32 ids / FP32 weights [T, k]),
         BF16 bits [T, H] out. With stages=True also the call's intermediate stages (mx_prefill_stage_offsets):
-        (y, {"down_q" [rows, I], "down_s" [rows, I/32], "pair_row" [T, k], "row0" [E + 1]})."""
+        (y, {"down_q" [rows, I], "down_s" [rows, I/32], "pair_row" [T, k], "row0" [E + 1],
+        "expert_out" [T, k + 1, H] (token t's experts in ascending ID, the shared expert last)})."""
         bits = bf16_input(x, self.config.hidden)
         t = bits.shape[0]
         k = self.config.top_k
@@ -232,14 +233,15 @@ class MoELayer:
             if not stages:
                 return y
             cfg = self.config
-            at = (C.c_uint64 * 4)()
+            at = (C.c_uint64 * 5)()
             self.lib.prefill_stage_offsets(self.handle, t, at)
             rows = t * cfg.top_k + (t if cfg.shared else 0)
             i = cfg.intermediate
             return y, {"down_q": self.ctx.download(ws + at[0], (rows, i), np.uint8),
                        "down_s": self.ctx.download(ws + at[1], (rows, i // 32), np.uint8),
                        "pair_row": self.ctx.download(ws + at[2], (t, cfg.top_k), np.int32),
-                       "row0": self.ctx.download(ws + at[3], (cfg.experts + 1,), np.int32)}
+                       "row0": self.ctx.download(ws + at[3], (cfg.experts + 1,), np.int32),
+                       "expert_out": self.ctx.download(ws + at[4], (t, cfg.top_k + 1, cfg.hidden), np.uint16)}
         finally:
             for d in [xd, yd] + [d for d in dev if d is not None]:
                 d.free()
