@@ -91,6 +91,11 @@ int mx_copy_kernel(mx_ctx* ctx, void* dst, const void* src, uint64_t bytes, void
  * (src/vesper/tiered.py:78-95). data and digests 16-byte aligned and not overlapping. */
 int mx_sha256_chunks(mx_ctx* ctx, const void* data, uint64_t bytes, void* digests, void* stream);
 
+/* The same digest table of `bytes` HOST bytes (0 < bytes <= 2^30), computed on the host with `threads`
+ * threads (1..64); no context or device. Replaces hash_chunks (src/vesper/integrity.py:21-34), the host
+ * table of a verified store read that the GPU audit compares a slot with. */
+int mx_host_sha256_chunks(const void* data, uint64_t bytes, void* digests, int32_t threads);
+
 /* Batched admission audit: for each of the n slots (device pointers, `bytes` each) hash every 4 KiB chunk
  * as mx_sha256_chunks does, compare with expected[i] (device digest table, ceil(bytes / 4096) x 32 bytes)
  * and add slot i's count of differing chunks to mismatches[counters[i]] (device; counters NULL = i). The

@@ -88,6 +88,33 @@ def test_tiered_runtime_over_store_matches_resident_expert(direct_io_dir, mode):
         assert runtime.snapshot()["counters"]["integrity_failures"] == 1
 
 
+@pytest.mark.parametrize("mode", ["readback", "gpu-sha256"])
+def test_tiered_runtime_batch_prefetch_matches_resident_expert(direct_io_dir, mode):
+    """TieredExpertRuntime.prefetch promotes a batch through the store's read-ahead pipeline (reads and host
+    checks of later experts beside the uploads and audits of earlier ones): every expert lands in its own
+    slot, and the calls that follow are GPU hits whose stage dicts equal ResidentExpert's bit for bit."""
+    rng = np.random.default_rng(37)
+    ids = (2, 5, 6, 11)
+    experts = {e: mxfp4_expert(rng, REFERENCE_PROFILE.hidden, REFERENCE_PROFILE.intermediate) for e in ids}
+    store = direct_io_dir / "store"
+    build_store([(0, e, a) for e, a in experts.items()], store, max_experts=4)
+    x = activations(rng, 1, REFERENCE_PROFILE.hidden)[0]
+    weight = np.float32(0.61)
+    with TieredExpertRuntime(store, cache_config(mode, 4, 0, REFERENCE_PROFILE, 4)) as runtime:
+        print(f"tiered {mode} batch prefetch", flush=True)
+        assert runtime.prefetch([f"0:{e}" for e in ids]) == ["store"] * 4
+        for e in ids:
+            got = runtime.forward(f"0:{e}", x, weight)
+            assert runtime.last_event["source_tier"] == "primary_gpu"
+            with ResidentExpert(experts[e]) as resident:
+                ref = resident.forward(x, weight)
+            for name, value in ref.items():
+                np.testing.assert_array_equal(got[name], value[0], err_msg=f"{e} {name}")
+        c = runtime.snapshot()["counters"]
+        assert c["store_reads_completed"] == 4 and c["primary_hits"] == 4 and c["integrity_failures"] == 0
+    assert runtime.cleanup["host_buffer_reservations_bytes"] == 0
+
+
 class Resident:
     """The decode layer on the same weights, no shared expert: its output is the routed sum rounded once."""
 

@@ -162,3 +162,22 @@ def test_verify_compares_the_table_the_device_returns():
             else:
                 with pytest.raises(ValueError, match="differ from verified original"):
                     audit.verify(0x1000, expected, comparison=comparison)
+
+
+def test_native_host_digest_table_equals_hashlib():
+    """mx_host_sha256_chunks (the store's host digest tables, OpenSSL on host threads) against hashlib chunk by
+    chunk, for a short last chunk, a single chunk and several thread counts; refusals as hash_chunks'."""
+    import hashlib
+    from vesper_amd.integrity import digest_shape, hash_chunks_native
+    rng = np.random.default_rng(3)
+    for size, threads in ((4096 * 37 + 123, 1), (4096 * 37 + 123, 5), (4096, 4), (1000, 2), (4096 * 64, 64)):
+        data = rng.integers(0, 256, size, dtype=np.uint8)
+        table = np.zeros(digest_shape(size), np.uint8)
+        hash_chunks_native(data, table, threads)
+        for c in range(table.shape[0]):
+            assert table[c].tobytes() == hashlib.sha256(data[4096 * c:4096 * (c + 1)].tobytes()).digest(), (size, c)
+    data = rng.integers(0, 256, 8192, dtype=np.uint8)
+    with pytest.raises(ValueError):
+        hash_chunks_native(data, np.zeros((3, 32), np.uint8))
+    with pytest.raises(ValueError):
+        hash_chunks_native(data.astype(np.int16), np.zeros((4, 32), np.uint8))

@@ -172,3 +172,72 @@ def test_expert_fixture_round_trip_and_store_from_fixtures(direct_io_dir):
     (direct_io_dir / "fx" / "manifest.json").write_text(json.dumps(m))
     with pytest.raises(ValueError, match="source hash"):
         load_expert_fixture(path, TINY)
+
+
+class HostSlots:
+    """A GPU backend stand-in whose slots are host arrays; verify() hashes the slot's 4 KiB chunks against the
+    store's digest table of the verified read (what HipCacheBackend.verify does on the device)."""
+
+    def __init__(self, store, slots):
+        from vesper_amd.integrity import digest_shape, hash_chunks
+        self.primary_slots, self.helper_slots, self.store = slots, 0, store
+        self.staging = [np.zeros(store.size, np.uint8), np.zeros(store.size, np.uint8)]
+        self.slots = [np.zeros(store.size, np.uint8) for _ in range(slots)]
+        self._shape, self._hash = digest_shape, hash_chunks
+
+    def write(self, tier, slot, data):
+        self.slots[slot][:] = data
+
+    def read(self, tier, slot, target):
+        target[:] = self.slots[slot]
+
+    def verify(self, tier, slot, key):
+        table = np.empty(self._shape(self.store.size), np.uint8)
+        self._hash(self.slots[slot], table)
+        if not np.array_equal(table, self.store.expected_chunks[key]):
+            raise ValueError("GPU expert bytes differ from verified original SHA-256 chunks")
+        return table.nbytes
+
+
+@pytest.mark.parametrize("gpu", [False, True])
+def test_batch_promotion_reads_ahead_with_the_same_tiers_and_refusals(direct_io_dir, gpu):
+    """TieredCache.promote over a real NativeStore: the store's prefetch pipeline reads and checks the batch's
+    store entries ahead of their uploads (three reader threads, six host buffers); the slots hold the written
+    bytes, the counters and tier walk are those of single requests, a damaged entry fails the batch at that
+    key with nothing published for it (earlier keys stay promoted), and the pipeline's buffers leave the
+    budget afterwards."""
+    from vesper_amd.cache import TieredCache
+    rng = np.random.default_rng(11)
+    keys = [(0, e) for e in range(6)]
+    items = experts(rng, keys)
+    build_store(items, direct_io_dir / "store", max_experts=6, profile=TINY)
+    b = MemoryBudget(cap=64 * MiB, available_floor=0)
+    with NativeStore(direct_io_dir / "store", b, max_experts=6, profile=TINY) as store:
+        store.gpu_integrity = gpu
+        backend = HostSlots(store, 3)
+        cache = TieredCache(store, backend, b, 0, available=lambda: 1 << 40, gpu_verify=gpu)
+        held = b.reserved
+        assert cache.promote(["0:0", "0:1", "0:2"]) == ["store"] * 3
+        snap = cache.snapshot()
+        assert snap["primary_keys"] == ["0:0", "0:1", "0:2"] and snap["counters"]["store_reads_completed"] == 3
+        for key, (layer, expert, arrays) in zip(["0:0", "0:1", "0:2"], items):
+            slot = snap["primary_keys"].index(key)
+            np.testing.assert_array_equal(backend.slots[slot], concat(arrays))
+        # a hit, then a store read that demotes the least recent expert (no RAM tier: dropped)
+        assert cache.promote(["0:0", "0:3"]) == ["primary_gpu", "store"]
+        assert cache.snapshot()["primary_keys"] == ["0:2", "0:0", "0:3"]
+        tables = sum(t.nbytes for t in store.expected_chunks.values())   # kept for the GPU audit
+        assert store.read_calls == 4 and b.reserved == held + tables and len(store.expected_chunks) == (4 if gpu else 0)
+        # damage entry 0:5 on disk: the batch fails there, 0:4 stays promoted
+        path = direct_io_dir / "store" / "experts.bin"
+        data = bytearray(path.read_bytes())
+        data[5 * TINY.expert_bytes + 100] ^= 1
+        path.write_bytes(bytes(data))
+        with pytest.raises(ValueError, match="differ"):
+            cache.promote(["0:4", "0:5", "0:1"])
+        snap = cache.snapshot()
+        assert "0:4" in snap["primary_keys"] and "0:5" not in snap["primary_keys"]
+        c = snap["counters"]
+        assert c["integrity_failures"] == 1 and c["requests_failed"] == 1 and c["requests_completed"] == 6
+        assert b.reserved == held + sum(t.nbytes for t in store.expected_chunks.values())
+        cache.close()

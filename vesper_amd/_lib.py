@@ -137,6 +137,7 @@ SIGNATURES = {
     "mx_fp8_grouped_projection": ([_P, _P, _I32, _I32, _I32, _P, _P, _I32, _P, _P, _P], C.c_int),
     "mx_kv_round32": ([_P, _P, _I64, _P, _P, _P, _P], C.c_int),
     "mx_sha256_chunks": ([_P, _P, _U64, _P, _P], C.c_int),
+    "mx_host_sha256_chunks": ([_P, _U64, _P, _I32], C.c_int),
     "mx_sha256_verify": ([_P, C.POINTER(_P), C.POINTER(_P), _P, _I32, _U64, _P, _P], C.c_int),
     "mx_audit_gate": ([_P, _P, _I32, _P, _I32, _P, _U64, _P], C.c_int),
     "mx_owned_size": ([_P, _P, C.POINTER(_U64)], C.c_int),

@@ -65,7 +65,8 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
             if verbose and out.strip():
                 print(out)
     tmp = LIB.with_suffix(".so.tmp")
-    _run([compiler, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objects)])
+    # libcrypto: the host digest tables (mx_host_sha256_chunks)
+    _run([compiler, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objects), "-lcrypto"])
     os.replace(tmp, LIB)
     build_hostcheck()
     return LIB

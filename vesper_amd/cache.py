@@ -21,6 +21,10 @@ digest table of the verified store read (backend.verify), which makes the host-s
 readbacks redundant, so they are counted as deferred. A failed check raises ValueError and publishes
 nothing.
 
+promote(keys) runs a batch of requests in order; with a NativeStore source the store reads and host checks
+of the batch run ahead of the uploads on the store's prefetch pipeline (reading, hashing and uploading
+different experts at once), with the same tier rules, counters and refusals as single requests.
+
 The source is a NativeStore (size, entries, read_into, validate) and the backend a
 vesper_amd.tiered.HipCacheBackend (primary_slots, staging, read, write, verify); the tests drive both with
 fakes. The reference's helper-GPU tier needs a second device, which this single-GPU build does not use: a
@@ -215,8 +219,9 @@ class TieredCache:
         self.stats["primary_gpu_audit_digest_d2h_bytes"] += digest_bytes
 
     # -- moves between tiers ---------------------------------------------------------------------------------
-    def _stage_in(self, key) -> str:
-        """Put `key`'s bytes into the promotion buffer; returns the tier they came from."""
+    def _stage_in(self, key, pipeline=None) -> str:
+        """Put `key`'s bytes into the promotion buffer; returns the tier they came from. A store read comes
+        from `pipeline` (already read and checked there) when one is given."""
         home = self._homes.get(key)
         if home is not None:   # a RAM copy (GPU residents never get here); it leaves RAM as it moves up
             with self.timings.section("host.ram_copy"):
@@ -228,7 +233,17 @@ class TieredCache:
         self.stats["store_read_attempts"] += 1
         self.stats["store_bytes_requested"] += self.size
         try:
-            self.source.read_into(key, self.incoming)
+            if pipeline is None or pipeline.next_key() != key:   # a key the batch itself moved out of its tier
+                self.source.read_into(key, self.incoming)
+            else:
+                index, data, table = pipeline.get(key)
+                try:
+                    with self.timings.section("host.store_staging_copy"):
+                        np.copyto(self.incoming, data)
+                finally:
+                    pipeline.release(index)
+                if table is not None:
+                    self.source.adopt_table(key, table)
         except ValueError:
             self.stats["integrity_failures"] += 1
             raise
@@ -253,7 +268,7 @@ class TieredCache:
             self._homes[key] = _Home(RAM, next(self._clock), data=copy)
         self.stats["primary_evictions"] += 1
 
-    def _resident(self, key):
+    def _resident(self, key, pipeline=None):
         """(slot, origin tier) of `key` in a GPU slot, promoting it if needed."""
         if key not in self.source.entries:
             raise KeyError("Requested expert is absent from the pinned native store")
@@ -262,7 +277,7 @@ class TieredCache:
             home.stamp = next(self._clock)
             self.stats["primary_hits"] += 1
             return home.slot, GPU
-        origin = self._stage_in(key)
+        origin = self._stage_in(key, pipeline)
         if not self._free:
             self._move_down()
         slot = self._free[0]
@@ -298,6 +313,46 @@ class TieredCache:
                 self.stats["requests_completed"] += 1
             finally:
                 self.active = False
+
+    def promote(self, keys, *, depth: int = 6, readers: int = 3) -> list:
+        """Bring `keys` into GPU slots in order, each as one request (the same tier rules, counters, checks
+        and refusals as acquire), returning each key's origin tier. When the source offers a prefetch
+        pipeline (NativeStore.prefetch), the store reads and host checks of the keys found in no tier run
+        ahead on it -- reading later entries and hashing them while earlier ones upload -- with at most
+        `depth` entries held in host buffers. A failed read or check fails the batch at that key; keys
+        before it stay promoted. With more keys than slots, the batch's own earlier keys move down."""
+        keys = list(keys)
+        with self.lock:
+            if self.closed:
+                raise RuntimeError("Cache is closed")
+            if self.active:
+                raise RuntimeError("Nested requests could replace a live compute slot")
+            for key in keys:
+                if key not in self.source.entries:
+                    raise KeyError("Requested expert is absent from the pinned native store")
+            fetch = [k for k in dict.fromkeys(keys) if k not in self._homes]
+            pipeline = None
+            if fetch and callable(getattr(self.source, "prefetch", None)):
+                pipeline = self.source.prefetch(fetch, depth=depth, readers=readers)
+            origins = []
+            try:
+                for key in keys:
+                    self._begin()
+                    try:
+                        self.enforce_pressure()
+                        origins.append(self._resident(key, pipeline))
+                        self.enforce_pressure()
+                    except BaseException:
+                        self.stats["requests_failed"] += 1
+                        raise
+                    else:
+                        self.stats["requests_completed"] += 1
+                    finally:
+                        self.active = False
+            finally:
+                if pipeline is not None:
+                    pipeline.close()
+            return [origin for _, origin in origins]
 
     def snapshot(self) -> dict:
         with self.lock:

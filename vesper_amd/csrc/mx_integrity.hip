@@ -11,7 +11,14 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
+#include <thread>
+#include <vector>
+
+// OpenSSL 3 marks the one-shot SHA256() deprecated in favour of EVP; it remains the plain FIPS 180-4 digest
+#define OPENSSL_SUPPRESS_DEPRECATED
+#include <openssl/sha.h>
 
 #include "mx_internal.h"
 
@@ -235,6 +242,29 @@ extern "C" int mx_audit_gate(mx_ctx* ctx, const uint32_t* counters, int32_t n_co
   hipLaunchKernelGGL(audit_gate_kernel, dim3((unsigned)(blocks < 256 ? blocks : 256)), dim3(256), 0, as_stream(stream),
                      counters, g, n, y, count);
   MX_LAUNCH_CHECK("audit_gate_kernel");
+  return MX_OK;
+}
+
+// Host digest tables (the store's verified reads in GPU-integrity mode): OpenSSL's SHA-256 per chunk, the
+// chunk range split over `threads` host threads. The interpreter lock is released around the whole call, so
+// several experts of a batch promotion hash side by side without per-chunk Python work.
+extern "C" int mx_host_sha256_chunks(const void* data, uint64_t bytes, void* digests, int32_t threads) {
+  MX_REQUIRE(data != nullptr && digests != nullptr, "mx_host_sha256_chunks: null pointer");
+  MX_REQUIRE(bytes > 0 && bytes <= kMaxPayload, "Invalid bounded integrity payload size");
+  MX_REQUIRE(threads >= 1 && threads <= 64, "mx_host_sha256_chunks: threads must be in [1, 64]");
+  const uint64_t chunks = (bytes + kChunkBytes - 1) / kChunkBytes;
+  const uint8_t* d = (const uint8_t*)data;
+  uint8_t* o = (uint8_t*)digests;
+  MX_REQUIRE(o + chunks * 32 <= d || d + bytes <= o, "Digest destination must not overwrite source bytes");
+  auto range = [&](uint64_t first, uint64_t last) {
+    for (uint64_t c = first; c < last; ++c)
+      SHA256(d + c * kChunkBytes, std::min<uint64_t>(kChunkBytes, bytes - c * kChunkBytes), o + 32 * c);
+  };
+  const uint64_t parts = std::min<uint64_t>((uint64_t)threads, chunks);
+  std::vector<std::thread> pool;
+  for (uint64_t i = 1; i < parts; ++i) pool.emplace_back(range, chunks * i / parts, chunks * (i + 1) / parts);
+  range(0, chunks / parts);
+  for (std::thread& t : pool) t.join();
   return MX_OK;
 }
 

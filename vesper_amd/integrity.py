@@ -25,7 +25,9 @@ MAX_PAYLOAD = 1 << 30
 
 # Host hashing threads: hashlib releases the GIL while it hashes a buffer of more than 2 KiB, so independent
 # large digests (the whole expert and its tensors) run on separate cores.
-HASHERS = ThreadPoolExecutor(max_workers=4, thread_name_prefix="vesper-sha256")
+# host hashing threads: the digests of one read run beside each other, and a batch promotion hashes several
+# experts at once (the GPU box's host share is 16 cores)
+HASHERS = ThreadPoolExecutor(max_workers=8, thread_name_prefix="vesper-sha256")
 
 
 def digest_shape(size):
@@ -48,11 +50,29 @@ def hash_chunks(data: np.ndarray, target: np.ndarray):
         raise ValueError("Integrity digest destination has the wrong size")
     if np.shares_memory(data, target):
         raise ValueError("Digest destination must not overwrite source bytes")
-    payload = memoryview(data)
-    # one thread: per-chunk digests are too short for the hashing threads to pay (measured slower)
-    table = b"".join(hashlib.sha256(payload[start:start + CHUNK_BYTES]).digest()
-                     for start in range(0, data.size, CHUNK_BYTES))
-    target[...] = np.frombuffer(table, np.uint8).reshape(target.shape)
+    _hash_range(memoryview(data), target, 0, target.shape[0])
+
+
+def _hash_range(payload, target: np.ndarray, first: int, last: int):
+    """Digests of chunks [first, last) of `payload` into rows [first, last) of `target`."""
+    table = b"".join(hashlib.sha256(payload[i * CHUNK_BYTES:(i + 1) * CHUNK_BYTES]).digest()
+                     for i in range(first, last))
+    target[first:last] = np.frombuffer(table, np.uint8).reshape(last - first, DIGEST_BYTES)
+
+
+def hash_chunks_native(data: np.ndarray, target: np.ndarray, threads: int = 4):
+    """hash_chunks computed by the library on `threads` host threads (mx_host_sha256_chunks: OpenSSL's
+    SHA-256 per chunk, no per-chunk interpreter work, the interpreter lock released for the whole call)."""
+    import ctypes as C
+    from . import _lib
+    if not _is_byte_vector(data):
+        raise ValueError("Integrity input must be a contiguous byte array")
+    if target.dtype != np.uint8 or target.shape != digest_shape(data.size) or not target.flags.c_contiguous:
+        raise ValueError("Integrity digest destination has the wrong size")
+    if np.shares_memory(data, target):
+        raise ValueError("Digest destination must not overwrite source bytes")
+    _lib.load().host_sha256_chunks(C.c_void_p(data.ctypes.data), data.size, C.c_void_p(target.ctypes.data),
+                                   int(threads))
 
 
 def _overlapping(*arrays) -> bool:

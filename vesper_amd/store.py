@@ -23,6 +23,8 @@ from __future__ import annotations
 
 import hashlib
 import json
+import threading
+from concurrent.futures import ThreadPoolExecutor
 import os
 import re
 import zipfile
@@ -32,7 +34,7 @@ from pathlib import Path
 import numpy as np
 
 from .disk import PAGE, DirectReader
-from .integrity import HASHERS, digest_shape, hash_chunks
+from .integrity import HASHERS, digest_shape, hash_chunks_native
 from .resources import MemoryBudget, MiB
 from .timing import Timings
 
@@ -286,6 +288,7 @@ class NativeStore:
         self.timings = Timings()
         self.gpu_integrity, self.expected_chunks = False, {}
         self.read_calls, self.bytes_read = 0, 0
+        self._count_lock = threading.Lock()
         with (self.directory / "manifest.json").open("rb") as stream:
             raw = stream.read(MiB + 1)
         if len(raw) > MiB:
@@ -343,6 +346,31 @@ class NativeStore:
                 if digest != tensor["sha256"]:
                     raise ValueError("Native expert tensor differs from its original source hash")
 
+    def check_bytes(self, key: str, data: np.ndarray):
+        """validate(key, data, tensors=True) from any thread (no timing section), counted as one store read."""
+        entry = self.entries[key]
+        if data.dtype != np.uint8 or data.shape != (self.size,) or not data.flags.c_contiguous:
+            raise ValueError("Native-store payload layout differs from one expert")
+        layout = self.manifest["layout"]
+        named = entry["provenance"]["tensors"]
+        digests = _hex_parallel([data] + [data[layout[t["name"]]["offset"]:layout[t["name"]]["offset"]
+                                                 + layout[t["name"]]["bytes"]] for t in named])
+        with self._count_lock:
+            self.read_calls += 1
+            self.bytes_read += self.size
+        if digests[0] != entry["sha256"]:
+            raise ValueError("Native expert bytes differ from the store hash")
+        for tensor, digest in zip(named, digests[1:]):
+            if digest != tensor["sha256"]:
+                raise ValueError("Native expert tensor differs from its original source hash")
+
+    def adopt_table(self, key: str, table: np.ndarray):
+        """Keep a verified read's 4 KiB digest table for the GPU audit (charged to the budget)."""
+        if key in self.expected_chunks:
+            return
+        self.budget.acquire(table.nbytes, category="integrity")
+        self.expected_chunks[key] = table
+
     def _after_read(self, key: str, target: np.ndarray):
         """Check the bytes just read against the manifest; with gpu_integrity, also build their 4 KiB digest
         table for the GPU audit -- on a hashing thread while the manifest digests run (the table's Python loop
@@ -356,7 +384,7 @@ class NativeStore:
         self.budget.acquire(shape[0] * shape[1], category="integrity")
         try:
             table = np.empty(shape, np.uint8)
-            pending = HASHERS.submit(hash_chunks, target, table)
+            pending = HASHERS.submit(hash_chunks_native, target, table)
             try:
                 self.validate(key, target, tensors=True)
             finally:
@@ -367,6 +395,13 @@ class NativeStore:
         except BaseException:
             self.budget.release(shape[0] * shape[1], category="integrity")
             raise
+
+    def prefetch(self, keys, *, depth: int = 6, readers: int = 3, chunk_parts: int = 4) -> "StorePipeline":
+        """A pipeline that reads and verifies `keys` (store entries, in order) ahead of their use; see
+        StorePipeline."""
+        if self.reader is None:
+            raise RuntimeError("Native store is closed")
+        return StorePipeline(self, keys, depth=depth, readers=readers, chunk_parts=chunk_parts)
 
     def read_into(self, key: str, target: np.ndarray):
         """Direct read of `key` into the reader's buffer, copied into `target` (one expert of bytes), then
@@ -379,3 +414,101 @@ class NativeStore:
         with self.timings.section("host.store_staging_copy"):
             np.copyto(target, self.reader.array())
         self._after_read(key, target)
+
+
+def _page_aligned(size: int) -> np.ndarray:
+    """`size` bytes starting on a page boundary (what an O_DIRECT read may target)."""
+    raw = np.empty(size + PAGE, np.uint8)
+    skip = (-raw.ctypes.data) % PAGE
+    return raw[skip:skip + size]
+
+
+class StorePipeline:
+    """Reads and verifies a sequence of store entries ahead of their upload (a batch promotion).
+
+    `readers` threads each take the next entry in order, read it with O_DIRECT straight into one of `depth`
+    page-aligned host buffers (reserved in the store's budget), and check it as read_into does: the whole
+    expert's and each tensor's SHA-256 against the manifest and, in GPU-integrity mode, the 4 KiB digest
+    table for the upload audit -- the digests on the shared hashing threads, so several entries hash at
+    once. get(key) returns the verified buffer of the next entry in order (waiting for it) or raises its
+    read or check error; the caller copies it out and calls release(). Reads of later entries, their
+    hashing and the caller's uploads of earlier ones therefore overlap. Budget: depth x one expert."""
+
+    def __init__(self, store: NativeStore, keys, *, depth: int = 6, readers: int = 3, chunk_parts: int = 4):
+        keys = list(keys)
+        self.chunk_parts = chunk_parts
+        if depth < 1 or readers < 1 or readers > depth:
+            raise ValueError("A store pipeline needs 1 <= readers <= depth")
+        for key in keys:
+            if key not in store.entries:
+                raise KeyError("Requested expert is absent from the pinned native store")
+        self.store, self.keys, self.size = store, keys, store.size
+        self.depth = depth
+        store.budget.acquire(depth * self.size, category="scratch")
+        self._buffers = [_page_aligned(self.size) for _ in range(depth)]
+        self._free = list(range(depth))
+        self._cond = threading.Condition()
+        self._closed = False
+        self._handle = os.open(store.path, os.O_RDONLY | os.O_DIRECT)
+        self._pool = ThreadPoolExecutor(max_workers=readers, thread_name_prefix="vesper-store-read")
+        self._futures = [self._pool.submit(self._fetch, key) for key in keys]
+        self._next = 0
+
+    def _take_buffer(self) -> int:
+        with self._cond:
+            while not self._free and not self._closed:
+                self._cond.wait()
+            if self._closed:
+                raise RuntimeError("Store pipeline is closed")
+            return self._free.pop(0)
+
+    def release(self, index: int):
+        with self._cond:
+            self._free.append(index)
+            self._cond.notify()
+
+    def _fetch(self, key):
+        index = self._take_buffer()
+        try:
+            data = self._buffers[index]
+            if os.preadv(self._handle, [memoryview(data)], self.store.entries[key]["offset"]) != self.size:
+                raise OSError("Short direct read")
+            self.store.check_bytes(key, data)
+            table = None
+            if self.store.gpu_integrity and key not in self.store.expected_chunks:
+                table = np.empty(digest_shape(self.size), np.uint8)
+                hash_chunks_native(data, table, self.chunk_parts)
+                table.setflags(write=False)
+            return index, data, table
+        except BaseException:
+            self.release(index)
+            raise
+
+    def next_key(self):
+        """The entry get() returns next (None when all are consumed)."""
+        return self.keys[self._next] if self._next < len(self.keys) else None
+
+    def get(self, key):
+        """(buffer index, verified bytes, digest table or None) of the next entry, which must be `key`."""
+        if self._next >= len(self.keys) or self.keys[self._next] != key:
+            raise RuntimeError("Store pipeline entries are consumed in order")
+        future = self._futures[self._next]
+        self._next += 1
+        return future.result()
+
+    def close(self):
+        with self._cond:
+            self._closed = True
+            self._cond.notify_all()
+        for future in self._futures:
+            future.cancel()
+        self._pool.shutdown(wait=True)
+        os.close(self._handle)
+        self._buffers, self._futures = [], []
+        self.store.budget.release(self.depth * self.size, category="scratch")
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *_):
+        self.close()

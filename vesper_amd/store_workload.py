@@ -12,7 +12,9 @@ Per mode, the median per expert of each stage (the runtime's own timing sections
 copy into pinned staging, the host SHA-256 checks (whole expert and each tensor against the manifest), the
 H2D copy + tiling into the slot, and the upload audit (readback: D2H + host SHA-256; gpu-sha256: the 4 KiB
 digest table on the host and the hash on the GPU). Reported rates: expert bytes / the whole promotion
-("store_to_hbm"), / the direct read alone ("direct_read") and / the H2D + tiling alone.
+("store_to_hbm"), / the direct read alone ("direct_read") and / the H2D + tiling alone. Then the same
+experts as one pipelined batch per mode ("batch": TieredExpertRuntime.prefetch into as many GPU slots), whose
+rate is the batch's bytes over its wall time.
 """
 
 from __future__ import annotations
@@ -116,6 +118,31 @@ def promote(store: Path, keys: list, mode: str, profile) -> dict:
             "integrity_failures": counters["integrity_failures"]}
 
 
+def promote_batch(store: Path, keys: list, mode: str, profile, depth: int = 6, readers: int = 3) -> dict:
+    """keys[0] promoted alone (warm-up), then keys[1:] as one pipelined batch (TieredExpertRuntime.prefetch:
+    store reads and host checks of later experts overlap the uploads and audits of earlier ones) into as
+    many GPU slots; wall time of the batch."""
+    from .resources import GiB, MiB
+    from .tiered import CacheConfig, TieredExpertRuntime
+    batch = keys[1:]
+    config = CacheConfig(host_cap_bytes=2048 * MiB, ram_cache_bytes=0, available_floor=GiB,
+                         primary_slots=len(batch), helper_device=None, helper_slots=0, integrity_mode=mode,
+                         max_store_experts=len(keys), device_cap_bytes=2048 * MiB, profile=False)
+    size = profile.expert_bytes
+    with TieredExpertRuntime(store, config, model=profile) as runtime:
+        runtime.prefetch(keys[:1])
+        start = time.perf_counter()
+        origins = runtime.prefetch(batch, depth=depth, readers=readers)
+        wall = time.perf_counter() - start
+        if origins != ["store"] * len(batch):
+            raise RuntimeError(f"expected store reads for the batch, got {origins}")
+        counters = runtime.snapshot()["counters"]
+    return {"experts": len(batch), "expert_bytes": size, "ms": round(wall * 1e3, 2),
+            "ms_per_expert": round(wall * 1e3 / len(batch), 3),
+            "store_to_hbm_GB_per_s": round(len(batch) * size / wall / 1e9, 2), "pipeline_depth": depth,
+            "reader_threads": readers, "integrity_failures": counters["integrity_failures"]}
+
+
 def run(experts: int = 8, seed: int = 20261018) -> dict:
     from .store import REFERENCE_PROFILE
     directory = scratch_directory()
@@ -123,9 +150,15 @@ def run(experts: int = 8, seed: int = 20261018) -> dict:
         keys = write_store(directory / "store", experts + 1, seed, REFERENCE_PROFILE)
         out = {mode: promote(directory / "store", keys, mode, REFERENCE_PROFILE)
                for mode in ("readback", "gpu-sha256")}
-        out["note"] = ("one expert per request, store read -> pinned staging -> HBM slot (tiled), with the "
-                       "mode's checks; medians over the timed experts; the whole-expert and per-tensor digests hash "
-                       "on up to 4 host threads beside each other, the chunk table on one of them")
+        out["batch"] = {mode: promote_batch(directory / "store", keys, mode, REFERENCE_PROFILE)
+                        for mode in ("readback", "gpu-sha256")}
+        if os.environ.get("VESPER_STORE_SWEEP"):
+            out["batch_sweep"] = {f"{d}x{r}": promote_batch(directory / "store", keys, "gpu-sha256",
+                                                            REFERENCE_PROFILE, d, r)
+                                  for d, r in ((3, 2), (6, 3), (8, 4))}
+        out["note"] = ("readback / gpu-sha256: one expert per request, store read -> pinned staging -> HBM slot "
+                       "(tiled), with the mode's checks; medians over the timed experts. batch: the same experts "
+                       "as one pipelined promotion (reads, host SHA-256 and uploads of different experts overlap)")
         return out
     finally:
         shutil.rmtree(directory, ignore_errors=True)

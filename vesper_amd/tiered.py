@@ -403,6 +403,14 @@ class TieredExpertRuntime:
                 return _run_tiled_expert(self.ctx, self.work, self.backend.slot_ptr(slot), self.model.hidden,
                                          self.model.intermediate, self.model.swiglu_limit, x, routing_weight)
 
+    def prefetch(self, keys, *, depth: int = 6, readers: int = 3) -> list:
+        """Promote experts "layer:expert" into GPU slots as one pipelined batch (TieredCache.promote: store
+        reads and host checks of later experts overlap the uploads and audits of earlier ones); returns each
+        key's origin tier. Later forward() calls for them are GPU hits while they keep their slots."""
+        if self.stack is None:
+            raise RuntimeError("Use the tiered runtime as a context manager")
+        return self.cache.promote(keys, depth=depth, readers=readers)
+
     def snapshot(self) -> dict:
         store, c = self.store, self.config
         footprint = {"primary_peak_explicit_bytes": self.ctx.owned_bytes()[1], "helper_peak_explicit_bytes": 0,
