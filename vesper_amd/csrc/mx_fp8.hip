@@ -147,22 +147,17 @@ struct Fp8Args {
                        // handoff buffer, which holds the empty pattern wherever this launch reads
   uint4* restore;      // with tickets: the other half, whose first restore_n 16-byte words the previous
   int64_t restore_n;   // launch wrote: every workgroup puts back the empty pattern over its share
-  const uint16_t* x;   // fused GEMV (block 128, few tokens): the BF16 input [T][K], quantized in the kernel
+  const uint16_t* x;   // fused tile GEMV (block 128, few tokens): the BF16 input [T][K], quantized in the kernel
   int64_t x_stride;    // activation elements per token: K, or groups x K when grouped
   int x_group_rows;    // grouped activations (block-32 GEMV): weight rows [g R, (g + 1) R) multiply
                        // activation group g, codes at xq + tok x_stride + g K; 0 = one group
 };
 
-// Fused per-128 quantization in the GEMV (block 128, up to kFusedMaxTokens tokens, up to kFusedChunks K
-// chunks per workgroup): each workgroup quantizes its own chunks of its tokens into LDS, [chunk][token]
-// rows of 128 codes + 16 bytes of padding, with act_quant128_v8_kernel's arithmetic, and the MFMAs read
-// the B operand and the activation scale from there. Saves the quantizer launch for decode-size calls;
-// at 16 tokens the repeated quantization in every workgroup costs more than the launch (measured).
+// Block-128 calls of up to kFusedMaxTokens tokens run on fp8_tile_gemv_kernel, which can quantize its own
+// activations into LDS rows of 128 codes + 16 bytes of padding; at 16 tokens the repeated quantization in
+// every workgroup costs more than the quantizer launch (measured).
 constexpr int kFusedMaxTokens = 4;
-constexpr int kFusedChunks = 16;
 constexpr int kFusedRow = 144;
-// the 16 lane groups of 16 threads quantize kFusedMaxTokens blocks each: every (token, chunk) block
-static_assert(16 * kFusedMaxTokens >= kFusedMaxTokens * kFusedChunks, "fused quantization leaves blocks out");
 
 template <int kBlock>
 struct Fp8Chunk {
@@ -170,11 +165,10 @@ struct Fp8Chunk {
   uint4 b0, b1;
   uint32_t sw;   // block 32: scale word (byte t = tile t); block 128: FP32 bits of the weight block scale
   uint32_t sx;   // block 32: 4 activation E8M0 codes of the chunk; block 128: FP32 bits of the act scale
-  int c;         // the chunk (fused: its activations are read from LDS at the MFMA)
 };
 
 // xsrow: this lane's token's activation scales (block 32: E8M0 bytes, block 128: FP32), chunk 0 first.
-template <int kBlock, bool kFused>
+template <int kBlock>
 __device__ __forceinline__ void fp8_load(Fp8Chunk<kBlock>& r, const Fp8Args& a, const uint8_t* wlane,
                                          const uint8_t* slane, const float* swrow, const uint8_t* xrow,
                                          const uint8_t* xsrow, int c, int q) {
@@ -184,11 +178,6 @@ __device__ __forceinline__ void fp8_load(Fp8Chunk<kBlock>& r, const Fp8Args& a, 
   for (int t = 0; t < kTiles; ++t) {
     r.a[t][0] = ldg128_nt(wlane + (size_t)c * 8192 + t * 2048);
     r.a[t][1] = ldg128_nt(wlane + (size_t)c * 8192 + t * 2048 + 1024);
-  }
-  r.c = c;
-  if constexpr (kFused) {
-    r.sw = __float_as_uint(ldgf(swrow + c));
-    return;
   }
   r.b0 = ldg128(xrow + (size_t)c * 128 + 16 * q);
   r.b1 = ldg128(xrow + (size_t)c * 128 + 64 + 16 * q);
@@ -201,17 +190,8 @@ __device__ __forceinline__ void fp8_load(Fp8Chunk<kBlock>& r, const Fp8Args& a, 
   }
 }
 
-// qrow: fused, this lane's token row of the workgroup's quantized activations in LDS (chunk cb at offset 0),
-// qs its scale column; unused otherwise.
-template <int kBlock, bool kFused>
-__device__ __forceinline__ void fp8_mma(Fp8Chunk<kBlock> r, v4f (&acc)[kTiles], int q, uint32_t keep,
-                                        const uint8_t* qrow, const float* qs, int cb) {
-  if constexpr (kFused) {
-    const uint8_t* row = qrow + (size_t)(r.c - cb) * kFusedMaxTokens * kFusedRow;
-    r.b0 = *reinterpret_cast<const uint4*>(row + 16 * q);
-    r.b1 = *reinterpret_cast<const uint4*>(row + 64 + 16 * q);
-    r.sx = __float_as_uint(qs[(r.c - cb) * kFusedMaxTokens]);
-  }
+template <int kBlock>
+__device__ __forceinline__ void fp8_mma(const Fp8Chunk<kBlock>& r, v4f (&acc)[kTiles], int q, uint32_t keep) {
   const uint4 b0 = make_uint4(r.b0.x & keep, r.b0.y & keep, r.b0.z & keep, r.b0.w & keep);
   const uint4 b1 = make_uint4(r.b1.x & keep, r.b1.y & keep, r.b1.z & keep, r.b1.w & keep);
   if constexpr (kBlock == 32) {
@@ -237,7 +217,7 @@ __device__ __forceinline__ void fp8_mma(Fp8Chunk<kBlock> r, v4f (&acc)[kTiles], 
 // when K is not split, else its FP32 partial sums. With K split and a.tickets set, the last workgroup of
 // the (row group, token tile) to arrive adds the partial sums in split order (fp8_splitk_reduce_kernel's
 // arithmetic) and writes the outputs; without tickets fp8_splitk_reduce_kernel does it.
-template <int kBlock, bool kFused>
+template <int kBlock>
 __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
   constexpr int P = 2;
   const int g = blockIdx.x;
@@ -274,72 +254,21 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
   const int cb = (C * z) / S, cw = (C * (z + 1)) / S - cb;   // this workgroup's chunk range
   const int c0 = cb + (cw * wave) / 4;
   const int cn = cb + (cw * (wave + 1)) / 4 - c0;
-  // fused: this workgroup's quantized activations, [chunk][token] rows (tokens past T read token ntok - 1's
-  // row: finite scale, codes masked at the MFMA)
-  __shared__ __attribute__((aligned(16))) uint8_t qx[kFused ? kFusedChunks * kFusedMaxTokens * kFusedRow : 16];
-  __shared__ float qsc[kFused ? kFusedChunks * kFusedMaxTokens : 1];
-  const int ntok = min(kTok, a.T - (int)blockIdx.y * kTok);
-  const int nq = min(n, ntok - 1);
-  const int sub = tid & 15, grp = tid >> 4;
-  uint4 xv[kFusedMaxTokens];
-  if constexpr (kFused) {
-    // block bi = grp + 16 j: token bi / cw, chunk cb + bi % cw; 16 lanes of 8 values each
-#pragma unroll
-    for (int j = 0; j < kFusedMaxTokens; ++j) {
-      const int bi = grp + 16 * j;
-      xv[j] = bi < ntok * cw
-                  ? ldg128(reinterpret_cast<const uint8_t*>(a.x + (size_t)(blockIdx.y * kTok + bi / cw) * a.K +
-                                                            (size_t)(cb + bi % cw) * 128 + 8 * sub))
-                  : make_uint4(0u, 0u, 0u, 0u);
-    }
-  }
   const uint32_t keep = live ? 0xFFFFFFFFu : 0u;
   Fp8Chunk<kBlock> buf[P];
   if (cn > 0) {
 #pragma unroll
-    for (int j = 0; j < P; ++j)
-      fp8_load<kBlock, kFused>(buf[j], a, wlane, slane, swrow, xrow, xsrow, c0 + min(j, cn - 1), q);
-  }
-  if constexpr (kFused) {
-#pragma unroll
-    for (int j = 0; j < kFusedMaxTokens; ++j) {
-      const int bi = grp + 16 * j;
-      if (bi < ntok * cw) {   // uniform over the 16 lanes of a block
-        const uint32_t w[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
-        float v[8];
-        float amax = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          v[2 * i] = mx::bf16_value(w[i] & 0xFFFFu);
-          v[2 * i + 1] = mx::bf16_value(w[i] >> 16);
-          amax = fmaxf(amax, fmaxf(fabsf(v[2 * i]), fabsf(v[2 * i + 1])));
-        }
-#pragma unroll
-        for (int m = 8; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
-        const float sc = mx::act128_scale(amax);
-        uint2 codes;
-        codes.x = mxd::e4m3x4(v[0] / sc, v[1] / sc, v[2] / sc, v[3] / sc);
-        codes.y = mxd::e4m3x4(v[4] / sc, v[5] / sc, v[6] / sc, v[7] / sc);
-        const int slot = (bi % cw) * kFusedMaxTokens + bi / cw;
-        *reinterpret_cast<uint2*>(qx + slot * kFusedRow + 8 * sub) = codes;
-        if (sub == 0) qsc[slot] = sc;
-      }
-    }
-    mxd::lds_barrier();   // LDS only: the weight loads above stay in flight
-  }
-  if (cn > 0) {
-    const uint8_t* qrow = qx + nq * kFusedRow;
-    const float* qs = qsc + nq;
+    for (int j = 0; j < P; ++j) fp8_load<kBlock>(buf[j], a, wlane, slane, swrow, xrow, xsrow, c0 + min(j, cn - 1), q);
     int i = 0;
     for (; i + P < cn; i += P) {
 #pragma unroll
       for (int j = 0; j < P; ++j) {
-        fp8_mma<kBlock, kFused>(buf[j], acc, q, keep, qrow, qs, cb);
-        fp8_load<kBlock, kFused>(buf[j], a, wlane, slane, swrow, xrow, xsrow, c0 + min(i + j + P, cn - 1), q);
+        fp8_mma<kBlock>(buf[j], acc, q, keep);
+        fp8_load<kBlock>(buf[j], a, wlane, slane, swrow, xrow, xsrow, c0 + min(i + j + P, cn - 1), q);
       }
     }
 #pragma unroll
-    for (int j = 0; j < P; ++j) fp8_mma<kBlock, kFused>(buf[j], acc, q, i + j < cn ? keep : 0u, qrow, qs, cb);
+    for (int j = 0; j < P; ++j) fp8_mma<kBlock>(buf[j], acc, q, i + j < cn ? keep : 0u);
   }
   __shared__ float red[4][kTiles][64][4];
 #pragma unroll
@@ -427,6 +356,189 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
     *reinterpret_cast<uint2*>(a.y + o) = packed;
     if (a.trace) *reinterpret_cast<float4*>(a.trace + o) = make_float4(out[0], out[1], out[2], out[3]);
   }
+}
+
+// Block-128 decode GEMV over 16-row tiles. A workgroup of W waves owns M consecutive 16-row MFMA tiles
+// (one token tile) over all of K: wave w takes tile w % M and the (w / M)-th of W / M contiguous K parts,
+// streams its chunks through a register ring of kTileRing chunks (2 KB of weights per chunk, non-temporal
+// loads) into one FP32 16 x 16 partial tile, acc = fma(d, f32(sa sw), acc) in chunk order, and each tile's
+// W / M partial tiles are added through LDS in K-part order. No K range is shared between workgroups, so no
+// partial sums leave the workgroup (no handoff, no reduce launch); the host picks W and M so that the launch
+// has a few thousand waves in a few hundred workgroups.
+// Fused (few tokens): each wave first quantizes its own chunks of the call's tokens (P passes of 4 blocks
+// of 128) into its LDS rows with act_quant128_v8_kernel's arithmetic, so the call needs no quantizer
+// launch.
+constexpr int kTileRing = 4;
+constexpr int kTileQRows = 16;   // fused: at most 4 passes of 4 blocks per wave
+
+struct TileChunk {
+  uint4 a0, a1;   // weights: the tile's two 1 KB halves of the chunk, 16 bytes per lane
+  uint4 b0, b1;   // activation codes (unfused)
+  float sx;       // activation scale (unfused)
+};
+
+template <bool kFused>
+__device__ __forceinline__ void tile_load(TileChunk& r, const uint8_t* wlane, const uint8_t* xrow,
+                                          const float* xsrow, int c, int q) {
+  r.a0 = ldg128_nt(wlane + (size_t)c * 8192);
+  r.a1 = ldg128_nt(wlane + (size_t)c * 8192 + 1024);
+  if constexpr (!kFused) {
+    r.b0 = ldg128(xrow + (size_t)c * 128 + 16 * q);
+    r.b1 = ldg128(xrow + (size_t)c * 128 + 64 + 16 * q);
+    r.sx = ldgf(xsrow + c);
+  }
+}
+
+// sw: the chunk's weight block scale; row / qs: fused, this lane's token's LDS row and scale for the chunk,
+// unused otherwise
+template <bool kFused>
+__device__ __forceinline__ void tile_mma(const TileChunk& r, v4f& acc, int q, uint32_t keep, float sw,
+                                         const uint8_t* row, const float* qs) {
+  uint4 b0 = r.b0, b1 = r.b1;
+  float sx = r.sx;
+  if constexpr (kFused) {
+    b0 = *reinterpret_cast<const uint4*>(row + 16 * q);
+    b1 = *reinterpret_cast<const uint4*>(row + 64 + 16 * q);
+    sx = *qs;
+  }
+  b0 = make_uint4(b0.x & keep, b0.y & keep, b0.z & keep, b0.w & keep);
+  b1 = make_uint4(b1.x & keep, b1.y & keep, b1.z & keep, b1.w & keep);
+  const float s = sx * sw;
+  const v4f d = mfma_fp8_fp8(r.a0, r.a1, b0, b1, v4f{0.f, 0.f, 0.f, 0.f}, 127, 127);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[i], s, acc[i]);
+}
+
+__device__ __forceinline__ float chunk_scale(float swl, int i) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(swl), i));
+}
+
+// grid (N / 16 / M, ceil(T / 16)), 64 W threads. The 4-tile shape serves the largest grids (q_b: 384
+// workgroups of 16 waves): fused with up to 2 passes its registers fit 8 waves per SIMD, two workgroups a
+// CU, so all are resident at once (the unfused ring, which also holds activation codes, would spill).
+template <bool kFused, int W, int M, int P>
+__global__ __launch_bounds__(64 * W, (M == 4 && kFused && P < 4) ? 8 : 2) void fp8_tile_gemv_kernel(Fp8Args a) {
+  static_assert(W % M == 0 && 4 * P <= kTileQRows, "tile GEMV shape");
+  constexpr int KP = W / M;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tile = blockIdx.x * M + w % M, kp = w / M;
+  const int q = lane >> 4, nn = lane & 15;
+  const int tok0 = blockIdx.y * kTok, tok = tok0 + nn;
+  const int ntok = min(kTok, a.T - tok0);
+  const bool live = nn < ntok;
+  const int rtok = live ? tok : a.T - 1;
+  const int C = a.K / 128;
+  const Fp8Blob off = fp8_blob(a.N, a.K, 128);
+  // tile t of row group g: chunk c's halves at (g C + c) 8192 + 2048 t + {0, 1024}
+  const uint8_t* wlane = a.blob + (size_t)(tile >> 2) * C * 8192 + (tile & 3) * 2048 + 16 * lane;
+  const float* swrow = reinterpret_cast<const float*>(a.blob + off.scales) + (size_t)(tile >> 3) * C;
+  const uint8_t* xrow = a.xq + (size_t)rtok * a.K;
+  const float* xsrow = reinterpret_cast<const float*>(a.xs) + (size_t)rtok * C;
+  const int c0 = (C * kp) / KP, n = (C * (kp + 1)) / KP - c0;
+  // fused: wave w's rows, block b = i ntok + token (chunk c0 + i), 128 codes + 16 bytes of padding each,
+  // and one spare row that takes the stores of lanes past the wave's blocks (no branch around the math:
+  // branches would make the compiler wait for the weight loads before quantizing)
+  constexpr int kRows = 4 * P + 1;
+  __shared__ __attribute__((aligned(16))) uint8_t qx[kFused ? W * kRows * kFusedRow : 16];
+  __shared__ float qsc[kFused ? W * kRows : 1];
+  const int sub = lane & 15, grp = lane >> 4;
+  const int nb = n * ntok, nl = max(n - 1, 0);
+  uint4 xv[kFused ? P : 1];
+  if constexpr (kFused) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int b = min(4 * p + grp, max(nb - 1, 0));
+      xv[p] = ldg128(reinterpret_cast<const uint8_t*>(a.x + (size_t)(tok0 + b % ntok) * a.K +
+                                                      (size_t)(c0 + b / ntok) * 128 + 8 * sub));
+    }
+  }
+  // the activation loads first, then the ring, then the quantization: loads return in order, so quantizing
+  // waits for the activations alone (scheduling barriers keep the compiler from interleaving the three)
+  __builtin_amdgcn_sched_barrier(0);
+  // the wave's weight block scales, lane i holding chunk c0 + i's (at most 64 chunks a wave, checked on the
+  // host); each chunk's is read out with v_readlane into a scalar register
+  const float swl = ldgf(swrow + c0 + min(lane, nl));
+  TileChunk buf[kTileRing];
+#pragma unroll
+  for (int j = 0; j < kTileRing; ++j) tile_load<kFused>(buf[j], wlane, xrow, xsrow, c0 + min(j, nl), q);
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (kFused) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int b = 4 * p + grp;
+      const uint32_t wd[4] = {xv[p].x, xv[p].y, xv[p].z, xv[p].w};
+      float v[8];
+      float amax = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = mx::bf16_value(wd[i] & 0xFFFFu);
+        v[2 * i + 1] = mx::bf16_value(wd[i] >> 16);
+        amax = fmaxf(amax, fmaxf(fabsf(v[2 * i]), fabsf(v[2 * i + 1])));
+      }
+#pragma unroll
+      for (int m = 8; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+      const float sc = mx::act128_scale(amax);
+      uint2 codes;
+      codes.x = mxd::e4m3x4(v[0] / sc, v[1] / sc, v[2] / sc, v[3] / sc);
+      codes.y = mxd::e4m3x4(v[4] / sc, v[5] / sc, v[6] / sc, v[7] / sc);
+      const int row = w * kRows + (b < nb ? b : 4 * P);
+      *reinterpret_cast<uint2*>(qx + row * kFusedRow + 8 * sub) = codes;
+      if (sub == 0) qsc[row] = sc;
+    }
+    // the rows are this wave's own: its LDS writes complete before its reads (no workgroup barrier)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+  v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+  const uint32_t keep = live ? 0xFFFFFFFFu : 0u;
+  const int qtok = kFused ? min(nn, ntok - 1) : 0;
+  const uint8_t* qrow = qx + (w * kRows + qtok) * kFusedRow;
+  const float* qs = qsc + w * kRows + qtok;
+  int i = 0;
+  for (; i + kTileRing < n; i += kTileRing) {
+#pragma unroll
+    for (int j = 0; j < kTileRing; ++j) {
+      // a ring: chunk i + j is multiplied, then its slot is refilled with chunk i + j + kTileRing before the
+      // next chunk is waited for (the barrier keeps the compiler from batching the loads after all four)
+      tile_mma<kFused>(buf[j], acc, q, keep, chunk_scale(swl, i + j), qrow + (i + j) * ntok * kFusedRow,
+                       qs + (i + j) * ntok);
+      tile_load<kFused>(buf[j], wlane, xrow, xsrow, c0 + min(i + j + kTileRing, nl), q);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kTileRing; ++j) {
+    const int ij = min(i + j, nl);
+    tile_mma<kFused>(buf[j], acc, q, i + j < n ? keep : 0u, chunk_scale(swl, ij), qrow + ij * ntok * kFusedRow,
+                     qs + ij * ntok);
+  }
+  __shared__ float4 red[W][64];
+  red[w][lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  __syncthreads();
+  if (w >= M || !live) return;
+  // wave w < M finishes tile w: K-part order, over the parts that own chunks (KP > C leaves some without)
+  float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+  bool first = true;
+#pragma unroll
+  for (int v = 0; v < KP; ++v) {
+    if ((C * (v + 1)) / KP == (C * v) / KP) continue;
+    const float4 r = red[w + M * v][lane];
+    if (first) {
+      t = r;
+      first = false;
+    } else {
+      t.x = t.x + r.x;
+      t.y = t.y + r.y;
+      t.z = t.z + r.z;
+      t.w = t.w + r.w;
+    }
+  }
+  const size_t o = (size_t)tok * a.N + 16 * tile + 4 * q;
+  uint2 packed;
+  packed.x = mx::bf16_bits(t.x) | (mx::bf16_bits(t.y) << 16);
+  packed.y = mx::bf16_bits(t.z) | (mx::bf16_bits(t.w) << 16);
+  *reinterpret_cast<uint2*>(a.y + o) = packed;
+  if (a.trace) *reinterpret_cast<float4*>(a.trace + o) = t;
 }
 
 // Split-K epilogue: y = BF16(sum over splits in order), 4 outputs per thread.
@@ -644,31 +756,66 @@ int fp8_splits(int N, int K, int T) {
     if (base_wgs >= 128) return 1;
     return std::max(1, std::min({8, (K / 128) / 8, (512 + base_wgs - 1) / base_wgs}));
   }
-  // GEMV: up to kFusedMaxTokens tokens (the call may quantize its own activations) every workgroup takes
-  // up to kFusedChunks = 16 chunks of its row group, else about 8; at most 16 splits. Fewer, longer
-  // workgroups measured faster than a fixed workgroup count on MI355X (us per call, T = 1 / 16): 2112 x 7168
-  // 7 splits 11.3 / 13.1 against 14 splits (the former ~512-workgroup rule) 12.5 / 16.9; 7168 x 16384 16
-  // splits 28.9 / 33.8 against 5 splits 30.1 / 33.3. At T = 1 with non-temporal weight loads: 24576 x 1536
-  // unsplit 10.3 us against 12.5 us with 2 splits (no split-K handoff); 2112 x 7168 4 splits 10.4 us, 7168 x
-  // 16384 8 splits 26.6 us, both as with 7 and 16.
+  // Split-K GEMV: up to kFusedMaxTokens tokens every workgroup takes up to 16 chunks of its row group, else
+  // about 8; at most 16 splits. Fewer, longer workgroups measured faster than a fixed workgroup count on
+  // MI355X (us per call, T = 1 / 16): 2112 x 7168 7 splits 11.3 / 13.1 against 14 splits (the former
+  // ~512-workgroup rule) 12.5 / 16.9; 7168 x 16384 16 splits 28.9 / 33.8 against 5 splits 30.1 / 33.3. At T =
+  // 1 with non-temporal weight loads: 24576 x 1536 unsplit 10.3 us against 12.5 us with 2 splits (no split-K
+  // handoff); 2112 x 7168 4 splits 10.4 us, 7168 x 16384 8 splits 26.6 us, both as with 7 and 16. (Block-128
+  // calls of up to 4 tokens now run on the tile GEMV, which splits K only within a workgroup.)
   const int chunks = K / 128;
-  const int s = T <= kFusedMaxTokens ? (chunks + kFusedChunks - 1) / kFusedChunks : chunks / 8;
+  const int s = T <= kFusedMaxTokens ? (chunks + 15) / 16 : chunks / 8;
   return std::max(1, std::min(16, s));
 }
 
-// Whether the block-128 GEMV can quantize its own activations: few tokens, and every workgroup's K range
-// (ceil(chunks / splits)) within its LDS buffer.
-bool fp8_fused_ok(int N, int K, int T, int block) {
-  if (block != 128 || T > kFusedMaxTokens || T > kGemvMaxTokens) return false;
-  const int chunks = K / 128, splits = fp8_splits(N, K, T);
-  return (chunks + splits - 1) / splits <= kFusedChunks;
+// Shape of the block-128 decode GEMV (fp8_tile_gemv_kernel): W waves and M tiles per workgroup. Many tiles
+// (q_b's 1536): 4 tiles of 4 K parts, 16 waves, so that the grid stays at a few hundred workgroups; few tiles
+// (q_kv_a's 132): 16 K parts of one tile; otherwise (o's 448) 8 K parts of one tile.
+struct TileShape {
+  int W, M;
+};
+
+TileShape fp8_tile_shape(int N, int T) {
+  const int tiles = (N / 16) * ((T + kTok - 1) / kTok);
+  if (tiles >= 1024) return {16, 4};
+  if (tiles * 16 <= 4096) return {16, 1};
+  return {8, 1};
 }
 
-// The product on quantized activations: GEMV (T <= 32) or the tiled GEMM, either with its K split over
-// fp8_splits(N, K, T) workgroups whose FP32 partial sums are added in split order: by the GEMV's last
-// workgroup per tile through the context's arrival counters and handoff buffer when they fit it
-// (kTicketPartialBytes), else written to `partial` (fp8_splits * T * N floats) and added by
-// fp8_splitk_reduce_kernel.
+// Whether fp8_tile_gemv_kernel takes the call: every wave's chunks within the 64 lanes that hold their weight
+// scales (K up to 64 x 128 x the K parts).
+bool fp8_tile_ok(int N, int K, int T) {
+  const TileShape sh = fp8_tile_shape(N, T);
+  const int kp = sh.W / sh.M;
+  return (K / 128 + kp - 1) / kp <= 64;
+}
+
+// Fused quantization passes (4 blocks of 128 each) for a wave's chunks x the tokens: 1, 2 or 4, or 0 when
+// they exceed the wave's LDS rows (the call then quantizes in its own launch).
+int fp8_tile_passes(int N, int K, int T) {
+  const TileShape sh = fp8_tile_shape(N, T);
+  const int kp = sh.W / sh.M, blocks = ((K / 128 + kp - 1) / kp) * T;
+  if (blocks > kTileQRows) return 0;
+  return blocks <= 4 ? 1 : blocks <= 8 ? 2 : 4;
+}
+
+// Whether a block-128 call runs on fp8_tile_gemv_kernel: up to kFusedMaxTokens tokens (above that the split-K
+// GEMV, whose 64-row workgroups load each activation chunk once for 4 tiles, measured faster).
+bool fp8_tile_call(int N, int K, int T, int block) {
+  return block == 128 && T <= kFusedMaxTokens && fp8_tile_ok(N, K, T);
+}
+
+// Whether the block-128 GEMV can quantize its own activations: a tile call whose every wave's blocks fit its
+// LDS rows.
+bool fp8_fused_ok(int N, int K, int T, int block) {
+  return fp8_tile_call(N, K, T, block) && fp8_tile_passes(N, K, T) > 0;
+}
+
+// The product on quantized activations: the tile GEMV (block 128, T <= kFusedMaxTokens: no K split across
+// workgroups), the split-K GEMV (T <= 32) or the tiled GEMM, the latter two with K split over fp8_splits(N,
+// K, T) workgroups whose FP32 partial sums are added in split order: by the GEMV's last workgroup per tile
+// through the context's arrival counters and handoff buffer when they fit it (kTicketPartialBytes), else
+// written to `partial` (fp8_splits * T * N floats) and added by fp8_splitk_reduce_kernel.
 // x_fused: the BF16 input when the GEMV quantizes it itself (fp8_fused_ok), else null (q and sc given).
 int launch_fp8_product(const uint8_t* blob, int N, int K, int block, const uint8_t* q, const void* sc, int T,
                        uint16_t* y, float* trace, float* partial, mx_ctx* ctx, hipStream_t st,
@@ -687,7 +834,28 @@ int launch_fp8_product(const uint8_t* blob, int N, int K, int block, const uint8
   a.partial = partial;
   a.x = x_fused;
   if (x_fused) a.xq = reinterpret_cast<const uint8_t*>(x_fused);   // not read: B comes from LDS
-  if (T <= kGemvMaxTokens) {
+  if (fp8_tile_call(N, K, T, block)) {
+    const TileShape sh = fp8_tile_shape(N, T);
+    const dim3 grid(N / 16 / sh.M, (T + kTok - 1) / kTok), threads(64 * sh.W);
+    const int P = x_fused ? fp8_tile_passes(N, K, T) : 0;
+    if (sh.M == 4) {
+      if (P == 1) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, 16, 4, 1>), grid, threads, 0, st, a);
+      else if (P == 2) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, 16, 4, 2>), grid, threads, 0, st, a);
+      else if (P == 4) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, 16, 4, 4>), grid, threads, 0, st, a);
+      else hipLaunchKernelGGL((fp8_tile_gemv_kernel<false, 16, 4, 1>), grid, threads, 0, st, a);
+    } else if (sh.W == 16) {
+      if (P == 1) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, 16, 1, 1>), grid, threads, 0, st, a);
+      else if (P == 2) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, 16, 1, 2>), grid, threads, 0, st, a);
+      else if (P == 4) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, 16, 1, 4>), grid, threads, 0, st, a);
+      else hipLaunchKernelGGL((fp8_tile_gemv_kernel<false, 16, 1, 1>), grid, threads, 0, st, a);
+    } else {
+      if (P == 1) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, 8, 1, 1>), grid, threads, 0, st, a);
+      else if (P == 2) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, 8, 1, 2>), grid, threads, 0, st, a);
+      else if (P == 4) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, 8, 1, 4>), grid, threads, 0, st, a);
+      else hipLaunchKernelGGL((fp8_tile_gemv_kernel<false, 8, 1, 1>), grid, threads, 0, st, a);
+    }
+    MX_LAUNCH_CHECK("fp8_tile_gemv_kernel");
+  } else if (T <= kGemvMaxTokens) {
     const int splits = fp8_splits(N, K, T);
     const dim3 grid(N / 64, (T + kTok - 1) / kTok, splits);
     if (splits > 1 && (size_t)grid.x * grid.y <= MX_TICKETS &&
@@ -702,9 +870,8 @@ int launch_fp8_product(const uint8_t* blob, int N, int K, int block, const uint8
       ctx->handoff_dirty[h] = ((uint64_t)splits * T * N * sizeof(float) + 15) / 16 * 16;
       ctx->handoff_half = 1 - h;
     }
-    if (block == 32) hipLaunchKernelGGL((fp8_gemv_kernel<32, false>), grid, dim3(256), 0, st, a);
-    else if (x_fused) hipLaunchKernelGGL((fp8_gemv_kernel<128, true>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((fp8_gemv_kernel<128, false>), grid, dim3(256), 0, st, a);
+    if (block == 32) hipLaunchKernelGGL(fp8_gemv_kernel<32>, grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(fp8_gemv_kernel<128>, grid, dim3(256), 0, st, a);
     MX_LAUNCH_CHECK("fp8_gemv_kernel");
     if (splits > 1 && !a.tickets) {
       const int64_t count = (int64_t)T * N;
@@ -798,7 +965,7 @@ int mx_fp8_projection(mx_ctx* ctx, const void* tiled, int32_t N, int32_t K, int3
   hipStream_t st = as_stream(stream);
   const uint64_t q_b = ((uint64_t)T * K + 255) & ~255ull;
   const uint64_t s_b = ((block == 32 ? (uint64_t)T * (K / 32) : (uint64_t)T * (K / 128) * 4) + 255) & ~255ull;
-  const uint64_t p_b = (uint64_t)fp8_splits(N, K, T) * T * N * 4;
+  const uint64_t p_b = fp8_tile_call(N, K, T, block) ? 0 : (uint64_t)fp8_splits(N, K, T) * T * N * 4;
   void* base = nullptr;
   if (int s = scratch(ctx, q_b + s_b + p_b + 256, &base)) return s;
   uint8_t* q = q_out ? q_out : (uint8_t*)base;
