@@ -87,3 +87,19 @@ def test_activation_quantizer_matches_oracle(host):
     q_ref, s_ref = quantize_activation(x)
     np.testing.assert_array_equal(s, s_ref)
     np.testing.assert_array_equal(q, q_ref)
+
+
+def test_act128_quotient_equals_the_division_over_the_quantizer_domain(host):
+    """The block-128 quantizers divide by the block scale with mx::act128_quotient (one reciprocal per
+    block, then x * inv corrected by one fused multiply-add). Exhaustively, over every BF16 x of either
+    sign (and NaN) and every scale act128_scale(amax) with |x| <= amax, amax up to infinity: the quotient
+    equals the IEEE division bit for bit wherever |x / s| >= 2^-90, and every E4M3 code equals the
+    division's -- so the quantizers' codes are those of act_quant_value(x, s), which the oracle follows."""
+    fn = host.mxh_act128_quotient_check
+    fn.restype = C.c_int64
+    fn.argtypes = [C.POINTER(C.c_int64), C.POINTER(C.c_float), C.POINTER(C.c_int64)]
+    codes, qmax, pairs = C.c_int64(), C.c_float(), C.c_int64()
+    differing = fn(C.byref(codes), C.byref(qmax), C.byref(pairs))
+    assert pairs.value > 850_000_000
+    assert codes.value == 0
+    assert differing == 0 or qmax.value < 2.0 ** -90

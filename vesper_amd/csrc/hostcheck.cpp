@@ -42,4 +42,43 @@ void mxh_act_quant32(const float* x, uint8_t* q, uint8_t* s, int64_t rows, int64
     }
 }
 
+// Exhaustive check of mx::act128_quotient against IEEE division over the quantizer's whole domain: every
+// positive BF16 amax up to infinity (amax below the floor shares the floor's scale, checked once), s =
+// act128_scale(amax), and every BF16 x of either sign with |x| <= amax, plus a NaN x (a block's amax passes
+// over NaN). Returns the number of (amax, x)
+// pairs whose quotient bits differ; *code_mismatches the number whose E4M3 codes differ, *max_quotient the
+// largest |x / s| among the differing quotients, *pairs the pairs checked.
+int64_t mxh_act128_quotient_check(int64_t* code_mismatches, float* max_quotient, int64_t* pairs) {
+  int64_t bad = 0, bad_code = 0, n = 0;
+  float qmax = 0.f;
+  const float floor = mx::u2f(mx::kAmaxFloorBits);
+  for (uint32_t a = 0; a <= 0x7F80u; ++a) {
+    const float amax = mx::u2f(a << 16);
+    const bool at_floor = !(amax > floor);
+    // below the floor every amax gives the floor's scale: check it once, with the largest such amax
+    if (at_floor && !(mx::u2f((a + 1) << 16) > floor)) continue;
+    const float s = mx::act128_scale(amax);
+    const float inv = 1.0f / s;
+    for (uint32_t v = 0; v <= a + 1; ++v)
+      for (uint32_t sign = 0; sign < 2; ++sign) {
+        // v = a + 1 stands for a NaN x
+        const float x = v <= a ? mx::u2f((v << 16) | (sign << 31)) : mx::u2f(0x7FC00000u | (sign << 31));
+        const float want = x / s, got = mx::act128_quotient(x, s, inv);
+        ++n;
+        if (want != want && got != got) continue;   // both NaN: E4M3 0x7F either way
+        if (mx::f2u(want) != mx::f2u(got)) {
+          ++bad;
+          qmax = std::fmax(qmax, std::fabs(want));
+          if (mx::e4m3_encode(want > 448.f ? 448.f : (want < -448.f ? -448.f : want)) !=
+              mx::e4m3_encode(got > 448.f ? 448.f : (got < -448.f ? -448.f : got)))
+            ++bad_code;
+        }
+      }
+  }
+  *code_mismatches = bad_code;
+  *max_quotient = qmax;
+  *pairs = n;
+  return bad;
+}
+
 }  // extern "C"

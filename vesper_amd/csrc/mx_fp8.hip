@@ -104,9 +104,22 @@ __global__ __launch_bounds__(256) void act_quant128_kernel(const uint16_t* __res
   if (lane == 0) s[b] = sc;
 }
 
+// E4M3 codes of 8 values over their block-128 scale sc: the quotients x / sc by mx::act128_quotient (one
+// reciprocal per block, then a multiply and two fused multiply-adds per value instead of an IEEE division;
+// the codes equal those of the division on every input), packed by mxd::e4m3x4 (equal to the encoder on
+// every input).
+__device__ __forceinline__ uint2 act128_codes8(const float (&v)[8], float sc) {
+  const float inv = 1.0f / sc;
+  uint2 c;
+  c.x = mxd::e4m3x4(mx::act128_quotient(v[0], sc, inv), mx::act128_quotient(v[1], sc, inv),
+                    mx::act128_quotient(v[2], sc, inv), mx::act128_quotient(v[3], sc, inv));
+  c.y = mxd::e4m3x4(mx::act128_quotient(v[4], sc, inv), mx::act128_quotient(v[5], sc, inv),
+                    mx::act128_quotient(v[6], sc, inv), mx::act128_quotient(v[7], sc, inv));
+  return c;
+}
+
 // The same quantizer with 8 values per lane (16-byte loads, 8-byte stores), 16 lanes per block, blocks in
-// a grid-stride loop; x 16-byte and q 8-byte aligned. The E4M3 packing is mxd::e4m3x4 (equal to the
-// encoder on every input) applied to the same IEEE quotients.
+// a grid-stride loop; x 16-byte and q 8-byte aligned.
 __global__ __launch_bounds__(256) void act_quant128_v8_kernel(const uint16_t* __restrict__ x, uint8_t* __restrict__ q,
                                                               float* __restrict__ s, int64_t blocks) {
   const int sub = threadIdx.x & 15;
@@ -125,10 +138,7 @@ __global__ __launch_bounds__(256) void act_quant128_v8_kernel(const uint16_t* __
 #pragma unroll
     for (int m = 8; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
     const float sc = mx::act128_scale(amax);
-    uint2 codes;
-    codes.x = mxd::e4m3x4(v[0] / sc, v[1] / sc, v[2] / sc, v[3] / sc);
-    codes.y = mxd::e4m3x4(v[4] / sc, v[5] / sc, v[6] / sc, v[7] / sc);
-    *reinterpret_cast<uint2*>(q + b * 128 + 8 * sub) = codes;
+    *reinterpret_cast<uint2*>(q + b * 128 + 8 * sub) = act128_codes8(v, sc);
     if (sub == 0) s[b] = sc;
   }
 }
@@ -414,10 +424,11 @@ __device__ __forceinline__ float chunk_scale(float swl, int i) {
 }
 
 // grid (N / 16 / M, ceil(T / 16)), 64 W threads. The 4-tile shape serves the largest grids (q_b: 384
-// workgroups of 16 waves): fused with up to 2 passes its registers fit 8 waves per SIMD, two workgroups a
-// CU, so all are resident at once (the unfused ring, which also holds activation codes, would spill).
+// workgroups of 16 waves): fused with one pass (one token) its registers fit 8 waves per SIMD, two
+// workgroups a CU, so all are resident at once (more passes, or the unfused ring, which also holds
+// activation codes, would spill).
 template <bool kFused, int W, int M, int P>
-__global__ __launch_bounds__(64 * W, (M == 4 && kFused && P < 4) ? 8 : 2) void fp8_tile_gemv_kernel(Fp8Args a) {
+__global__ __launch_bounds__(64 * W, (M == 4 && kFused && P == 1) ? 8 : 2) void fp8_tile_gemv_kernel(Fp8Args a) {
   static_assert(W % M == 0 && 4 * P <= kTileQRows, "tile GEMV shape");
   constexpr int KP = W / M;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -479,11 +490,8 @@ __global__ __launch_bounds__(64 * W, (M == 4 && kFused && P < 4) ? 8 : 2) void f
 #pragma unroll
       for (int m = 8; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
       const float sc = mx::act128_scale(amax);
-      uint2 codes;
-      codes.x = mxd::e4m3x4(v[0] / sc, v[1] / sc, v[2] / sc, v[3] / sc);
-      codes.y = mxd::e4m3x4(v[4] / sc, v[5] / sc, v[6] / sc, v[7] / sc);
       const int row = w * kRows + (b < nb ? b : 4 * P);
-      *reinterpret_cast<uint2*>(qx + row * kFusedRow + 8 * sub) = codes;
+      *reinterpret_cast<uint2*>(qx + row * kFusedRow + 8 * sub) = act128_codes8(v, sc);
       if (sub == 0) qsc[row] = sc;
     }
     // the rows are this wave's own: its LDS writes complete before its reads (no workgroup barrier)
