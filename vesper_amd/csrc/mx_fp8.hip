@@ -423,12 +423,9 @@ __device__ __forceinline__ float chunk_scale(float swl, int i) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(swl), i));
 }
 
-// grid (N / 16 / M, ceil(T / 16)), 64 W threads. The 4-tile shape serves the largest grids (q_b: 384
-// workgroups of 16 waves): fused with one pass (one token) its registers fit 8 waves per SIMD, two
-// workgroups a CU, so all are resident at once (more passes, or the unfused ring, which also holds
-// activation codes, would spill).
+// grid (N / 16 / M, ceil(T / 16)), 64 W threads.
 template <bool kFused, int W, int M, int P>
-__global__ __launch_bounds__(64 * W, (M == 4 && kFused && P == 1) ? 8 : 2) void fp8_tile_gemv_kernel(Fp8Args a) {
+__global__ __launch_bounds__(64 * W) void fp8_tile_gemv_kernel(Fp8Args a) {
   static_assert(W % M == 0 && 4 * P <= kTileQRows, "tile GEMV shape");
   constexpr int KP = W / M;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -777,17 +774,20 @@ int fp8_splits(int N, int K, int T) {
 }
 
 // Shape of the block-128 decode GEMV (fp8_tile_gemv_kernel): W waves and M tiles per workgroup. Many tiles
-// (q_b's 1536): 4 tiles of 4 K parts, 16 waves, so that the grid stays at a few hundred workgroups; few tiles
-// (q_kv_a's 132): 16 K parts of one tile; otherwise (o's 448) 8 K parts of one tile.
+// (q_b's 1536): 2 tiles of 4 K parts; few tiles (q_kv_a's 132): 8 K parts of one tile; otherwise (o's 448)
+// 2 tiles of 8 K parts. Measured on MI355X at T = 1 (us per call, weights rotated): q_b 7.7-8.6 with 2 x 4
+// against 9.6-10.2 with 4 tiles x 4 parts, 10.0 with 4 x 2 and 11.8-12.1 with 2 x 8; q_kv_a 6.6-6.7 with
+// 1 x 8 against 6.9-7.0 with 1 x 16; o 21.1-21.4 with 2 x 8 against 22.0-22.5 with 1 x 8 and 22.8 with
+// 1 x 16. A 6-chunk ring left o unchanged and slowed q_kv_a.
 struct TileShape {
   int W, M;
 };
 
 TileShape fp8_tile_shape(int N, int T) {
   const int tiles = (N / 16) * ((T + kTok - 1) / kTok);
-  if (tiles >= 1024) return {16, 4};
-  if (tiles * 16 <= 4096) return {16, 1};
-  return {8, 1};
+  if (tiles >= 1024) return {8, 2};
+  if (tiles * 16 <= 4096) return {8, 1};
+  return {16, 2};
 }
 
 // Whether fp8_tile_gemv_kernel takes the call: every wave's chunks within the 64 lanes that hold their weight
@@ -819,6 +819,16 @@ bool fp8_fused_ok(int N, int K, int T, int block) {
   return fp8_tile_call(N, K, T, block) && fp8_tile_passes(N, K, T) > 0;
 }
 
+// fp8_tile_gemv_kernel of shape (W, M): P fused quantization passes, or P = 0 when x comes quantized.
+template <int W, int M>
+void launch_tile_gemv(const Fp8Args& a, int P, dim3 grid, hipStream_t st) {
+  const dim3 threads(64 * W);
+  if (P == 1) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, W, M, 1>), grid, threads, 0, st, a);
+  else if (P == 2) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, W, M, 2>), grid, threads, 0, st, a);
+  else if (P == 4) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, W, M, 4>), grid, threads, 0, st, a);
+  else hipLaunchKernelGGL((fp8_tile_gemv_kernel<false, W, M, 1>), grid, threads, 0, st, a);
+}
+
 // The product on quantized activations: the tile GEMV (block 128, T <= kFusedMaxTokens: no K split across
 // workgroups), the split-K GEMV (T <= 32) or the tiled GEMM, the latter two with K split over fp8_splits(N,
 // K, T) workgroups whose FP32 partial sums are added in split order: by the GEMV's last workgroup per tile
@@ -844,24 +854,11 @@ int launch_fp8_product(const uint8_t* blob, int N, int K, int block, const uint8
   if (x_fused) a.xq = reinterpret_cast<const uint8_t*>(x_fused);   // not read: B comes from LDS
   if (fp8_tile_call(N, K, T, block)) {
     const TileShape sh = fp8_tile_shape(N, T);
-    const dim3 grid(N / 16 / sh.M, (T + kTok - 1) / kTok), threads(64 * sh.W);
+    const dim3 grid(N / 16 / sh.M, (T + kTok - 1) / kTok);
     const int P = x_fused ? fp8_tile_passes(N, K, T) : 0;
-    if (sh.M == 4) {
-      if (P == 1) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, 16, 4, 1>), grid, threads, 0, st, a);
-      else if (P == 2) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, 16, 4, 2>), grid, threads, 0, st, a);
-      else if (P == 4) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, 16, 4, 4>), grid, threads, 0, st, a);
-      else hipLaunchKernelGGL((fp8_tile_gemv_kernel<false, 16, 4, 1>), grid, threads, 0, st, a);
-    } else if (sh.W == 16) {
-      if (P == 1) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, 16, 1, 1>), grid, threads, 0, st, a);
-      else if (P == 2) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, 16, 1, 2>), grid, threads, 0, st, a);
-      else if (P == 4) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, 16, 1, 4>), grid, threads, 0, st, a);
-      else hipLaunchKernelGGL((fp8_tile_gemv_kernel<false, 16, 1, 1>), grid, threads, 0, st, a);
-    } else {
-      if (P == 1) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, 8, 1, 1>), grid, threads, 0, st, a);
-      else if (P == 2) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, 8, 1, 2>), grid, threads, 0, st, a);
-      else if (P == 4) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, 8, 1, 4>), grid, threads, 0, st, a);
-      else hipLaunchKernelGGL((fp8_tile_gemv_kernel<false, 8, 1, 1>), grid, threads, 0, st, a);
-    }
+    if (sh.W == 16) launch_tile_gemv<16, 2>(a, P, grid, st);
+    else if (sh.M == 2) launch_tile_gemv<8, 2>(a, P, grid, st);
+    else launch_tile_gemv<8, 1>(a, P, grid, st);
     MX_LAUNCH_CHECK("fp8_tile_gemv_kernel");
   } else if (T <= kGemvMaxTokens) {
     const int splits = fp8_splits(N, K, T);
