@@ -5,7 +5,7 @@
 BASELINE configuration 0's expert: 7168 x 2048 MXFP4 (uniform packed bytes, E8M0 codes in [118, 126];
 synthetic, generated in HBM and tiled), held in as many copies as take at least ROTATE_BYTES, consecutive
 calls using consecutive copies so that no call finds its weights in the GPU's caches from the call before.
-Each call (gate/up, SwiGLU, down: three launches) is timed with HIP events over `iters` back-to-back calls.
+Each call (gate/up with SwiGLU, down: two launches) is timed with HIP events over `iters` back-to-back calls.
 Algorithmic bytes per call: the expert's weight and scale bytes, x and y (BF16); FLOP 2 x 3 x T x H x I.
 """
 

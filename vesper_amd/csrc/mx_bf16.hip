@@ -15,16 +15,17 @@
 // 32-bit words; MFMA r of chunk c takes word r of every lane, i.e. K = 32 (4c + q) + 8r + 0..7 at lane group
 // q, and the activations are read with the same map, so every product pairs the right operands.
 //
-// Three launches on the caller's stream:
-//   gate/up (I/32 row groups x KS K-splits, 256 threads): the four waves split the workgroup's K range; all
-//     tokens in one pass (MFMA columns); partial sums per K-split to scratch [KS][T][2I];
-//   SwiGLU (T x I threads): g, u = the K-split partials summed in split order; h = silu(g) * u (* route
-//     weight) in FP32 (optionally written out with g and u), and h as two BF16 terms hi + lo for the down
-//     product (hi = bf16(h), lo = bf16(h - hi): their sum holds h to about 16 significant bits);
+// Two launches on the caller's stream:
+//   gate/up + SwiGLU (I/8 tiles, 8 waves each): workgroup j owns gate/up tile j (8 W1 rows and the same 8
+//     W3 rows) over all of K, the waves taking contiguous eighths of the chunks, all tokens in one pass
+//     (MFMA columns); the eight partial tiles are added through LDS in wave order, and the workgroup finishes
+//     its 8 intermediate positions: h = silu(g) * u (* route weight) in FP32 (optionally written out with g
+//     and u), and h as two BF16 terms hi + lo for the down product (hi = bf16(h), lo = bf16(h - hi): their
+//     sum holds h to about 16 significant bits);
 //   down (H/64 row blocks, 256 threads): W2 rows against hi and lo (two MFMAs per step), the four waves'
 //     sums added in wave order and rounded once to BF16.
-// Every sum runs in a fixed order (MFMA chains per wave, then waves, then splits), independent of T and of
-// scheduling, so a token's result does not depend on the batch it runs in.
+// Every sum runs in a fixed order (MFMA chains per wave, then waves), independent of T and of scheduling, so
+// a token's result does not depend on the batch it runs in.
 #include <algorithm>
 #include <cmath>
 
@@ -41,7 +42,7 @@ using mxd::tiled_offsets;
 using mxd::TiledOffsets;
 
 constexpr int kMaxTokens = 16;
-constexpr int kMaxSplits = 8;
+constexpr int kGuWaves = 8;      // gate/up: waves per tile, each a contiguous eighth of K
 constexpr int kMaxHidden = 8192;
 constexpr int kMaxInter = 4096;
 constexpr int kRing = 3;         // chunks of weights (and their activations) in flight per wave
@@ -52,18 +53,12 @@ using mxd::v4f;
 
 struct GateUpArgs {
   const uint8_t* blob;
-  const uint16_t* x;   // [T][H] BF16
-  float* part;         // [KS][T][2I]: g partials in [0, I), u partials in [I, 2I)
-  int H, I, T, splits;
-};
-
-struct SwigluArgs {
-  const float* part;
+  const uint16_t* x;      // [T][H] BF16
   const float* route_w;   // [T] or null
   float* h;               // [T][I] or null
   float* gu;              // [T][2I] or null
   uint16_t* hs;           // [2][T][I] BF16: hi, then lo
-  int I, T, splits;
+  int H, I, T;
 };
 
 struct DownArgs {
@@ -140,69 +135,90 @@ __device__ __forceinline__ void stream_group(const uint8_t* wp, const uint8_t* s
   }
 }
 
-// grid (I/32, KS), 256 threads. Row group g holds W1 and W3 rows [32g, 32g + 32): tile t's MFMA rows 0-7 are
-// W1 rows 32g + 8t + 0..7, rows 8-15 the same W3 rows. The workgroup's chunk range is split ks of the H/128
-// chunks, quartered over the waves.
-__global__ __launch_bounds__(256) void bf16_gateup_kernel(GateUpArgs a) {
-  __shared__ float red[4][4][64][4];
-  const int g = blockIdx.x, ks = blockIdx.y;
+// One 128-wide K chunk of one gate/up tile against up to 16 tokens: 4 MFMAs, one per word. w = this lane's 16
+// bytes of the tile, code = its E8M0 code, xv[r] = the tokens' BF16 operand for word r.
+__device__ __forceinline__ void tile_chunk_mfma(const uint4& w, uint32_t code, const uint4 (&xv)[4], v4f& acc) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp4_word_bf16(word_of(w, r), code), __builtin_bit_cast(v8bf, xv[r]),
+                                                  acc, 0, 0, 0);
+}
+
+// grid (I/8), 64 kGuWaves threads. Tile j = 4 g + t of row group g: MFMA rows 0-7 are W1 rows 8j + 0..7, rows
+// 8-15 the same W3 rows; chunk c of the tile at (g C + c) 4096 + 1024 t, its codes byte t of the chunk's scale
+// words. Wave w streams chunks [C w / 8, C (w + 1) / 8) through a register ring.
+__global__ __launch_bounds__(64 * kGuWaves) void bf16_gateup_swiglu_kernel(GateUpArgs a) {
+  __shared__ float4 red[kGuWaves][64];
+  __shared__ float tile[16][kMaxTokens + 1];
+  const int j = blockIdx.x, g = j >> 2, t = j & 3;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int H = a.H, I = a.I;
   const int chunks = H / 128;
-  const int c_lo = chunks * ks / a.splits, c_hi = chunks * (ks + 1) / a.splits;
-  const int n = c_hi - c_lo;
-  const int c0 = c_lo + n * wave / 4, c1 = c_lo + n * (wave + 1) / 4;
+  const int c0 = chunks * wave / kGuWaves, c1 = chunks * (wave + 1) / kGuWaves;
   const int q = lane >> 4, tok = min(lane & 15, a.T - 1);
-  const uint8_t* wp = a.blob + (size_t)g * chunks * 4096 + 16 * lane;
+  const uint8_t* wp = a.blob + (size_t)g * chunks * 4096 + t * 1024 + 16 * lane;
   const uint8_t* sp = a.blob + tiled_offsets(H, I).gu_s + (size_t)g * chunks * 256 + 4 * lane;
   const uint8_t* xrow = reinterpret_cast<const uint8_t*>(a.x + (size_t)tok * H) + 64 * q;
-  auto act = [&](int, int c, int r) { return xrow + (size_t)c * 256 + 16 * r; };
-  v4f acc[4];
+  uint4 w[kRing];
+  uint32_t sw[kRing];
+  uint4 xv[kRing][4];
+  auto load = [&](int k, int c) {
+    w[k] = ldg128_nt(wp + (size_t)c * 4096);
+    sw[k] = ldg32_nt(sp + (size_t)c * 256);
 #pragma unroll
-  for (int t = 0; t < 4; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
-  stream_group<1>(wp, sp, c0, c1, act, acc);
+    for (int r = 0; r < 4; ++r) xv[k][r] = ldg128(xrow + (size_t)c * 256 + 16 * r);
+  };
+  v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int k = 0; k < kRing; ++k)
+    if (c0 + k < c1) load(k, c0 + k);
+  for (int base = c0; base < c1; base += kRing) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[wave][t][lane][i] = acc[t][i];
-  __syncthreads();
-  // thread (t, lane): tile t's rows 4 (lane / 16) + 0..3 for token lane % 16, the 4 waves summed in order
-  const int t = tid >> 6, col = lane & 15;
-  if (col < a.T) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float s = ((red[0][t][lane][i] + red[1][t][lane][i]) + red[2][t][lane][i]) + red[3][t][lane][i];
-      const int m = 4 * q + i;
-      const int row = 32 * g + 8 * t + (m & 7);
-      a.part[((size_t)ks * a.T + col) * (2 * I) + (m < 8 ? row : I + row)] = s;
+    for (int k = 0; k < kRing; ++k) {
+      const int c = base + k;
+      if (c < c1) {
+        tile_chunk_mfma(w[k], (sw[k] >> (8 * t)) & 0xFF, xv[k], acc);
+        if (c + kRing < c1) load(k, c + kRing);
+      }
     }
   }
-}
-
-// grid ceil(T * I / 256), 256 threads.
-__global__ __launch_bounds__(256) void bf16_swiglu_kernel(SwigluArgs a) {
-  const int idx = blockIdx.x * 256 + threadIdx.x;
-  if (idx >= a.T * a.I) return;
-  const int tok = idx / a.I, i = idx - tok * a.I;
-  const size_t stride = (size_t)a.T * 2 * a.I;
-  const float* p = a.part + (size_t)tok * 2 * a.I;
-  float g = 0.f, u = 0.f;
-  for (int ks = 0; ks < a.splits; ++ks) {
-    g += p[ks * stride + i];
-    u += p[ks * stride + a.I + i];
+  red[wave][lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  __syncthreads();
+  if (wave == 0) {
+    // lane l holds MFMA rows 4 (l / 16) + 0..3 of token column l % 16; the waves' tiles added in wave order
+    float4 s = red[0][lane];
+#pragma unroll
+    for (int v = 1; v < kGuWaves; ++v) {
+      const float4 r = red[v][lane];
+      s.x = s.x + r.x;
+      s.y = s.y + r.y;
+      s.z = s.z + r.z;
+      s.w = s.w + r.w;
+    }
+    const int col = lane & 15;
+    tile[4 * q + 0][col] = s.x;
+    tile[4 * q + 1][col] = s.y;
+    tile[4 * q + 2][col] = s.z;
+    tile[4 * q + 3][col] = s.w;
   }
-  float h = g / (1.0f + expf(-g)) * u;
-  if (a.route_w) h *= a.route_w[tok];
+  __syncthreads();
+  // thread (token, i): intermediate position 8 j + i, gate row i and up row 8 + i of the tile
+  if (tid >= 8 * a.T) return;
+  const int n = tid >> 3, i = tid & 7, pos = 8 * j + i;
+  const float gv = tile[i][n], uv = tile[8 + i][n];
+  float h = gv / (1.0f + expf(-gv)) * uv;
+  if (a.route_w) h *= a.route_w[n];
+  const size_t idx = (size_t)n * I + pos;
   if (a.h) a.h[idx] = h;
   if (a.gu) {
-    a.gu[(size_t)tok * 2 * a.I + i] = g;
-    a.gu[(size_t)tok * 2 * a.I + a.I + i] = u;
+    a.gu[(size_t)n * 2 * I + pos] = gv;
+    a.gu[(size_t)n * 2 * I + I + pos] = uv;
   }
   const uint32_t hi = mx::bf16_bits(h);
   const float rest = h - __uint_as_float(hi << 16);
   a.hs[idx] = (uint16_t)hi;
-  a.hs[(size_t)a.T * a.I + idx] = (uint16_t)mx::bf16_bits(rest);
+  a.hs[(size_t)a.T * I + idx] = (uint16_t)mx::bf16_bits(rest);
 }
 
 // grid (H/64), 256 threads. Row block b holds W2 rows [64b, 64b + 64): tile t's MFMA rows are rows
@@ -251,9 +267,7 @@ bool is_aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) ==
 using mxi::as_stream;
 using mxi::use;
 
-static uint64_t bf16_scratch_bytes(int32_t I, int32_t T) {
-  return (uint64_t)kMaxSplits * T * 2 * I * sizeof(float) + (uint64_t)2 * T * I * sizeof(uint16_t);
-}
+static uint64_t bf16_scratch_bytes(int32_t I, int32_t T) { return (uint64_t)2 * T * I * sizeof(uint16_t); }
 
 int mx_expert_forward_bf16(mx_ctx* ctx, const void* tiled, int32_t H, int32_t I, const uint16_t* x, int32_t T,
                            const float* route_w, float* h, float* gu, uint16_t* y, void* stream) {
@@ -267,19 +281,12 @@ int mx_expert_forward_bf16(mx_ctx* ctx, const void* tiled, int32_t H, int32_t I,
   MX_REQUIRE(x && y && is_aligned(x, 16) && is_aligned(y, 8), "mx_expert_forward_bf16: x (16-byte) and y (8-byte) required");
   MX_REQUIRE(!h || is_aligned(h, 4), "mx_expert_forward_bf16: h must be 4-byte aligned");
   hipStream_t st = as_stream(stream);
-  const int groups = I / 32;
-  // enough K-splits to give the chip about 256 gate/up workgroups, at least 8 chunks per split
-  const int splits = std::max(1, std::min({kMaxSplits, (256 + groups - 1) / groups, (H / 128) / 8}));
   void* base = nullptr;
   if (int s = mxi::scratch(ctx, bf16_scratch_bytes(I, T), &base)) return s;
-  float* part = (float*)base;
-  uint16_t* hs = reinterpret_cast<uint16_t*>(part + (size_t)kMaxSplits * T * 2 * I);
-  GateUpArgs ga{(const uint8_t*)tiled, x, part, H, I, T, splits};
-  hipLaunchKernelGGL(bf16_gateup_kernel, dim3(groups, splits, 1), dim3(256), 0, st, ga);
-  MX_LAUNCH_CHECK("bf16_gateup_kernel");
-  SwigluArgs sa{part, route_w, h, gu, hs, I, T, splits};
-  hipLaunchKernelGGL(bf16_swiglu_kernel, dim3((T * I + 255) / 256), dim3(256), 0, st, sa);
-  MX_LAUNCH_CHECK("bf16_swiglu_kernel");
+  uint16_t* hs = (uint16_t*)base;
+  GateUpArgs ga{(const uint8_t*)tiled, x, route_w, h, gu, hs, H, I, T};
+  hipLaunchKernelGGL(bf16_gateup_swiglu_kernel, dim3(I / 8), dim3(64 * kGuWaves), 0, st, ga);
+  MX_LAUNCH_CHECK("bf16_gateup_swiglu_kernel");
   DownArgs da{(const uint8_t*)tiled, hs, y, H, I, T};
   hipLaunchKernelGGL(bf16_down_kernel, dim3(H / 64), dim3(256), 0, st, da);
   MX_LAUNCH_CHECK("bf16_down_kernel");
