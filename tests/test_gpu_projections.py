@@ -222,6 +222,32 @@ def test_gemv_quantizing_in_lds_equals_the_quantizer_path(gpu_ctx, tokens, rows,
         np.testing.assert_array_equal(y_f, ref["output_bf16"])
 
 
+@pytest.mark.parametrize("rows,width,tokens", [(4096, 2048, 1), (4096, 2048, 3), (16384, 1024, 1), (16384, 1024, 4),
+                                               (4096, 16384, 1), (4096, 16384, 2)])
+def test_tile_gemv_shapes_equal_the_quantizer_path_and_the_oracle(gpu_ctx, rows, width, tokens):
+    """The block-128 tile GEMV's other workgroup shapes (the test above runs 1 tile x 8 K parts): 2 tiles x 8
+    parts (256-1023 tiles) and 2 tiles x 4 parts (1024 tiles and more), with 1, 2 and 4 in-kernel
+    quantization passes, and the unfused tile kernel where a wave's blocks exceed its LDS rows (16384 wide
+    at 2 tokens). Random inputs: the same bits with or without codes requested; exact inputs: the oracle's
+    bits."""
+    rng = np.random.default_rng(tokens * 7 + rows + width)
+    w, sw = fp8_weights(rng, rows, width, 128)
+    arrays = {"layers.0.attn.p.weight": w, "layers.0.attn.p.scale": sw}
+    with NativeProjections(arrays, block=128, layout={"p": (rows, width)}) as proj:
+        bits = bf16_bits(rng.standard_normal((tokens, width)).astype(np.float32))
+        (t_q, y_q), (t_f, y_f) = project_both_ways(proj, gpu_ctx, "p", bits, rows, width)
+        np.testing.assert_array_equal(t_f.view(np.uint32), t_q.view(np.uint32))
+        np.testing.assert_array_equal(y_f, y_q)
+    w, sw, x = exact_case(128, tokens, rows, width, 2, 4, 11 * tokens + rows + width)
+    arrays = {"layers.0.attn.p.weight": w, "layers.0.attn.p.scale": sw}
+    with NativeProjections(arrays, block=128, layout={"p": (rows, width)}) as proj:
+        bits = bf16_bits(x)
+        ref = fp8_projection(bf16_values(bits), w, sw, 128)
+        (_, _), (t_f, y_f) = project_both_ways(proj, gpu_ctx, "p", bits, rows, width)
+        np.testing.assert_array_equal(t_f.view(np.uint32), ref["output_fp32"].view(np.uint32))
+        np.testing.assert_array_equal(y_f, ref["output_bf16"])
+
+
 def check_exact(block, w, sw, x):
     bits = bf16_bits(x)
     got = run_projection(block, w, sw, bits)
