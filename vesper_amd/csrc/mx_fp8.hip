@@ -375,9 +375,9 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
 // W / M partial tiles are added through LDS in K-part order. No K range is shared between workgroups, so no
 // partial sums leave the workgroup (no handoff, no reduce launch); the host picks W and M so that the launch
 // has a few thousand waves in a few hundred workgroups.
-// Fused (few tokens): each wave first quantizes its own chunks of the call's tokens (P passes of 4 blocks
-// of 128) into its LDS rows with act_quant128_v8_kernel's arithmetic, so the call needs no quantizer
-// launch.
+// Fused (few tokens): the M waves of a K part first quantize its chunks of the call's tokens (P passes of 4
+// blocks of 128 each) into the part's LDS rows with act_quant128_v8_kernel's arithmetic, so the call needs no
+// quantizer launch.
 constexpr int kTileRing = 4;
 constexpr int kTileQRows = 16;   // fused: at most 4 passes of 4 blocks per wave
 
@@ -426,7 +426,7 @@ __device__ __forceinline__ float chunk_scale(float swl, int i) {
 // grid (N / 16 / M, ceil(T / 16)), 64 W threads.
 template <bool kFused, int W, int M, int P>
 __global__ __launch_bounds__(64 * W) void fp8_tile_gemv_kernel(Fp8Args a) {
-  static_assert(W % M == 0 && 4 * P <= kTileQRows, "tile GEMV shape");
+  static_assert(W % M == 0 && 4 * P * M <= kTileQRows, "tile GEMV shape");
   constexpr int KP = W / M;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -444,19 +444,20 @@ __global__ __launch_bounds__(64 * W) void fp8_tile_gemv_kernel(Fp8Args a) {
   const uint8_t* xrow = a.xq + (size_t)rtok * a.K;
   const float* xsrow = reinterpret_cast<const float*>(a.xs) + (size_t)rtok * C;
   const int c0 = (C * kp) / KP, n = (C * (kp + 1)) / KP - c0;
-  // fused: wave w's rows, block b = i ntok + token (chunk c0 + i), 128 codes + 16 bytes of padding each,
-  // and one spare row that takes the stores of lanes past the wave's blocks (no branch around the math:
+  // fused: K part kp's rows, block b = i ntok + token (chunk c0 + i), 128 codes + 16 bytes of padding each,
+  // quantized by the part's M waves together (wave w % M takes blocks 4 P (w % M) + 0 .. 4 P - 1), then one
+  // spare row per wave that takes the stores of lanes past the part's blocks (no branch around the math:
   // branches would make the compiler wait for the weight loads before quantizing)
-  constexpr int kRows = 4 * P + 1;
-  __shared__ __attribute__((aligned(16))) uint8_t qx[kFused ? W * kRows * kFusedRow : 16];
-  __shared__ float qsc[kFused ? W * kRows : 1];
+  constexpr int kPartRows = 4 * P * M;
+  __shared__ __attribute__((aligned(16))) uint8_t qx[kFused ? (KP * kPartRows + W) * kFusedRow : 16];
+  __shared__ float qsc[kFused ? KP * kPartRows + W : 1];
   const int sub = lane & 15, grp = lane >> 4;
-  const int nb = n * ntok, nl = max(n - 1, 0);
+  const int nb = n * ntok, nl = max(n - 1, 0), b0 = 4 * P * (w % M);
   uint4 xv[kFused ? P : 1];
   if constexpr (kFused) {
 #pragma unroll
     for (int p = 0; p < P; ++p) {
-      const int b = min(4 * p + grp, max(nb - 1, 0));
+      const int b = min(b0 + 4 * p + grp, max(nb - 1, 0));
       xv[p] = ldg128(reinterpret_cast<const uint8_t*>(a.x + (size_t)(tok0 + b % ntok) * a.K +
                                                       (size_t)(c0 + b / ntok) * 128 + 8 * sub));
     }
@@ -474,7 +475,7 @@ __global__ __launch_bounds__(64 * W) void fp8_tile_gemv_kernel(Fp8Args a) {
   if constexpr (kFused) {
 #pragma unroll
     for (int p = 0; p < P; ++p) {
-      const int b = 4 * p + grp;
+      const int b = b0 + 4 * p + grp;
       const uint32_t wd[4] = {xv[p].x, xv[p].y, xv[p].z, xv[p].w};
       float v[8];
       float amax = 0.f;
@@ -487,18 +488,22 @@ __global__ __launch_bounds__(64 * W) void fp8_tile_gemv_kernel(Fp8Args a) {
 #pragma unroll
       for (int m = 8; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
       const float sc = mx::act128_scale(amax);
-      const int row = w * kRows + (b < nb ? b : 4 * P);
+      const int row = b < nb ? kp * kPartRows + b : KP * kPartRows + w;
       *reinterpret_cast<uint2*>(qx + row * kFusedRow + 8 * sub) = act128_codes8(v, sc);
       if (sub == 0) qsc[row] = sc;
     }
-    // the rows are this wave's own: its LDS writes complete before its reads (no workgroup barrier)
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if constexpr (M == 1) {
+      // the rows are this wave's own: its LDS writes complete before its reads (no workgroup barrier)
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    } else {
+      mxd::lds_barrier();   // the part's rows come from M waves; LDS only, the weight loads stay in flight
+    }
   }
   v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
   const uint32_t keep = live ? 0xFFFFFFFFu : 0u;
   const int qtok = kFused ? min(nn, ntok - 1) : 0;
-  const uint8_t* qrow = qx + (w * kRows + qtok) * kFusedRow;
-  const float* qs = qsc + w * kRows + qtok;
+  const uint8_t* qrow = qx + (kp * kPartRows + qtok) * kFusedRow;
+  const float* qs = qsc + kp * kPartRows + qtok;
   int i = 0;
   for (; i + kTileRing < n; i += kTileRing) {
 #pragma unroll
@@ -798,13 +803,15 @@ bool fp8_tile_ok(int N, int K, int T) {
   return (K / 128 + kp - 1) / kp <= 64;
 }
 
-// Fused quantization passes (4 blocks of 128 each) for a wave's chunks x the tokens: 1, 2 or 4, or 0 when
-// they exceed the wave's LDS rows (the call then quantizes in its own launch).
+// Fused quantization passes (4 blocks of 128 each per wave) for a K part's chunks x the tokens, shared by the
+// part's M waves: 1, 2 or 4, or 0 when they exceed the part's LDS rows (the call then quantizes in its own
+// launch).
 int fp8_tile_passes(int N, int K, int T) {
   const TileShape sh = fp8_tile_shape(N, T);
   const int kp = sh.W / sh.M, blocks = ((K / 128 + kp - 1) / kp) * T;
   if (blocks > kTileQRows) return 0;
-  return blocks <= 4 ? 1 : blocks <= 8 ? 2 : 4;
+  const int per_wave = (blocks + sh.M - 1) / sh.M;
+  return per_wave <= 4 ? 1 : per_wave <= 8 ? 2 : 4;
 }
 
 // Whether a block-128 call runs on fp8_tile_gemv_kernel: up to kFusedMaxTokens tokens (above that the split-K
@@ -825,8 +832,9 @@ void launch_tile_gemv(const Fp8Args& a, int P, dim3 grid, hipStream_t st) {
   const dim3 threads(64 * W);
   if (P == 1) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, W, M, 1>), grid, threads, 0, st, a);
   else if (P == 2) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, W, M, 2>), grid, threads, 0, st, a);
-  else if (P == 4) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, W, M, 4>), grid, threads, 0, st, a);
-  else hipLaunchKernelGGL((fp8_tile_gemv_kernel<false, W, M, 1>), grid, threads, 0, st, a);
+  else if (P == 4) {
+    if constexpr (16 * M <= kTileQRows) hipLaunchKernelGGL((fp8_tile_gemv_kernel<true, W, M, 4>), grid, threads, 0, st, a);
+  } else hipLaunchKernelGGL((fp8_tile_gemv_kernel<false, W, M, 1>), grid, threads, 0, st, a);
 }
 
 // The product on quantized activations: the tile GEMV (block 128, T <= kFusedMaxTokens: no K split across
