@@ -355,7 +355,8 @@ int mx_layer_destroy(mx_layer* layer);
 int mx_layer_set_expert(mx_layer* layer, int32_t expert, const void* tiled, void* stream);
 
 /* y[T][H] = MoE(x[T][H]) for 1 <= T <= max_tokens, inputs resident in HBM: router -> top-k + plan ->
- * fused gate/up + SwiGLU + down-input quantization -> down -> ordered combine (shared last).
+ * fused gate/up + SwiGLU + down-input quantization -> down -> ordered combine (shared last). At one token
+ * the top-k and plan run inside the gate/up launch (four launches).
  * `diagnostics` != 0 also writes the per-stage buffers that mx_layer_buffer exposes. */
 int mx_moe_decode(mx_layer* layer, const uint16_t* x_bf16, int32_t tokens, uint16_t* y_bf16,
                   int32_t diagnostics, void* stream);
@@ -454,8 +455,9 @@ int mx_layer_profile(mx_layer* layer, int32_t enable, float* stage_ms, int32_t* 
 
 /* Measurement hook: re-launch one stage of the layer's most recent mx_moe_decode call `iters` times
  * back to back on `stream` (each stage is idempotent given its inputs) and report the average
- * duration per launch from HIP events around the loop. Stages: MX_STAGE_*. No reference counterpart
- * (the reference times whole Python calls); used by the benchmark's roofline figure. */
+ * duration per launch from HIP events around the loop. Stages: MX_STAGE_*. After a one-token call the
+ * route-plan stage is part of the gate/up launch and launches nothing. No reference counterpart (the
+ * reference times whole Python calls); used by the benchmark's roofline figure. */
 #define MX_STAGE_ROUTER 0
 #define MX_STAGE_ROUTE_PLAN 1
 #define MX_STAGE_GATEUP 2

@@ -623,6 +623,22 @@ struct ExpertArgs {
   uint16_t* w3;
   uint16_t* din;
   float* trace;
+  // one-token decode with the routing folded into gate/up (gateup_kernel<true>): every workgroup selects the
+  // token's experts from the router's outputs itself, and workgroup (0, 0) writes the routing and the plan
+  // that the later launches read
+  const float* selection;        // [E] selection values of the token
+  const float* scores;           // [E] scores of the token
+  TopkOut topk;                  // the routing outputs (indices, weights, raw scores, denominator, tie flag)
+  Plan* plan_out;
+  int E, k, has_shared;
+  float route_scale;
+};
+
+// The gate/up workgroup's view of its slot: from the plan, or selected in the workgroup (gateup_kernel<true>).
+struct SlotView {
+  int n_slots, expert, ntok, row0, weighted;
+  int32_t tok[kMaxTokens];
+  float w[kMaxTokens];
 };
 
 // Operand layout of V_MFMA_SCALE_F32_16X16X128_F8F6F4 (measured on gfx950 with one-hot probe kernels):
@@ -1132,17 +1148,16 @@ __device__ __forceinline__ v4f reduce_tiles(const v4f (&acc)[kTiles], int wave, 
 // SwiGLU epilogue of gate/up tile t of row group g: in `mine` (the in-order chains), lane (n, q) holds token
 // column n; lanes with q < 2 hold W1 rows 4q + i of the tile (D[4q + i][n]) and lane + 32 the matching W3
 // rows. Writes the down input of token n to s_din[n][8t + 4q + i] (and the diagnostic copies when requested).
-__device__ __forceinline__ void gateup_tile_epilogue(const ExpertArgs& a, int s, int g, int t, const v4f& mine,
-                                                     int lane, int ntok, float (*s_din)[32]) {
-  const Plan* __restrict__ plan = a.plan;
+__device__ __forceinline__ void gateup_tile_epilogue(const ExpertArgs& a, const SlotView& sv, int g, int t,
+                                                     const v4f& mine, int lane, int ntok, float (*s_din)[32]) {
   float upv[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) upv[i] = __shfl_xor(mine[i], 32, 64);
   const int q = lane >> 4, n = lane & 15;
   if (q < 2 && n < ntok) {
-    const int row0 = plan->slot_row0[s];
-    const bool weighted = plan->slot_weighted[s] != 0;
-    const float rw = plan->slot_w[s][n];
+    const int row0 = sv.row0;
+    const bool weighted = sv.weighted != 0;
+    const float rw = sv.w[n];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int li = t * 8 + 4 * q + i;           // row within the 32-row block
@@ -1161,8 +1176,8 @@ __device__ __forceinline__ void gateup_tile_epilogue(const ExpertArgs& a, int s,
 
 // Per-token quantization of row group g's 32-row block of the down input (one E8M0 block per token):
 // 16 consecutive threads j2 = 0..15 take token tn, 2 values each.
-__device__ __forceinline__ void gateup_quantize_block(const ExpertArgs& a, int s, int g, int tn, int j2, int ntok,
-                                                      const float (*s_din)[32]) {
+__device__ __forceinline__ void gateup_quantize_block(const ExpertArgs& a, const SlotView& sv, int g, int tn, int j2,
+                                                      int ntok, const float (*s_din)[32]) {
   if (tn >= ntok) return;
   const int I = a.I;
   const float v0 = s_din[tn][2 * j2], v1 = s_din[tn][2 * j2 + 1];
@@ -1174,26 +1189,100 @@ __device__ __forceinline__ void gateup_quantize_block(const ExpertArgs& a, int s
   const float sc = mx::e8m0_value(code);
   const float inv = 1.0f / sc;   // exact: sc is a power of two
   const uint32_t q0 = mx::act_quant_pow2(v0, inv), q1 = mx::act_quant_pow2(v1, inv);
-  const size_t r = (size_t)(a.plan->slot_row0[s] + tn);
+  const size_t r = (size_t)(sv.row0 + tn);
   *reinterpret_cast<uint16_t*>(a.dq + r * I + g * 32 + 2 * j2) = (uint16_t)(q0 | (q1 << 8));
   if (j2 == 0) a.ds[r * (I / 32) + g] = (uint8_t)code;
+}
+
+// One-token decode, routing folded into gate/up: wave 0 selects the token's k experts from the router's
+// selection values and scores (topk_token_wave, the same selection and weights as route_plan_kernel), and
+// slot s is the selected expert with s smaller selected IDs (row s, the token's route weight), or the shared
+// expert for s = k (row k) -- route_plan_kernel's plan for one token, where pairs run expert-major. Workgroup
+// (0, 0) also writes the routing outputs and the plan itself (build_plan) for the down and combine launches
+// that follow on the stream; every workgroup computes the same selection from the same inputs.
+__device__ void select_slot_one_token(const ExpertArgs& a, int s, SlotView& sv) {
+  __shared__ int32_t s_idx[kMaxTopK];
+  __shared__ float s_w[kMaxTopK];
+  const bool first = blockIdx.x == 0 && blockIdx.y == 0;
+  if (threadIdx.x < 64) {
+    const TopkOut staged{s_idx, s_w, first ? a.topk.raw : nullptr, first ? a.topk.den : nullptr,
+                         first ? a.topk.tied : nullptr};
+    topk_token_wave(a.selection, a.scores, a.E, a.k, a.route_scale, 0, staged);
+  }
+  __syncthreads();
+  if (first) {
+    for (int i = threadIdx.x; i < a.k; i += blockDim.x) {
+      a.topk.indices[i] = s_idx[i];
+      a.topk.weights[i] = s_w[i];
+    }
+    build_plan_pairs(a.plan_out, s_idx, s_w, 1, a.k, a.E, a.has_shared);   // one token: k < 32 pairs
+  }
+  if (threadIdx.x == 0) {
+    sv.n_slots = a.k + a.has_shared;
+    sv.ntok = 1;
+    sv.tok[0] = 0;
+    if (s < a.k) {
+      int e = 0;
+      float w = 0.f;
+      for (int j = 0; j < a.k; ++j) {
+        int below = 0;
+        for (int i = 0; i < a.k; ++i) below += s_idx[i] < s_idx[j];
+        if (below == s) {
+          e = s_idx[j];
+          w = s_w[j];
+        }
+      }
+      sv.expert = e;
+      sv.row0 = s;
+      sv.weighted = 1;
+      sv.w[0] = w;
+    } else {
+      sv.expert = a.E;
+      sv.row0 = a.k;
+      sv.weighted = 0;
+      sv.w[0] = 1.0f;
+    }
+  }
+  __syncthreads();
 }
 
 // grid (I/32, slots), 256 threads, tiled experts. The workgroup computes intermediate rows [32g, 32g + 32) of
 // W1 and W3 for the slot's tokens: tile t holds W1 rows 32g + 8t + (0..7) as MFMA rows 0-7 and the same W3
 // rows as MFMA rows 8-15. Wave t streams tile t over all of K (the exact in-order core), applies the SwiGLU
 // epilogue, and the workgroup quantizes its 32-row block of the down input per token (one E8M0 block).
+// kPlanInGateup: the one-token form that selects its experts itself (a separate instantiation: the
+// selection's LDS and registers stay out of the many-token kernel, whose occupancy they would lower).
+template <bool kPlanInGateup>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void gateup_kernel(ExpertArgs a) {
-  const Plan* __restrict__ plan = a.plan;
   const int s = blockIdx.y, g = blockIdx.x;
-  if (s >= plan->n_slots) return;
   const int tid = threadIdx.x, lane = tid & 63;
+  __shared__ SlotView sv;
+  if constexpr (kPlanInGateup) {
+    select_slot_one_token(a, s, sv);
+  } else {
+    const Plan* __restrict__ plan = a.plan;
+    if (tid == 0) {
+      sv.n_slots = plan->n_slots;
+      if (s < sv.n_slots) {
+        sv.expert = plan->slot_expert[s];
+        sv.ntok = plan->slot_ntok[s];
+        sv.row0 = plan->slot_row0[s];
+        sv.weighted = plan->slot_weighted[s];
+      }
+    }
+    if (tid < kMaxTokens && s < plan->n_slots) {
+      sv.tok[tid] = plan->slot_tok[s][tid];
+      sv.w[tid] = plan->slot_w[s][tid];
+    }
+    __syncthreads();
+  }
+  if (s >= sv.n_slots) return;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q = lane >> 4, m = lane & 15, n = lane & 15;
-  const int ntok = plan->slot_ntok[s];
+  const int ntok = sv.ntok;
   const int H = a.H, I = a.I;
   const size_t chunks = H / 128;
-  const uint8_t* blob = a.tiles[plan->slot_expert[s]];
+  const uint8_t* blob = a.tiles[sv.expert];
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];   // kXStages x xstage_bytes(a.tokens)
   const uint32_t ring0 = mxd::lds_addr(ring);
   SharedCopies sc;
@@ -1204,7 +1293,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void g
   for (int i = 0; i < kMaxTokens / 4; ++i) {   // tokens wave, wave + 4, ... of the slot
     const int j = wave + 4 * i;
     sc.act_tok[i] = j;
-    sc.act_row[i] = (uint32_t)plan->slot_tok[s][j < ntok ? j : 0] * (uint32_t)(2 * H);
+    sc.act_row[i] = (uint32_t)sv.tok[j < ntok ? j : 0] * (uint32_t)(2 * H);
     if (j < ntok) sc.n_act = i + 1;
   }
   sc.dummy = exact_dummy_page;
@@ -1221,9 +1310,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void g
   v4f acc;
   stream_exact(wbase, 16 * lane, sc, xaddr, caddr, (int)chunks, acc);
   __shared__ float s_din[kMaxTokens][32];
-  gateup_tile_epilogue(a, s, g, wave, acc, lane, ntok, s_din);
+  gateup_tile_epilogue(a, sv, g, wave, acc, lane, ntok, s_din);
   __syncthreads();
-  gateup_quantize_block(a, s, g, tid >> 4, tid & 15, ntok, s_din);
+  gateup_quantize_block(a, sv, g, tid >> 4, tid & 15, ntok, s_din);
 }
 
 // Output rows [64b, 64b + 64) of slot s's W2 as 4 tiles of 16 rows; after the cross-wave sum wave t writes
@@ -1454,6 +1543,7 @@ struct mx_layer {
   uint16_t* last_y = nullptr;
   int last_T = 0;
   bool last_diag = false;
+  bool last_plan_in_gateup = false;   // the last decode call folded its routing into gate/up (one token)
   std::vector<std::pair<void*, uint64_t>> allocs;
   // profiling: events bracket each kernel of a call; a ring of kProfRing calls is recorded without
   // host synchronisation and folded into the totals when full or when the profile is read.
@@ -1599,6 +1689,7 @@ int launch_stage(mx_layer* L, int stage, hipStream_t st) {
     return MX_OK;
   }
   if (stage == MX_STAGE_ROUTE_PLAN) {
+    if (L->last_plan_in_gateup) return MX_OK;   // selected inside the gate/up launch
     hipLaunchKernelGGL(route_plan_kernel, dim3(1), dim3(64 * T), 0, st, (const float*)L->selection,
                        (const float*)L->scores, T, c.experts, c.top_k, c.route_scale,
                        TopkOut{L->indices, L->weights, L->raw, L->den, L->tied}, L->plan, L->has_shared);
@@ -1635,8 +1726,21 @@ int launch_stage(mx_layer* L, int stage, hipStream_t st) {
   const int slots = routed + L->has_shared;
   if (stage == MX_STAGE_GATEUP) {
     a.tokens = T;
-    hipLaunchKernelGGL(gateup_kernel, dim3(c.intermediate / 32, slots), dim3(256), kXStages * xstage_bytes(T), st,
-                       a);
+    if (L->last_plan_in_gateup) {
+      a.selection = (const float*)L->selection;
+      a.scores = (const float*)L->scores;
+      a.topk = TopkOut{L->indices, L->weights, L->raw, L->den, L->tied};
+      a.plan_out = L->plan;
+      a.E = c.experts;
+      a.k = c.top_k;
+      a.has_shared = L->has_shared;
+      a.route_scale = c.route_scale;
+      hipLaunchKernelGGL(gateup_kernel<true>, dim3(c.intermediate / 32, slots), dim3(256), kXStages * xstage_bytes(T),
+                         st, a);
+    } else {
+      hipLaunchKernelGGL(gateup_kernel<false>, dim3(c.intermediate / 32, slots), dim3(256), kXStages * xstage_bytes(T),
+                         st, a);
+    }
     MX_LAUNCH_CHECK("gateup_kernel");
   } else {
     hipLaunchKernelGGL(down_kernel<true>, dim3(c.hidden / 64, slots), dim3(256), 0, st, a);
@@ -1806,6 +1910,8 @@ int mx_moe_decode(mx_layer* L, const uint16_t* x, int32_t T, uint16_t* y, int32_
   L->last_y = y;
   L->last_T = T;
   L->last_diag = diagnostics != 0;
+  // one token: the gate/up launch selects the experts itself (no route_plan launch)
+  L->last_plan_in_gateup = T == 1;
   // event i + 1 closes profiled stage i: router (GEMV + top-k/plan), gate/up, down, combine
   static const int kEventAfter[5] = {-1, 1, 2, 3, 4};
   for (int stage = 0; stage < 5; ++stage) {
@@ -1834,6 +1940,7 @@ int mx_moe_decode_routed(mx_layer* L, const uint16_t* x, int32_t T, const int32_
   L->last_y = y;
   L->last_T = T;
   L->last_diag = false;
+  L->last_plan_in_gateup = false;
   for (int stage = MX_STAGE_GATEUP; stage <= MX_STAGE_COMBINE; ++stage)
     if (int s = launch_stage(L, stage, st)) return s;
   return MX_OK;
@@ -1963,7 +2070,7 @@ static int tiled_call_on(mx_ctx* ctx, uint8_t* b8, const void* tiled, int32_t H,
     a.trace = stages->trace;
   }
   a.tokens = T;
-  hipLaunchKernelGGL(gateup_kernel, dim3(I / 32, 1), dim3(256), kXStages * xstage_bytes(T), st, a);
+  hipLaunchKernelGGL(gateup_kernel<false>, dim3(I / 32, 1), dim3(256), kXStages * xstage_bytes(T), st, a);
   MX_LAUNCH_CHECK("gateup_kernel");
   hipLaunchKernelGGL(down_kernel<true>, dim3(H / 64, 1), dim3(256), 0, st, a);
   MX_LAUNCH_CHECK("down_kernel");
