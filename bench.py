@@ -351,7 +351,7 @@ def main():
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
         "per_batch": {str(t): {k: (round(v, 3) if isinstance(v, float) else v) for k, v in d.items()}
                       for t, d in per_t.items()},
-        "roofline": {"kernel": "gateup_kernel (T=16)", "bound": "hbm", "achieved": round(achieved, 1),
+        "roofline": {"kernel": "gateup_kernel<false> (T=16)", "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(head["gateup_bytes_layer0"]), "launch_us": round(gu_us, 2),
                      "algorithmic_bytes": head["gateup_bytes_layer0"],
