@@ -507,16 +507,10 @@ struct ExactStream {
     global_to_lds16(xbase + (size_t)c * 256 + boff + 64 * b,
                     __builtin_amdgcn_readfirstlane(st + kXStageB + (4 * wave + b) * 1024));
   }
+  // all of chunk c's copies
   __device__ __forceinline__ void copy(int c) const {
-    const uint32_t st = lds0 + (uint32_t)(c % kXStages) * kXStageBytes;
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-      global_to_lds16(wsrc + (size_t)c * 4096 + t * 1024, __builtin_amdgcn_readfirstlane(st + kXStageA + (4 * wave + t) * 1024));
-    global_to_lds4(ssrc + (size_t)c * 256, __builtin_amdgcn_readfirstlane(st + kXStageAS + 256 * wave));
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-      global_to_lds16(xbase + (size_t)c * 256 + boff + 64 * b,
-                      __builtin_amdgcn_readfirstlane(st + kXStageB + (4 * wave + b) * 1024));
+    for (int b = 0; b < 4; ++b) copy_block(c, b);
   }
 };
 
