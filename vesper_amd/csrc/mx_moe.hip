@@ -186,9 +186,6 @@ __device__ void topk_token_wave_t(const float* __restrict__ selection, const flo
     scr[j] = ok ? scores[e] : 0.f;
     key[j] = ok ? ordered_key(sel[j]) : 0u;
   }
-  // 1. threshold search. Each round finds the next distinct key and how many experts hold it: lanes
-  //    holding at least 1, 2, ... kPer of their keys at that value, counted by ballots.
-  uint64_t bound = 1ull << 32;   // exclusive upper bound on keys still to rank
   int taken = 0, tied = 0;
   uint32_t thr = 0;
   // While every round finds exactly one expert at a nonzero, non-NaN value, the rounds themselves are
@@ -196,7 +193,61 @@ __device__ void topk_token_wave_t(const float* __restrict__ selection, const flo
   // network below produces for distinct values; lane r keeps round r's expert.
   bool distinct = true;
   int32_t round_id = 0;
-  for (int round = 0; round < k; ++round) {
+  // 1a. Distinct rounds from sorted lanes: each lane orders its keys once (descending; invalid slots hold
+  //     key 0), then a round is the wave maximum of the lanes' first keys, and the lane holding it shifts
+  //     its keys down by one. A round whose value is held twice (by two lanes' first keys, or by the
+  //     holder's next key) or is a signed zero or NaN ends this pass, and the threshold search below runs
+  //     from the start; otherwise this pass is that search's rounds with a single candidate per lane
+  //     (one wave maximum and two ballots a round instead of a scan of every key and kPer + 1 ballots).
+  {
+    uint32_t sk[kPer];
+    int sj[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      sk[j] = lane * per + j < E ? key[j] : 0u;
+      sj[j] = j;
+    }
+#pragma unroll
+    for (int i = 1; i < kPer; ++i)
+#pragma unroll
+      for (int m = i; m >= 1; --m)
+        if (sk[m] > sk[m - 1]) {
+          const uint32_t tk = sk[m];
+          sk[m] = sk[m - 1];
+          sk[m - 1] = tk;
+          const int tj = sj[m];
+          sj[m] = sj[m - 1];
+          sj[m - 1] = tj;
+        }
+    for (int round = 0; round < k; ++round) {
+      const uint32_t best = wave_max_u(sk[0]);
+      const bool mine = sk[0] == best;
+      const uint64_t holders = __ballot(mine);
+      const uint64_t twice = kPer > 1 ? __ballot(mine && sk[kPer > 1 ? 1 : 0] == best) : 0ull;
+      if (__popcll(holders) != 1 || twice != 0ull || best == kKeyPosZero || best == kKeyNegZero ||
+          best > kKeyPosInf || best < kKeyNegInf) {
+        distinct = false;
+        break;
+      }
+      const int hit = __builtin_ctzll(holders);
+      const int32_t id = hit * per + __builtin_amdgcn_readlane(sj[0], hit);
+      if (lane == round) round_id = id;
+      if (mine) {
+#pragma unroll
+        for (int j = 0; j + 1 < kPer; ++j) {
+          sk[j] = sk[j + 1];
+          sj[j] = sj[j + 1];
+        }
+        sk[kPer - 1] = 0u;
+      }
+    }
+  }
+  // 1b. threshold search. Each round finds the next distinct key and how many experts hold it: lanes
+  //    holding at least 1, 2, ... kPer of their keys at that value, counted by ballots.
+  uint64_t bound = 1ull << 32;   // exclusive upper bound on keys still to rank
+  const bool sorted_pass = distinct;
+  distinct = true;
+  for (int round = 0; !sorted_pass && round < k; ++round) {
     uint32_t m = 0;
     bool any = false;
 #pragma unroll
