@@ -335,8 +335,8 @@ __global__ __launch_bounds__(256) void fp8_gemv_kernel(Fp8Args a) {
 #pragma unroll
     for (int zz = 0; zz < 16; ++zz)
       if (zz < S)
-        missing |= (__float_as_uint(p[zz][0].x) == mxd::kHandoffEmpty) |
-                    (__float_as_uint(p[zz][1].x) == mxd::kHandoffEmpty);
+        missing |= (int)(__float_as_uint(p[zz][0].x) == mxd::kHandoffEmpty) |
+                    (int)(__float_as_uint(p[zz][1].x) == mxd::kHandoffEmpty);
     if (missing) {
 #pragma unroll
       for (int zz = 0; zz < 16; ++zz)

@@ -103,10 +103,6 @@ __device__ __forceinline__ int wave_scan_i(int v, int /*lane*/) {
   return v;
 }
 
-__device__ __forceinline__ int wave_sum_i(int v) {
-  return __builtin_amdgcn_readlane(wave_scan_i(v, 0), 63);
-}
-
 // FP32 wavefront sum in the fixed DPP order (row scans, then across rows), result in every lane.
 __device__ __forceinline__ float wave_sum_f(float v) {
   auto step = [](float x, int y) { return x + __int_as_float(y); };
@@ -700,11 +696,6 @@ struct SlotView {
 //   scale_a / scale_b: lane l scales row / column l%16 over the 32-wide K block l/16.
 //   D: lane l, register i holds row 4*(l/16) + i, column l%16.
 // So the FP8 side of a 128-wide K chunk is read as two 16-byte pieces at 16q and 64 + 16q.
-__device__ __forceinline__ void load_b_operand(const uint8_t* chunk, int q, uint4& b0, uint4& b1) {
-  b0 = *reinterpret_cast<const uint4*>(chunk + 16 * q);
-  b1 = *reinterpret_cast<const uint4*>(chunk + 64 + 16 * q);
-}
-
 __device__ __forceinline__ v4f mfma_fp4xfp8(uint4 a, uint4 b0, uint4 b1, v4f c, int sa, int sb) {
   v8i av = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
   v8i bv = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
@@ -850,21 +841,6 @@ __device__ __forceinline__ void stream_ksplit(const W& ws, const X& x, int chunk
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 
-// 8 E2M1 values (one word, low nibble first) times 2^(code - 127), as 8 BF16 MFMA operand values (exact; the
-// conversion's scale operand carries the E8M0 code in its exponent field).
-__device__ __forceinline__ v8bf fp4_word_scaled(uint32_t word, uint32_t code) {
-  const float scale = __uint_as_float(code << 23);
-  const v2bf p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 0);
-  const v2bf p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 1);
-  const v2bf p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 2);
-  const v2bf p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 3);
-  return v8bf{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
-}
-
-__device__ __forceinline__ uint32_t ldg_u8(const uint8_t* p) {
-  return *(const __attribute__((address_space(1))) uint8_t*)(p);
-}
-
 // The core's loop runs its own memory pipeline. Each wave streams its tile's weights into a register ring;
 // the operands all four waves share -- the chunk's 256 bytes of scale words and the slot's activations -- are
 // copied once per workgroup into an LDS ring (direct global -> LDS copies) and read from there. Loads, copies
@@ -889,10 +865,7 @@ __device__ __forceinline__ u32x4_t asm_ldg128(const uint8_t* base, uint32_t off)
   asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(v) : "v"(off), "s"(base));
   return v;
 }
-// Direct global -> LDS copies of 4 (16) bytes per lane at base + off: lane l's bytes land at lds + 4 l (16 l).
-__device__ __forceinline__ void asm_copy4(const uint8_t* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" : : "v"(off), "s"(base), "s"(lds) : "m0");
-}
+// Direct global -> LDS copy of 16 bytes per lane at base + off: lane l's bytes land at lds + 16 l.
 __device__ __forceinline__ void asm_copy16(const uint8_t* base, uint32_t off, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base), "s"(lds) : "m0");
 }

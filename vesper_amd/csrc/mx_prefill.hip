@@ -7,13 +7,14 @@
 //   plan      count pairs per expert, expert-major row offsets (shared expert last) and 128-row tiles;
 //             a stable per-expert scatter gives each expert's rows in ascending token order
 //             (participation, src/vesper/moe.py:18-30) and each (token, rank) pair its row
-//   gate/up   grid (ceil(I/256), tiles), 8 multiplying waves: 8 groups of 32 intermediate rows (W1 + W3
-//             interleaved per MFMA tile, as in the tiled layout), each wave one group for all 128 tokens of
-//             the tile; 4 copy waves bring each 128-wide K chunk of the weights and of the tokens' E4M3
-//             rows global -> LDS; epilogue SwiGLU + route weight + the per-token quantization of each
+//   gate/up   grid (ceil(I/256), tiles), 8 waves: 8 groups of 32 intermediate rows (W1 + W3 interleaved
+//             per MFMA tile, as in the tiled layout), each wave one group for all 128 tokens of the tile in
+//             the block spec's exact order (one BF16 MFMA per 32-block, in-order FP32 additions), every wave
+//             copying its share of each 128-wide K chunk -- weights and the tokens' exact BF16 activation
+//             rows -- global -> LDS; epilogue SwiGLU + route weight + the per-token quantization of each
 //             32-row block of the down input
-//   down      grid (ceil(H/512), tiles), the same over 64-row groups of W2 with the tile's contiguous
-//             down-input rows
+//   down      grid (ceil(H/512), tiles), 8 multiplying waves over 64-row groups of W2 (scaled MXFP4 x E4M3
+//             MFMA) with the tile's contiguous down-input rows, 4 copy waves bringing each chunk to LDS
 //   combine   per token: its expert rows in ascending expert ID, then the shared row; FP32 from +0,
 //             one BF16 rounding (aggregation_probe.cu:4-25). The down GEMM writes each row to the
 //             token's contiguous [k + 1][H] block in that order, so the combine streams it.
@@ -417,18 +418,19 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(GemmArgs a) {
 //
 // grid (ceil(I / 256), tiles), 512 threads: 8 waves, wave w one group of 32 intermediate rows (4 MFMA
 // tiles, W1 rows 8t + 0..7 and the same W3 rows in tile t) for all 128 rows of the tile, 128 accumulator
-// registers. Every wave copies its share of chunk c + 1's operands global -> LDS (global_load_lds, kXCopies
+// registers. Every wave copies its share of chunk c + 1's operands global -> LDS (global_load_lds, nine
 // instructions: its group's four weight pieces and scale words, and token tile w's four BF16 activation
-// blocks) into a 2-stage ring; a step waits for this wave's copies of chunk c, meets the barrier, issues
-// chunk c + 1 and multiplies chunk c. (Half-chunk steps through a 4-stage ring, which copy three steps
-// ahead, and FP8 activations through a 3-stage ring, converted per wave, both measured slower: per-step
-// costs -- the barrier, the first LDS reads, the last additions -- and the conversions outweigh the deeper
-// prefetch.) Operands come from LDS with the bf16 MFMA's lane map (A lane
-// (m, q) = row m, K 8q..8q+7 of a block: word q of lane (m, b)'s 16 bytes in the tiled layout; B lane
-// (n, q) = token n, the same K: the copy puts them at lane slot 16 q + n of the (token tile, block) KB),
-// read by inline assembly and waited for explicitly (the compiler cannot see that the copies write LDS).
+// blocks) into a 2-stage ring; a step waits for this wave's copies of chunk c, meets the barrier and
+// multiplies chunk c, issuing chunk c + 1's copies a block at a time between its blocks. (Half-chunk steps
+// through a 4-stage ring, which copy three steps ahead, and FP8 activations through a 3-stage ring,
+// converted per wave, both measured slower: per-step costs -- the barrier, the first LDS reads, the last
+// additions -- and the conversions outweigh the deeper prefetch.) Operands come from LDS with the bf16
+// MFMA's lane map (A lane (m, q) = row m, K 8q..8q+7 of a block: word q of lane (m, b)'s 16 bytes in the
+// tiled layout; B lane (n, q) = token n, the same K: the copy puts them at lane slot 16 q + n of the (token
+// tile, block) KB). The reads are plain LDS loads: the copies are inline assembly, which the compiler does
+// not see writing LDS, so it places no wait for them before a read -- the wave's own vmcnt wait and the
+// barrier at the top of each step order them.
 constexpr int kXThreads = 512;
-constexpr int kXCopies = 9;
 constexpr int kXStages = 2;
 // a stage: the 8 groups' weight tiles (group w, tile t at 1 KB x (4 w + t)), their scale words (256 B per
 // group), then the activations: token tile u, block b at 1 KB x (4 u + b)
