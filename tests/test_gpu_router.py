@@ -121,3 +121,46 @@ def test_gate_projection_matches_float64_oracle():
     with GateProjection(wb) as gate:
         got = gate.project(x)
     assert max_rel_err(got, gate_logits(bf16_values(wb), x)) < 1e-5
+
+
+def test_selection_handover_at_every_round():
+    """The device ranks untied winners over each lane's sorted keys (4 experts per lane at E = 256) and
+    hands over to the threshold search from the start at the first round whose value is tied, a zero or
+    below every winner. Every hand-over position is covered: the values at places r and r + 1 of the
+    ranking (from 0; r = 7: the k-th winner and the first loser; r = 8 and 9: below the cut, no hand-over)
+    are a tie between two lanes, a tie inside one lane, a +0 / -0 pair, or a +0 above a negative value.
+    Indices, weights and the tie flag bit-exact against the oracle in every row."""
+    from oracle.router import route_weights, topk_indices
+    rng = np.random.default_rng(4242)
+    k, scale, experts = 8, 2.5, 256
+    rows = []
+    for r in range(10):
+        for pattern in ("two lanes", "one lane", "signed zeros", "zero above negative"):
+            perm = rng.permutation(experts)
+            partner = (perm[r] + 4) % experts if pattern == "two lanes" else perm[r] ^ 1
+            if pattern in ("two lanes", "one lane"):
+                j = int(np.flatnonzero(perm == partner)[0])
+                perm[[r + 1, j]] = perm[[j, r + 1]]
+                assert (perm[r] // 4 == perm[r + 1] // 4) == (pattern == "one lane")
+            sel = np.empty(experts, np.float32)
+            if pattern in ("two lanes", "one lane"):
+                sel[perm] = (1.0 - np.arange(experts) / 512.0).astype(np.float32)
+                sel[perm[r + 1]] = sel[perm[r]]
+            else:
+                pos = np.arange(experts)
+                vals = np.where(pos < r, 0.5 - pos / 1024.0, -(pos + 1) / 1024.0).astype(np.float32)
+                vals[r] = np.float32(0.0)
+                if pattern == "signed zeros":
+                    vals[r + 1] = np.float32(-0.0)
+                sel[perm] = vals
+            rows.append(sel)
+    selection = np.stack(rows)
+    scores = rng.uniform(0.01, 1.0, selection.shape).astype(np.float32)
+    with RouterProbe(experts=experts, top_k=k, score_func="sigmoid", route_scale=scale) as probe:
+        got = probe.inspect_selection(scores, selection)
+    for row in range(len(rows)):
+        ids = topk_indices(selection[row], k)
+        _, _, weights = route_weights(scores[row], ids, scale)
+        assert got["indices"][row].tolist() == ids.tolist(), row
+        np.testing.assert_array_equal(got["weights"][row].view(np.uint32), weights.view(np.uint32), err_msg=str(row))
+        assert bool(got["tied"][row]) == tie_flag(selection[row], k), row
