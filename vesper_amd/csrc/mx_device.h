@@ -133,6 +133,22 @@ __device__ __forceinline__ v4f mfma_fp4_fp8_sel(uint4 a, uint4 b0, uint4 b1, v4f
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 4, 0, kByte, (int)sa4, 0, sb);
 }
 
+// Maximum over each aligned group of lanes, in every lane of the group, by DPP (VALU steps instead of
+// LDS-routed swizzles; a maximum is exact in any order): 16-lane rows by rotations of 8, 4, 2 and 1, and
+// quads by two quad permutations. Every lane of a group must be active.
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false)));   // row_ror:8
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false)));   // row_ror:4
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x122, 0xF, 0xF, false)));   // row_ror:2
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x121, 0xF, 0xF, false)));   // row_ror:1
+  return v;
+}
+__device__ __forceinline__ float quad_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));   // [1,0,3,2]
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));   // [2,3,0,1]
+  return v;
+}
+
 // E4M3 codes of four FP32 values clamped to [-448, 448] (NaN -> 0x7F), packed low value first: equal to
 // mx::e4m3_encode(clamp(v)) for every FP32 input. The gfx950 pair conversion (round to nearest even,
 // OCP E4M3) was checked against mx::e4m3_encode on every FP32 value with |v| <= 448; it encodes NaN as

@@ -78,8 +78,7 @@ __global__ __launch_bounds__(256) void act_quant32_v8_kernel(const uint16_t* __r
       f[2 * j + 1] = mx::bf16_value(w[j] >> 16);
       amax = fmaxf(amax, fmaxf(fabsf(f[2 * j]), fabsf(f[2 * j + 1])));
     }
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 4));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 4));
+    amax = mxd::quad_max(amax);   // the block's 4 lanes are one quad
     amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
     const uint32_t code = mx::act_scale_code(amax);
     const float sc = mx::e8m0_value(code);

@@ -104,15 +104,6 @@ __global__ __launch_bounds__(256) void act_quant128_kernel(const uint16_t* __res
   if (lane == 0) s[b] = sc;
 }
 
-// maximum over each 16-lane row of the wave, in every lane of the row (DPP row rotations by 8, 4, 2, 1)
-__device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false)));
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false)));
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x122, 0xF, 0xF, false)));
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x121, 0xF, 0xF, false)));
-  return v;
-}
-
 // E4M3 codes of 8 values over their block-128 scale sc: the quotients x / sc by mx::act128_quotient (one
 // reciprocal per block, then a multiply and two fused multiply-adds per value instead of an IEEE division;
 // the codes equal those of the division on every input), packed by mxd::e4m3x4 (equal to the encoder on
@@ -144,7 +135,7 @@ __global__ __launch_bounds__(256) void act_quant128_v8_kernel(const uint16_t* __
       v[2 * i + 1] = mx::bf16_value(w[i] >> 16);
       amax = fmaxf(amax, fmaxf(fabsf(v[2 * i]), fabsf(v[2 * i + 1])));
     }
-    amax = row16_max(amax);
+    amax = mxd::row16_max(amax);
     const float sc = mx::act128_scale(amax);
     *reinterpret_cast<uint2*>(q + b * 128 + 8 * sub) = act128_codes8(v, sc);
     if (sub == 0) s[b] = sc;
@@ -493,7 +484,7 @@ __global__ __launch_bounds__(64 * W) void fp8_tile_gemv_kernel(Fp8Args a) {
         v[2 * i + 1] = mx::bf16_value(wd[i] >> 16);
         amax = fmaxf(amax, fmaxf(fabsf(v[2 * i]), fabsf(v[2 * i + 1])));
       }
-      amax = row16_max(amax);
+      amax = mxd::row16_max(amax);
       const float sc = mx::act128_scale(amax);
       const int row = b < nb ? kp * kPartRows + b : KP * kPartRows + w;
       *reinterpret_cast<uint2*>(qx + row * kFusedRow + 8 * sub) = act128_codes8(v, sc);

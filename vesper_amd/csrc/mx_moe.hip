@@ -1205,9 +1205,7 @@ __device__ __forceinline__ void gateup_quantize_block(const ExpertArgs& a, const
   if (tn >= ntok) return;
   const int I = a.I;
   const float v0 = s_din[tn][2 * j2], v1 = s_din[tn][2 * j2 + 1];
-  float amax = fmaxf(fabsf(v0), fabsf(v1));
-#pragma unroll
-  for (int mm = 8; mm >= 1; mm >>= 1) amax = fmaxf(amax, __shfl_xor(amax, mm, 16));
+  float amax = mxd::row16_max(fmaxf(fabsf(v0), fabsf(v1)));   // the token's 16 lanes are one row
   amax = fmaxf(amax, mx::u2f(mx::kAmaxFloorBits));
   const uint32_t code = mx::act_scale_code(amax);
   const float sc = mx::e8m0_value(code);
