@@ -1226,7 +1226,9 @@ __device__ void select_slot_one_token(const ExpertArgs& a, int s, SlotView& sv) 
   __shared__ int32_t s_idx[kMaxTopK];
   __shared__ float s_w[kMaxTopK];
   const bool first = blockIdx.x == 0 && blockIdx.y == 0;
-  if (threadIdx.x < 64) {
+  // the shared expert's slot (s = k) needs no selection, so its workgroups -- the last dispatched -- start
+  // streaming without waiting for it; workgroup (0, 0), which publishes the routing and the plan, is a routed slot
+  if (s < a.k && threadIdx.x < 64) {
     const TopkOut staged{s_idx, s_w, first ? a.topk.raw : nullptr, first ? a.topk.den : nullptr,
                          first ? a.topk.tied : nullptr};
     topk_token_wave(a.selection, a.scores, a.E, a.k, a.route_scale, 0, staged);
